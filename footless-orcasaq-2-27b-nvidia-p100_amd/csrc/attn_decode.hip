@@ -1,0 +1,446 @@
+// Full-attention decode / MTP-verify path for gfx950: the fp16 KV store, the
+// split-K flash-decode partials on MFMA, and the merge with the fused sigmoid
+// output gate.
+//
+// Reference behaviour restated (model/footless/cuda_sm60/kernels.cu):
+//   kv_store              465-484   rows pos0+t of a [max_pos][n_kv][256] cache
+//   attention_split_gqa   682-835   split partials (m, d, acc), per-token split
+//   attention_merge       1387-1424 M = max m, z = sum e acc / sum e d, f16_sat
+//   attn_gate             1572-1600 z = f16_sat(z * sigmoid(gate))
+//
+// Decode kernel design (one workgroup = one (sequence, kv head, split)):
+//   * The query rows of a kv head -- T tokens x G = 6 q heads, token-major,
+//     padded to 32 -- are the N columns of a 32x32x16 f16 MFMA; the split's
+//     KV rows stream through it in 32-row tiles as the M rows.
+//   * The 4 wavefronts split the head dimension: wave w owns d in [64w, 64w+64).
+//     For S^T = K Q^T each wave contracts its 64 dims (4 MFMAs) and the four
+//     partial 32x32 score tiles are summed through LDS in a fixed order, so
+//     every wave holds the identical full score tile; for O^T = V^T P^T each
+//     wave produces its own 64 output dims (2 MFMA blocks), so there is no
+//     cross-wave merge of O at the end.
+//   * The S^T accumulator layout puts one query column in each lane pair
+//     (lane l and l^32), so the online-softmax max / sum is a 16-value
+//     in-lane reduction plus one lane exchange, and the probabilities P are
+//     already the B operand of the PV MFMA (the KV order inside a 16-row
+//     k-step is permuted to match; V is read with the same permutation).
+//   * K goes straight from HBM into MFMA A-operand registers (a lane reads 64
+//     contiguous bytes of its row); V is loaded with 128-byte row segments per
+//     8 lanes and transposed into a per-wave LDS slice. The next tile's loads
+//     are issued before the current tile's math.
+//   * Tiles are 32-row aligned in absolute position and every tile a token's
+//     range does not cover is an exact no-op for that token (masked scores,
+//     p = 0, corr = 1), so a token's partial is the same bits whichever other
+//     tokens share the launch: a verify row equals the T = 1 call at its
+//     position (the reference asserts this, runtime.py:2062-2069).
+#include "fl_common.hpp"
+
+#include <limits.h>
+
+namespace {
+
+constexpr int DEC_TILE = 32;
+constexpr int DEC_HD = 256;
+constexpr int DEC_WAVES = 4;
+constexpr int DEC_THREADS = 64 * DEC_WAVES;
+constexpr int VT_PITCH = 40;   // halves per d row of the transposed V slice (32 + 8 pad)
+
+struct DecSeqs {
+    const f16* k[FL_MAX_SEQS];
+    const f16* v[FL_MAX_SEQS];
+    int pos0[FL_MAX_SEQS];
+};
+
+// Token range of split s for a token of length `seqlen`: St = clamp(seqlen /
+// split_rows, 1, split) splits over its nt = ceil(seqlen / 32) tiles, split s
+// taking tiles [nt s / St, nt (s+1) / St) (the reference's per-token rule,
+// kernels.cu:535-544, on tile boundaries). Empty (lo == hi == 0) for s >= St.
+__host__ __device__ __forceinline__ int split_count(int seqlen, int split_rows, int split) {
+    int st = seqlen / split_rows;
+    return st < 1 ? 1 : (st > split ? split : st);
+}
+
+__host__ __device__ __forceinline__ void split_range(int seqlen, int s, int split_rows, int split,
+                                                     int& lo, int& hi) {
+    const int st = split_count(seqlen, split_rows, split);
+    if (s >= st) {
+        lo = 0;
+        hi = 0;
+        return;
+    }
+    const int nt = (seqlen + DEC_TILE - 1) / DEC_TILE;
+    const int t0 = (int)((long long)nt * s / st);
+    const int t1 = (int)((long long)nt * (s + 1) / st);
+    lo = t0 * DEC_TILE;
+    hi = t1 * DEC_TILE < seqlen ? t1 * DEC_TILE : seqlen;
+}
+
+// ---------------------------------------------------------------------------
+// kv_store: 16-byte copies, one lane per 8 halves of a (token, kv head) row.
+// ---------------------------------------------------------------------------
+__global__ void kv_store_kernel(const uint4* __restrict__ k, const uint4* __restrict__ v,
+                                uint4* __restrict__ kc, uint4* __restrict__ vc, size_t layer_off,
+                                int pos0, int T, int row_u4) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= T * row_u4) return;
+    const int t = i / row_u4;
+    const size_t dst = layer_off + (size_t)(pos0 + t) * row_u4 + (i - t * row_u4);
+    kc[dst] = k[i];
+    vc[dst] = v[i];
+}
+
+// ---------------------------------------------------------------------------
+// split partials
+// ---------------------------------------------------------------------------
+struct DecTileRegs {
+    f16x8 k[4];   // K[row ql][64w + 32hh + 8ks + 0..7], ks = 0..3
+    f16x8 v[4];   // V[row 4(l&7) + i][64w + 8(l>>3) + 0..7], i = 0..3
+};
+
+__device__ __forceinline__ void dec_load_tile(DecTileRegs& r, const f16* __restrict__ kbase,
+                                              const f16* __restrict__ vbase, size_t row_stride,
+                                              int j, int uhi, int lane, int w) {
+    const int ql = lane & 31, hh = lane >> 5;
+    const int krow = j * DEC_TILE + ql;
+    if (krow < uhi) {
+        const f16x8* src = (const f16x8*)(kbase + (size_t)krow * row_stride + 64 * w + 32 * hh);
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) r.k[ks] = __builtin_nontemporal_load(src + ks);
+    } else {
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) r.k[ks] = (f16x8)(0);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int vrow = j * DEC_TILE + 4 * (lane & 7) + i;
+        if (vrow < uhi)
+            r.v[i] = __builtin_nontemporal_load(
+                (const f16x8*)(vbase + (size_t)vrow * row_stride + 64 * w + 8 * (lane >> 3)));
+        else
+            r.v[i] = (f16x8)(0);
+    }
+}
+
+__global__ void __launch_bounds__(DEC_THREADS)
+attn_decode_split_kernel(const f16* __restrict__ qg, DecSeqs seqs, float* __restrict__ pacc,
+                         float* __restrict__ pm, float* __restrict__ pd, int n_q_heads,
+                         int n_kv, int q_pitch, int T, int split, int split_rows, float sl2) {
+    __shared__ __attribute__((aligned(16))) f32x4 s_part[2][DEC_WAVES][4][64];
+    __shared__ __attribute__((aligned(16))) f16 s_vt[DEC_WAVES][64][VT_PITCH];
+
+    const int s = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int hh = lane >> 5, ql = lane & 31;
+    const int G = n_q_heads / n_kv;
+    const int R = T * G;
+    const int pos0 = seqs.pos0[b];
+    const size_t row_stride = (size_t)n_kv * DEC_HD;
+    const f16* kbase = seqs.k[b] + (size_t)h * DEC_HD;
+    const f16* vbase = seqs.v[b] + (size_t)h * DEC_HD;
+
+    // the union of the launch's tokens' ranges for this split
+    int ulo = INT_MAX, uhi = 0;
+    for (int t = 0; t < T; ++t) {
+        int lo, hi;
+        split_range(pos0 + t + 1, s, split_rows, split, lo, hi);
+        if (hi > lo) {
+            ulo = lo < ulo ? lo : ulo;
+            uhi = hi > uhi ? hi : uhi;
+        }
+    }
+    // this lane's query column: token tq, q head h*G + gq
+    const bool qvalid = ql < R;
+    const int tq = qvalid ? ql / G : 0;
+    const int gq = qvalid ? ql - tq * G : 0;
+    int qlo = 0, qhi = 0;
+    if (qvalid) split_range(pos0 + tq + 1, s, split_rows, split, qlo, qhi);
+
+    f16x8 qreg[4];
+    {
+        const f16* qrow = qg + (((size_t)b * T + tq) * n_q_heads + h * G + gq) * q_pitch + 64 * w + 32 * hh;
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) qreg[ks] = qvalid ? *(const f16x8*)(qrow + 8 * ks) : (f16x8)(0);
+    }
+
+    f32x16 o0 = (f32x16)(0.f), o1 = (f32x16)(0.f);
+    float m_run = -1e30f, l_run = 0.f;
+
+    auto body = [&](const DecTileRegs& r, int j) {
+        // partial scores of this wave's 64 dims
+        f32x16 sacc = (f32x16)(0.f);
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks)
+            sacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(r.k[ks], qreg[ks], sacc, 0, 0, 0);
+        const int buf = j & 1;
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4)
+            s_part[buf][w][r4][lane] =
+                (f32x4){sacc[4 * r4], sacc[4 * r4 + 1], sacc[4 * r4 + 2], sacc[4 * r4 + 3]};
+        // V slice, transposed to [d][kv] in this wave's LDS region
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const f16x4 col = {r.v[0][e], r.v[1][e], r.v[2][e], r.v[3][e]};
+            *(f16x4*)&s_vt[w][8 * (lane >> 3) + e][4 * (lane & 7)] = col;
+        }
+        __syncthreads();
+        // full scores, summed in wave order
+        float sc[16];
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4) {
+            const f32x4 a0 = s_part[buf][0][r4][lane], a1 = s_part[buf][1][r4][lane];
+            const f32x4 a2 = s_part[buf][2][r4][lane], a3 = s_part[buf][3][r4][lane];
+            const f32x4 t4 = ((a0 + a1) + a2) + a3;
+            sc[4 * r4] = t4[0];
+            sc[4 * r4 + 1] = t4[1];
+            sc[4 * r4 + 2] = t4[2];
+            sc[4 * r4 + 3] = t4[3];
+        }
+        // online softmax of this lane's column over the tile's 32 rows
+        float mt = -INFINITY;
+#pragma unroll
+        for (int rr = 0; rr < 16; ++rr) {
+            const int row = j * DEC_TILE + 8 * (rr >> 2) + 4 * hh + (rr & 3);
+            const bool ok = row >= qlo && row < qhi;
+            sc[rr] = ok ? sc[rr] * sl2 : -INFINITY;
+            mt = fmaxf(mt, sc[rr]);
+        }
+        mt = fmaxf(mt, lane_xor(mt, 32));
+        const float m_new = fmaxf(m_run, mt);
+        const float corr = fast_exp2(m_run - m_new);
+        float psum = 0.f;
+        f16x8 pk0, pk1;
+#pragma unroll
+        for (int rr = 0; rr < 16; ++rr) {
+            const float p = fast_exp2(sc[rr] - m_new);
+            psum += p;
+            if (rr < 8) pk0[rr] = (f16)p;
+            else pk1[rr - 8] = (f16)p;
+        }
+        psum += lane_xor(psum, 32);
+        l_run = l_run * corr + psum;
+        m_run = m_new;
+        o0 *= corr;
+        o1 *= corr;
+        // O^T += V^T P^T over the tile's two 16-row k-steps
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+            const f16x8 pb = ks ? pk1 : pk0;
+            {
+                const f16x4 lo4 = *(const f16x4*)&s_vt[w][ql][16 * ks + 4 * hh];
+                const f16x4 hi4 = *(const f16x4*)&s_vt[w][ql][16 * ks + 8 + 4 * hh];
+                const f16x8 a = {lo4[0], lo4[1], lo4[2], lo4[3], hi4[0], hi4[1], hi4[2], hi4[3]};
+                o0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pb, o0, 0, 0, 0);
+            }
+            {
+                const f16x4 lo4 = *(const f16x4*)&s_vt[w][32 + ql][16 * ks + 4 * hh];
+                const f16x4 hi4 = *(const f16x4*)&s_vt[w][32 + ql][16 * ks + 8 + 4 * hh];
+                const f16x8 a = {lo4[0], lo4[1], lo4[2], lo4[3], hi4[0], hi4[1], hi4[2], hi4[3]};
+                o1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pb, o1, 0, 0, 0);
+            }
+        }
+    };
+
+    if (uhi > ulo) {
+        const int j0 = ulo / DEC_TILE;
+        const int j1 = (uhi + DEC_TILE - 1) / DEC_TILE;
+        DecTileRegs ra, rb;
+        dec_load_tile(ra, kbase, vbase, row_stride, j0, uhi, lane, w);
+        for (int j = j0; j < j1; j += 2) {
+            if (j + 1 < j1) dec_load_tile(rb, kbase, vbase, row_stride, j + 1, uhi, lane, w);
+            body(ra, j);
+            if (j + 1 >= j1) break;
+            if (j + 2 < j1) dec_load_tile(ra, kbase, vbase, row_stride, j + 2, uhi, lane, w);
+            body(rb, j + 1);
+        }
+    }
+
+    if (qvalid) {
+        const size_t part = (((size_t)b * T + tq) * n_q_heads + h * G + gq) * split + s;
+        float* dst = pacc + part * DEC_HD + 64 * w + 4 * hh;
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4) {
+            *(f32x4*)(dst + 8 * r4) = (f32x4){o0[4 * r4], o0[4 * r4 + 1], o0[4 * r4 + 2], o0[4 * r4 + 3]};
+            *(f32x4*)(dst + 32 + 8 * r4) =
+                (f32x4){o1[4 * r4], o1[4 * r4 + 1], o1[4 * r4 + 2], o1[4 * r4 + 3]};
+        }
+        if (w == 0 && hh == 0) {
+            pm[part] = l_run > 0.f ? m_run * FL_LN2 : -1e30f;
+            pd[part] = l_run;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// merge (+ gate): one block of head_dim threads per (row, q head)
+// ---------------------------------------------------------------------------
+__global__ void attn_merge_kernel(const float* __restrict__ pacc, const float* __restrict__ pm,
+                                  const float* __restrict__ pd, f16* __restrict__ z,
+                                  const f16* __restrict__ gate, int n_q_heads, int head_dim,
+                                  int z_pitch, int g_pitch, int g_off, int split) {
+    const int head = blockIdx.x, row = blockIdx.y, d = threadIdx.x;
+    const size_t p0 = ((size_t)row * n_q_heads + head) * split;
+    float M = -1e30f;
+    for (int s = 0; s < split; ++s) M = fmaxf(M, pm[p0 + s]);
+    float num = 0.f, den = 0.f;
+    for (int s = 0; s < split; ++s) {
+        const float e = fast_exp2((pm[p0 + s] - M) * FL_LOG2E);
+        num = fmaf(e, pacc[(p0 + s) * head_dim + d], num);
+        den = fmaf(e, pd[p0 + s], den);
+    }
+    f16 zv = f16_sat(num * (1.f / den));
+    if (gate != nullptr) {
+        const float g = (float)gate[((size_t)row * n_q_heads + head) * g_pitch + g_off + d];
+        zv = f16_sat((float)zv * sigmoid_f(g));
+    }
+    z[((size_t)row * n_q_heads + head) * z_pitch + d] = zv;
+}
+
+__global__ void attn_gate_kernel(f16* __restrict__ z, const f16* __restrict__ g, int n_heads,
+                                 int head_dim, int z_pitch, int g_pitch, int g_off) {
+    const int t = blockIdx.y;
+    const int n = n_heads * head_dim;
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
+        const int hd = i / head_dim, dd = i - hd * head_dim;
+        const float gv = (float)g[((size_t)t * n_heads + hd) * g_pitch + g_off + dd];
+        f16* p = z + ((size_t)t * n_heads + hd) * z_pitch + dd;
+        *p = f16_sat((float)*p * sigmoid_f(gv));
+    }
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+int launch_split(const f16* qg, const DecSeqs& seqs, float* pacc, float* pm, float* pd, int B,
+                 int T, int n_q_heads, int n_kv, int q_pitch, int split, int split_rows,
+                 float scale, hipStream_t stream) {
+    dim3 grid(split, n_kv, B);
+    hipLaunchKernelGGL(attn_decode_split_kernel, grid, dim3(DEC_THREADS), 0, stream, qg, seqs, pacc,
+                       pm, pd, n_q_heads, n_kv, q_pitch, T, split, split_rows, scale * FL_LOG2E);
+    return fl::check_launch("attn_decode_split");
+}
+
+int check_decode_geometry(int T, int n_q_heads, int n_kv, int head_dim, int q_pitch, int split,
+                          int split_rows) {
+    FL_REQUIRE(head_dim == DEC_HD, "head_dim must be 256");
+    FL_REQUIRE(n_kv > 0 && n_q_heads > 0 && n_q_heads % n_kv == 0, "n_q_heads % n_kv_heads");
+    FL_REQUIRE(T >= 1 && T * (n_q_heads / n_kv) <= 32, "T * (n_q_heads / n_kv_heads) <= 32");
+    FL_REQUIRE(q_pitch >= head_dim && q_pitch % 8 == 0, "q_pitch >= head_dim, multiple of 8");
+    FL_REQUIRE(split >= 1 && split <= 65535, "split in [1, 65535]");
+    FL_REQUIRE(split_rows >= DEC_TILE, "split_rows >= 32");
+    return FL_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int fl_kv_store(const void* k, const void* v, void* kcache, void* vcache, int layer, int pos0,
+                int T, int n_kv_heads, int head_dim, int max_pos, fl_stream_t stream) {
+    FL_REQUIRE(k && v && kcache && vcache, "null pointer");
+    FL_REQUIRE(T >= 0 && pos0 >= 0 && layer >= 0, "T, pos0, layer >= 0");
+    FL_REQUIRE(head_dim % 8 == 0 && n_kv_heads > 0, "head_dim % 8 == 0");
+    FL_REQUIRE(pos0 + T <= max_pos, "pos0 + T <= max_pos");
+    FL_REQUIRE(aligned16(k) && aligned16(v) && aligned16(kcache) && aligned16(vcache),
+               "16-byte aligned buffers");
+    if (T == 0) return FL_OK;
+    const int row_u4 = n_kv_heads * head_dim / 8;
+    const size_t layer_off = (size_t)layer * max_pos * row_u4;
+    const int n = T * row_u4;
+    hipLaunchKernelGGL(kv_store_kernel, dim3((n + 255) / 256), dim3(256), 0, (hipStream_t)stream,
+                       (const uint4*)k, (const uint4*)v, (uint4*)kcache, (uint4*)vcache, layer_off,
+                       pos0, T, row_u4);
+    return fl::check_launch("kv_store");
+}
+
+int fl_attention_split_gqa(const void* q, const void* kcache, const void* vcache, float* pacc,
+                           float* pm, float* pd, int layer, int n_q_heads, int n_kv_heads,
+                           int head_dim, int q_pitch, int pos0, int max_pos, float scale,
+                           int split_rows, int T, int split, fl_stream_t stream) {
+    int rc = check_decode_geometry(T, n_q_heads, n_kv_heads, head_dim, q_pitch, split, split_rows);
+    if (rc) return rc;
+    FL_REQUIRE(q && kcache && vcache && pacc && pm && pd, "null pointer");
+    FL_REQUIRE(pos0 >= 0 && layer >= 0 && pos0 + T <= max_pos, "pos0 + T <= max_pos");
+    FL_REQUIRE(aligned16(q) && aligned16(kcache) && aligned16(vcache) && aligned16(pacc),
+               "16-byte aligned buffers");
+    DecSeqs seqs = {};
+    const size_t off = (size_t)layer * max_pos * n_kv_heads * head_dim;
+    seqs.k[0] = (const f16*)kcache + off;
+    seqs.v[0] = (const f16*)vcache + off;
+    seqs.pos0[0] = pos0;
+    return launch_split((const f16*)q, seqs, pacc, pm, pd, 1, T, n_q_heads, n_kv_heads, q_pitch,
+                        split, split_rows, scale, (hipStream_t)stream);
+}
+
+int fl_attention_merge(const float* pacc, const float* pm, const float* pd, void* z,
+                       int n_q_heads, int head_dim, int z_pitch, int T, int split,
+                       const void* gate, int g_pitch, int g_off, fl_stream_t stream) {
+    FL_REQUIRE(pacc && pm && pd && z, "null pointer");
+    FL_REQUIRE(head_dim >= 1 && head_dim <= 1024 && z_pitch >= head_dim, "head_dim, z_pitch");
+    FL_REQUIRE(T >= 1 && split >= 1 && n_q_heads >= 1, "T, split, n_q_heads >= 1");
+    FL_REQUIRE(gate == nullptr || g_off + head_dim <= g_pitch, "g_off + head_dim <= g_pitch");
+    hipLaunchKernelGGL(attn_merge_kernel, dim3(n_q_heads, T), dim3(head_dim), 0,
+                       (hipStream_t)stream, pacc, pm, pd, (f16*)z, (const f16*)gate, n_q_heads,
+                       head_dim, z_pitch, g_pitch, g_off, split);
+    return fl::check_launch("attn_merge");
+}
+
+int fl_attn_gate(void* z, const void* g, int n_heads, int head_dim, int z_pitch, int g_pitch,
+                 int g_off, int T, fl_stream_t stream) {
+    FL_REQUIRE(z && g, "null pointer");
+    FL_REQUIRE(T >= 1 && n_heads >= 1 && head_dim >= 1, "T, n_heads, head_dim >= 1");
+    FL_REQUIRE(z_pitch >= head_dim && g_off + head_dim <= g_pitch, "pitches");
+    const int n = n_heads * head_dim;
+    hipLaunchKernelGGL(attn_gate_kernel, dim3((n + 255) / 256, T), dim3(256), 0,
+                       (hipStream_t)stream, (f16*)z, (const f16*)g, n_heads, head_dim, z_pitch,
+                       g_pitch, g_off);
+    return fl::check_launch("attn_gate");
+}
+
+size_t fl_attn_decode_work_bytes(int B, int T, int n_q_heads, int head_dim, int split) {
+    if (B < 1 || T < 1 || n_q_heads < 1 || head_dim < 1 || split < 1) return 0;
+    const size_t parts = (size_t)B * T * n_q_heads * split;
+    const size_t acc = parts * head_dim * sizeof(float);
+    return acc + 2 * parts * sizeof(float);
+}
+
+int fl_attn_decode(const void* qg, int q_pitch, const void* const* kcache,
+                   const void* const* vcache, const int* pos0, const int* cap, int B, int T,
+                   int n_q_heads, int n_kv_heads, int head_dim, float scale, int split_rows,
+                   int split, const void* gate, int g_pitch, int g_off, void* z, int z_pitch,
+                   void* work, size_t work_bytes, fl_stream_t stream) {
+    int rc = check_decode_geometry(T, n_q_heads, n_kv_heads, head_dim, q_pitch, split, split_rows);
+    if (rc) return rc;
+    FL_REQUIRE(B >= 1 && B <= FL_MAX_SEQS, "1 <= B <= FL_MAX_SEQS");
+    FL_REQUIRE(qg && kcache && vcache && pos0 && cap && z && work, "null pointer");
+    FL_REQUIRE(z_pitch >= head_dim, "z_pitch >= head_dim");
+    FL_REQUIRE(gate == nullptr || g_off + head_dim <= g_pitch, "g_off + head_dim <= g_pitch");
+    FL_REQUIRE(aligned16(qg) && aligned16(work), "16-byte aligned qg / work");
+    if (work_bytes < fl_attn_decode_work_bytes(B, T, n_q_heads, head_dim, split)) {
+        fl::set_error("work: %zu bytes, fl_attn_decode_work_bytes asks %zu", work_bytes,
+                      fl_attn_decode_work_bytes(B, T, n_q_heads, head_dim, split));
+        return FL_ESCRATCH;
+    }
+    DecSeqs seqs = {};
+    int grid_split = 1;
+    for (int b = 0; b < B; ++b) {
+        FL_REQUIRE(kcache[b] && vcache[b], "null cache pointer");
+        FL_REQUIRE(aligned16(kcache[b]) && aligned16(vcache[b]), "16-byte aligned caches");
+        FL_REQUIRE(pos0[b] >= 0 && pos0[b] + T <= cap[b], "pos0[b] + T <= cap[b]");
+        seqs.k[b] = (const f16*)kcache[b];
+        seqs.v[b] = (const f16*)vcache[b];
+        seqs.pos0[b] = pos0[b];
+        const int st = split_count(pos0[b] + T, split_rows, split);
+        grid_split = st > grid_split ? st : grid_split;
+    }
+    const size_t parts = (size_t)B * T * n_q_heads * grid_split;
+    float* pacc = (float*)work;
+    float* pm = pacc + parts * head_dim;
+    float* pd = pm + parts;
+    rc = launch_split((const f16*)qg, seqs, pacc, pm, pd, B, T, n_q_heads, n_kv_heads, q_pitch,
+                      grid_split, split_rows, scale, (hipStream_t)stream);
+    if (rc) return rc;
+    hipLaunchKernelGGL(attn_merge_kernel, dim3(n_q_heads, B * T), dim3(head_dim), 0,
+                       (hipStream_t)stream, pacc, pm, pd, (f16*)z, (const f16*)gate, n_q_heads,
+                       head_dim, z_pitch, g_pitch, g_off, grid_split);
+    return fl::check_launch("attn_merge");
+}
+
+}  // extern "C"

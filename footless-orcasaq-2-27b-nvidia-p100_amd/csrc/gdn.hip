@@ -1,0 +1,475 @@
+// Gated DeltaNet decode / recurrent path for gfx950: causal conv1d, the q/k
+// L2 norm, the beta / decay gates, the gated delta rule, and the fused
+// batched decode step.
+//
+// Reference behaviour restated (model/footless/cuda_sm60/kernels.cu):
+//   conv1d_causal        1606-1679  E = [state | x], y = silu(w . E), state tail
+//   conv1d_causal_rows   1681-1714  verify rows with a state per row
+//   l2norm_scaled         360-391   y = x / sqrt(sum x^2 + eps) * scale
+//   gdn_scalars          1716-1748  beta = sigmoid(b), decay = exp(-e^A softplus)
+//   gdn_scan(_rows)      1750-1901, 2809-2914   the delta rule, S in place
+//   gdn_scan_rows_f      2943-3070  the fused decode / verify step
+//
+// State layout: S [n_vheads][V rows][K cols] fp32, a head is 64 KiB. The
+// delta-rule kernels give a workgroup 32 rows of one head (8 lanes a row,
+// 16 columns a lane = four float4 at columns c0 + 32j, c0 = 4 (lane % 8)),
+// so each 8-lane group reads a row's 128 contiguous bytes per load and the
+// row's dot products reduce inside the group with DPP (quad_perm xor 1,
+// xor 2, then the half-row mirror). The state of the workgroup's rows stays
+// in registers for the whole call: loaded once, stored once.
+#include "fl_common.hpp"
+
+#pragma clang fp contract(off)
+
+namespace {
+
+constexpr int GR_ROWS = 32;       // state rows a workgroup
+constexpr int GR_THREADS = 256;   // 8 lanes a row
+constexpr int GR_K = 128;
+constexpr int GR_TC = 16;         // tokens staged a time by the scan
+
+// Sum over the 8 lanes of a row group; every lane gets the same bits.
+__device__ __forceinline__ float row8_sum(float v) {
+    v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, true));
+    v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, true));
+    v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xF, 0xF, true));
+    return v;
+}
+
+__device__ __forceinline__ float softplus20(float x) { return x <= 20.f ? log1pf(expf(x)) : x; }
+
+// One token of the delta rule on a lane's 16 columns (`reg`), with k and q
+// (fp32 values of fp16 numbers) at columns c0 + 32j + 0..3. Returns the row's
+// output o = S_new . q (identical in the 8 lanes of the row). The dots run in
+// two chains (even / odd register) summed, then over the row's lanes -- the
+// reference's gdn_scan_rows order (kernels.cu:2866-2905).
+__device__ __forceinline__ float delta_rule_token(float (&reg)[16], const float* kk,
+                                                  const float* qq, float vt, float bt, float dt) {
+    float m0 = 0.f, m1 = 0.f;
+#pragma unroll
+    for (int c = 0; c < 16; c += 2) {
+        reg[c] = reg[c] * dt;
+        reg[c + 1] = reg[c + 1] * dt;
+        m0 = fmaf(reg[c], kk[c], m0);
+        m1 = fmaf(reg[c + 1], kk[c + 1], m1);
+    }
+    const float m = row8_sum(m0 + m1);
+    const float delta = bt * (vt - m);
+    float o0 = 0.f, o1 = 0.f;
+#pragma unroll
+    for (int c = 0; c < 16; c += 4) {
+        reg[c] = fmaf(delta, kk[c], reg[c]);
+        reg[c + 1] = fmaf(delta, kk[c + 1], reg[c + 1]);
+        reg[c + 2] = fmaf(delta, kk[c + 2], reg[c + 2]);
+        reg[c + 3] = fmaf(delta, kk[c + 3], reg[c + 3]);
+        o0 = fmaf(reg[c], qq[c], o0);
+        o1 = fmaf(reg[c + 1], qq[c + 1], o1);
+        o0 = fmaf(reg[c + 2], qq[c + 2], o0);
+        o1 = fmaf(reg[c + 3], qq[c + 3], o1);
+    }
+    return row8_sum(o0 + o1);
+}
+
+__device__ __forceinline__ void load_row16(float (&reg)[16], const float* src) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const f32x4 v4 = *(const f32x4*)(src + 32 * j);
+        reg[4 * j] = v4[0];
+        reg[4 * j + 1] = v4[1];
+        reg[4 * j + 2] = v4[2];
+        reg[4 * j + 3] = v4[3];
+    }
+}
+
+__device__ __forceinline__ void store_row16(float* dst, const float (&reg)[16]) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+        *(f32x4*)(dst + 32 * j) = (f32x4){reg[4 * j], reg[4 * j + 1], reg[4 * j + 2], reg[4 * j + 3]};
+}
+
+// gather a lane's 16 columns of a staged 128-wide fp32 row
+__device__ __forceinline__ void gather16(float (&dst)[16], const float* row, int c0) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const f32x4 v4 = *(const f32x4*)(row + c0 + 32 * j);
+        dst[4 * j] = v4[0];
+        dst[4 * j + 1] = v4[1];
+        dst[4 * j + 2] = v4[2];
+        dst[4 * j + 3] = v4[3];
+    }
+}
+
+// ---------------------------------------------------------------------------
+// a8 / a9: conv
+// ---------------------------------------------------------------------------
+__global__ void conv1d_causal_kernel(const f16* __restrict__ x, const f16* __restrict__ w,
+                                     const f16* __restrict__ st_in, f16* __restrict__ y,
+                                     f16* __restrict__ st_out, int dim, int T, int pos0,
+                                     int row_stride, int width) {
+    const int t = blockIdx.y;
+    const int d = blockIdx.x * blockDim.x + threadIdx.x;
+    if (d >= dim) return;
+    const int sl = width - 1;
+    const f16* st = st_in + (size_t)d * sl;
+    float acc = 0.f;
+    for (int j = 0; j < width; ++j) {
+        const int i = t + j;
+        float e = 0.f;
+        if (i < sl) {
+            if (pos0 > 0) e = (float)st[i];
+        } else {
+            e = (float)x[(size_t)(i - sl) * row_stride + d];
+        }
+        acc = fmaf((float)w[(size_t)d * width + j], e, acc);
+    }
+    y[(size_t)t * row_stride + d] = f16_sat(silu_f(acc));
+    if (t == T - 1) {
+        f16* so = st_out + (size_t)d * sl;
+        for (int k = 0; k < sl; ++k) {
+            const int i = T + k;
+            float e = 0.f;
+            if (i < sl) {
+                if (pos0 > 0) e = (float)st[i];
+            } else {
+                e = (float)x[(size_t)(i - sl) * row_stride + d];
+            }
+            so[k] = f16_sat(e);
+        }
+    }
+}
+
+__global__ void conv1d_causal_rows_kernel(const f16* __restrict__ x, const f16* __restrict__ w,
+                                          const f16* st_in, f16* __restrict__ y, f16* st0,
+                                          f16* st1, f16* st2, int dim, int T, int pos0,
+                                          int row_stride) {
+    const int d = blockIdx.x * blockDim.x + threadIdx.x;
+    if (d >= dim) return;
+    float e[3];
+#pragma unroll
+    for (int i = 0; i < 3; ++i) e[i] = pos0 > 0 ? (float)st_in[(size_t)d * 3 + i] : 0.f;
+    float wv[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) wv[j] = (float)w[(size_t)d * 4 + j];
+    f16* dst[3] = {st0, st1, st2};
+#pragma unroll
+    for (int t = 0; t < 3; ++t) {
+        if (t >= T) break;
+        const float xt = (float)x[(size_t)t * row_stride + d];
+        float acc = 0.f;
+        acc = fmaf(wv[0], e[0], acc);
+        acc = fmaf(wv[1], e[1], acc);
+        acc = fmaf(wv[2], e[2], acc);
+        acc = fmaf(wv[3], xt, acc);
+        y[(size_t)t * row_stride + d] = f16_sat(silu_f(acc));
+        e[0] = e[1];
+        e[1] = e[2];
+        e[2] = (float)f16_sat(xt);
+        f16* so = dst[t] + (size_t)d * 3;
+        so[0] = f16_sat(e[0]);
+        so[1] = f16_sat(e[1]);
+        so[2] = f16_sat(e[2]);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// a10: L2 norm, one 128-thread block a (row, token)
+// ---------------------------------------------------------------------------
+__global__ void l2norm_kernel(const f16* __restrict__ x, f16* __restrict__ y, int n, int rows,
+                              int pitch, float eps, float scale) {
+    __shared__ float red[2];
+    const int t = blockIdx.y, r = blockIdx.x;
+    const f16* xr = x + ((size_t)t * rows + r) * pitch;
+    f16* yr = y + ((size_t)t * rows + r) * pitch;
+    float ss = 0.f;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        const float v = (float)xr[i];
+        ss = fmaf(v, v, ss);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) ss += lane_xor(ss, o);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    const float den = sqrtf((red[0] + red[1]) + eps);
+    for (int i = threadIdx.x; i < n; i += blockDim.x) yr[i] = f16_sat(((float)xr[i] / den) * scale);
+}
+
+// ---------------------------------------------------------------------------
+// a11: gates
+// ---------------------------------------------------------------------------
+__global__ void gdn_scalars_kernel(const float* __restrict__ a, const float* __restrict__ b,
+                                   const float* __restrict__ A_log,
+                                   const float* __restrict__ dt_bias, float* __restrict__ beta,
+                                   float* __restrict__ decay, int n_heads, int a_stride,
+                                   int b_stride) {
+    const int t = blockIdx.y;
+    const int h = blockIdx.x * blockDim.x + threadIdx.x;
+    if (h >= n_heads) return;
+    beta[(size_t)t * n_heads + h] = sigmoid_f(b[(size_t)t * b_stride + h]);
+    const float sp = softplus20(a[(size_t)t * a_stride + h] + dt_bias[h]);
+    decay[(size_t)t * n_heads + h] = expf(-expf(A_log[h]) * sp);
+}
+
+// ---------------------------------------------------------------------------
+// a12: the delta rule over T tokens, 16 tokens of k / q / v / gates staged in
+// LDS at a time. grid (V / 32, n_vheads), block 256.
+// ---------------------------------------------------------------------------
+__global__ void __launch_bounds__(GR_THREADS)
+gdn_scan_kernel(const f16* __restrict__ q, const f16* __restrict__ k, const f16* __restrict__ v,
+                const float* __restrict__ beta, const float* __restrict__ decay,
+                float* __restrict__ S, f16* __restrict__ y, int T, int n_vheads, int V,
+                int qk_stride, int v_stride, int y_stride, float out_scale, int group,
+                float* __restrict__ Ck, long long ck_step) {
+    __shared__ __attribute__((aligned(16))) float sk[GR_TC][GR_K];
+    __shared__ __attribute__((aligned(16))) float sq[GR_TC][GR_K];
+    __shared__ float sv[GR_TC][GR_ROWS];
+    __shared__ float sb[GR_TC], sd[GR_TC];
+    const int hv = blockIdx.y, hk = hv / group;
+    const int tid = threadIdx.x, ri = tid >> 3, c0 = 4 * (tid & 7);
+    const int vi = blockIdx.x * GR_ROWS + ri;
+    float* Srow = S + ((size_t)hv * V + vi) * GR_K + c0;
+    float reg[16];
+    load_row16(reg, Srow);
+    for (int t0 = 0; t0 < T; t0 += GR_TC) {
+        const int n = min(GR_TC, T - t0);
+        __syncthreads();
+        for (int i = tid; i < n * 64; i += GR_THREADS) {
+            const int tt = i >> 6, c = (i & 63) * 2;
+            const size_t a = (size_t)(t0 + tt) * qk_stride + (size_t)hk * GR_K + c;
+            sk[tt][c] = (float)k[a];
+            sk[tt][c + 1] = (float)k[a + 1];
+            sq[tt][c] = (float)q[a];
+            sq[tt][c + 1] = (float)q[a + 1];
+        }
+        for (int i = tid; i < n * GR_ROWS; i += GR_THREADS) {
+            const int tt = i / GR_ROWS, r = i - tt * GR_ROWS;
+            sv[tt][r] = (float)v[(size_t)(t0 + tt) * v_stride + (size_t)hv * V + blockIdx.x * GR_ROWS + r];
+        }
+        if (tid < n) {
+            sb[tid] = beta[(size_t)(t0 + tid) * n_vheads + hv];
+            sd[tid] = decay[(size_t)(t0 + tid) * n_vheads + hv];
+        }
+        __syncthreads();
+        for (int tt = 0; tt < n; ++tt) {
+            float kk[16], qq[16];
+            gather16(kk, sk[tt], c0);
+            gather16(qq, sq[tt], c0);
+            const float o = delta_rule_token(reg, kk, qq, sv[tt][ri], sb[tt], sd[tt]);
+            if (c0 == 0) y[(size_t)(t0 + tt) * y_stride + (size_t)hv * V + vi] = f16_sat(o * out_scale);
+            const int t = t0 + tt;
+            if (Ck != nullptr && t < T - 1)
+                store_row16(Ck + (size_t)t * ck_step + ((size_t)hv * V + vi) * GR_K + c0, reg);
+        }
+    }
+    store_row16(Srow, reg);
+}
+
+// ---------------------------------------------------------------------------
+// a13: the fused decode / verify step of B sequences.
+// grid (V / 32, n_vheads, B), block 256.
+// ---------------------------------------------------------------------------
+struct GdnSeqs {
+    float* S[FL_MAX_SEQS];
+    const f16* cst_in[FL_MAX_SEQS];
+    f16* cst_out[FL_MAX_SEQS];
+    float* Ck[FL_MAX_SEQS];
+    int pos0[FL_MAX_SEQS];
+};
+
+// conv1d_causal at T = 1 for channel d (width 4): returns the fp16-rounded
+// output, writes the new state when st_out is given.
+__device__ __forceinline__ float conv1_ch(const f16* __restrict__ x, const f16* __restrict__ w,
+                                          const f16* __restrict__ st_in, f16* st_out, int d,
+                                          int pos0) {
+    const f16* st = st_in + (size_t)d * 3;
+    const float s0 = pos0 > 0 ? (float)st[0] : 0.f;
+    const float s1 = pos0 > 0 ? (float)st[1] : 0.f;
+    const float s2 = pos0 > 0 ? (float)st[2] : 0.f;
+    const float xv = (float)x[d];
+    float acc = 0.f;
+    acc = fmaf((float)w[(size_t)d * 4 + 0], s0, acc);
+    acc = fmaf((float)w[(size_t)d * 4 + 1], s1, acc);
+    acc = fmaf((float)w[(size_t)d * 4 + 2], s2, acc);
+    acc = fmaf((float)w[(size_t)d * 4 + 3], xv, acc);
+    if (st_out != nullptr) {
+        f16* so = st_out + (size_t)d * 3;
+        so[0] = f16_sat(s1);
+        so[1] = f16_sat(s2);
+        so[2] = f16_sat(xv);
+    }
+    return (float)f16_sat(silu_f(acc));
+}
+
+__global__ void __launch_bounds__(GR_THREADS)
+gdn_decode_kernel(const f16* __restrict__ x, int x_stride, int conv_fused,
+                  const f16* __restrict__ conv_w, GdnSeqs seqs, const float* __restrict__ ga,
+                  const float* __restrict__ gb, int ab_stride, const float* __restrict__ A_log,
+                  const float* __restrict__ dt_bias, f16* __restrict__ y, int y_stride,
+                  long long ck_step, int T, int n_kheads, int n_vheads, int V, float out_scale,
+                  float l2eps, int group) {
+    __shared__ __attribute__((aligned(16))) float sk[GR_K];
+    __shared__ __attribute__((aligned(16))) float sq[GR_K];
+    __shared__ float red[4];
+    const int rb = blockIdx.x, hv = blockIdx.y, b = blockIdx.z;
+    const int hk = hv / group;
+    const int tid = threadIdx.x, ri = tid >> 3, c0 = 4 * (tid & 7);
+    const int vi = rb * GR_ROWS + ri;
+    float* Srow = seqs.S[b] + ((size_t)hv * V + vi) * GR_K + c0;
+    float* Ck = seqs.Ck[b];
+    const int pos0 = seqs.pos0[b];
+    float reg[16];
+    load_row16(reg, Srow);
+    const float dtb = dt_bias[hv], al = expf(A_log[hv]);
+    const int ch_k = n_kheads * GR_K + hk * GR_K, ch_q = hk * GR_K;
+    const int ch_v = 2 * n_kheads * GR_K + hv * V + vi;
+    for (int t = 0; t < T; ++t) {
+        const size_t bt_row = (size_t)b * T + t;
+        const f16* xr = x + bt_row * x_stride;
+        const float bt = sigmoid_f(gb[bt_row * ab_stride + hv]);
+        const float dt = expf(-al * softplus20(ga[bt_row * ab_stride + hv] + dtb));
+        // this thread's q (tid >= 128) or k (tid < 128) channel, and the row's v
+        const int half_ = tid >> 7, i = tid & 127;
+        float xv, vt;
+        if (conv_fused) {
+            const bool own = (hv % group) == 0 && rb == 0;   // one workgroup stores q / k state
+            xv = conv1_ch(xr, conv_w, seqs.cst_in[b], own ? seqs.cst_out[b] : nullptr,
+                          (half_ ? ch_q : ch_k) + i, pos0);
+            vt = conv1_ch(xr, conv_w, seqs.cst_in[b], c0 == 0 ? seqs.cst_out[b] : nullptr, ch_v,
+                          pos0);
+        } else {
+            xv = (float)xr[(half_ ? ch_q : ch_k) + i];
+            vt = (float)xr[ch_v];
+        }
+        // L2 norms: k over waves 0-1, q over waves 2-3
+        float ss = xv * xv;
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) ss += lane_xor(ss, o);
+        if ((tid & 63) == 0) red[tid >> 6] = ss;
+        __syncthreads();
+        const float den = sqrtf((red[2 * half_] + red[2 * half_ + 1]) + l2eps);
+        (half_ ? sq : sk)[i] = (float)f16_sat(xv / den);
+        __syncthreads();
+        float kk[16], qq[16];
+        gather16(kk, sk, c0);
+        gather16(qq, sq, c0);
+        const float o = delta_rule_token(reg, kk, qq, vt, bt, dt);
+        if (c0 == 0) y[bt_row * y_stride + (size_t)hv * V + vi] = f16_sat(o * out_scale);
+        if (Ck != nullptr && t < T - 1)
+            store_row16(Ck + (size_t)t * ck_step + ((size_t)hv * V + vi) * GR_K + c0, reg);
+        __syncthreads();   // sk / sq / red are rewritten by the next token
+    }
+    store_row16(Srow, reg);
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+}  // namespace
+
+extern "C" {
+
+int fl_conv1d_causal(const void* x, const void* w, const void* st_in, void* y, void* st_out,
+                     int dim, int T, int pos0, int row_stride, int width, fl_stream_t stream) {
+    FL_REQUIRE(x && w && st_in && y && st_out, "null pointer");
+    FL_REQUIRE(st_in != st_out, "st_in and st_out must be distinct buffers");
+    FL_REQUIRE(dim >= 1 && T >= 1 && pos0 >= 0 && row_stride >= dim, "dim, T, pos0, row_stride");
+    FL_REQUIRE(width >= 2 && width <= 16, "2 <= width <= 16");
+    hipLaunchKernelGGL(conv1d_causal_kernel, dim3((dim + 255) / 256, T), dim3(256), 0,
+                       (hipStream_t)stream, (const f16*)x, (const f16*)w, (const f16*)st_in,
+                       (f16*)y, (f16*)st_out, dim, T, pos0, row_stride, width);
+    return fl::check_launch("conv1d_causal");
+}
+
+int fl_conv1d_causal_rows(const void* x, const void* w, const void* st_in, void* y, void* st0,
+                          void* st1, void* st2, int dim, int T, int pos0, int row_stride,
+                          fl_stream_t stream) {
+    FL_REQUIRE(x && w && st_in && y, "null pointer");
+    FL_REQUIRE(T >= 1 && T <= 3, "1 <= T <= 3");
+    FL_REQUIRE(st0 && (T < 2 || st1) && (T < 3 || st2), "a state buffer per row");
+    FL_REQUIRE(dim >= 1 && pos0 >= 0 && row_stride >= dim, "dim, pos0, row_stride");
+    hipLaunchKernelGGL(conv1d_causal_rows_kernel, dim3((dim + 255) / 256), dim3(256), 0,
+                       (hipStream_t)stream, (const f16*)x, (const f16*)w, (const f16*)st_in,
+                       (f16*)y, (f16*)st0, (f16*)st1, (f16*)st2, dim, T, pos0, row_stride);
+    return fl::check_launch("conv1d_causal_rows");
+}
+
+int fl_l2norm_scaled(const void* x, void* y, int n, int rows, int pitch, float eps, float scale,
+                     int T, fl_stream_t stream) {
+    FL_REQUIRE(x && y, "null pointer");
+    FL_REQUIRE(n >= 1 && n <= 1024 && pitch >= n && rows >= 1 && T >= 1, "n, rows, pitch, T");
+    hipLaunchKernelGGL(l2norm_kernel, dim3(rows, T), dim3(128), 0, (hipStream_t)stream,
+                       (const f16*)x, (f16*)y, n, rows, pitch, eps, scale);
+    return fl::check_launch("l2norm_scaled");
+}
+
+int fl_gdn_scalars(const float* a, const float* b, const float* A_log, const float* dt_bias,
+                   float* beta, float* decay, int T, int n_heads, int a_stride, int b_stride,
+                   fl_stream_t stream) {
+    FL_REQUIRE(a && b && A_log && dt_bias && beta && decay, "null pointer");
+    FL_REQUIRE(T >= 1 && n_heads >= 1 && a_stride >= n_heads && b_stride >= n_heads,
+               "T, n_heads, strides");
+    hipLaunchKernelGGL(gdn_scalars_kernel, dim3((n_heads + 255) / 256, T), dim3(256), 0,
+                       (hipStream_t)stream, a, b, A_log, dt_bias, beta, decay, n_heads, a_stride,
+                       b_stride);
+    return fl::check_launch("gdn_scalars");
+}
+
+int fl_gdn_scan(const void* q, const void* k, const void* v, const float* beta,
+                const float* decay, float* S, void* y, int T, int n_kheads, int n_vheads, int K,
+                int V, int qk_stride, int v_stride, int y_stride, float out_scale, int group,
+                float* Ck, long long ck_step, fl_stream_t stream) {
+    FL_REQUIRE(q && k && v && beta && decay && S && y, "null pointer");
+    FL_REQUIRE(K == GR_K, "K must be 128");
+    FL_REQUIRE(V >= GR_ROWS && V % GR_ROWS == 0, "V % 32 == 0");
+    FL_REQUIRE(group >= 1 && n_vheads >= 1 && (n_vheads - 1) / group < n_kheads,
+               "n_vheads / group <= n_kheads");
+    FL_REQUIRE(T >= 1, "T >= 1");
+    FL_REQUIRE(aligned16(S) && (Ck == nullptr || (aligned16(Ck) && ck_step % 4 == 0)),
+               "16-byte aligned S / Ck");
+    hipLaunchKernelGGL(gdn_scan_kernel, dim3(V / GR_ROWS, n_vheads), dim3(GR_THREADS), 0,
+                       (hipStream_t)stream, (const f16*)q, (const f16*)k, (const f16*)v, beta,
+                       decay, S, (f16*)y, T, n_vheads, V, qk_stride, v_stride, y_stride,
+                       out_scale, group, Ck, ck_step);
+    return fl::check_launch("gdn_scan");
+}
+
+int fl_gdn_decode(const void* x, int x_stride, int conv_fused, const void* conv_w,
+                  const void* const* cst_in, void* const* cst_out, const int* pos0,
+                  const float* a, const float* b, int ab_stride, const float* A_log,
+                  const float* dt_bias, float* const* S, void* y, int y_stride, float* const* Ck,
+                  long long ck_step, int B, int T, int n_kheads, int n_vheads, int K, int V,
+                  float out_scale, float l2eps, fl_stream_t stream) {
+    FL_REQUIRE(x && a && b && A_log && dt_bias && S && y && pos0, "null pointer");
+    FL_REQUIRE(B >= 1 && B <= FL_MAX_SEQS, "1 <= B <= FL_MAX_SEQS");
+    FL_REQUIRE(T >= 1 && T <= 3, "1 <= T <= 3");
+    FL_REQUIRE(K == GR_K, "K must be 128");
+    FL_REQUIRE(V >= GR_ROWS && V % GR_ROWS == 0, "V % 32 == 0");
+    FL_REQUIRE(n_kheads >= 1 && n_vheads % n_kheads == 0, "n_vheads % n_kheads == 0");
+    FL_REQUIRE(x_stride >= 2 * n_kheads * K + n_vheads * V, "x_stride covers q|k|v");
+    FL_REQUIRE(ab_stride >= n_vheads && y_stride >= n_vheads * V, "ab_stride, y_stride");
+    FL_REQUIRE(!conv_fused || (T == 1 && conv_w && cst_in && cst_out), "conv_fused: T == 1 and "
+               "conv_w, cst_in, cst_out");
+    GdnSeqs seqs = {};
+    for (int i = 0; i < B; ++i) {
+        FL_REQUIRE(S[i] && aligned16(S[i]), "16-byte aligned S[b]");
+        seqs.S[i] = S[i];
+        seqs.pos0[i] = pos0[i];
+        FL_REQUIRE(pos0[i] >= 0, "pos0 >= 0");
+        if (conv_fused) {
+            FL_REQUIRE(cst_in[i] && cst_out[i] && cst_in[i] != cst_out[i],
+                       "cst_in[b], cst_out[b] distinct");
+            seqs.cst_in[i] = (const f16*)cst_in[i];
+            seqs.cst_out[i] = (f16*)cst_out[i];
+        }
+        if (Ck != nullptr && Ck[i] != nullptr) {
+            FL_REQUIRE(aligned16(Ck[i]) && ck_step % 4 == 0, "16-byte aligned Ck");
+            seqs.Ck[i] = Ck[i];
+        }
+    }
+    hipLaunchKernelGGL(gdn_decode_kernel, dim3(V / GR_ROWS, n_vheads, B), dim3(GR_THREADS), 0,
+                       (hipStream_t)stream, (const f16*)x, x_stride, conv_fused,
+                       (const f16*)conv_w, seqs, a, b, ab_stride, A_log, dt_bias, (f16*)y,
+                       y_stride, ck_step, T, n_kheads, n_vheads, V, out_scale, l2eps,
+                       n_vheads / n_kheads);
+    return fl::check_launch("gdn_decode");
+}
+
+}  // extern "C"

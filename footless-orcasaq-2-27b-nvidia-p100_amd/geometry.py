@@ -1,0 +1,34 @@
+"""OrcaSAQ-2-27B hot-path geometry, as the reference runtime fixes it
+(model/footless/cuda_sm60/runtime.py:73-116), and the decode split policy
+this build uses on MI355X."""
+
+N_HEADS = 24            # full-attention q heads          runtime.py:78
+N_KV = 4                # kv heads                        runtime.py:79
+HEAD_DIM = 256          #                                 runtime.py:80
+GQA_GROUP = N_HEADS // N_KV
+ATTN_SCALE = HEAD_DIM ** -0.5                           # runtime.py:83
+Q_PITCH = 2 * HEAD_DIM  # a head's row of the q|gate buffer: q(256) | gate(256) (kernels.cu:64-68)
+GATE_OFF = HEAD_DIM
+
+GDN_K_HEADS = 16        #                                 runtime.py:86
+GDN_V_HEADS = 48        #                                 runtime.py:87
+GDN_K = 128             #                                 runtime.py:88
+GDN_V = 128             #                                 runtime.py:89
+GDN_GROUP = GDN_V_HEADS // GDN_K_HEADS                  # runtime.py:90
+CONV_WIDTH = 4          #                                 runtime.py:91
+QKV_ROWS = 10240        # q(2048) | k(2048) | v(6144)      runtime.py:92-94
+Q_SCALE = GDN_K ** -0.5                                 # runtime.py:101
+L2_EPS = 1e-6           #                                 runtime.py:116
+
+# Decode / verify split policy on MI355X. A token's split count is
+# clamp(seqlen / SPLIT_ROWS, 1, SPLIT_MAX) (the reference's per-token rule,
+# kernels.cu:535-544, with its ATT_SPLIT = 32 / ATT_GQA_ROWS = 32 of
+# runtime.py:213-219 re-chosen): at 4 sequences x 4 kv heads, 64 splits a
+# long sequence give 1024 workgroups for 256 CUs, while a split keeps at least
+# 512 rows (16 tiles) so the partials stay a few percent of the KV bytes.
+SPLIT_ROWS = 512
+SPLIT_MAX = 64
+# The largest T the decode attention takes (MTP verify rows; runtime.py:299).
+SPLIT_T_MAX = 4
+
+GDN_CHUNK = 64

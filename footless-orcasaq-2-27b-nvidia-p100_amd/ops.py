@@ -1,0 +1,315 @@
+"""The hot-path op surface over libfl355 (PyTorch-ROCm tensors in, HIP kernels out).
+
+Each function carries the name of the reference kernel it replaces and that
+kernel's argument meaning (model/footless/cuda_sm60/kernels.cu); the grid the
+reference's host computed (runtime.py) becomes the `T` / `split` arguments.
+Buffers are torch tensors on the current HIP device; launches go on torch's
+current stream. Views into a larger row buffer (q / k / v inside the
+10240-wide q|k|v row, q inside the q|gate row) are passed as tensors whose
+data pointer is the view's start, with the row stride given explicitly, as
+the reference passed an offset pointer and a stride.
+
+Errors: where a reference kernel returned without writing on a geometry it
+does not handle (kernels.cu:22-28), these raise ValueError before anything
+is launched. Every tensor's storage is checked to cover the rows the kernel
+will touch.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib
+from .geometry import (ATTN_SCALE, GATE_OFF, GDN_CHUNK, GDN_GROUP, GDN_K, GDN_K_HEADS, GDN_V,
+                       GDN_V_HEADS, HEAD_DIM, L2_EPS, N_HEADS, N_KV, Q_PITCH, Q_SCALE, QKV_ROWS,
+                       SPLIT_MAX, SPLIT_ROWS)
+
+F16, F32 = torch.float16, torch.float32
+
+
+def _stream():
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _ptr(t: torch.Tensor | None, dtype, name: str, span: int = 0):
+    """Device pointer of `t` after checking dtype / device and that its
+    storage holds `span` elements from its start."""
+    if t is None:
+        return None
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name}: expected a torch.Tensor, got {type(t).__name__}")
+    if t.dtype != dtype:
+        raise TypeError(f"{name}: dtype {t.dtype}, expected {dtype}")
+    if t.device.type != "cuda":
+        raise ValueError(f"{name}: must be a GPU tensor (got {t.device})")
+    if span:
+        st = t.untyped_storage()
+        have = (st.nbytes() - (t.data_ptr() - st.data_ptr())) // t.element_size()
+        if have < span:
+            raise ValueError(f"{name}: storage holds {have} elements from its start, "
+                             f"the call touches {span}")
+    return t.data_ptr()
+
+
+def _contig(t: torch.Tensor, name: str):
+    if not t.is_contiguous():
+        raise ValueError(f"{name}: must be contiguous")
+
+
+# ---------------------------------------------------------------------------
+# full attention
+# ---------------------------------------------------------------------------
+
+def kv_store(k, v, kcache, vcache, *, layer: int = 0, pos0: int, T: int | None = None,
+             n_kv_heads: int = N_KV, head_dim: int = HEAD_DIM, max_pos: int | None = None):
+    """kernels.cu:465-484 (runtime.py:2813-2815): k, v [T, n_kv, head_dim] fp16
+    into rows pos0.. of kcache / vcache [layers?, max_pos, n_kv, head_dim]."""
+    T = k.shape[0] if T is None else T
+    max_pos = kcache.shape[-3] if max_pos is None else max_pos
+    row = n_kv_heads * head_dim
+    _contig(k, "k"), _contig(v, "v"), _contig(kcache, "kcache"), _contig(vcache, "vcache")
+    _lib.call("fl_kv_store", _ptr(k, F16, "k", T * row), _ptr(v, F16, "v", T * row),
+              _ptr(kcache, F16, "kcache", (layer + 1) * max_pos * row),
+              _ptr(vcache, F16, "vcache", (layer + 1) * max_pos * row),
+              layer, pos0, T, n_kv_heads, head_dim, max_pos, _stream())
+
+
+def attention_split_gqa(q, kcache, vcache, pacc, pm, pd, *, layer: int = 0,
+                        n_q_heads: int = N_HEADS, n_kv_heads: int = N_KV,
+                        head_dim: int = HEAD_DIM, q_pitch: int = Q_PITCH, pos0: int,
+                        max_pos: int | None = None, scale: float = ATTN_SCALE,
+                        split_rows: int = SPLIT_ROWS, T: int, split: int = SPLIT_MAX):
+    """kernels.cu:820-835 (runtime.py:2830-2837): split partials of T tokens at
+    pos0.. -- pacc [T, n_q_heads, split, head_dim], pm / pd [T, n_q_heads, split]
+    fp32, pm in natural-log units. The per-token split rule is geometry.py's."""
+    max_pos = kcache.shape[-3] if max_pos is None else max_pos
+    row = n_kv_heads * head_dim
+    parts = T * n_q_heads * split
+    _lib.call("fl_attention_split_gqa",
+              _ptr(q, F16, "q", (T - 1) * n_q_heads * q_pitch + n_q_heads * q_pitch),
+              _ptr(kcache, F16, "kcache", (layer + 1) * max_pos * row),
+              _ptr(vcache, F16, "vcache", (layer + 1) * max_pos * row),
+              _ptr(pacc, F32, "pacc", parts * head_dim), _ptr(pm, F32, "pm", parts),
+              _ptr(pd, F32, "pd", parts), layer, n_q_heads, n_kv_heads, head_dim, q_pitch, pos0,
+              max_pos, float(scale), split_rows, T, split, _stream())
+
+
+def attention_merge(pacc, pm, pd, z, *, n_q_heads: int = N_HEADS, head_dim: int = HEAD_DIM,
+                    z_pitch: int = HEAD_DIM, T: int, split: int, gate=None,
+                    g_pitch: int = Q_PITCH, g_off: int = GATE_OFF):
+    """kernels.cu:1398-1424 (runtime.py:2844-2846), with attn_gate
+    (kernels.cu:1585-1600) fused when `gate` (a q|gate buffer view) is given."""
+    parts = T * n_q_heads * split
+    _lib.call("fl_attention_merge", _ptr(pacc, F32, "pacc", parts * head_dim),
+              _ptr(pm, F32, "pm", parts), _ptr(pd, F32, "pd", parts),
+              _ptr(z, F16, "z", T * n_q_heads * z_pitch), n_q_heads, head_dim, z_pitch, T, split,
+              _ptr(gate, F16, "gate", T * n_q_heads * g_pitch), g_pitch, g_off, _stream())
+
+
+def attn_gate(z, g, *, n_heads: int = N_HEADS, head_dim: int = HEAD_DIM,
+              z_pitch: int = HEAD_DIM, g_pitch: int = Q_PITCH, g_off: int = GATE_OFF, T: int):
+    """kernels.cu:1585-1600 (runtime.py:2860-2862): z = f16_sat(z * sigmoid(g))."""
+    _lib.call("fl_attn_gate", _ptr(z, F16, "z", T * n_heads * z_pitch),
+              _ptr(g, F16, "g", T * n_heads * g_pitch), n_heads, head_dim, z_pitch, g_pitch,
+              g_off, T, _stream())
+
+
+def attn_decode_work_bytes(B: int, T: int, n_q_heads: int = N_HEADS, head_dim: int = HEAD_DIM,
+                           split: int = SPLIT_MAX) -> int:
+    return int(_lib.lib().fl_attn_decode_work_bytes(B, T, n_q_heads, head_dim, split))
+
+
+def attn_decode(qg, kcaches, vcaches, pos0s, *, z=None, gate: bool = True,
+                n_kv_heads: int = N_KV, scale: float = ATTN_SCALE, split_rows: int = SPLIT_ROWS,
+                split: int = SPLIT_MAX, work=None):
+    """The decode / MTP-verify attention block of B sequences (runtime.py:
+    2828-2862 and the per-sequence loop of 2865-2878): split partials + merge
+    + sigmoid gate. qg [B, T, n_q_heads, q_pitch] fp16 with q | gate per head;
+    kcaches / vcaches: per-sequence layer caches [cap, n_kv, head_dim] fp16;
+    pos0s: each sequence's first query position. Returns z [B, T, n_q_heads,
+    head_dim] fp16."""
+    B, T, n_q_heads, q_pitch = qg.shape
+    head_dim = kcaches[0].shape[-1]
+    _contig(qg, "qg")
+    if z is None:
+        z = torch.empty((B, T, n_q_heads, head_dim), dtype=F16, device=qg.device)
+    need = attn_decode_work_bytes(B, T, n_q_heads, head_dim, split)
+    if work is None:
+        work = torch.empty(need, dtype=torch.uint8, device=qg.device)
+    if len(kcaches) != B or len(vcaches) != B or len(pos0s) != B:
+        raise ValueError("one cache pair and one pos0 per sequence")
+    caps = []
+    for b in range(B):
+        for name, c in (("kcache", kcaches[b]), ("vcache", vcaches[b])):
+            _contig(c, name)
+            _ptr(c, F16, name, c.shape[-3] * n_kv_heads * head_dim)
+        caps.append(kcaches[b].shape[-3])
+    _lib.call("fl_attn_decode", _ptr(qg, F16, "qg", B * T * n_q_heads * q_pitch), q_pitch,
+              _lib.ptr_array([c.data_ptr() for c in kcaches]),
+              _lib.ptr_array([c.data_ptr() for c in vcaches]), _lib.int_array(pos0s),
+              _lib.int_array(caps), B, T, n_q_heads, n_kv_heads, head_dim, float(scale),
+              split_rows, split, qg.data_ptr() if gate else None, q_pitch, GATE_OFF if gate else 0,
+              _ptr(z, F16, "z", B * T * n_q_heads * head_dim), z.shape[-1],
+              _ptr(work, torch.uint8, "work", need), work.numel(), _stream())
+    return z
+
+
+def attention_prefill(q, kcache, vcache, *, pos0: int, T: int | None = None, z=None,
+                      k_new=None, v_new=None, layer: int = 0, n_q_heads: int = N_HEADS,
+                      n_kv_heads: int = N_KV, q_pitch: int | None = None,
+                      scale: float = ATTN_SCALE, max_pos: int | None = None):
+    """attention_prefill_fh + attention_merge_fh (kernels.cu:2461-2807, host
+    _attn_fh runtime.py:2943-2959), with kv_store (kernels.cu:465-484) of
+    k_new / v_new [T, n_kv, head_dim] fused in front when given. q [T,
+    n_q_heads, q_pitch] fp16 (q first in a head's row). Returns z [T,
+    n_q_heads, head_dim] fp16."""
+    T = q.shape[0] if T is None else T
+    q_pitch = q.shape[-1] if q_pitch is None else q_pitch
+    head_dim = kcache.shape[-1]
+    max_pos = kcache.shape[-3] if max_pos is None else max_pos
+    row = n_kv_heads * head_dim
+    if z is None:
+        z = torch.empty((T, n_q_heads, head_dim), dtype=F16, device=q.device)
+    _lib.call("fl_attention_prefill", _ptr(q, F16, "q", T * n_q_heads * q_pitch), q_pitch,
+              _ptr(k_new, F16, "k_new", T * row), _ptr(v_new, F16, "v_new", T * row),
+              _ptr(kcache, F16, "kcache", (layer + 1) * max_pos * row),
+              _ptr(vcache, F16, "vcache", (layer + 1) * max_pos * row), layer, n_q_heads,
+              n_kv_heads, head_dim, pos0, max_pos, float(scale), T,
+              _ptr(z, F16, "z", T * n_q_heads * z.shape[-1]), z.shape[-1], _stream())
+    return z
+
+
+# ---------------------------------------------------------------------------
+# Gated DeltaNet
+# ---------------------------------------------------------------------------
+
+def conv1d_causal(x, w, st_in, y, st_out, *, dim: int = QKV_ROWS, T: int, pos0: int,
+                  row_stride: int = QKV_ROWS, width: int = 4):
+    """kernels.cu:1634-1679 (runtime.py:3035-3038). st_in and st_out distinct."""
+    _lib.call("fl_conv1d_causal", _ptr(x, F16, "x", (T - 1) * row_stride + dim),
+              _ptr(w, F16, "w", dim * width), _ptr(st_in, F16, "st_in", dim * (width - 1)),
+              _ptr(y, F16, "y", (T - 1) * row_stride + dim),
+              _ptr(st_out, F16, "st_out", dim * (width - 1)), dim, T, pos0, row_stride, width,
+              _stream())
+
+
+def conv1d_causal_rows(x, w, st_in, y, st0, st1=None, st2=None, *, dim: int = QKV_ROWS, T: int,
+                       pos0: int, row_stride: int = QKV_ROWS):
+    """kernels.cu:1686-1714 (runtime.py:3021-3026): verify rows T <= 3, the
+    state after row t into st_t."""
+    n = (T - 1) * row_stride + dim
+    _lib.call("fl_conv1d_causal_rows", _ptr(x, F16, "x", n), _ptr(w, F16, "w", dim * 4),
+              _ptr(st_in, F16, "st_in", dim * 3), _ptr(y, F16, "y", n),
+              _ptr(st0, F16, "st0", dim * 3), _ptr(st1, F16, "st1", dim * 3),
+              _ptr(st2, F16, "st2", dim * 3), dim, T, pos0, row_stride, _stream())
+
+
+def l2norm_scaled(x, y, *, n: int = GDN_K, rows: int, pitch: int = GDN_K, eps: float = L2_EPS,
+                  scale: float = 1.0, T: int):
+    """kernels.cu:373-391 (runtime.py:3070-3071)."""
+    span = (T * rows - 1) * pitch + n
+    _lib.call("fl_l2norm_scaled", _ptr(x, F16, "x", span), _ptr(y, F16, "y", span), n, rows,
+              pitch, float(eps), float(scale), T, _stream())
+
+
+def gdn_scalars(a, b, A_log, dt_bias, beta, decay, *, T: int, n_heads: int = GDN_V_HEADS,
+                a_stride: int | None = None, b_stride: int | None = None):
+    """kernels.cu:1732-1748 (runtime.py:3072-3076)."""
+    a_stride = n_heads if a_stride is None else a_stride
+    b_stride = n_heads if b_stride is None else b_stride
+    _lib.call("fl_gdn_scalars", _ptr(a, F32, "a", (T - 1) * a_stride + n_heads),
+              _ptr(b, F32, "b", (T - 1) * b_stride + n_heads), _ptr(A_log, F32, "A_log", n_heads),
+              _ptr(dt_bias, F32, "dt_bias", n_heads), _ptr(beta, F32, "beta", T * n_heads),
+              _ptr(decay, F32, "decay", T * n_heads), T, n_heads, a_stride, b_stride, _stream())
+
+
+def gdn_scan(q, k, v, beta, decay, S, y, *, T: int, n_kheads: int = GDN_K_HEADS,
+             n_vheads: int = GDN_V_HEADS, K: int = GDN_K, V: int = GDN_V,
+             qk_stride: int = QKV_ROWS, v_stride: int = QKV_ROWS, y_stride: int | None = None,
+             out_scale: float = Q_SCALE, group: int = GDN_GROUP, ck=None, ck_step: int = 0):
+    """gdn_scan_rows / gdn_scan (kernels.cu:2831-2914, 1794-1901; runtime.py:
+    3094-3108): the delta rule over T tokens, S [n_vheads, V, K] fp32 in place;
+    ck (optional) receives the state after every token but the last at
+    ck + t * ck_step."""
+    y_stride = n_vheads * V if y_stride is None else y_stride
+    _contig(S, "S")
+    if ck is not None:
+        _contig(ck, "ck")
+    _lib.call("fl_gdn_scan", _ptr(q, F16, "q", (T - 1) * qk_stride + n_kheads * K),
+              _ptr(k, F16, "k", (T - 1) * qk_stride + n_kheads * K),
+              _ptr(v, F16, "v", (T - 1) * v_stride + n_vheads * V),
+              _ptr(beta, F32, "beta", T * n_vheads), _ptr(decay, F32, "decay", T * n_vheads),
+              _ptr(S, F32, "S", n_vheads * V * K),
+              _ptr(y, F16, "y", (T - 1) * y_stride + n_vheads * V), T, n_kheads, n_vheads, K, V,
+              qk_stride, v_stride, y_stride, float(out_scale), group,
+              _ptr(ck, F32, "ck", max(T - 2, 0) * ck_step + n_vheads * V * K) if ck is not None
+              else None, ck_step, _stream())
+
+
+def gdn_decode(x, S, a, b, A_log, dt_bias, y=None, *, T: int, pos0s, conv_fused: bool = False,
+               conv_w=None, cst_in=None, cst_out=None, ck=None, ck_step: int = 0,
+               n_kheads: int = GDN_K_HEADS, n_vheads: int = GDN_V_HEADS, K: int = GDN_K,
+               V: int = GDN_V, x_stride: int = QKV_ROWS, ab_stride: int = GDN_V_HEADS,
+               out_scale: float = Q_SCALE, l2eps: float = L2_EPS):
+    """gdn_scan_rows_f (+ gdn_conv1) for B sequences (kernels.cu:2916-3070;
+    runtime.py:3040-3053 and the per-row loop 3131-3142). x [B, T, x_stride]
+    fp16: the raw q|k|v projection row when conv_fused (T == 1, the conv runs
+    in the kernel from cst_in[b] into cst_out[b]), else the conv output.
+    S: list of B states [n_vheads, V, K] fp32 updated in place; a, b [B, T,
+    ab_stride] fp32; ck: optional list of B checkpoint buffers. Returns y
+    [B, T, n_vheads * V] fp16."""
+    B = len(S)
+    _contig(x, "x"), _contig(a, "a"), _contig(b, "b")
+    if y is None:
+        y = torch.empty((B, T, n_vheads * V), dtype=F16, device=x.device)
+    state = n_vheads * V * K
+    s_ptrs = [_ptr(s, F32, "S[b]", state) for s in S]
+    ci = co = None
+    if conv_fused:
+        if cst_in is None or cst_out is None or conv_w is None:
+            raise ValueError("conv_fused needs conv_w, cst_in and cst_out")
+        ci = _lib.ptr_array([_ptr(c, F16, "cst_in[b]", x_stride * 3) for c in cst_in])
+        co = _lib.ptr_array([_ptr(c, F16, "cst_out[b]", x_stride * 3) for c in cst_out])
+    ck_arr = None
+    if ck is not None:
+        ck_arr = _lib.ptr_array([_ptr(c, F32, "ck[b]", max(T - 2, 0) * ck_step + state)
+                                 if c is not None else None for c in ck])
+    _lib.call("fl_gdn_decode", _ptr(x, F16, "x", B * T * x_stride), x_stride,
+              1 if conv_fused else 0, _ptr(conv_w, F16, "conv_w", x_stride * 4), ci, co,
+              _lib.int_array(pos0s), _ptr(a, F32, "a", B * T * ab_stride),
+              _ptr(b, F32, "b", B * T * ab_stride), _ptr(A_log, F32, "A_log", n_vheads),
+              _ptr(dt_bias, F32, "dt_bias", n_vheads), _lib.ptr_array(s_ptrs),
+              _ptr(y, F16, "y", B * T * y.shape[-1]), y.shape[-1], ck_arr, ck_step, B, T,
+              n_kheads, n_vheads, K, V, float(out_scale), float(l2eps), _stream())
+    return y
+
+
+def gdn_chunked_work_bytes(T: int, n_vheads: int = GDN_V_HEADS, K: int = GDN_K, V: int = GDN_V,
+                           chunk: int = GDN_CHUNK) -> int:
+    return int(_lib.lib().fl_gdn_chunked_work_bytes(T, n_vheads, K, V, chunk))
+
+
+def gdn_prefill_chunked(q, k, v, beta, decay, S, y=None, *, T: int, n_kheads: int = GDN_K_HEADS,
+                        n_vheads: int = GDN_V_HEADS, K: int = GDN_K, V: int = GDN_V,
+                        qk_stride: int = QKV_ROWS, v_stride: int = QKV_ROWS,
+                        out_scale: float = Q_SCALE, group: int = GDN_GROUP,
+                        chunk: int = GDN_CHUNK, work=None):
+    """The chunked WY/UT scan (not in the reference; replaces gdn_scan_rows
+    for prefill, runtime.py:3094-3100): same arguments and results as
+    gdn_scan. Returns y [T, n_vheads * V] fp16."""
+    _contig(S, "S")
+    if y is None:
+        y = torch.empty((T, n_vheads * V), dtype=F16, device=q.device)
+    need = gdn_chunked_work_bytes(T, n_vheads, K, V, chunk)
+    if work is None:
+        work = torch.empty(need, dtype=torch.uint8, device=q.device)
+    _lib.call("fl_gdn_prefill_chunked", _ptr(q, F16, "q", (T - 1) * qk_stride + n_kheads * K),
+              _ptr(k, F16, "k", (T - 1) * qk_stride + n_kheads * K),
+              _ptr(v, F16, "v", (T - 1) * v_stride + n_vheads * V),
+              _ptr(beta, F32, "beta", T * n_vheads), _ptr(decay, F32, "decay", T * n_vheads),
+              _ptr(S, F32, "S", n_vheads * V * K),
+              _ptr(y, F16, "y", (T - 1) * y.shape[-1] + n_vheads * V), T, n_kheads, n_vheads, K,
+              V, qk_stride, v_stride, y.shape[-1], float(out_scale), group, chunk,
+              _ptr(work, torch.uint8, "work", need), work.numel(), _stream())
+    return y

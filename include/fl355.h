@@ -1,0 +1,209 @@
+/*
+ * fl355.h -- C ABI of libfl355.so, the MI355X (gfx950) implementation of the
+ * footless attention / Gated DeltaNet hot path.
+ *
+ * Every entry point takes raw device pointers, plain integers / floats and a
+ * HIP stream, enqueues its kernels on that stream and returns an int status
+ * (FL_OK = 0). Where the reference kernel returned without writing on a
+ * geometry it could not handle (model/footless/cuda_sm60/kernels.cu:22-28),
+ * these entry points enqueue nothing and return FL_EINVAL; fl_last_error()
+ * then names the argument. The caller owns every buffer (weights, caches,
+ * states, scratch), as the reference's runtime does (runtime.py:886-967);
+ * no entry point allocates device memory.
+ *
+ * Storage types: "f16" = IEEE binary16 (uint16_t bits), "f32" = float.
+ * Each declaration names the reference launch it replaces: the kernel
+ * (kernels.cu:line) and the runtime call site (runtime.py:line) that a
+ * maintainer rebinds (INTEGRATION.md shows the ctypes stub).
+ */
+#ifndef FL355_H
+#define FL355_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* fl_stream_t; /* hipStream_t; NULL = default stream */
+
+#define FL_OK 0
+#define FL_EINVAL 1   /* geometry / argument the kernels do not support */
+#define FL_ELAUNCH 2  /* the HIP runtime refused a launch */
+#define FL_ESCRATCH 3 /* caller scratch smaller than *_work_bytes asked for */
+
+#define FL_MAX_SEQS 16 /* sequences one batched decode call carries */
+
+int fl_abi_version(void);
+const char* fl_strerror(int status);
+/* Detail of the last failure on the calling thread ("" if none). */
+const char* fl_last_error(void);
+
+/* ---------------------------------------------------------------- a4 ----
+ * kv_store: k, v [T][n_kv_heads][head_dim] f16 -> cache rows pos0 + t of a
+ * position-addressable [layers][max_pos][n_kv_heads][head_dim] f16 cache.
+ * Replaces kernels.cu:465-484 kv_store, launched at runtime.py:2813-2815.
+ * Differs: pos0 + T > max_pos is FL_EINVAL (the reference skipped the rows). */
+int fl_kv_store(const void* k, const void* v, void* kcache, void* vcache, int layer,
+                int pos0, int T, int n_kv_heads, int head_dim, int max_pos,
+                fl_stream_t stream);
+
+/* ------------------------------------------------------------- a1 -------
+ * attention_split_gqa for one sequence: split-K flash-decode partials of T
+ * query tokens at positions pos0..pos0+T-1 (token t attends rows
+ * [0, pos0 + t]), q [T][n_q_heads][q_pitch] f16 (q = first head_dim of a
+ * head's row), q head h reads kv head h / (n_q_heads / n_kv_heads).
+ * Token t's split count is St = clamp((pos0+t+1) / split_rows, 1, split);
+ * split s covers the 32-row tiles [nt*s/St, nt*(s+1)/St) of its nt =
+ * ceil(seqlen/32) tiles; s >= St writes an empty partial (m = -1e30, d = 0).
+ * Outputs pacc [T][n_q_heads][split][head_dim] f32, pm / pd
+ * [T][n_q_heads][split] f32, pm in natural-log units of the scaled score
+ * (the reference's partial contract, kernels.cu:93-99).
+ * Replaces kernels.cu:820-835 (+ 522-680), runtime.py:2830-2837.
+ * Supported: head_dim == 256, T * n_q_heads / n_kv_heads <= 32,
+ * split_rows >= 32. */
+int fl_attention_split_gqa(const void* q, const void* kcache, const void* vcache,
+                           float* pacc, float* pm, float* pd, int layer, int n_q_heads,
+                           int n_kv_heads, int head_dim, int q_pitch, int pos0, int max_pos,
+                           float scale, int split_rows, int T, int split,
+                           fl_stream_t stream);
+
+/* ------------------------------------------------------------ a2 + a3 ---
+ * attention_merge (+ attn_gate when gate != NULL): z[t][h][:] =
+ * f16_sat(sum_s e_s acc_s / sum_s e_s d_s), e_s = exp(m_s - max m), then
+ * z = f16_sat(z * sigmoid(gate[t][h][g_off + d])) with gate rows of g_pitch
+ * per head. z is written at z_pitch per head.
+ * Replaces kernels.cu:1398-1424 (runtime.py:2844-2846) and kernels.cu:
+ * 1585-1600 (runtime.py:2860-2862); the fused form of kernels.cu:1342-1385. */
+int fl_attention_merge(const float* pacc, const float* pm, const float* pd, void* z,
+                       int n_q_heads, int head_dim, int z_pitch, int T, int split,
+                       const void* gate, int g_pitch, int g_off, fl_stream_t stream);
+
+/* a3 alone: z = f16_sat(z * sigmoid(g)), kernels.cu:1585-1600. */
+int fl_attn_gate(void* z, const void* g, int n_heads, int head_dim, int z_pitch,
+                 int g_pitch, int g_off, int T, fl_stream_t stream);
+
+/* ------------------------------------------------- a1 + a2 + a3 batched ---
+ * The decode / MTP-verify attention of B sequences in two launches: the
+ * split partials of every (sequence, kv head, split) and the gated merge.
+ * qg [B][T][n_q_heads][q_pitch] f16, q at offset 0 of a head's row and the
+ * gate at g_off (gate may be NULL: no gate); kcache[b] / vcache[b] host
+ * arrays of B device pointers to each sequence's layer cache
+ * [cap[b]][n_kv_heads][head_dim] f16; pos0[b], cap[b] host arrays.
+ * z [B][T][n_q_heads][z_pitch] f16. work: caller scratch of at least
+ * fl_attn_decode_work_bytes(B, T, n_q_heads, head_dim, split) bytes.
+ * Each token's values equal a T = 1 call at its own position, bit for bit
+ * (the split depends on the token's own length only; runtime.py:2062-2069).
+ * Replaces the per-sequence loop of runtime.py:2865-2878 / 2828-2862. */
+size_t fl_attn_decode_work_bytes(int B, int T, int n_q_heads, int head_dim, int split);
+int fl_attn_decode(const void* qg, int q_pitch, const void* const* kcache,
+                   const void* const* vcache, const int* pos0, const int* cap, int B, int T,
+                   int n_q_heads, int n_kv_heads, int head_dim, float scale, int split_rows,
+                   int split, const void* gate, int g_pitch, int g_off, void* z, int z_pitch,
+                   void* work, size_t work_bytes, fl_stream_t stream);
+
+/* ------------------------------------------------------------ a5 + a6 ---
+ * Causal GQA prefill attention of T tokens at pos0.. over one layer cache
+ * [max_pos][n_kv_heads][head_dim] f16: query (t, h) attends rows
+ * [0, pos0 + t] of kv head h / G, z [T][n_q_heads][z_pitch] f16.
+ * k_new / v_new [T][n_kv_heads][head_dim] f16, when not NULL, are first
+ * stored into cache rows pos0.. (the fused kv_store, a4).
+ * Replaces kernels.cu:2768-2807 attention_prefill_fh (+ merge_fh) launched
+ * by runtime.py:2943-2959 (and kv_store at runtime.py:2813-2815).
+ * `scale` multiplies q.k (the reference passes sl2 = scale * log2 e).
+ * Supported: head_dim == 256, pos0 + T <= max_pos. */
+int fl_attention_prefill(const void* q, int q_pitch, const void* k_new, const void* v_new,
+                         void* kcache, void* vcache, int layer, int n_q_heads, int n_kv_heads,
+                         int head_dim, int pos0, int max_pos, float scale, int T, void* z,
+                         int z_pitch, fl_stream_t stream);
+
+/* ---------------------------------------------------------------- a8 ----
+ * conv1d_causal over `dim` channels of rows x [T][row_stride] f16: E =
+ * [st_in (width-1 frames, ZERO if pos0 == 0) | x], y[t][d] =
+ * f16_sat(silu(sum_j w[d][j] E[t+j])), st_out = last width-1 frames of E.
+ * w [dim][width] f16, states [dim][width-1] f16; st_in != st_out.
+ * Replaces kernels.cu:1634-1679, runtime.py:3035-3038. */
+int fl_conv1d_causal(const void* x, const void* w, const void* st_in, void* y, void* st_out,
+                     int dim, int T, int pos0, int row_stride, int width, fl_stream_t stream);
+
+/* a9 conv1d_causal_rows: T <= 3 verify rows, the state after row t into st_t
+ * (st0 may be st_in). Replaces kernels.cu:1686-1714, runtime.py:3021-3026. */
+int fl_conv1d_causal_rows(const void* x, const void* w, const void* st_in, void* y, void* st0,
+                          void* st1, void* st2, int dim, int T, int pos0, int row_stride,
+                          fl_stream_t stream);
+
+/* ---------------------------------------------------------------- a10 ---
+ * l2norm_scaled: y = f16_sat((x / sqrt(sum x^2 + eps)) * scale) per row of n
+ * (n <= 1024), rows [T][rows][pitch] f16.
+ * Replaces kernels.cu:373-391, runtime.py:3070-3071. */
+int fl_l2norm_scaled(const void* x, void* y, int n, int rows, int pitch, float eps, float scale,
+                     int T, fl_stream_t stream);
+
+/* ---------------------------------------------------------------- a11 ---
+ * gdn_scalars: beta = sigmoid(b), decay = exp(-exp(A_log[h]) *
+ * softplus(a + dt_bias[h])), softplus threshold 20. a, b [T][stride] f32;
+ * beta, decay [T][n_heads] f32. Replaces kernels.cu:1732-1748,
+ * runtime.py:3072-3076. */
+int fl_gdn_scalars(const float* a, const float* b, const float* A_log, const float* dt_bias,
+                   float* beta, float* decay, int T, int n_heads, int a_stride, int b_stride,
+                   fl_stream_t stream);
+
+/* ---------------------------------------------------------------- a12 ---
+ * The gated delta rule over T tokens, S [n_vheads][V][K] f32 in place:
+ *   S *= decay; m = S k; delta = beta (v - m); S += delta k^T;
+ *   y = f16_sat((S q) * out_scale)
+ * q, k rows at qk_stride (head hk at hk*K), v at v_stride, y at y_stride;
+ * v-head hv reads q/k head hv / group. Ck (nullable): the state after every
+ * token but the last at Ck + t*ck_step floats.
+ * Replaces kernels.cu:2831-2914 gdn_scan_rows (runtime.py:3094-3100) and
+ * kernels.cu:1794-1901 gdn_scan (runtime.py:3102-3108). K == 128, V % 32 == 0. */
+int fl_gdn_scan(const void* q, const void* k, const void* v, const float* beta,
+                const float* decay, float* S, void* y, int T, int n_kheads, int n_vheads,
+                int K, int V, int qk_stride, int v_stride, int y_stride, float out_scale,
+                int group, float* Ck, long long ck_step, fl_stream_t stream);
+
+/* ---------------------------------------------------------------- a13 ---
+ * The fused GDN decode / verify step of B sequences (T <= 3): the gates
+ * (a11), the L2 norm of q and k (a10, eps l2eps, fp16-rounded, scale 1),
+ * and the delta rule (a12) with checkpoints, in one launch. With
+ * conv_fused = 1 (T == 1 only) x is the RAW q|k|v projection row and the
+ * conv (a8, width 4) runs in the kernel from cst_in[b] into cst_out[b]
+ * (distinct buffers); with conv_fused = 0 x is the conv output.
+ * x [B][T][x_stride] f16 with q at channel 0, k at n_kheads*K, v at
+ * 2*n_kheads*K; conv_w [x channels][4] f16; a, b [B][T][ab_stride] f32;
+ * A_log, dt_bias [n_vheads] f32; S[b] [n_vheads][V][K] f32 in place;
+ * y [B][T][y_stride] f16; Ck[b] (nullable) as in fl_gdn_scan. Host arrays
+ * S, cst_in, cst_out, Ck, pos0 hold one entry per sequence.
+ * Replaces kernels.cu:2954-3070 gdn_scan_rows_f (+ gdn_conv1 2916-2941),
+ * runtime.py:3040-3053 and the per-row loop runtime.py:3131-3142.
+ * K == 128, V % 32 == 0, B <= FL_MAX_SEQS. */
+int fl_gdn_decode(const void* x, int x_stride, int conv_fused, const void* conv_w,
+                  const void* const* cst_in, void* const* cst_out, const int* pos0,
+                  const float* a, const float* b, int ab_stride, const float* A_log,
+                  const float* dt_bias, float* const* S, void* y, int y_stride,
+                  float* const* Ck, long long ck_step, int B, int T, int n_kheads,
+                  int n_vheads, int K, int V, float out_scale, float l2eps,
+                  fl_stream_t stream);
+
+/* ---------------------------------------------------------------- a14 ---
+ * Chunked (WY / UT transform) GDN prefill: the same recurrence as
+ * fl_gdn_scan over T tokens in chunks of `chunk` tokens, fp32 state carried
+ * between chunks; S in place, y as fl_gdn_scan. NOT in the reference (the
+ * reference runs a12 sequentially and names the chunked scan as undone,
+ * kernels.cu:1788-1791); it replaces that call (runtime.py:3094-3100) for
+ * prefill. work: caller scratch of fl_gdn_chunked_work_bytes(...) bytes (the
+ * per-chunk W, U and decayed Q K^T of the WY form). chunk == 64,
+ * K == V == 128. */
+size_t fl_gdn_chunked_work_bytes(int T, int n_vheads, int K, int V, int chunk);
+int fl_gdn_prefill_chunked(const void* q, const void* k, const void* v, const float* beta,
+                           const float* decay, float* S, void* y, int T, int n_kheads,
+                           int n_vheads, int K, int V, int qk_stride, int v_stride,
+                           int y_stride, float out_scale, int group, int chunk, void* work,
+                           size_t work_bytes, fl_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FL355_H */

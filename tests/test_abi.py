@@ -1,0 +1,93 @@
+"""The C ABI on the CPU: libfl355.so loads without a GPU, exports every
+entry point include/fl355.h declares, and its argument checks refuse bad
+geometry before anything is launched (no device call is made by these)."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+REPO = Path(__file__).resolve().parent.parent
+
+
+def declared_entry_points():
+    text = (REPO / "include" / "fl355.h").read_text()
+    return sorted(set(re.findall(r"^\s*(?:int|size_t|const char\*)\s+(fl_\w+)\(", text, re.M)))
+
+
+def test_header_declares_the_path():
+    names = declared_entry_points()
+    for want in ("fl_kv_store", "fl_attention_split_gqa", "fl_attention_merge", "fl_attn_gate",
+                 "fl_attn_decode", "fl_attention_prefill", "fl_conv1d_causal",
+                 "fl_conv1d_causal_rows", "fl_l2norm_scaled", "fl_gdn_scalars", "fl_gdn_scan",
+                 "fl_gdn_decode", "fl_gdn_prefill_chunked"):
+        assert want in names
+
+
+def test_library_exports_every_declared_symbol(fl):
+    lib = fl._lib.lib()
+    missing = [n for n in declared_entry_points() if not hasattr(lib, n)]
+    assert not missing, missing
+    # and the Python binding covers every one of them
+    assert set(declared_entry_points()) <= set(fl._lib.SIGNATURES)
+
+
+def test_status_strings(fl):
+    lib = fl._lib.lib()
+    assert lib.fl_abi_version() == 1
+    assert lib.fl_strerror(0) == b"ok"
+    assert lib.fl_strerror(1) == b"invalid argument"
+
+
+def _call(fl, name, *args):
+    return getattr(fl._lib.lib(), name)(*args)
+
+
+def test_argument_checks_refuse_before_launch(fl):
+    lib = fl._lib.lib()
+    fake = ctypes.c_void_p(0x1000)   # never dereferenced: every call below fails its checks
+    # kv_store past the cache end
+    assert _call(fl, "fl_kv_store", fake, fake, fake, fake, 0, 10, 5, 4, 256, 12, None) == 1
+    assert b"max_pos" in lib.fl_last_error()
+    # decode: 6 tokens x 6 heads > 32 columns
+    assert _call(fl, "fl_attention_split_gqa", fake, fake, fake, fake, fake, fake, 0, 24, 4, 256,
+                 512, 0, 100, 0.0625, 512, 6, 8, None) == 1
+    # head_dim other than 256
+    assert _call(fl, "fl_attention_prefill", fake, 128, None, None, fake, fake, 0, 24, 4, 128, 0,
+                 64, 1.0, 8, fake, 128, None) == 1
+    # conv with aliased state buffers
+    assert _call(fl, "fl_conv1d_causal", fake, fake, fake, fake, fake, 64, 1, 1, 64, 4, None) == 1
+    assert b"distinct" in lib.fl_last_error()
+    # scan with K != 128
+    assert _call(fl, "fl_gdn_scan", fake, fake, fake, fake, fake, fake, fake, 4, 16, 48, 64, 128,
+                 10240, 10240, 6144, 0.1, 3, None, 0, None) == 1
+    # chunked scan with a chunk other than 64
+    assert _call(fl, "fl_gdn_prefill_chunked", fake, fake, fake, fake, fake, fake, fake, 100, 16,
+                 48, 128, 128, 10240, 10240, 6144, 0.1, 3, 32, fake, 1 << 30, None) == 1
+
+
+def test_work_size_queries(fl):
+    lib = fl._lib.lib()
+    assert lib.fl_attn_decode_work_bytes(4, 3, 24, 256, 64) == 4 * 3 * 24 * 64 * (256 + 2) * 4
+    n_chunks = (8192 + 63) // 64
+    assert lib.fl_gdn_chunked_work_bytes(8192, 48, 128, 128, 64) == \
+        n_chunks * 48 * (64 * 128 * 2 + 64 * 64 + 64) * 4
+    assert lib.fl_gdn_chunked_work_bytes(8192, 48, 128, 128, 32) == 0
+
+
+def test_scratch_too_small_is_reported(fl):
+    fake = ctypes.c_void_p(0x1000)
+    arr = fl._lib.ptr_array([0x2000])
+    ints = fl._lib.int_array([100])
+    caps = fl._lib.int_array([200])
+    rc = _call(fl, "fl_attn_decode", fake, 512, arr, arr, ints, caps, 1, 1, 24, 4, 256, 0.0625,
+               512, 64, None, 512, 256, fake, 256, fake, 16, None)
+    assert rc == 3 and b"work" in fl._lib.lib().fl_last_error()
+
+
+def test_op_layer_refuses_cpu_tensors(fl):
+    torch = pytest.importorskip("torch")
+    k = torch.zeros((1, 4, 256), dtype=torch.float16)
+    with pytest.raises(ValueError):
+        fl.ops.kv_store(k, k, torch.zeros((8, 4, 256), dtype=torch.float16),
+                        torch.zeros((8, 4, 256), dtype=torch.float16), pos0=0)

@@ -1,0 +1,183 @@
+"""GPU parity of the full-attention path against the CPU oracle.
+
+Bar: attention outputs within max-abs 2e-3 / rel 1e-2 of the
+reference math in fp16; the KV store bit-exact. Size-independent properties
+at BASELINE's full sizes: a verify row equals the T = 1 call at its position
+bit for bit, a batched call equals per-sequence calls bit for bit, the split
+count does not change the result beyond rounding.
+"""
+import numpy as np
+import pytest
+import torch
+
+from conftest import close, rand_cache, rand_qg
+
+pytestmark = pytest.mark.gpu
+
+SCALE = 256 ** -0.5
+ATOL, RTOL = 2e-3, 1e-2
+
+
+def to_dev(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def test_kv_store_bit_exact(fl, dev, rng):
+    layers, max_pos, T, pos0, layer = 3, 300, 37, 200, 1
+    kc = torch.zeros((layers, max_pos, 4, 256), dtype=torch.float16, device=dev)
+    vc = torch.zeros_like(kc)
+    k = rng.standard_normal((T, 4, 256)).astype(np.float16)
+    v = rng.standard_normal((T, 4, 256)).astype(np.float16)
+    fl.ops.kv_store(to_dev(k, dev), to_dev(v, dev), kc, vc, layer=layer, pos0=pos0)
+    torch.cuda.synchronize()
+    kh, vh = kc.cpu().numpy(), vc.cpu().numpy()
+    assert np.array_equal(kh[layer, pos0:pos0 + T], k) and np.array_equal(vh[layer, pos0:pos0 + T], v)
+    kh[layer, pos0:pos0 + T] = 0
+    vh[layer, pos0:pos0 + T] = 0
+    assert not kh.any() and not vh.any()
+    with pytest.raises(ValueError):
+        fl.ops.kv_store(to_dev(k, dev), to_dev(v, dev), kc, vc, layer=layer, pos0=max_pos - 3)
+
+
+@pytest.mark.parametrize("L,T", [(1, 1), (2, 2), (31, 1), (32, 1), (33, 3), (100, 4),
+                                 (1000, 3), (4096, 1), (5000, 2)])
+def test_split_and_merge_vs_oracle(fl, dev, orc, rng, L, T):
+    kc, vc = rand_cache(rng, L)
+    qg = rand_qg(rng, T)
+    pos0 = L - T
+    split = 8
+    kd, vd, qd = to_dev(kc, dev), to_dev(vc, dev), to_dev(qg, dev)
+    pacc = torch.empty((T, 24, split, 256), dtype=torch.float32, device=dev)
+    pm = torch.empty((T, 24, split), dtype=torch.float32, device=dev)
+    pd = torch.empty_like(pm)
+    z = torch.empty((T, 24, 256), dtype=torch.float16, device=dev)
+    fl.ops.attention_split_gqa(qd, kd, vd, pacc, pm, pd, pos0=pos0, split_rows=64, T=T, split=split)
+    fl.ops.attention_merge(pacc, pm, pd, z, T=T, split=split, gate=qd)
+    torch.cuda.synchronize()
+    want = orc.attention_decode(qg, kc, vc, pos0, max_pos=L, scale=SCALE)
+    err, ok = close(z.cpu().numpy(), want, ATOL, RTOL)
+    assert ok, f"L={L} T={T}: max|err| {err}"
+
+
+@pytest.mark.parametrize("Lmax", [8192, 32768, 102400])
+def test_config2_decode_verify_vs_oracle(fl, dev, orc, Lmax):
+    """Config 2: B=4, T=3 verify rows, lengths seeded-uniform in [0.9 Lmax, Lmax]."""
+    rng = np.random.default_rng(Lmax)
+    B, T = 4, 3
+    lens = rng.integers(int(np.ceil(0.9 * Lmax)), Lmax + 1, size=B)
+    caches = [rand_cache(rng, int(L)) for L in lens]
+    qg = np.stack([rand_qg(rng, T) for _ in range(B)])
+    pos0s = [int(L) - T for L in lens]
+    z = fl.ops.attn_decode(to_dev(qg, dev), [to_dev(c[0], dev) for c in caches],
+                           [to_dev(c[1], dev) for c in caches], pos0s)
+    torch.cuda.synchronize()
+    zh = z.cpu().numpy()
+    for b in range(B):
+        want = orc.attention_decode(qg[b], caches[b][0], caches[b][1], pos0s[b],
+                                    max_pos=int(lens[b]), scale=SCALE)
+        err, ok = close(zh[b], want, ATOL, RTOL)
+        assert ok, f"Lmax={Lmax} seq {b} (L={lens[b]}): max|err| {err}"
+
+
+def test_verify_rows_equal_t1_calls_bit_exact(fl, dev, rng):
+    L = 40000
+    kc, vc = rand_cache(rng, L)
+    qg = rand_qg(rng, 4)
+    kd, vd = to_dev(kc, dev), to_dev(vc, dev)
+    pos0 = L - 4
+    zv = fl.ops.attn_decode(to_dev(qg[None], dev), [kd], [vd], [pos0])
+    for t in range(4):
+        z1 = fl.ops.attn_decode(to_dev(qg[None, t:t + 1], dev), [kd], [vd], [pos0 + t])
+        assert torch.equal(zv[0, t], z1[0, 0]), t
+
+
+def test_batched_equals_single_bit_exact(fl, dev, rng):
+    lens = [3000, 17, 9000, 1]
+    caches = [rand_cache(rng, L) for L in lens]
+    qg = np.stack([rand_qg(rng, 1) for _ in lens])
+    ks = [to_dev(c[0], dev) for c in caches]
+    vs = [to_dev(c[1], dev) for c in caches]
+    zb = fl.ops.attn_decode(to_dev(qg, dev), ks, vs, [L - 1 for L in lens])
+    for b, L in enumerate(lens):
+        z1 = fl.ops.attn_decode(to_dev(qg[b:b + 1], dev), [ks[b]], [vs[b]], [L - 1])
+        assert torch.equal(zb[b], z1[0]), b
+
+
+def test_split_count_independence(fl, dev, rng):
+    L = 20000
+    kc, vc = rand_cache(rng, L)
+    qg = rand_qg(rng, 2)
+    kd, vd, qd = to_dev(kc, dev), to_dev(vc, dev), to_dev(qg[None], dev)
+    za = fl.ops.attn_decode(qd, [kd], [vd], [L - 2], split_rows=32, split=4)
+    zb = fl.ops.attn_decode(qd, [kd], [vd], [L - 2], split_rows=64, split=300)
+    err, ok = close(za.cpu().numpy(), zb.cpu().numpy().astype(np.float64), 1e-3, 1e-2)
+    assert ok, err
+
+
+def test_gate_is_sigmoid(fl, dev, rng):
+    L = 700
+    kc, vc = rand_cache(rng, L)
+    qg = rand_qg(rng, 1)
+    kd, vd = to_dev(kc, dev), to_dev(vc, dev)
+    z0 = fl.ops.attn_decode(to_dev(qg[None], dev), [kd], [vd], [L - 1], gate=False)
+    qg[..., 256:] = 0.0
+    zg = fl.ops.attn_decode(to_dev(qg[None], dev), [kd], [vd], [L - 1], gate=True)
+    want = (z0.float() * 0.5).half()
+    assert torch.equal(zg, want)
+
+
+def test_decode_rejects_bad_geometry(fl, dev, rng):
+    kc, vc = rand_cache(rng, 64)
+    kd, vd = to_dev(kc, dev), to_dev(vc, dev)
+    qg = to_dev(rand_qg(rng, 6)[None], dev)       # 6 tokens x 6 heads = 36 > 32 columns
+    with pytest.raises(ValueError):
+        fl.ops.attn_decode(qg, [kd], [vd], [10])
+    with pytest.raises(ValueError):                # pos0 + T beyond the cache
+        fl.ops.attn_decode(to_dev(rand_qg(rng, 1)[None], dev), [kd], [vd], [64])
+
+
+# --------------------------------------------------------------------------
+# prefill
+# --------------------------------------------------------------------------
+
+@pytest.mark.parametrize("T,pos0", [(1, 0), (8, 0), (13, 0), (40, 3), (300, 0), (129, 1000),
+                                    (1024, 1000), (2048, 0)])
+def test_prefill_vs_oracle(fl, dev, orc, rng, T, pos0):
+    L = pos0 + T
+    kc, vc = rand_cache(rng, L)
+    qg = rand_qg(rng, T)
+    # the new rows arrive through the fused kv_store; older rows are already cached
+    kd = torch.zeros((L, 4, 256), dtype=torch.float16, device=dev)
+    vd = torch.zeros_like(kd)
+    kd[:pos0] = to_dev(kc[:pos0], dev)
+    vd[:pos0] = to_dev(vc[:pos0], dev)
+    z = fl.ops.attention_prefill(to_dev(qg, dev), kd, vd, pos0=pos0,
+                                 k_new=to_dev(kc[pos0:], dev), v_new=to_dev(vc[pos0:], dev))
+    torch.cuda.synchronize()
+    assert np.array_equal(kd.cpu().numpy(), kc) and np.array_equal(vd.cpu().numpy(), vc)
+    want = orc.attention_prefill(qg, kc, vc, q_pitch=512, pos0=pos0, max_pos=L, scale=SCALE, T=T)
+    err, ok = close(z.cpu().numpy(), want, ATOL, RTOL)
+    assert ok, f"T={T} pos0={pos0}: max|err| {err}"
+
+
+@pytest.mark.parametrize("L", [8192, 32768])
+def test_prefill_config3_sampled_rows(fl, dev, orc, L):
+    """Config 3 at full size: q pre-scaled by 1/16 (scale 1 in the kernel); sampled
+    rows against the float64 closed form, every row finite."""
+    rng = np.random.default_rng(L)
+    kc, vc = rand_cache(rng, L)
+    qg = rand_qg(rng, L)
+    q = np.ascontiguousarray(qg[..., :256])
+    kd = torch.zeros((L, 4, 256), dtype=torch.float16, device=dev)
+    vd = torch.zeros_like(kd)
+    z = fl.ops.attention_prefill(to_dev(q, dev), kd, vd, pos0=0, scale=1.0,
+                                 k_new=to_dev(kc, dev), v_new=to_dev(vc, dev))
+    torch.cuda.synchronize()
+    zh = z.cpu().numpy()
+    assert np.isfinite(zh.astype(np.float32)).all()
+    for t in sorted({0, 1, 63, 64, 127, L // 2 + 5, L - 2, L - 1,
+                     *rng.integers(0, L, 4).tolist()}):
+        want = orc.attention_exact(q[t:t + 1], kc, vc, q_pitch=256, pos0=t, max_pos=L,
+                                   scale=1.0, T=1)
+        err, ok = close(zh[t:t + 1], want, ATOL, RTOL)
+        assert ok, f"L={L} row {t}: max|err| {err}"

@@ -1,0 +1,232 @@
+"""GPU parity of the Gated DeltaNet path against the CPU oracle.
+
+Bar: GDN recurrent state within rel 1e-4 (fp32) after 1024
+decode steps (config 1); outputs y within max-abs 2e-3 / rel 1e-2 (fp16);
+conv states bit-exact (they are fp16 copies of inputs). The chunked WY scan
+(config 4) against the step-by-step recurrence.
+"""
+import numpy as np
+import pytest
+import torch
+
+from conftest import close
+
+pytestmark = pytest.mark.gpu
+
+QS = 128 ** -0.5
+ROW = 10240
+NV, NK = 48, 16
+STATE_RTOL = 1e-4
+
+
+def to_dev(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def rel_err(got, want):
+    return float(np.abs(np.asarray(got, np.float64) - want).max() / np.abs(want).max())
+
+
+def ulp16_diff(a, b):
+    ai = a.view(np.int16).astype(np.int32)
+    bi = b.view(np.int16).astype(np.int32)
+    ai = np.where(ai < 0, -32768 - ai, ai)
+    bi = np.where(bi < 0, -32768 - bi, bi)
+    return int(np.abs(ai - bi).max())
+
+
+@pytest.mark.parametrize("T,pos0", [(1, 0), (1, 9), (5, 0), (8, 3), (64, 100)])
+def test_conv1d_vs_oracle(fl, dev, orc, rng, T, pos0):
+    x = rng.standard_normal((T, ROW)).astype(np.float16)
+    w = (rng.standard_normal((ROW, 4)) * 0.5).astype(np.float16)
+    st = rng.standard_normal((ROW, 3)).astype(np.float16)
+    y = torch.empty((T, ROW), dtype=torch.float16, device=dev)
+    so = torch.empty((ROW, 3), dtype=torch.float16, device=dev)
+    fl.ops.conv1d_causal(to_dev(x, dev), to_dev(w, dev), to_dev(st, dev), y, so, T=T, pos0=pos0)
+    torch.cuda.synchronize()
+    y_r, so_r = orc.conv1d_causal(x, w, st, dim=ROW, T=T, pos0=pos0, row_stride=ROW)
+    assert np.array_equal(so.cpu().numpy(), so_r)
+    assert ulp16_diff(y.cpu().numpy(), y_r) <= 1
+
+
+@pytest.mark.parametrize("T", [1, 2, 3])
+def test_conv_rows_vs_oracle(fl, dev, orc, rng, T):
+    x = rng.standard_normal((T, ROW)).astype(np.float16)
+    w = (rng.standard_normal((ROW, 4)) * 0.5).astype(np.float16)
+    st = rng.standard_normal((ROW, 3)).astype(np.float16)
+    y = torch.empty((T, ROW), dtype=torch.float16, device=dev)
+    sts = [torch.empty((ROW, 3), dtype=torch.float16, device=dev) for _ in range(3)]
+    fl.ops.conv1d_causal_rows(to_dev(x, dev), to_dev(w, dev), to_dev(st, dev), y, *sts[:T], T=T,
+                              pos0=4)
+    torch.cuda.synchronize()
+    y_r, sts_r = orc.conv1d_causal_rows(x, w, st, dim=ROW, T=T, pos0=4, row_stride=ROW)
+    assert ulp16_diff(y.cpu().numpy(), y_r) <= 1
+    for t in range(T):
+        assert np.array_equal(sts[t].cpu().numpy(), sts_r[t])
+
+
+def test_l2norm_and_gates_vs_oracle(fl, dev, orc, rng):
+    T = 5
+    x = rng.standard_normal((T, ROW)).astype(np.float16)
+    x[2, 128:256] = 0
+    y = torch.zeros((T, ROW), dtype=torch.float16, device=dev)
+    fl.ops.l2norm_scaled(to_dev(x, dev), y, rows=80, T=T)
+    a = (rng.standard_normal((T, NV)) * 5).astype(np.float32)
+    a[0, :4] = [100.0, -40.0, 20.0, 20.0001]
+    b = rng.standard_normal((T, NV)).astype(np.float32)
+    A_log = rng.standard_normal(NV).astype(np.float32)
+    dt = rng.standard_normal(NV).astype(np.float32)
+    beta = torch.empty((T, NV), dtype=torch.float32, device=dev)
+    decay = torch.empty_like(beta)
+    fl.ops.gdn_scalars(to_dev(a, dev), to_dev(b, dev), to_dev(A_log, dev), to_dev(dt, dev),
+                       beta, decay, T=T)
+    torch.cuda.synchronize()
+    y_r = orc.l2norm_scaled(x, n=128, rows=80, pitch=128, eps=1e-6, scale=1.0, T=T)
+    assert ulp16_diff(y.cpu().numpy(), y_r) <= 1
+    b_r, d_r = orc.gdn_scalars(a, b, A_log, dt, T=T, n_heads=NV)
+    assert np.abs(beta.cpu().numpy() - b_r).max() <= 2e-7
+    assert np.abs(decay.cpu().numpy() - d_r).max() / d_r.max() <= 2e-6
+
+
+def _scan_inputs(rng, T):
+    c = rng.standard_normal((T, ROW)).astype(np.float16)
+    ln = np.zeros_like(c)
+    for t in range(T):
+        for r in range(32):
+            seg = c[t, 128 * r:128 * r + 128].astype(np.float64)
+            ln[t, 128 * r:128 * r + 128] = seg / np.linalg.norm(seg)
+    ln[:, 4096:] = c[:, 4096:]
+    beta = (1 / (1 + np.exp(-rng.standard_normal((T, NV))))).astype(np.float32)
+    decay = np.exp(-np.log1p(np.exp(rng.standard_normal((T, NV))))).astype(np.float32)
+    S0 = (rng.standard_normal((NV, 128, 128)) * 0.02).astype(np.float32)
+    return ln, beta, decay, S0
+
+
+@pytest.mark.parametrize("T", [1, 3, 40])
+def test_gdn_scan_vs_oracle(fl, dev, orc, rng, T):
+    ln, beta, decay, S0 = _scan_inputs(rng, T)
+    lnd = to_dev(ln, dev)
+    S = to_dev(S0, dev)
+    ck = torch.zeros((max(T - 1, 1), NV, 128, 128), dtype=torch.float32, device=dev)
+    y = torch.empty((T, NV * 128), dtype=torch.float16, device=dev)
+    fl.ops.gdn_scan(lnd[:, :2048], lnd[:, 2048:4096], lnd[:, 4096:], to_dev(beta, dev),
+                    to_dev(decay, dev), S, y, T=T, ck=ck, ck_step=NV * 128 * 128)
+    torch.cuda.synchronize()
+    S_r = S0.copy()
+    ck_r = np.zeros((max(T - 1, 1), NV, 128, 128), np.float32)
+    y_r = orc.gdn_scan(ln[:, :2048], ln[:, 2048:4096], ln[:, 4096:], beta, decay, S_r, T=T,
+                       qk_stride=ROW, v_stride=ROW, out_scale=QS, ck=ck_r, ck_step=NV * 128 * 128)
+    Sh = S.cpu().numpy()
+    print(f"gdn_scan T={T}: state bit-exact {np.array_equal(Sh, S_r)}, "
+          f"rel {rel_err(Sh, S_r):.2e}, y ulps {ulp16_diff(y.cpu().numpy(), y_r)}")
+    assert rel_err(Sh, S_r) <= STATE_RTOL
+    err, ok = close(y.cpu().numpy(), y_r, 2e-3, 1e-2)
+    assert ok, err
+    if T > 1:
+        assert rel_err(ck.cpu().numpy(), ck_r) <= STATE_RTOL
+
+
+def _decode_weights(rng):
+    w = (rng.standard_normal((ROW, 4)) * 0.5).astype(np.float16)
+    A_log = np.zeros(NV, np.float32)
+    dt = np.zeros(NV, np.float32)
+    return w, A_log, dt
+
+
+def test_config1_decode_1024_steps_vs_oracle(fl, dev, orc):
+    """Config 1: B=4, S0 ~ N(0, 0.02), conv fused, fp16 conv ring, 1024 steps;
+    the fp32 state within rel 1e-4 of the oracle's after the last step."""
+    rng = np.random.default_rng(1)
+    B, steps = 4, 1024
+    w, A_log, dt = _decode_weights(rng)
+    S0 = (rng.standard_normal((B, NV, 128, 128)) * 0.02).astype(np.float32)
+    wd, Ad, dtd = to_dev(w, dev), to_dev(A_log, dev), to_dev(dt, dev)
+    S_d = [to_dev(S0[b], dev) for b in range(B)]
+    ring = [[torch.zeros((ROW, 3), dtype=torch.float16, device=dev) for _ in range(2)]
+            for _ in range(B)]
+    S_r = [S0[b].copy() for b in range(B)]
+    ring_r = [[np.zeros((ROW, 3), np.float16) for _ in range(2)] for _ in range(B)]
+    worst_y = 0.0
+    for step in range(steps):
+        x = rng.standard_normal((B, 1, ROW)).astype(np.float16)
+        a = rng.standard_normal((B, 1, NV)).astype(np.float32)
+        bb = rng.standard_normal((B, 1, NV)).astype(np.float32)
+        ph = step & 1
+        y = fl.ops.gdn_decode(to_dev(x, dev), S_d, to_dev(a, dev), to_dev(bb, dev), Ad, dtd, T=1,
+                              pos0s=[step] * B, conv_fused=True, conv_w=wd,
+                              cst_in=[ring[b][ph] for b in range(B)],
+                              cst_out=[ring[b][ph ^ 1] for b in range(B)])
+        yh = y.cpu().numpy()
+        for b in range(B):
+            y_r = orc.gdn_decode(None, S_r[b], a[b], bb[b], A_log, dt, T=1, out_scale=QS,
+                                 cx=x[b], cw=w, cst_in=ring_r[b][ph], cst_out=ring_r[b][ph ^ 1],
+                                 pos0=step)
+            worst_y = max(worst_y, float(np.abs(yh[b].astype(np.float64) - y_r).max()))
+    worst_s = max(rel_err(S_d[b].cpu().numpy(), S_r[b]) for b in range(B))
+    for b in range(B):
+        assert np.array_equal(ring[b][0].cpu().numpy(), ring_r[b][0])
+    print(f"config 1: 1024 steps, state rel {worst_s:.2e}, max|dy| {worst_y:.2e}")
+    assert worst_s <= STATE_RTOL
+    assert worst_y <= 2e-3
+
+
+def test_verify_t3_checkpoints_and_rollback(fl, dev, orc, rng):
+    """MTP verify (runtime.py:3017-3053): conv rows then the fused scan with
+    checkpoints; each checkpoint equals the state after that many T=1 steps."""
+    T = 3
+    w, A_log, dt = _decode_weights(rng)
+    A_log[:] = rng.standard_normal(NV) * 0.3
+    x = rng.standard_normal((1, T, ROW)).astype(np.float16)
+    st = rng.standard_normal((ROW, 3)).astype(np.float16)
+    a = rng.standard_normal((1, T, NV)).astype(np.float32)
+    bb = rng.standard_normal((1, T, NV)).astype(np.float32)
+    S0 = (rng.standard_normal((NV, 128, 128)) * 0.02).astype(np.float32)
+    c = torch.empty((1, T, ROW), dtype=torch.float16, device=dev)
+    sts = [torch.empty((ROW, 3), dtype=torch.float16, device=dev) for _ in range(3)]
+    fl.ops.conv1d_causal_rows(to_dev(x[0], dev), to_dev(w, dev), to_dev(st, dev), c[0], *sts,
+                              T=T, pos0=20)
+    S = to_dev(S0, dev)
+    ck = torch.zeros((T - 1, NV, 128, 128), dtype=torch.float32, device=dev)
+    y = fl.ops.gdn_decode(c, [S], to_dev(a, dev), to_dev(bb, dev), to_dev(A_log, dev),
+                          to_dev(dt, dev), T=T, pos0s=[20], ck=[ck], ck_step=NV * 128 * 128)
+    # T = 1 steps on the GPU from the same start: checkpoint t == state after t+1 steps
+    S1 = to_dev(S0, dev)
+    for t in range(T):
+        y1 = fl.ops.gdn_decode(c[:, t:t + 1].contiguous(), [S1], to_dev(a[:, t:t + 1], dev),
+                               to_dev(bb[:, t:t + 1], dev), to_dev(A_log, dev), to_dev(dt, dev),
+                               T=1, pos0s=[20 + t])
+        assert torch.equal(y1[0, 0], y[0, t])
+        want = S1 if t == T - 1 else ck[t]
+        assert torch.equal(S1, want), t
+    torch.cuda.synchronize()
+    # and against the oracle
+    S_r = S0.copy()
+    y_c, _ = orc.conv1d_causal_rows(x[0], w, st, dim=ROW, T=T, pos0=20, row_stride=ROW)
+    ck_r = np.zeros((T - 1, NV, 128, 128), np.float32)
+    y_r = orc.gdn_decode(y_c, S_r, a[0], bb[0], A_log, dt, T=T, out_scale=QS, ck=ck_r,
+                         ck_step=NV * 128 * 128)
+    assert rel_err(S.cpu().numpy(), S_r) <= STATE_RTOL
+    assert rel_err(ck.cpu().numpy(), ck_r) <= STATE_RTOL
+    err, ok = close(y[0].cpu().numpy(), y_r, 2e-3, 1e-2)
+    assert ok, err
+
+
+@pytest.mark.parametrize("T", [1, 37, 64, 200, 8192])
+def test_chunked_vs_recurrence(fl, dev, orc, T):
+    """Config 4 (T = 8192) and ragged lengths: the chunked WY scan against the
+    oracle's step-by-step recurrence on the same fp16 inputs."""
+    rng = np.random.default_rng(T)
+    ln, beta, decay, S0 = _scan_inputs(rng, T)
+    lnd = to_dev(ln, dev)
+    S = to_dev(S0, dev)
+    y = fl.ops.gdn_prefill_chunked(lnd[:, :2048], lnd[:, 2048:4096], lnd[:, 4096:],
+                                   to_dev(beta, dev), to_dev(decay, dev), S, T=T)
+    torch.cuda.synchronize()
+    S_r = S0.copy()
+    y_r = orc.gdn_scan(ln[:, :2048], ln[:, 2048:4096], ln[:, 4096:], beta, decay, S_r, T=T,
+                       qk_stride=ROW, v_stride=ROW, out_scale=QS)
+    Sh = S.cpu().numpy()
+    print(f"chunked T={T}: state rel {rel_err(Sh, S_r):.2e}")
+    assert rel_err(Sh, S_r) <= STATE_RTOL
+    err, ok = close(y.cpu().numpy(), y_r, 2e-3, 1e-2)
+    assert ok, f"T={T}: max|dy| {err}"
