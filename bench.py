@@ -1,0 +1,343 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X attention / Gated DeltaNet hot path.
+
+Primary line (BASELINE.json's metric on configs[1]): the fused GDN decode
+step of 4 sequences (conv + L2 norm + gates + delta rule, one launch per
+step), states of 48 GDN layers rotated (604 MB, past the 256 MB Infinity
+Cache) as a decode through the model does. A step is one launch over one
+layer's states for the 4 sequences; K steps are captured in one HIP graph
+and replayed between HIP events on the launch stream.
+
+`extra` carries the other configs: GQA decode + MTP verify (config 2, B=4,
+T=3, 8k / 32k / 100k), causal prefill attention (config 3, 2k / 8k / 32k),
+the chunked GDN prefill (config 4) and config 0's single decode step.
+`cpu_baseline` is the PyTorch fp32 CPU implementation (oracle/torch_ref.py)
+of the same GDN decode step on the host's cores, over a bounded sample.
+
+Usage: python bench.py [--gpus 1] [--steps 1024] [--warmup 48] [--quick]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+sys.path.insert(0, str(REPO))
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
+MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA, TFLOP/s
+METRIC = "attn/GDN decode µs/step + HBM GB/s %peak; prefill tokens/s + MFMA util"
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+# ---------------------------------------------------------------------------
+# timing helpers
+# ---------------------------------------------------------------------------
+
+def graph_of(torch, fn, n):
+    """Capture n calls fn(i) into one HIP graph (launch overhead out of the timing)."""
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn(0)                                    # one eager call on the capture stream
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(g):
+        for i in range(n):
+            fn(i)
+    return g
+
+
+def time_graph(torch, g, reps=1):
+    st, en = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    st.record()
+    for _ in range(reps):
+        g.replay()
+    en.record()
+    torch.cuda.synchronize()
+    return st.elapsed_time(en) / reps          # ms
+
+
+# ---------------------------------------------------------------------------
+# config 1: GDN decode (primary)
+# ---------------------------------------------------------------------------
+
+GDN_LAYERS = 48
+B = 4
+
+
+def gdn_decode_bytes(B=4, nv=48, V=128, K=128, row=10240):
+    state = 2 * B * nv * V * K * 4            # S read + write
+    ring = 2 * B * row * 3 * 2                # conv state read + write
+    x = B * row * 2                           # raw q|k|v rows
+    w = row * 4 * 2                           # conv weights
+    ab = 2 * B * nv * 4 + 2 * nv * 4          # a, b, A_log, dt_bias
+    y = B * nv * V * 2
+    return state + ring + x + w + ab + y
+
+
+def bench_gdn_decode(torch, fl, steps, warmup):
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(1)
+    L, row, nv = GDN_LAYERS, 10240, 48
+    S = torch.randn((L, B, nv, 128, 128), generator=g, device=dev) * 0.02
+    rings = torch.zeros((L, B, 2, row, 3), dtype=torch.float16, device=dev)
+    x = torch.randn((L, B, 1, row), generator=g, device=dev).half()
+    a = torch.randn((L, B, 1, nv), generator=g, device=dev)
+    b = torch.randn((L, B, 1, nv), generator=g, device=dev)
+    w = (torch.randn((L, row, 4), generator=g, device=dev) * 0.5).half()
+    A_log = torch.zeros((L, nv), device=dev)
+    dt_bias = torch.zeros((L, nv), device=dev)
+    y = torch.empty((L, B, 1, nv * 128), dtype=torch.float16, device=dev)
+
+    def step(i):
+        l, ph = i % L, (i // L) & 1
+        fl.ops.gdn_decode(x[l], [S[l, j] for j in range(B)], a[l], b[l], A_log[l], dt_bias[l],
+                          y[l], T=1, pos0s=[100 + i // L] * B, conv_fused=True, conv_w=w[l],
+                          cst_in=[rings[l, j, ph] for j in range(B)],
+                          cst_out=[rings[l, j, ph ^ 1] for j in range(B)])
+
+    # graph replay == eager, on a copy of the state (one layer, 2 tokens)
+    S0, r0 = S.clone(), rings.clone()
+    for i in (0, L):
+        step(i)
+    eager = (S[0].clone(), rings[0].clone())
+    S.copy_(S0)
+    rings.copy_(r0)
+    g2 = graph_of(torch, lambda i: step(0 if i == 0 else L), 2)
+    S.copy_(S0)
+    rings.copy_(r0)
+    g2.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(S[0], eager[0]) and torch.equal(rings[0], eager[1]), \
+        "graph replay differs from eager launches"
+    del S0, r0, g2
+
+    gw = graph_of(torch, step, warmup) if warmup else None
+    gt = graph_of(torch, lambda i: step(warmup + i), steps)
+    if gw is not None:
+        time_graph(torch, gw)
+    ms = time_graph(torch, gt)
+    us = ms * 1e3 / steps
+    nbytes = gdn_decode_bytes()
+    return {"us_per_step": us, "bytes": nbytes, "gbs": nbytes / (us * 1e-6) / 1e9,
+            "steps": steps, "ms": ms}
+
+
+# ---------------------------------------------------------------------------
+# config 2: GQA decode + MTP verify; config 0
+# ---------------------------------------------------------------------------
+
+def bench_attn_decode(torch, fl, Lmax, Bq=4, T=3, iters=20, seed=0):
+    dev = torch.device("cuda:0")
+    import numpy as np
+
+    rng = np.random.default_rng(seed + Lmax)
+    lens = [int(v) for v in rng.integers(int(np.ceil(0.9 * Lmax)), Lmax + 1, size=Bq)]
+    g = torch.Generator(device=dev).manual_seed(seed)
+    kv_bytes = sum(lens) * 4 * 256 * 2 * 2
+    n_sets = max(1, -(-600_000_000 // kv_bytes))     # rotate > 256 MB MALL
+    sets = []
+    for _ in range(n_sets):
+        ks = [torch.randn((L, 4, 256), generator=g, device=dev).half() for L in lens]
+        vs = [torch.randn((L, 4, 256), generator=g, device=dev).half() for L in lens]
+        sets.append((ks, vs))
+    qg = torch.randn((Bq, T, 24, 512), generator=g, device=dev).half()
+    qg[..., :256] *= 1 / 16
+    z = torch.empty((Bq, T, 24, 256), dtype=torch.float16, device=dev)
+    work = torch.empty(fl.ops.attn_decode_work_bytes(Bq, T), dtype=torch.uint8, device=dev)
+    pos0 = [L - T for L in lens]
+
+    def call(i):
+        ks, vs = sets[i % n_sets]
+        fl.ops.attn_decode(qg, ks, vs, pos0, z=z, work=work)
+
+    gr = graph_of(torch, call, iters)
+    time_graph(torch, gr)
+    ms = time_graph(torch, gr, reps=3)
+    us = ms * 1e3 / iters
+    nbytes = kv_bytes + Bq * T * 24 * 512 * 2 + Bq * T * 24 * 256 * 2
+    flops = sum(4 * T * 24 * 256 * L for L in lens)
+    return {"config": f"decode_verify_B{Bq}_T{T}_L{Lmax}", "us_per_step": round(us, 2),
+            "GBs": round(nbytes / (us * 1e-6) / 1e9, 1),
+            "hbm_frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 3),
+            "TFLOPs": round(flops / (us * 1e-6) / 1e12, 1), "lens": lens}
+
+
+# ---------------------------------------------------------------------------
+# config 3: causal prefill attention
+# ---------------------------------------------------------------------------
+
+def bench_prefill(torch, fl, L, iters=3):
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(L)
+    q = (torch.randn((L, 24, 256), generator=g, device=dev) / 16).half()
+    k = torch.randn((L, 4, 256), generator=g, device=dev).half()
+    v = torch.randn((L, 4, 256), generator=g, device=dev).half()
+    kc = torch.zeros((L, 4, 256), dtype=torch.float16, device=dev)
+    vc = torch.zeros_like(kc)
+    z = torch.empty((L, 24, 256), dtype=torch.float16, device=dev)
+
+    def call(i):
+        fl.ops.attention_prefill(q, kc, vc, pos0=0, scale=1.0, z=z, k_new=k, v_new=v)
+
+    gr = graph_of(torch, call, iters)
+    time_graph(torch, gr)
+    ms = time_graph(torch, gr)
+    us = ms * 1e3 / iters
+    flops = 4 * 24 * 256 * L * (L + 1) / 2
+    tf = flops / (us * 1e-6) / 1e12
+    return {"config": f"prefill_L{L}", "us": round(us, 1), "tok_s": round(L / (us * 1e-6)),
+            "TFLOPs": round(tf, 1), "mfma_frac": round(tf / MFMA_F16_PEAK_TFLOPS, 3)}
+
+
+# ---------------------------------------------------------------------------
+# config 4: chunked GDN prefill
+# ---------------------------------------------------------------------------
+
+def bench_chunked(torch, fl, L=8192, iters=3):
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(4)
+    c = torch.randn((L, 10240), generator=g, device=dev)
+    for s0 in range(0, 4096, 128):
+        seg = c[:, s0:s0 + 128]
+        seg /= seg.norm(dim=-1, keepdim=True)
+    c = c.half()
+    beta = torch.sigmoid(torch.randn((L, 48), generator=g, device=dev))
+    decay = torch.exp(-torch.nn.functional.softplus(torch.randn((L, 48), generator=g, device=dev)))
+    S = torch.randn((48, 128, 128), generator=g, device=dev) * 0.02
+    y = torch.empty((L, 6144), dtype=torch.float16, device=dev)
+    work = torch.empty(fl.ops.gdn_chunked_work_bytes(L), dtype=torch.uint8, device=dev)
+
+    def call(i):
+        fl.ops.gdn_prefill_chunked(c[:, :2048], c[:, 2048:4096], c[:, 4096:], beta, decay, S, y,
+                                   T=L, work=work)
+
+    gr = graph_of(torch, call, iters)
+    time_graph(torch, gr)
+    ms = time_graph(torch, gr)
+    us = ms * 1e3 / iters
+    nbytes = L * 16 * 128 * 2 * 2 + L * 48 * 128 * 2 * 2 + L * 48 * 4 * 2 + 2 * 48 * 128 * 128 * 4
+    n_chunks = -(-L // 64)
+    flops = n_chunks * 48 * (10 * 64 * 64 * 128 + 6 * 64 * 128 * 128)
+    return {"config": f"gdn_chunked_L{L}", "us": round(us, 1),
+            "GBs": round(nbytes / (us * 1e-6) / 1e9, 1),
+            "hbm_frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 3),
+            "TFLOPs": round(flops / (us * 1e-6) / 1e12, 2),
+            "mfma_frac": round(flops / (us * 1e-6) / 1e12 / MFMA_F16_PEAK_TFLOPS, 4)}
+
+
+# ---------------------------------------------------------------------------
+# CPU baseline: PyTorch fp32 on the host's cores
+# ---------------------------------------------------------------------------
+
+def cpu_baseline(budget_s=12.0):
+    import torch
+
+    from oracle import torch_ref as tr
+
+    threads = tr.set_threads()
+    gen = torch.Generator().manual_seed(7)
+    row, nv = 10240, 48
+    x = torch.randn((B, row), generator=gen).half()
+    w = (torch.randn((row, 4), generator=gen) * 0.5).half()
+    st = torch.zeros((B, row, 3), dtype=torch.float16)
+    S = torch.randn((B, nv, 128, 128), generator=gen) * 0.02
+    a = torch.randn((B, nv), generator=gen)
+    b = torch.randn((B, nv), generator=gen)
+    A_log = torch.zeros(nv)
+    dt = torch.zeros(nv)
+    tr.gdn_decode_step(x, w, st, S, a, b, A_log, dt, pos0=1)   # warm-up
+    n, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < budget_s and n < 2000:
+        _, st = tr.gdn_decode_step(x, w, st, S, a, b, A_log, dt, pos0=2 + n)
+        n += 1
+    dt_s = (time.perf_counter() - t0) / n
+    return {"value": round(dt_s * 1e6, 1), "unit": "us/step", "cores": threads, "kind": "port",
+            "gbs": round(gdn_decode_bytes() / dt_s / 1e9, 2),
+            "sample": f"{n} fused GDN decode steps (B=4, one layer's state), oracle/torch_ref.py "
+                      f"fp32 on {os.cpu_count()} host cpus"}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=1024)
+    ap.add_argument("--warmup", type=int, default=48)
+    ap.add_argument("--quick", action="store_true", help="primary line only, no extra configs")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported (this build runs "
+              "the hot path on a single MI355X; multi-GPU sharding is design-only)",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import __graft_entry__ as ge
+
+    fl = ge.load_package()
+    torch.cuda.init()
+    log(f"bench: device {torch.cuda.get_device_name(0)}")
+
+    log("bench: config 1 (GDN decode, B=4, 48 layer states rotated) ...")
+    torch.cuda.synchronize()
+    prim = bench_gdn_decode(torch, fl, args.steps, args.warmup)
+    torch.cuda.synchronize()
+    log(f"bench: config 1: {prim['us_per_step']:.2f} us/step, {prim['gbs']:.0f} GB/s")
+
+    extra = []
+    if not args.quick:
+        for fn, kw in ((bench_attn_decode, {"Lmax": 4096, "Bq": 1, "T": 1}),
+                       (bench_attn_decode, {"Lmax": 8192}), (bench_attn_decode, {"Lmax": 32768}),
+                       (bench_attn_decode, {"Lmax": 102400}), (bench_prefill, {"L": 2048}),
+                       (bench_prefill, {"L": 8192}), (bench_prefill, {"L": 32768}),
+                       (bench_chunked, {})):
+            r = fn(torch, fl, **kw)
+            log(f"bench: {r}")
+            extra.append(r)
+            torch.cuda.empty_cache()
+
+    cpu = None if args.no_cpu else cpu_baseline()
+    if cpu:
+        log(f"bench: cpu baseline {cpu}")
+
+    gbs = prim["gbs"]
+    line = {
+        "metric": METRIC,
+        "value": round(gbs, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(prim["us_per_step"] / 1e3, 6),
+        "us_per_step": round(prim["us_per_step"], 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded N(0,1) inputs, S0 ~ N(0, 0.02), A_log = dt_bias = 0)",
+        "config": {"workload": "gdn_decode_B4_fused_conv_48_layer_states", "batch": B,
+                   "k_heads": 16, "v_heads": 48, "d_k": 128, "d_v": 128, "conv_width": 4,
+                   "layer_states_rotated": GDN_LAYERS, "parallelism": "none (1 GPU)"},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "bytes_per_launch": prim["bytes"]},
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

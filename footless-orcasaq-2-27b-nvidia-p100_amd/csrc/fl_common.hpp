@@ -24,10 +24,36 @@ __device__ __forceinline__ f16 f16_sat(float v) {
     return (f16)(v != v ? v : fminf(fmaxf(v, -65504.f), 65504.f));
 }
 
-// sigmoid / silu with the correctly rounded divide (hipcc's default for `/`)
-// and the accurate expf (kernels.cu:229-235 uses a precise divide as well).
-__device__ __forceinline__ float sigmoid_f(float x) { return 1.f / (1.f + expf(-x)); }
-__device__ __forceinline__ float silu_f(float x) { return x / (1.f + expf(-x)); }
+// exp(x) from IEEE operations only, so the CPU oracle (which carries the same
+// routine) rounds every value the same way: Cody-Waite reduction x = n ln2 + r
+// with ln2 split in two (the high part has trailing zero bits, so n * hi is
+// exact), |r| <= ln2 / 2, then the degree-7 Taylor polynomial of e^r (the
+// truncation error r^8 / 8! is below 0.1 ulp) and the exact scaling by 2^n.
+// Accuracy ~1 ulp. Used where an fp32 result is rounded to fp16 and fed back
+// into the recurrence (the conv's silu), so a last-bit difference from a
+// platform exp cannot flip an fp16 value between the kernels and the oracle.
+__device__ __forceinline__ float det_expf(float x) {
+#pragma clang fp contract(off)
+    if (x > 88.72f) return INFINITY;
+    if (x < -103.98f) return 0.f;
+    const float n = rintf(x * 1.44269504f);
+    float r = fmaf(n, -0.693145751953125f, x);
+    r = fmaf(n, -1.4286068203094173e-06f, r);
+    float p = 1.f / 5040.f;
+    p = fmaf(p, r, 1.f / 720.f);
+    p = fmaf(p, r, 1.f / 120.f);
+    p = fmaf(p, r, 1.f / 24.f);
+    p = fmaf(p, r, 1.f / 6.f);
+    p = fmaf(p, r, 0.5f);
+    p = fmaf(p, r, 1.f);
+    p = fmaf(p, r, 1.f);
+    return ldexpf(p, (int)n);
+}
+
+// sigmoid / silu with the correctly rounded divide (hipcc's default for `/`,
+// as kernels.cu:229-235 asks with __fdiv_rn) over det_expf.
+__device__ __forceinline__ float sigmoid_f(float x) { return 1.f / (1.f + det_expf(-x)); }
+__device__ __forceinline__ float silu_f(float x) { return x / (1.f + det_expf(-x)); }
 
 // exp2 on the hardware transcendental unit (v_exp_f32); -inf -> 0.
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }

@@ -38,6 +38,19 @@ __device__ __forceinline__ float row8_sum(float v) {
 
 __device__ __forceinline__ float softplus20(float x) { return x <= 20.f ? log1pf(expf(x)) : x; }
 
+// Sum of squares over a 128-thread row in the reference's order (kernels.cu:
+// 214-227, block_reduce_sum over 4 warps of 32): a tree inside each 32-lane
+// half of the wavefront (lane 0 of the half ends with the warp's sum), the
+// four warp sums then combined as (r0 + r2) + (r1 + r3). `red` holds 8 floats;
+// `w0` is the first of the row's four 32-lane warps. Every thread gets the
+// total. Matching the order keeps the fp16-rounded normalised values
+// identical to the oracle's.
+__device__ __forceinline__ float warp32_tree(float v) {
+#pragma unroll
+    for (int o = 16; o > 0; o >>= 1) v += lane_xor(v, o);
+    return v;
+}
+
 // One token of the delta rule on a lane's 16 columns (`reg`), with k and q
 // (fp32 values of fp16 numbers) at columns c0 + 32j + 0..3. Returns the row's
 // output o = S_new . q (identical in the 8 lanes of the row). The dots run in
@@ -176,7 +189,7 @@ __global__ void conv1d_causal_rows_kernel(const f16* __restrict__ x, const f16* 
 // ---------------------------------------------------------------------------
 __global__ void l2norm_kernel(const f16* __restrict__ x, f16* __restrict__ y, int n, int rows,
                               int pitch, float eps, float scale) {
-    __shared__ float red[2];
+    __shared__ float red[4];
     const int t = blockIdx.y, r = blockIdx.x;
     const f16* xr = x + ((size_t)t * rows + r) * pitch;
     f16* yr = y + ((size_t)t * rows + r) * pitch;
@@ -185,11 +198,10 @@ __global__ void l2norm_kernel(const f16* __restrict__ x, f16* __restrict__ y, in
         const float v = (float)xr[i];
         ss = fmaf(v, v, ss);
     }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) ss += lane_xor(ss, o);
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+    ss = warp32_tree(ss);
+    if ((threadIdx.x & 31) == 0) red[threadIdx.x >> 5] = ss;
     __syncthreads();
-    const float den = sqrtf((red[0] + red[1]) + eps);
+    const float den = sqrtf(((red[0] + red[2]) + (red[1] + red[3])) + eps);
     for (int i = threadIdx.x; i < n; i += blockDim.x) yr[i] = f16_sat(((float)xr[i] / den) * scale);
 }
 
@@ -308,7 +320,7 @@ gdn_decode_kernel(const f16* __restrict__ x, int x_stride, int conv_fused,
                   float l2eps, int group) {
     __shared__ __attribute__((aligned(16))) float sk[GR_K];
     __shared__ __attribute__((aligned(16))) float sq[GR_K];
-    __shared__ float red[4];
+    __shared__ float red[8];
     const int rb = blockIdx.x, hv = blockIdx.y, b = blockIdx.z;
     const int hk = hv / group;
     const int tid = threadIdx.x, ri = tid >> 3, c0 = 4 * (tid & 7);
@@ -339,13 +351,12 @@ gdn_decode_kernel(const f16* __restrict__ x, int x_stride, int conv_fused,
             xv = (float)xr[(half_ ? ch_q : ch_k) + i];
             vt = (float)xr[ch_v];
         }
-        // L2 norms: k over waves 0-1, q over waves 2-3
-        float ss = xv * xv;
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) ss += lane_xor(ss, o);
-        if ((tid & 63) == 0) red[tid >> 6] = ss;
+        // L2 norms: k over threads 0-127, q over 128-255, in the reference's order
+        const float ss = warp32_tree(xv * xv);
+        if ((tid & 31) == 0) red[tid >> 5] = ss;
         __syncthreads();
-        const float den = sqrtf((red[2 * half_] + red[2 * half_ + 1]) + l2eps);
+        const int w0 = 4 * half_;
+        const float den = sqrtf(((red[w0] + red[w0 + 2]) + (red[w0 + 1] + red[w0 + 3])) + l2eps);
         (half_ ? sq : sk)[i] = (float)f16_sat(xv / den);
         __syncthreads();
         float kk[16], qq[16];

@@ -278,7 +278,7 @@ def gdn_decode(x, S, a, b, A_log, dt_bias, y=None, *, T: int, pos0s, conv_fused:
     _lib.call("fl_gdn_decode", _ptr(x, F16, "x", B * T * x_stride), x_stride,
               1 if conv_fused else 0, _ptr(conv_w, F16, "conv_w", x_stride * 4), ci, co,
               _lib.int_array(pos0s), _ptr(a, F32, "a", B * T * ab_stride),
-              _ptr(b, F32, "b", B * T * ab_stride), _ptr(A_log, F32, "A_log", n_vheads),
+              _ptr(b, F32, "b", B * T * ab_stride), ab_stride, _ptr(A_log, F32, "A_log", n_vheads),
               _ptr(dt_bias, F32, "dt_bias", n_vheads), _lib.ptr_array(s_ptrs),
               _ptr(y, F16, "y", B * T * y.shape[-1]), y.shape[-1], ck_arr, ck_step, B, T,
               n_kheads, n_vheads, K, V, float(out_scale), float(l2eps), _stream())

@@ -95,9 +95,32 @@ ORC_API uint16_t orc_f16_sat(float v) {
 
 static inline float rt16(float v) { return orc_h2f(orc_f16_sat(v)); }
 
-/* kernels.cu:234-235 */
-static inline float sigmoid_f(float x) { return 1.f / (1.f + expf(-x)); }
-static inline float silu_f(float x) { return x / (1.f + expf(-x)); }
+/* exp(x) from IEEE operations only (Cody-Waite reduction with a two-part
+ * ln2, degree-7 Taylor polynomial of e^r on |r| <= ln2/2, exact scaling by
+ * 2^n): the same operations as the kernels' det_expf, so an fp32 value that
+ * is then rounded to fp16 (the conv's silu) rounds identically on both sides.
+ * The reference's __expf is a fast-math approximation; neither side
+ * reproduces it. Pinned against libm's exp in tests/test_oracle_gdn.py. */
+ORC_API float orc_det_expf(float x) {
+    if (x > 88.72f) return INFINITY;
+    if (x < -103.98f) return 0.f;
+    const float n = rintf(x * 1.44269504f);
+    float r = fmaf(n, -0.693145751953125f, x);
+    r = fmaf(n, -1.4286068203094173e-06f, r);
+    float p = 1.f / 5040.f;
+    p = fmaf(p, r, 1.f / 720.f);
+    p = fmaf(p, r, 1.f / 120.f);
+    p = fmaf(p, r, 1.f / 24.f);
+    p = fmaf(p, r, 1.f / 6.f);
+    p = fmaf(p, r, 0.5f);
+    p = fmaf(p, r, 1.f);
+    p = fmaf(p, r, 1.f);
+    return ldexpf(p, (int)n);
+}
+
+/* kernels.cu:234-235: precise divide */
+static inline float sigmoid_f(float x) { return 1.f / (1.f + orc_det_expf(-x)); }
+static inline float silu_f(float x) { return x / (1.f + orc_det_expf(-x)); }
 
 /* __shfl_down tree of warp_reduce_sum (kernels.cu:200-204): lane 0's value */
 static float tree_down(float* a, int n) {

@@ -71,6 +71,8 @@ def lib() -> ctypes.CDLL:
             fn.restype = _I if name in ("orc_gdn_scan", "orc_gdn_decode", "orc_gdn_chunked") else None
         L.orc_f16_sat.argtypes = [_F]
         L.orc_f16_sat.restype = ctypes.c_uint16
+        L.orc_det_expf.argtypes = [_F]
+        L.orc_det_expf.restype = _F
         _lib = L
     return _lib
 
@@ -266,6 +268,10 @@ def gdn_chunked(q, k, v, beta, decay, S, *, T, n_kheads=16, n_vheads=48, K=128, 
                                n_vheads * V, float(out_scale), group, chunk)
     assert rc == 0, "orc_gdn_chunked rejected the geometry"
     return y
+
+
+def det_expf(x: float) -> float:
+    return lib().orc_det_expf(float(x))
 
 
 def f16_sat(x: float) -> np.float16:

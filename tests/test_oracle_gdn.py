@@ -46,6 +46,18 @@ def test_gdn_scalars_known_answers(orc):
     assert abs(d2[0, 2] - np.exp(-np.log1p(np.exp(0.75)))) < 1e-6   # softplus(a + dt_bias)
 
 
+def test_det_expf_against_libm(orc):
+    """The exp both the oracle and the kernels use for silu / sigmoid: within
+    2 ulp of the correctly rounded value over the range the path sees."""
+    xs = np.concatenate([np.linspace(-87, 88, 20001), np.linspace(-1, 1, 2001),
+                         [0.0, -0.0, 1e-8, -1e-8, 20.0, -20.0, 0.5 * np.log(2)]]).astype(np.float32)
+    got = np.array([orc.det_expf(x) for x in xs], np.float32)
+    want = np.exp(xs.astype(np.float64))
+    ulp = np.spacing(want.astype(np.float32)).astype(np.float64)
+    assert (np.abs(got - want) / ulp).max() <= 2.0
+    assert orc.det_expf(100.0) == np.inf and orc.det_expf(-110.0) == 0.0
+
+
 def test_conv1d_closed_form(orc):
     dim, T = 2, 3
     x = np.array([[1.0, -1.0], [2.0, 0.5], [-3.0, 4.0]], np.float16)
