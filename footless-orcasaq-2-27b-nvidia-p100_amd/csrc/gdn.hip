@@ -287,30 +287,79 @@ struct GdnSeqs {
     int pos0[FL_MAX_SEQS];
 };
 
-// conv1d_causal at T = 1 for channel d (width 4): returns the fp16-rounded
-// output, writes the new state when st_out is given.
-__device__ __forceinline__ float conv1_ch(const f16* __restrict__ x, const f16* __restrict__ w,
-                                          const f16* __restrict__ st_in, f16* st_out, int d,
-                                          int pos0) {
+__device__ __forceinline__ void load_row16_nt(float (&reg)[16], const float* src) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const f32x4 v4 = __builtin_nontemporal_load((const f32x4*)(src + 32 * j));
+        reg[4 * j] = v4[0];
+        reg[4 * j + 1] = v4[1];
+        reg[4 * j + 2] = v4[2];
+        reg[4 * j + 3] = v4[3];
+    }
+}
+
+__device__ __forceinline__ void store_row16_nt(float* dst, const float (&reg)[16]) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+        __builtin_nontemporal_store((f32x4){reg[4 * j], reg[4 * j + 1], reg[4 * j + 2], reg[4 * j + 3]},
+                                    (f32x4*)(dst + 32 * j));
+}
+
+// Sum of squares of a 128-wide row held two per lane (lane l: x[l], x[l+64])
+// in the reference's order: 32-lane trees give r0 (x[0..31], lane 0), r1
+// (x[32..63], lane 32), r2 (x[64..95], lane 0), r3 (x[96..127], lane 32);
+// the total is (r0 + r2) + (r1 + r3) (kernels.cu:214-227 over 4 warps).
+__device__ __forceinline__ float sumsq128(float lo, float hi) {
+    const float a = warp32_tree(lo * lo) + warp32_tree(hi * hi);   // lane 0: r0+r2, lane 32: r1+r3
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a), 0)) +
+           __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a), 32));
+}
+
+// conv1_ch split in two so the loads can be issued ahead of the state's.
+struct ConvIn {
+    float s0, s1, s2, xv;
+    f16x4 w;
+};
+
+__device__ __forceinline__ ConvIn conv1_load(const f16* __restrict__ x, const f16* __restrict__ w,
+                                             const f16* __restrict__ st_in, int d, int pos0) {
+    ConvIn c;
     const f16* st = st_in + (size_t)d * 3;
-    const float s0 = pos0 > 0 ? (float)st[0] : 0.f;
-    const float s1 = pos0 > 0 ? (float)st[1] : 0.f;
-    const float s2 = pos0 > 0 ? (float)st[2] : 0.f;
-    const float xv = (float)x[d];
+    c.s0 = pos0 > 0 ? (float)st[0] : 0.f;
+    c.s1 = pos0 > 0 ? (float)st[1] : 0.f;
+    c.s2 = pos0 > 0 ? (float)st[2] : 0.f;
+    c.xv = (float)x[d];
+    c.w = *(const f16x4*)(w + (size_t)d * 4);
+    return c;
+}
+
+// conv1d_causal at T = 1 for channel d (width 4, kernels.cu:1634-1679 /
+// 2916-2941): the fp16-rounded silu output; the new state (s1, s2, x) into
+// st_out when given.
+__device__ __forceinline__ float conv1_apply(const ConvIn& c, f16* st_out, int d) {
     float acc = 0.f;
-    acc = fmaf((float)w[(size_t)d * 4 + 0], s0, acc);
-    acc = fmaf((float)w[(size_t)d * 4 + 1], s1, acc);
-    acc = fmaf((float)w[(size_t)d * 4 + 2], s2, acc);
-    acc = fmaf((float)w[(size_t)d * 4 + 3], xv, acc);
+    acc = fmaf((float)c.w[0], c.s0, acc);
+    acc = fmaf((float)c.w[1], c.s1, acc);
+    acc = fmaf((float)c.w[2], c.s2, acc);
+    acc = fmaf((float)c.w[3], c.xv, acc);
     if (st_out != nullptr) {
         f16* so = st_out + (size_t)d * 3;
-        so[0] = f16_sat(s1);
-        so[1] = f16_sat(s2);
-        so[2] = f16_sat(xv);
+        so[0] = f16_sat(c.s1);
+        so[1] = f16_sat(c.s2);
+        so[2] = f16_sat(c.xv);
     }
     return (float)f16_sat(silu_f(acc));
 }
 
+// The decode / verify step: a workgroup of 4 wavefronts owns 32 state rows
+// of one v head (8 lanes a row, 8 rows a wave). Per token every thread
+// convolves (or reads) one q / k channel of the row's k head into LDS (k:
+// threads 0-127, q: 128-255) -- the one workgroup barrier -- then every wave
+// forms both L2 norms itself with in-wave reductions in the reference's
+// order, normalises the 256 values into its own LDS slice and runs the delta
+// rule on its 8 rows. Token 0's conv / gate inputs are issued before the
+// state's loads so the prologue computes while the state streams in; the
+// state is read and written with non-temporal loads / stores (once a step).
 __global__ void __launch_bounds__(GR_THREADS)
 gdn_decode_kernel(const f16* __restrict__ x, int x_stride, int conv_fused,
                   const f16* __restrict__ conv_w, GdnSeqs seqs, const float* __restrict__ ga,
@@ -318,57 +367,81 @@ gdn_decode_kernel(const f16* __restrict__ x, int x_stride, int conv_fused,
                   const float* __restrict__ dt_bias, f16* __restrict__ y, int y_stride,
                   long long ck_step, int T, int n_kheads, int n_vheads, int V, float out_scale,
                   float l2eps, int group) {
-    __shared__ __attribute__((aligned(16))) float sk[GR_K];
-    __shared__ __attribute__((aligned(16))) float sq[GR_K];
-    __shared__ float red[8];
+    __shared__ __attribute__((aligned(16))) float sraw[2 * GR_K];          // k | q, raw
+    __shared__ __attribute__((aligned(16))) float snorm[4][2][GR_K];       // per wave: k | q
     const int rb = blockIdx.x, hv = blockIdx.y, b = blockIdx.z;
     const int hk = hv / group;
-    const int tid = threadIdx.x, ri = tid >> 3, c0 = 4 * (tid & 7);
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int ri = tid >> 3, c0 = 4 * (tid & 7);
     const int vi = rb * GR_ROWS + ri;
     float* Srow = seqs.S[b] + ((size_t)hv * V + vi) * GR_K + c0;
     float* Ck = seqs.Ck[b];
     const int pos0 = seqs.pos0[b];
-    float reg[16];
-    load_row16(reg, Srow);
-    const float dtb = dt_bias[hv], al = expf(A_log[hv]);
-    const int ch_k = n_kheads * GR_K + hk * GR_K, ch_q = hk * GR_K;
+    const int half_ = tid >> 7, i = tid & 127;
+    const int ch = (half_ ? hk * GR_K : n_kheads * GR_K + hk * GR_K) + i;   // q | k channel
     const int ch_v = 2 * n_kheads * GR_K + hv * V + vi;
+    // token 0's inputs first, then the state: the prologue runs while S streams in
+    const float dtb = dt_bias[hv], A = A_log[hv];
+    const float ga0 = ga[(size_t)b * T * ab_stride + hv], gb0 = gb[(size_t)b * T * ab_stride + hv];
+    ConvIn cq, cv;
+    const f16* x0 = x + (size_t)b * T * x_stride;
+    if (conv_fused) {
+        cq = conv1_load(x0, conv_w, seqs.cst_in[b], ch, pos0);
+        cv = conv1_load(x0, conv_w, seqs.cst_in[b], ch_v, pos0);
+    } else {
+        cq.xv = (float)x0[ch];
+        cv.xv = (float)x0[ch_v];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    float reg[16];
+    load_row16_nt(reg, Srow);
+    __builtin_amdgcn_sched_barrier(0);
+    const float al = expf(A);
     for (int t = 0; t < T; ++t) {
         const size_t bt_row = (size_t)b * T + t;
-        const f16* xr = x + bt_row * x_stride;
-        const float bt = sigmoid_f(gb[bt_row * ab_stride + hv]);
-        const float dt = expf(-al * softplus20(ga[bt_row * ab_stride + hv] + dtb));
-        // this thread's q (tid >= 128) or k (tid < 128) channel, and the row's v
-        const int half_ = tid >> 7, i = tid & 127;
+        if (t > 0) {   // verify rows: the conv output of row t (conv_fused is T == 1 only)
+            const f16* xr = x + bt_row * x_stride;
+            cq.xv = (float)xr[ch];
+            cv.xv = (float)xr[ch_v];
+        }
+        const float a_t = t == 0 ? ga0 : ga[bt_row * ab_stride + hv];
+        const float b_t = t == 0 ? gb0 : gb[bt_row * ab_stride + hv];
+        const float bt = sigmoid_f(b_t);
+        const float dt = expf(-al * softplus20(a_t + dtb));
         float xv, vt;
         if (conv_fused) {
             const bool own = (hv % group) == 0 && rb == 0;   // one workgroup stores q / k state
-            xv = conv1_ch(xr, conv_w, seqs.cst_in[b], own ? seqs.cst_out[b] : nullptr,
-                          (half_ ? ch_q : ch_k) + i, pos0);
-            vt = conv1_ch(xr, conv_w, seqs.cst_in[b], c0 == 0 ? seqs.cst_out[b] : nullptr, ch_v,
-                          pos0);
+            xv = conv1_apply(cq, own ? seqs.cst_out[b] : nullptr, ch);
+            vt = conv1_apply(cv, c0 == 0 ? seqs.cst_out[b] : nullptr, ch_v);
         } else {
-            xv = (float)xr[(half_ ? ch_q : ch_k) + i];
-            vt = (float)xr[ch_v];
+            xv = cq.xv;
+            vt = cv.xv;
         }
-        // L2 norms: k over threads 0-127, q over 128-255, in the reference's order
-        const float ss = warp32_tree(xv * xv);
-        if ((tid & 31) == 0) red[tid >> 5] = ss;
+        sraw[tid] = xv;
         __syncthreads();
-        const int w0 = 4 * half_;
-        const float den = sqrtf(((red[w0] + red[w0 + 2]) + (red[w0 + 1] + red[w0 + 3])) + l2eps);
-        (half_ ? sq : sk)[i] = (float)f16_sat(xv / den);
-        __syncthreads();
+        // both norms in this wave, the reference's order
+        const float k_lo = sraw[lane], k_hi = sraw[lane + 64];
+        const float q_lo = sraw[GR_K + lane], q_hi = sraw[GR_K + lane + 64];
+        const float den_k = sqrtf(sumsq128(k_lo, k_hi) + l2eps);
+        const float den_q = sqrtf(sumsq128(q_lo, q_hi) + l2eps);
+        float* sn = &snorm[w][0][0];
+        sn[lane] = (float)f16_sat(k_lo / den_k);
+        sn[lane + 64] = (float)f16_sat(k_hi / den_k);
+        sn[GR_K + lane] = (float)f16_sat(q_lo / den_q);
+        sn[GR_K + lane + 64] = (float)f16_sat(q_hi / den_q);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         float kk[16], qq[16];
-        gather16(kk, sk, c0);
-        gather16(qq, sq, c0);
+        gather16(kk, sn, c0);
+        gather16(qq, sn + GR_K, c0);
         const float o = delta_rule_token(reg, kk, qq, vt, bt, dt);
         if (c0 == 0) y[bt_row * y_stride + (size_t)hv * V + vi] = f16_sat(o * out_scale);
         if (Ck != nullptr && t < T - 1)
-            store_row16(Ck + (size_t)t * ck_step + ((size_t)hv * V + vi) * GR_K + c0, reg);
-        __syncthreads();   // sk / sq / red are rewritten by the next token
+            store_row16_nt(Ck + (size_t)t * ck_step + ((size_t)hv * V + vi) * GR_K + c0, reg);
+        if (t + 1 < T) __syncthreads();   // sraw is rewritten by the next token
     }
-    store_row16(Srow, reg);
+    store_row16_nt(Srow, reg);
 }
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
