@@ -43,6 +43,12 @@ constexpr int DEC_HD = 256;
 constexpr int DEC_WAVES = 4;
 constexpr int DEC_THREADS = 64 * DEC_WAVES;
 constexpr int VT_PITCH = 40;   // halves per d row of the transposed V slice (32 + 8 pad)
+#ifndef DEC_NBUF
+#define DEC_NBUF 2                // register tile buffers (prefetch depth + 1)
+#endif
+#ifndef DEC_NT_V
+#define DEC_NT_V true             // V rows streamed with non-temporal loads
+#endif
 
 struct DecSeqs {
     const f16* k[FL_MAX_SEQS];
@@ -96,6 +102,7 @@ struct DecTileRegs {
     f16x8 v[4];   // V[row 4(l&7) + i][64w + 8(l>>3) + 0..7], i = 0..3
 };
 
+template <bool NT_V>
 __device__ __forceinline__ void dec_load_tile(DecTileRegs& r, const f16* __restrict__ kbase,
                                               const f16* __restrict__ vbase, size_t row_stride,
                                               int j, int uhi, int lane, int w) {
@@ -104,7 +111,7 @@ __device__ __forceinline__ void dec_load_tile(DecTileRegs& r, const f16* __restr
     if (krow < uhi) {
         const f16x8* src = (const f16x8*)(kbase + (size_t)krow * row_stride + 64 * w + 32 * hh);
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) r.k[ks] = __builtin_nontemporal_load(src + ks);
+        for (int ks = 0; ks < 4; ++ks) r.k[ks] = src[ks];
     } else {
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) r.k[ks] = (f16x8)(0);
@@ -112,14 +119,15 @@ __device__ __forceinline__ void dec_load_tile(DecTileRegs& r, const f16* __restr
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int vrow = j * DEC_TILE + 4 * (lane & 7) + i;
+        const f16x8* src = (const f16x8*)(vbase + (size_t)vrow * row_stride + 64 * w + 8 * (lane >> 3));
         if (vrow < uhi)
-            r.v[i] = __builtin_nontemporal_load(
-                (const f16x8*)(vbase + (size_t)vrow * row_stride + 64 * w + 8 * (lane >> 3)));
+            r.v[i] = NT_V ? __builtin_nontemporal_load(src) : *src;
         else
             r.v[i] = (f16x8)(0);
     }
 }
 
+template <int NBUF, bool NT_V>
 __global__ void __launch_bounds__(DEC_THREADS)
 attn_decode_split_kernel(const f16* __restrict__ qg, DecSeqs seqs, float* __restrict__ pacc,
                          float* __restrict__ pm, float* __restrict__ pd, int n_q_heads,
@@ -240,16 +248,24 @@ attn_decode_split_kernel(const f16* __restrict__ qg, DecSeqs seqs, float* __rest
     };
 
     if (uhi > ulo) {
+        // NBUF register tile buffers: the loads of tile j + NBUF - 1 are issued
+        // before the math of tile j
         const int j0 = ulo / DEC_TILE;
         const int j1 = (uhi + DEC_TILE - 1) / DEC_TILE;
-        DecTileRegs ra, rb;
-        dec_load_tile(ra, kbase, vbase, row_stride, j0, uhi, lane, w);
-        for (int j = j0; j < j1; j += 2) {
-            if (j + 1 < j1) dec_load_tile(rb, kbase, vbase, row_stride, j + 1, uhi, lane, w);
-            body(ra, j);
-            if (j + 1 >= j1) break;
-            if (j + 2 < j1) dec_load_tile(ra, kbase, vbase, row_stride, j + 2, uhi, lane, w);
-            body(rb, j + 1);
+        DecTileRegs rbuf[NBUF];
+#pragma unroll
+        for (int p = 0; p < NBUF - 1; ++p)
+            if (j0 + p < j1) dec_load_tile<NT_V>(rbuf[p], kbase, vbase, row_stride, j0 + p, uhi, lane, w);
+        for (int j = j0; j < j1; j += NBUF) {
+#pragma unroll
+            for (int u = 0; u < NBUF; ++u) {
+                const int jj = j + u;
+                if (jj >= j1) break;
+                if (jj + NBUF - 1 < j1)
+                    dec_load_tile<NT_V>(rbuf[(u + NBUF - 1) % NBUF], kbase, vbase, row_stride,
+                                        jj + NBUF - 1, uhi, lane, w);
+                body(rbuf[u], jj);
+            }
         }
     }
 
@@ -312,7 +328,8 @@ int launch_split(const f16* qg, const DecSeqs& seqs, float* pacc, float* pm, flo
                  int T, int n_q_heads, int n_kv, int q_pitch, int split, int split_rows,
                  float scale, hipStream_t stream) {
     dim3 grid(split, n_kv, B);
-    hipLaunchKernelGGL(attn_decode_split_kernel, grid, dim3(DEC_THREADS), 0, stream, qg, seqs, pacc,
+    hipLaunchKernelGGL((attn_decode_split_kernel<DEC_NBUF, DEC_NT_V>), grid, dim3(DEC_THREADS), 0,
+                       stream, qg, seqs, pacc,
                        pm, pd, n_q_heads, n_kv, q_pitch, T, split, split_rows, scale * FL_LOG2E);
     return fl::check_launch("attn_decode_split");
 }

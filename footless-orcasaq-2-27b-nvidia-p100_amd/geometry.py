@@ -25,8 +25,10 @@ L2_EPS = 1e-6           #                                 runtime.py:116
 # kernels.cu:535-544, with its ATT_SPLIT = 32 / ATT_GQA_ROWS = 32 of
 # runtime.py:213-219 re-chosen): at 4 sequences x 4 kv heads, 64 splits a
 # long sequence give 1024 workgroups for 256 CUs, while a split keeps at least
-# 512 rows (16 tiles) so the partials stay a few percent of the KV bytes.
-SPLIT_ROWS = 512
+# 256 rows (8 tiles) so the partials stay a small fraction of the KV bytes
+# (measured on MI355X: 256 beats 512 and 1024 at 4k / 8k / 32k contexts and
+# ties at 100k).
+SPLIT_ROWS = 256
 SPLIT_MAX = 64
 # The largest T the decode attention takes (MTP verify rows; runtime.py:299).
 SPLIT_T_MAX = 4
