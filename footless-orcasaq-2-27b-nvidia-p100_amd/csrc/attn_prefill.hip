@@ -9,14 +9,20 @@
 // tiles launch first (kernels.cu:2522).
 //
 // Kernel design: a workgroup owns 128 rows (4 wavefronts x 32) of one kv
-// head and walks the causal KV range in 64-row tiles staged in LDS (K as
-// rows, V transposed to [d][kv]). Per wave and tile:
+// head and walks the causal KV range in 64-row tiles. Per wave and tile:
 //   S^T (64 kv x 32 rows) = K Q^T      32 MFMA 32x32x16 f16 (Q in registers)
 //   online softmax per query column     one lane pair holds a column
 //   O^T (256 d x 32 rows) += V^T P^T    32 MFMA, P straight from the S^T
 //                                       accumulators (KV order permuted to
 //                                       match, V^T read with it)
 // fp32 accumulation throughout; O^T lives in 128 accumulator registers.
+// K and V tiles stay in their cache layout ([kv][256] rows) and are copied
+// HBM -> LDS by global_load_lds (no registers), two stages deep: the copy of
+// tile j+1 runs while tile j is computed. Rows are XOR-swizzled in 16-byte
+// chunks (chunk c of row r at c ^ (r % 8)) to spread LDS banks. The V^T
+// operand is read with ds_read_b64_tr_b16: in each 16-lane group, lane j
+// points at row kb + j/4, columns n0 + 4 (j%4)..+3 of the tile, and lane i
+// receives V[kb..kb+3][n0 + i] -- four kv rows of one output dim.
 #include "fl_common.hpp"
 
 namespace {
@@ -26,15 +32,52 @@ constexpr int PF_THREADS = 64 * PF_WAVES;
 constexpr int PF_BQ = 32 * PF_WAVES;   // rows a workgroup
 constexpr int PF_BK = 64;              // kv rows a tile
 constexpr int PF_HD = 256;
-constexpr int PK_PITCH = PF_HD + 8;    // halves per staged K row (528 B)
-constexpr int PV_PITCH = PF_BK + 8;    // halves per staged V^T row (144 B)
+constexpr int ROW_B = PF_HD * 2;       // bytes a K / V row
+constexpr int TILE_B = PF_BK * ROW_B;  // 32 KiB
+constexpr int STAGE_B = 2 * TILE_B;    // K then V
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+// byte offset of 16-byte chunk c (0..31) of tile row r
+__device__ __forceinline__ int swz(int r, int c) { return r * ROW_B + ((c ^ (r & 7)) << 4); }
+
+// s_waitcnt vmcnt(n) (n < 64), every other counter left alone
+#define WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt((((n) & 15) | (((n) >> 4) << 14)) | 0x0F70)
+
+// A workgroup barrier that is also a compiler memory barrier but adds no
+// s_waitcnt: __syncthreads() would drain vmcnt, i.e. wait for the next tile's
+// copies too. The copies a barrier must cover are waited for explicitly
+// (WAIT_VMCNT), and every LDS read of a tile has been consumed by an MFMA
+// before the barrier that lets the tile be overwritten.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_barrier" ::: "memory"); }
+
+// Issue the copy of one 64-row K tile and V tile into an LDS stage: 64 KiB as
+// 64 wave instructions of 1 KiB (two rows each), 16 a wave. Rows past kv_end
+// read row kv_end - 1 (in bounds; masked by the causal mask, p = 0).
+__device__ __forceinline__ void issue_tile(char* stage, const f16* __restrict__ kb,
+                                           const f16* __restrict__ vb, size_t rs, int kv0,
+                                           int kv_end, int w, int lane) {
+#pragma unroll
+    for (int n = 0; n < 8; ++n) {
+        const int r = 16 * w + 2 * n + (lane >> 5);
+        const int c = (lane & 31) ^ (r & 7);
+        const int kv = min(kv0 + r, kv_end - 1);
+        const size_t off = (size_t)kv * rs + 8 * c;
+        __builtin_amdgcn_global_load_lds((const void*)(kb + off),
+                                         (lds_void*)(stage + (16 * w + 2 * n) * ROW_B), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds((const void*)(vb + off),
+                                         (lds_void*)(stage + TILE_B + (16 * w + 2 * n) * ROW_B), 16,
+                                         0, 0);
+    }
+}
 
 __global__ void __launch_bounds__(PF_THREADS)
 attn_prefill_kernel(const f16* __restrict__ q, int q_pitch, const f16* __restrict__ kc,
                     const f16* __restrict__ vc, f16* __restrict__ z, int z_pitch, int n_q_heads,
                     int n_kv, int pos0, int T, float sl2, int n_row_tiles) {
-    __shared__ __attribute__((aligned(16))) f16 sK[PF_BK][PK_PITCH];
-    __shared__ __attribute__((aligned(16))) f16 sVt[PF_HD][PV_PITCH];
+    extern __shared__ __attribute__((aligned(16))) char smem[];
 
     const int tile = n_row_tiles - 1 - (int)blockIdx.x;   // heaviest first
     const int h = blockIdx.y;
@@ -52,6 +95,13 @@ attn_prefill_kernel(const f16* __restrict__ q, int q_pitch, const f16* __restric
     const int wqmax = wlast >= R0 + 32 * w ? pos0 + wlast / G : -1;   // the wave's last query position
     const int blast = min(R0 + PF_BQ - 1, RT - 1);
     const int kv_end = pos0 + blast / G + 1;                          // rows any query here sees
+    const int n_tiles = (kv_end + PF_BK - 1) / PF_BK;
+
+    const size_t rs = (size_t)n_kv * PF_HD;
+    const f16* kb = kc + (size_t)h * PF_HD;
+    const f16* vb = vc + (size_t)h * PF_HD;
+
+    issue_tile(smem, kb, vb, rs, 0, kv_end, w, lane);
 
     f16x8 qreg[16];   // Q[row][128 hh + 8 ks + 0..7]
     {
@@ -64,42 +114,29 @@ attn_prefill_kernel(const f16* __restrict__ q, int q_pitch, const f16* __restric
     for (int mb = 0; mb < 8; ++mb) o[mb] = (f32x16)(0.f);
     float m_run = -1e30f, l_run = 0.f;
 
-    const size_t rs = (size_t)n_kv * PF_HD;
-    const f16* kb = kc + (size_t)h * PF_HD;
-    const f16* vb = vc + (size_t)h * PF_HD;
+    // the ds_read_b64_tr_b16 source coordinates of this lane for V^T block mb:
+    // row kb0 + (lane%16)/4, columns 32 mb + 16 ((lane%32)/16) + 4 (lane%4)
+    const int tr_r = (lane & 15) >> 2;
+    const int tr_d = 16 * ((lane & 31) >> 4) + 4 * (lane & 3);
 
-    for (int kv0 = 0; kv0 < kv_end; kv0 += PF_BK) {
-        // ---- stage K (rows) and V (transposed) ----
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int idx = tid + PF_THREADS * i;
-            const int r = idx >> 5, c = idx & 31;
-            const int kv = kv0 + r;
-            const f16x8 val = kv < kv_end ? *(const f16x8*)(kb + (size_t)kv * rs + 8 * c) : (f16x8)(0);
-            *(f16x8*)&sK[r][8 * c] = val;
+    for (int j = 0; j < n_tiles; ++j) {
+        char* cur = smem + (j & 1) * STAGE_B;
+        if (j + 1 < n_tiles) {
+            issue_tile(smem + ((j + 1) & 1) * STAGE_B, kb, vb, rs, (j + 1) * PF_BK, kv_end, w, lane);
+            WAIT_VMCNT(16);   // this tile's 16 copies done, the next tile's in flight
+        } else {
+            WAIT_VMCNT(0);
         }
-#pragma unroll
-        for (int pass = 0; pass < 2; ++pass) {
-            const int rbase = 4 * (tid & 15);
-            const int dblk = 8 * (tid >> 4) + 128 * pass;
-            f16x8 vv[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int kv = kv0 + rbase + i;
-                vv[i] = kv < kv_end ? *(const f16x8*)(vb + (size_t)kv * rs + dblk) : (f16x8)(0);
-            }
-#pragma unroll
-            for (int e = 0; e < 8; ++e)
-                *(f16x4*)&sVt[dblk + e][rbase] = (f16x4){vv[0][e], vv[1][e], vv[2][e], vv[3][e]};
-        }
-        __syncthreads();
-
+        lds_barrier();
+        const int kv0 = j * PF_BK;
         if (kv0 <= wqmax) {
+            const char* K = cur;
+            const char* Vt = cur + TILE_B;
             f32x16 s0 = (f32x16)(0.f), s1 = (f32x16)(0.f);
 #pragma unroll
             for (int ks = 0; ks < 16; ++ks) {
-                const f16x8 a0 = *(const f16x8*)&sK[ql][128 * hh + 8 * ks];
-                const f16x8 a1 = *(const f16x8*)&sK[32 + ql][128 * hh + 8 * ks];
+                const f16x8 a0 = *(const f16x8*)(K + swz(ql, 16 * hh + ks));
+                const f16x8 a1 = *(const f16x8*)(K + swz(32 + ql, 16 * hh + ks));
                 s0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, qreg[ks], s0, 0, 0, 0);
                 s1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, qreg[ks], s1, 0, 0, 0);
             }
@@ -130,17 +167,23 @@ attn_prefill_kernel(const f16* __restrict__ q, int q_pitch, const f16* __restric
             for (int mb = 0; mb < 8; ++mb) o[mb] *= corr;
 #pragma unroll
             for (int kq = 0; kq < 4; ++kq) {
-                const int kb0 = 32 * (kq >> 1) + 16 * (kq & 1) + 4 * hh;
+                const int r0 = 16 * kq + 4 * hh + tr_r;
 #pragma unroll
                 for (int mb = 0; mb < 8; ++mb) {
-                    const f16x4 lo4 = *(const f16x4*)&sVt[32 * mb + ql][kb0];
-                    const f16x4 hi4 = *(const f16x4*)&sVt[32 * mb + ql][kb0 + 8];
-                    const f16x8 a = {lo4[0], lo4[1], lo4[2], lo4[3], hi4[0], hi4[1], hi4[2], hi4[3]};
+                    const int d = 32 * mb + tr_d;
+                    const int off = ((d & 7) << 1);
+                    const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                        (lds_s16x4*)(Vt + swz(r0, d >> 3) + off));
+                    const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                        (lds_s16x4*)(Vt + swz(r0 + 8, d >> 3) + off));
+                    const f16x4 lf = __builtin_bit_cast(f16x4, lo);
+                    const f16x4 hf = __builtin_bit_cast(f16x4, hi);
+                    const f16x8 a = {lf[0], lf[1], lf[2], lf[3], hf[0], hf[1], hf[2], hf[3]};
                     o[mb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pk[kq], o[mb], 0, 0, 0);
                 }
             }
         }
-        __syncthreads();
+        lds_barrier();   // this stage is refilled two tiles on
     }
 
     if (rvalid) {
@@ -180,10 +223,22 @@ extern "C" int fl_attention_prefill(const void* q, int q_pitch, const void* k_ne
                                    head_dim, max_pos, stream);
         if (rc) return rc;
     }
+    static bool lds_attr_set = false;   // 128 KiB of dynamic LDS is above the default limit
+    if (!lds_attr_set) {
+        if (hipFuncSetAttribute((const void*)attn_prefill_kernel,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, 2 * STAGE_B) !=
+            hipSuccess) {
+            fl::set_error("attn_prefill: cannot raise the dynamic LDS limit to %d bytes",
+                          2 * STAGE_B);
+            return FL_ELAUNCH;
+        }
+        lds_attr_set = true;
+    }
     const size_t off = (size_t)layer * max_pos * n_kv_heads * head_dim;
     const int rows = T * (n_q_heads / n_kv_heads);
     const int n_row_tiles = (rows + PF_BQ - 1) / PF_BQ;
-    hipLaunchKernelGGL(attn_prefill_kernel, dim3(n_row_tiles, n_kv_heads), dim3(PF_THREADS), 0,
+    hipLaunchKernelGGL(attn_prefill_kernel, dim3(n_row_tiles, n_kv_heads), dim3(PF_THREADS),
+                       2 * STAGE_B,
                        (hipStream_t)stream, (const f16*)q, q_pitch, (const f16*)kcache + off,
                        (const f16*)vcache + off, (f16*)z, z_pitch, n_q_heads, n_kv_heads, pos0, T,
                        scale * FL_LOG2E, n_row_tiles);
