@@ -33,6 +33,14 @@ HIPCC_FLAGS = [
     f"-I{CSRC}",
 ]
 
+# Per-source extras. attn_prefill: MFMA accumulators in VGPRs, so the rare
+# online-softmax rescale of O is a plain multiply instead of making the
+# register allocator keep a VGPR copy of all 128 AGPR accumulators live
+# across the tile loop.
+FILE_FLAGS = {
+    "attn_prefill": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
+
 
 def hipcc() -> str:
     path = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
@@ -43,7 +51,7 @@ def hipcc() -> str:
 
 def _compile(src: Path) -> Path:
     obj = BUILD_DIR / (src.stem + ".o")
-    cmd = [hipcc(), *HIPCC_FLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [hipcc(), *HIPCC_FLAGS, *FILE_FLAGS.get(src.stem, []), "-c", str(src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed on {src.name}:\n{res.stderr}")

@@ -34,7 +34,12 @@ constexpr int PF_BK = 64;              // kv rows a tile
 constexpr int PF_HD = 256;
 constexpr int ROW_B = PF_HD * 2;       // bytes a K / V row
 constexpr int TILE_B = PF_BK * ROW_B;  // 32 KiB
-constexpr int STAGE_B = 2 * TILE_B;    // K then V
+constexpr int LDS_B = 4 * TILE_B;      // K stage 0 | K stage 1 | V stage 0 | V stage 1
+constexpr int V_OFF = 2 * TILE_B;
+// A column's running max only moves when a tile's max exceeds it by more
+// than this (log2 units): P = 2^(s - m) stays <= 256, exact in fp16 range,
+// and the O / l rescale is skipped on almost every tile.
+constexpr float RESCALE_LOG2 = 8.f;
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) void lds_void;
@@ -53,23 +58,79 @@ __device__ __forceinline__ int swz(int r, int c) { return r * ROW_B + ((c ^ (r &
 // before the barrier that lets the tile be overwritten.
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_barrier" ::: "memory"); }
 
-// Issue the copy of one 64-row K tile and V tile into an LDS stage: 64 KiB as
-// 64 wave instructions of 1 KiB (two rows each), 16 a wave. Rows past kv_end
-// read row kv_end - 1 (in bounds; masked by the causal mask, p = 0).
-__device__ __forceinline__ void issue_tile(char* stage, const f16* __restrict__ kb,
-                                           const f16* __restrict__ vb, size_t rs, int kv0,
-                                           int kv_end, int w, int lane) {
+// The eight ds_read_b64_tr_b16 of one (kq, half) step of P V, then a wait
+// for them. be / bo are this lane's base addresses for even / odd output
+// blocks mb (the row swizzle flips bit 0 of mb with the lane's row bit 2),
+// everything else is an immediate: +128 per pair of blocks, +8 KiB per 16
+// kv rows, +4 KiB for the second row of a pair. One asm block, because the
+// compiler cannot tell these reads from the in-flight global_load_lds copies
+// of the next tile and would drain vmcnt (wait for that copy) before them.
+template <int KQ, int HALF>
+__device__ __forceinline__ void tr_read8(s16x4 (&r)[8], uint32_t be, uint32_t bo) {
+    constexpr int M0 = 16 * ROW_B * KQ + 128 * (2 * HALF);
+    constexpr int M1 = M0 + 128;
+    asm volatile(
+        "ds_read_b64_tr_b16 %0, %8 offset:%10\n\t"
+        "ds_read_b64_tr_b16 %1, %8 offset:%11\n\t"
+        "ds_read_b64_tr_b16 %2, %9 offset:%10\n\t"
+        "ds_read_b64_tr_b16 %3, %9 offset:%11\n\t"
+        "ds_read_b64_tr_b16 %4, %8 offset:%12\n\t"
+        "ds_read_b64_tr_b16 %5, %8 offset:%13\n\t"
+        "ds_read_b64_tr_b16 %6, %9 offset:%12\n\t"
+        "ds_read_b64_tr_b16 %7, %9 offset:%13\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3]), "=&v"(r[4]), "=&v"(r[5]),
+          "=&v"(r[6]), "=&v"(r[7])
+        : "v"(be), "v"(bo), "i"(M0), "i"(M0 + 8 * ROW_B), "i"(M1), "i"(M1 + 8 * ROW_B));
+}
+
+// O^T[mb] += V^T P^T for the 16 kv rows of step KQ, output blocks 4 HALF..+3
+template <int KQ, int HALF>
+__device__ __forceinline__ void pv_step(f32x16 (&o)[8], const f16x8& pk, uint32_t be,
+                                        uint32_t bo) {
+    s16x4 rd[8];
+    tr_read8<KQ, HALF>(rd, be, bo);
 #pragma unroll
-    for (int n = 0; n < 8; ++n) {
-        const int r = 16 * w + 2 * n + (lane >> 5);
-        const int c = (lane & 31) ^ (r & 7);
-        const int kv = min(kv0 + r, kv_end - 1);
-        const size_t off = (size_t)kv * rs + 8 * c;
-        __builtin_amdgcn_global_load_lds((const void*)(kb + off),
-                                         (lds_void*)(stage + (16 * w + 2 * n) * ROW_B), 16, 0, 0);
-        __builtin_amdgcn_global_load_lds((const void*)(vb + off),
-                                         (lds_void*)(stage + TILE_B + (16 * w + 2 * n) * ROW_B), 16,
-                                         0, 0);
+    for (int u = 0; u < 4; ++u) {
+        const f16x4 lf = __builtin_bit_cast(f16x4, rd[2 * u]);
+        const f16x4 hf = __builtin_bit_cast(f16x4, rd[2 * u + 1]);
+        const f16x8 av = {lf[0], lf[1], lf[2], lf[3], hf[0], hf[1], hf[2], hf[3]};
+        o[4 * HALF + u] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, pk, o[4 * HALF + u], 0, 0, 0);
+    }
+}
+
+// Issue the copy of one 64-row K tile and V tile into LDS stage st: 64 KiB as
+// 64 wave instructions of 1 KiB (two rows each), 16 a wave. Wave w copies
+// rows 16 w .. 16 w + 15; lane l of the n-th instruction row 16 w + 2 n +
+// l / 32, source chunk (l % 32) ^ (row % 8), so the tile lands swizzled. The
+// row base is wave-uniform (a scalar address), the lane part one of four
+// per-lane offsets loff[n % 4]. On the last tile rows past kv_end read row
+// kv_end - 1 instead (in bounds; masked by the causal mask, p = 0).
+__device__ __forceinline__ void issue_tile(char* smem, int st, const char* kb, const char* vb,
+                                           uint32_t rsb, int kv0, int kv_end, int w, int lane,
+                                           const uint32_t (&loff)[4]) {
+    if (kv0 + PF_BK <= kv_end) {
+#pragma unroll
+        for (int n = 0; n < 8; ++n) {
+            const size_t rb = (size_t)(kv0 + 16 * w + 2 * n) * rsb;
+            char* dst = smem + st * TILE_B + (16 * w + 2 * n) * ROW_B;
+            __builtin_amdgcn_global_load_lds((const void*)(kb + rb + loff[n & 3]), (lds_void*)dst,
+                                             16, 0, 0);
+            __builtin_amdgcn_global_load_lds((const void*)(vb + rb + loff[n & 3]),
+                                             (lds_void*)(dst + V_OFF), 16, 0, 0);
+        }
+    } else {
+#pragma unroll
+        for (int n = 0; n < 8; ++n) {
+            const int r = 16 * w + 2 * n + (lane >> 5);
+            const int c = (lane & 31) ^ (r & 7);
+            const int kv = min(kv0 + r, kv_end - 1);
+            const size_t off = (size_t)kv * rsb + 16 * c;
+            char* dst = smem + st * TILE_B + (16 * w + 2 * n) * ROW_B;
+            __builtin_amdgcn_global_load_lds((const void*)(kb + off), (lds_void*)dst, 16, 0, 0);
+            __builtin_amdgcn_global_load_lds((const void*)(vb + off), (lds_void*)(dst + V_OFF),
+                                             16, 0, 0);
+        }
     }
 }
 
@@ -81,7 +142,8 @@ attn_prefill_kernel(const f16* __restrict__ q, int q_pitch, const f16* __restric
 
     const int tile = n_row_tiles - 1 - (int)blockIdx.x;   // heaviest first
     const int h = blockIdx.y;
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int ql = lane & 31, hh = lane >> 5;
     const int G = n_q_heads / n_kv;
     const int RT = T * G;
@@ -91,17 +153,24 @@ attn_prefill_kernel(const f16* __restrict__ q, int q_pitch, const f16* __restric
     const int t = rvalid ? row / G : 0;
     const int g = rvalid ? row - t * G : 0;
     const int qpos = rvalid ? pos0 + t : -1;
-    const int wlast = min(R0 + 32 * w + 31, RT - 1);
-    const int wqmax = wlast >= R0 + 32 * w ? pos0 + wlast / G : -1;   // the wave's last query position
+    const int wfirst = R0 + 32 * w;
+    const int wlast = min(wfirst + 31, RT - 1);
+    const int wqmax = wlast >= wfirst ? pos0 + wlast / G : -1;   // the wave's last query position
+    const int wqmin = pos0 + wfirst / G;                          // and its first
     const int blast = min(R0 + PF_BQ - 1, RT - 1);
-    const int kv_end = pos0 + blast / G + 1;                          // rows any query here sees
+    const int kv_end = pos0 + blast / G + 1;                      // rows any query here sees
     const int n_tiles = (kv_end + PF_BK - 1) / PF_BK;
 
-    const size_t rs = (size_t)n_kv * PF_HD;
-    const f16* kb = kc + (size_t)h * PF_HD;
-    const f16* vb = vc + (size_t)h * PF_HD;
+    const uint32_t rsb = (uint32_t)n_kv * ROW_B;   // bytes between cache rows
+    const char* kb = (const char*)(kc + (size_t)h * PF_HD);
+    const char* vb = (const char*)(vc + (size_t)h * PF_HD);
+    uint32_t loff[4];
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+        loff[m] = (lane >> 5) * rsb + 16 * ((lane & 31) ^ ((2 * m + (lane >> 5)) & 7));
+    const uint32_t lds_base = (uint32_t)(uintptr_t)((__attribute__((address_space(3))) char*)smem);
 
-    issue_tile(smem, kb, vb, rs, 0, kv_end, w, lane);
+    issue_tile(smem, 0, kb, vb, rsb, 0, kv_end, w, lane, loff);
 
     f16x8 qreg[16];   // Q[row][128 hh + 8 ks + 0..7]
     {
@@ -114,15 +183,26 @@ attn_prefill_kernel(const f16* __restrict__ q, int q_pitch, const f16* __restric
     for (int mb = 0; mb < 8; ++mb) o[mb] = (f32x16)(0.f);
     float m_run = -1e30f, l_run = 0.f;
 
-    // the ds_read_b64_tr_b16 source coordinates of this lane for V^T block mb:
-    // row kb0 + (lane%16)/4, columns 32 mb + 16 ((lane%32)/16) + 4 (lane%4)
+    // K operand, k-step ks = 8 a + b: row ql (and 32 + ql) chunk 16 hh + ks,
+    // stored at chunk 16 hh + 8 a + (b ^ ql % 8): a per-lane base for each b,
+    // 128 a and 16 KiB (rows 32..63) as immediates.
+    uint32_t kofs[8];
+#pragma unroll
+    for (int b = 0; b < 8; ++b) kofs[b] = ql * ROW_B + 256 * hh + 16 * (b ^ (ql & 7));
+    // V^T operand (ds_read_b64_tr_b16): this lane points at tile row
+    // 16 kq + 4 hh + tr_r (and + 8), output dims 32 mb + tr_d .. + 3; with the
+    // swizzle that is chunk 4 (mb ^ hh) + (tr_d / 8 ^ tr_r) of the row.
     const int tr_r = (lane & 15) >> 2;
     const int tr_d = 16 * ((lane & 31) >> 4) + 4 * (lane & 3);
+    const uint32_t tr_lane = (4 * hh + tr_r) * ROW_B + 16 * ((tr_d >> 3) ^ tr_r) + 2 * (tr_d & 7);
+    const uint32_t tr_even = tr_lane + 64 * hh, tr_odd = tr_lane + 64 * (1 - hh);
 
+    typedef __attribute__((address_space(3))) const f16x8 lds_f16x8;
+    typedef __attribute__((address_space(3))) const char lds_char;
     for (int j = 0; j < n_tiles; ++j) {
-        char* cur = smem + (j & 1) * STAGE_B;
+        const int st = j & 1;
         if (j + 1 < n_tiles) {
-            issue_tile(smem + ((j + 1) & 1) * STAGE_B, kb, vb, rs, (j + 1) * PF_BK, kv_end, w, lane);
+            issue_tile(smem, st ^ 1, kb, vb, rsb, (j + 1) * PF_BK, kv_end, w, lane, loff);
             WAIT_VMCNT(16);   // this tile's 16 copies done, the next tile's in flight
         } else {
             WAIT_VMCNT(0);
@@ -130,58 +210,63 @@ attn_prefill_kernel(const f16* __restrict__ q, int q_pitch, const f16* __restric
         lds_barrier();
         const int kv0 = j * PF_BK;
         if (kv0 <= wqmax) {
-            const char* K = cur;
-            const char* Vt = cur + TILE_B;
+            lds_char* K = (lds_char*)smem + st * TILE_B;
             f32x16 s0 = (f32x16)(0.f), s1 = (f32x16)(0.f);
 #pragma unroll
             for (int ks = 0; ks < 16; ++ks) {
-                const f16x8 a0 = *(const f16x8*)(K + swz(ql, 16 * hh + ks));
-                const f16x8 a1 = *(const f16x8*)(K + swz(32 + ql, 16 * hh + ks));
+                lds_char* ka = K + kofs[ks & 7] + 128 * (ks >> 3);
+                const f16x8 a0 = *(lds_f16x8*)ka;
+                const f16x8 a1 = *(lds_f16x8*)(ka + 32 * ROW_B);
                 s0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, qreg[ks], s0, 0, 0, 0);
                 s1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, qreg[ks], s1, 0, 0, 0);
             }
+            // raw scores; the causal mask only on tiles that cross the diagonal
             float sc[32];
-            float mt = -INFINITY;
+            if (kv0 + PF_BK - 1 <= wqmin) {
 #pragma unroll
-            for (int rr = 0; rr < 16; ++rr) {
-                const int kvr = kv0 + 8 * (rr >> 2) + 4 * hh + (rr & 3);
-                sc[rr] = kvr <= qpos ? s0[rr] * sl2 : -INFINITY;
-                sc[16 + rr] = kvr + 32 <= qpos ? s1[rr] * sl2 : -INFINITY;
-                mt = fmaxf(mt, fmaxf(sc[rr], sc[16 + rr]));
+                for (int rr = 0; rr < 16; ++rr) {
+                    sc[rr] = s0[rr];
+                    sc[16 + rr] = s1[rr];
+                }
+            } else {
+#pragma unroll
+                for (int rr = 0; rr < 16; ++rr) {
+                    const int kvr = kv0 + 8 * (rr >> 2) + 4 * hh + (rr & 3);
+                    sc[rr] = kvr <= qpos ? s0[rr] : -INFINITY;
+                    sc[16 + rr] = kvr + 32 <= qpos ? s1[rr] : -INFINITY;
+                }
             }
-            mt = fmaxf(mt, lane_xor(mt, 32));
-            const float m_new = fmaxf(m_run, mt);
-            const float corr = fast_exp2(m_run - m_new);
+            float mt = sc[0];
+#pragma unroll
+            for (int rr = 1; rr < 32; ++rr) mt = fmaxf(mt, sc[rr]);
+            mt = fmaxf(mt, lane_xor(mt, 32)) * sl2;
+            if (__any(mt > m_run + RESCALE_LOG2)) {   // always on a wave's first tile, rarely after
+                const float m_new = fmaxf(m_run, mt);
+                const float corr = fast_exp2(m_run - m_new);
+                m_run = m_new;
+                l_run *= corr;
+#pragma unroll
+                for (int mb = 0; mb < 8; ++mb) o[mb] *= corr;
+            }
             float psum = 0.f;
             f16x8 pk[4];
 #pragma unroll
             for (int rr = 0; rr < 32; ++rr) {
-                const float p = fast_exp2(sc[rr] - m_new);
+                const float p = fast_exp2(fmaf(sc[rr], sl2, -m_run));
                 psum += p;
                 pk[rr >> 3][rr & 7] = (f16)p;
             }
-            psum += lane_xor(psum, 32);
-            l_run = l_run * corr + psum;
-            m_run = m_new;
-#pragma unroll
-            for (int mb = 0; mb < 8; ++mb) o[mb] *= corr;
-#pragma unroll
-            for (int kq = 0; kq < 4; ++kq) {
-                const int r0 = 16 * kq + 4 * hh + tr_r;
-#pragma unroll
-                for (int mb = 0; mb < 8; ++mb) {
-                    const int d = 32 * mb + tr_d;
-                    const int off = ((d & 7) << 1);
-                    const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                        (lds_s16x4*)(Vt + swz(r0, d >> 3) + off));
-                    const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                        (lds_s16x4*)(Vt + swz(r0 + 8, d >> 3) + off));
-                    const f16x4 lf = __builtin_bit_cast(f16x4, lo);
-                    const f16x4 hf = __builtin_bit_cast(f16x4, hi);
-                    const f16x8 a = {lf[0], lf[1], lf[2], lf[3], hf[0], hf[1], hf[2], hf[3]};
-                    o[mb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pk[kq], o[mb], 0, 0, 0);
-                }
-            }
+            l_run += psum + lane_xor(psum, 32);
+            const uint32_t vt = lds_base + (uint32_t)(V_OFF + st * TILE_B);
+            const uint32_t be = vt + tr_even, bo = vt + tr_odd;
+            pv_step<0, 0>(o, pk[0], be, bo);
+            pv_step<0, 1>(o, pk[0], be, bo);
+            pv_step<1, 0>(o, pk[1], be, bo);
+            pv_step<1, 1>(o, pk[1], be, bo);
+            pv_step<2, 0>(o, pk[2], be, bo);
+            pv_step<2, 1>(o, pk[2], be, bo);
+            pv_step<3, 0>(o, pk[3], be, bo);
+            pv_step<3, 1>(o, pk[3], be, bo);
         }
         lds_barrier();   // this stage is refilled two tiles on
     }
@@ -226,10 +311,10 @@ extern "C" int fl_attention_prefill(const void* q, int q_pitch, const void* k_ne
     static bool lds_attr_set = false;   // 128 KiB of dynamic LDS is above the default limit
     if (!lds_attr_set) {
         if (hipFuncSetAttribute((const void*)attn_prefill_kernel,
-                                hipFuncAttributeMaxDynamicSharedMemorySize, 2 * STAGE_B) !=
+                                hipFuncAttributeMaxDynamicSharedMemorySize, LDS_B) !=
             hipSuccess) {
             fl::set_error("attn_prefill: cannot raise the dynamic LDS limit to %d bytes",
-                          2 * STAGE_B);
+                          LDS_B);
             return FL_ELAUNCH;
         }
         lds_attr_set = true;
@@ -238,7 +323,7 @@ extern "C" int fl_attention_prefill(const void* q, int q_pitch, const void* k_ne
     const int rows = T * (n_q_heads / n_kv_heads);
     const int n_row_tiles = (rows + PF_BQ - 1) / PF_BQ;
     hipLaunchKernelGGL(attn_prefill_kernel, dim3(n_row_tiles, n_kv_heads), dim3(PF_THREADS),
-                       2 * STAGE_B,
+                       LDS_B,
                        (hipStream_t)stream, (const f16*)q, q_pitch, (const f16*)kcache + off,
                        (const f16*)vcache + off, (f16*)z, z_pitch, n_q_heads, n_kv_heads, pos0, T,
                        scale * FL_LOG2E, n_row_tiles);

@@ -160,6 +160,27 @@ def test_prefill_vs_oracle(fl, dev, orc, rng, T, pos0):
     assert ok, f"T={T} pos0={pos0}: max|err| {err}"
 
 
+@pytest.mark.parametrize("T,pos0", [(512, 0), (300, 200)])
+def test_prefill_growing_scores(fl, dev, orc, rng, T, pos0):
+    """Scores that climb along the sequence (a sawtooth of up to ~11 log2 units a
+    64-row tile), so a column's running max keeps moving after its first tile and
+    the O / l rescale path runs, against the oracle's running-max restatement."""
+    L = pos0 + T
+    kc, vc = rand_cache(rng, L)
+    pos = np.arange(L)
+    ramp = (0.12 * (pos % 384)).astype(np.float32)            # q.k * scale ~ ramp (natural units)
+    kc = (kc.astype(np.float32) * 0.25 + ramp[:, None, None]).astype(np.float16)
+    qg = rand_qg(rng, T)
+    qg[..., :256] = (1 / 16 + 0.01 * rng.standard_normal((T, 24, 256))).astype(np.float16)
+    kd = torch.from_numpy(kc).to(dev)
+    vd = torch.from_numpy(vc).to(dev)
+    z = fl.ops.attention_prefill(to_dev(qg, dev), kd, vd, pos0=pos0)
+    torch.cuda.synchronize()
+    want = orc.attention_prefill(qg, kc, vc, q_pitch=512, pos0=pos0, max_pos=L, scale=SCALE, T=T)
+    err, ok = close(z.cpu().numpy(), want, ATOL, RTOL)
+    assert ok, f"T={T} pos0={pos0}: max|err| {err}"
+
+
 @pytest.mark.parametrize("L", [8192, 32768])
 def test_prefill_config3_sampled_rows(fl, dev, orc, L):
     """Config 3 at full size: q pre-scaled by 1/16 (scale 1 in the kernel); sampled
