@@ -55,50 +55,107 @@ __device__ __forceinline__ int sw(int r) { return ((r & 3) << 2) | ((r >> 2) & 3
 // s_waitcnt vmcnt(n) (n < 64), every other counter left alone
 #define WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt((((n) & 15) | (((n) >> 4) << 14)) | 0x0F70)
 
-// A workgroup barrier that is also a compiler memory barrier but adds no
-// s_waitcnt: __syncthreads() would drain vmcnt, i.e. wait for the next tile's
-// copies too. The copies a barrier must cover are waited for explicitly
-// (WAIT_VMCNT), and every LDS read of a tile has been consumed by an MFMA
-// before the barrier that lets the tile be overwritten.
-__device__ __forceinline__ void lds_barrier() { asm volatile("s_barrier" ::: "memory"); }
-
-// The eight ds_read_b64_tr_b16 of one (kq, half) step of P V, then a wait
-// for them. b[2 u + s] is this lane's address for output block 4 HALF + u,
-// row pair member s (the swizzle makes it depend on u and s); the rest is
-// one immediate, +8 KiB per 16 kv rows and +256 B for the upper four output
-// blocks. One asm block, because the compiler cannot tell these reads from
-// the in-flight global_load_lds copies of the next tile and would drain
-// vmcnt (wait for that copy) before them.
-template <int KQ, int HALF>
-__device__ __forceinline__ void tr_read8(s16x4 (&r)[8], const uint32_t (&b)[8]) {
-    constexpr int IMM = 16 * ROW_B * KQ + 256 * HALF;
-    asm volatile(
-        "ds_read_b64_tr_b16 %0, %8 offset:%16\n\t"
-        "ds_read_b64_tr_b16 %1, %9 offset:%16\n\t"
-        "ds_read_b64_tr_b16 %2, %10 offset:%16\n\t"
-        "ds_read_b64_tr_b16 %3, %11 offset:%16\n\t"
-        "ds_read_b64_tr_b16 %4, %12 offset:%16\n\t"
-        "ds_read_b64_tr_b16 %5, %13 offset:%16\n\t"
-        "ds_read_b64_tr_b16 %6, %14 offset:%16\n\t"
-        "ds_read_b64_tr_b16 %7, %15 offset:%16\n\t"
-        "s_waitcnt lgkmcnt(0)"
-        : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3]), "=&v"(r[4]), "=&v"(r[5]),
-          "=&v"(r[6]), "=&v"(r[7])
-        : "v"(b[0]), "v"(b[1]), "v"(b[2]), "v"(b[3]), "v"(b[4]), "v"(b[5]), "v"(b[6]), "v"(b[7]),
-          "i"(IMM));
+// Workgroup barriers that are compiler memory barriers but add no vmcnt
+// wait: __syncthreads() would drain vmcnt, i.e. wait for the next tile's
+// copies too. tile_ready follows the explicit WAIT_VMCNT for this tile's
+// copies; tile_done also waits for this wave's outstanding LDS reads, so no
+// read of a stage can still be in flight when the copy that refills it is
+// issued after the barrier.
+__device__ __forceinline__ void tile_ready() { asm volatile("s_barrier" ::: "memory"); }
+__device__ __forceinline__ void tile_done() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
-// O^T[mb] += V^T P^T for the 16 kv rows of step KQ, output blocks 4 HALF..+3
+// One 16-byte-a-lane HBM -> LDS copy (global_load_lds_dwordx4): lane l's 16
+// bytes land at LDS m0 + 16 l. Issued as asm so that the compiler does not
+// track it as an LDS write in flight: it would otherwise drain vmcnt (wait for
+// the next tile's copy) before every LDS read it cannot prove disjoint. The
+// copies are waited for explicitly (WAIT_VMCNT + tile_ready). The s_nop is the
+// wait state between the m0 write and its use by the copy.
+__device__ __forceinline__ void copy16(const char* sbase, uint32_t voff, uint32_t lds) {
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(lds));
+}
+__device__ __forceinline__ void copy16_v(const char* vptr, uint32_t lds) {
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(vptr), "{m0}"(lds));
+}
+
+// The O^T accumulators live in AGPRs and are touched only through the asm
+// below. With compiler-generated MFMAs O would be either in VGPRs (leaving no
+// registers to read LDS ahead) or, in AGPRs, given a VGPR home because of the
+// rare rescale and copied out of the accumulators on every tile. Hazards the
+// compiler cannot see inside asm are covered here: s_nop 2 before each MFMA
+// (a VALU write of an A / B operand needs two wait states before the MFMA
+// reads it; without them the MFMA reads the register's previous contents),
+// s_nop 2 between a VALU result and v_accvgpr_write of it, and acc_settle()
+// before the accumulators are read (an MFMA result must leave the pipeline
+// before v_accvgpr_read; 24 wait states cover the 8-pass MFMA). MFMAs that
+// accumulate into the same registers back to back need no wait states.
+__device__ __forceinline__ void acc_zero(f32x16& acc, const f16x8& zero) {
+    asm volatile("s_nop 2\n\tv_mfma_f32_32x32x16_f16 %0, %1, %1, 0" : "=a"(acc) : "v"(zero));
+}
+__device__ __forceinline__ void acc_mfma(f32x16& acc, const f16x8& a, const f16x8& b) {
+    asm("s_nop 2\n\tv_mfma_f32_32x32x16_f16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+}
+__device__ __forceinline__ void acc_settle(f32x16 (&o)[8]) {
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7"
+                 : "+a"(o[0]), "+a"(o[1]), "+a"(o[2]), "+a"(o[3]), "+a"(o[4]), "+a"(o[5]),
+                   "+a"(o[6]), "+a"(o[7]));
+}
+// a0..a3 *= c, on accumulator registers
+__device__ __forceinline__ void scale4_acc(float& a0, float& a1, float& a2, float& a3, float c) {
+    float t0, t1;
+    asm volatile(
+        "v_accvgpr_read_b32 %4, %0\n\t"
+        "v_accvgpr_read_b32 %5, %1\n\t"
+        "v_mul_f32 %4, %4, %6\n\t"
+        "v_mul_f32 %5, %5, %6\n\t"
+        "s_nop 2\n\t"
+        "v_accvgpr_write_b32 %0, %4\n\t"
+        "v_accvgpr_write_b32 %1, %5\n\t"
+        "v_accvgpr_read_b32 %4, %2\n\t"
+        "v_accvgpr_read_b32 %5, %3\n\t"
+        "v_mul_f32 %4, %4, %6\n\t"
+        "v_mul_f32 %5, %5, %6\n\t"
+        "s_nop 2\n\t"
+        "v_accvgpr_write_b32 %2, %4\n\t"
+        "v_accvgpr_write_b32 %3, %5"
+        : "+a"(a0), "+a"(a1), "+a"(a2), "+a"(a3), "=&v"(t0), "=&v"(t1)
+        : "v"(c));
+}
+__device__ __forceinline__ void acc_scale(f32x16 (&o)[8], float c) {
+    acc_settle(o);
+#pragma unroll
+    for (int mb = 0; mb < 8; ++mb)
+#pragma unroll
+        for (int e = 0; e < 16; e += 4) {
+            float x0 = o[mb][e], x1 = o[mb][e + 1], x2 = o[mb][e + 2], x3 = o[mb][e + 3];
+            scale4_acc(x0, x1, x2, x3, c);
+            o[mb][e] = x0;
+            o[mb][e + 1] = x1;
+            o[mb][e + 2] = x2;
+            o[mb][e + 3] = x3;
+        }
+}
+
+// O^T[mb] += V^T P^T for the 16 kv rows of step KQ, output blocks 4 HALF..+3.
+// b[2 u + s] is this lane's LDS offset for output block 4 HALF + u, row pair
+// member s (the swizzle makes it depend on u and s); the rest is a constant,
+// +8 KiB per 16 kv rows and +256 B for the upper four output blocks.
 template <int KQ, int HALF>
-__device__ __forceinline__ void pv_step(f32x16 (&o)[8], const f16x8& pk, const uint32_t (&b)[8]) {
-    s16x4 rd[8];
-    tr_read8<KQ, HALF>(rd, b);
+__device__ __forceinline__ void pv_step(f32x16 (&o)[8], const f16x8& pk, const char* lds,
+                                        const uint32_t (&b)[8]) {
+    constexpr int IMM = 16 * ROW_B * KQ + 256 * HALF;
+    typedef __attribute__((address_space(3))) const char lds_char;
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-        const f16x4 lf = __builtin_bit_cast(f16x4, rd[2 * u]);
-        const f16x4 hf = __builtin_bit_cast(f16x4, rd[2 * u + 1]);
+        const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (lds_s16x4*)((lds_char*)lds + b[2 * u] + IMM));
+        const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (lds_s16x4*)((lds_char*)lds + b[2 * u + 1] + IMM));
+        const f16x4 lf = __builtin_bit_cast(f16x4, lo);
+        const f16x4 hf = __builtin_bit_cast(f16x4, hi);
         const f16x8 av = {lf[0], lf[1], lf[2], lf[3], hf[0], hf[1], hf[2], hf[3]};
-        o[4 * HALF + u] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, pk, o[4 * HALF + u], 0, 0, 0);
+        acc_mfma(o[4 * HALF + u], av, pk);
     }
 }
 
@@ -109,18 +166,17 @@ __device__ __forceinline__ void pv_step(f32x16 (&o)[8], const f16x8& pk, const u
 // row base is wave-uniform (a scalar address), the lane part the per-lane
 // offset loff[n]. On the last tile rows past kv_end read row
 // kv_end - 1 instead (in bounds; masked by the causal mask, p = 0).
-__device__ __forceinline__ void issue_tile(char* smem, int st, const char* kb, const char* vb,
-                                           uint32_t rsb, int kv0, int kv_end, int w, int lane,
-                                           const uint32_t (&loff)[8]) {
+__device__ __forceinline__ void issue_tile(uint32_t lds_base, int st, const char* kb,
+                                           const char* vb, uint32_t rsb, int kv0, int kv_end,
+                                           int w, int lane, const uint32_t (&loff)[8]) {
+    const uint32_t dst0 = lds_base + st * TILE_B + 16 * w * ROW_B;
     if (kv0 + PF_BK <= kv_end) {
 #pragma unroll
         for (int n = 0; n < 8; ++n) {
             const size_t rb = (size_t)(kv0 + 16 * w + 2 * n) * rsb;
-            char* dst = smem + st * TILE_B + (16 * w + 2 * n) * ROW_B;
-            __builtin_amdgcn_global_load_lds((const void*)(kb + rb + loff[n]), (lds_void*)dst,
-                                             16, 0, 0);
-            __builtin_amdgcn_global_load_lds((const void*)(vb + rb + loff[n]),
-                                             (lds_void*)(dst + V_OFF), 16, 0, 0);
+            const uint32_t dst = dst0 + 2 * n * ROW_B;
+            copy16(kb + rb, loff[n], dst);
+            copy16(vb + rb, loff[n], dst + V_OFF);
         }
     } else {
 #pragma unroll
@@ -129,10 +185,9 @@ __device__ __forceinline__ void issue_tile(char* smem, int st, const char* kb, c
             const int c = (lane & 31) ^ sw(r);
             const int kv = min(kv0 + r, kv_end - 1);
             const size_t off = (size_t)kv * rsb + 16 * c;
-            char* dst = smem + st * TILE_B + (16 * w + 2 * n) * ROW_B;
-            __builtin_amdgcn_global_load_lds((const void*)(kb + off), (lds_void*)dst, 16, 0, 0);
-            __builtin_amdgcn_global_load_lds((const void*)(vb + off), (lds_void*)(dst + V_OFF),
-                                             16, 0, 0);
+            const uint32_t dst = dst0 + 2 * n * ROW_B;
+            copy16_v(kb + off, dst);
+            copy16_v(vb + off, dst + V_OFF);
         }
     }
 }
@@ -173,7 +228,7 @@ attn_prefill_kernel(const f16* __restrict__ q, int q_pitch, const f16* __restric
         loff[n] = (lane >> 5) * rsb + 16 * ((lane & 31) ^ sw(2 * n + (lane >> 5)));
     const uint32_t lds_base = (uint32_t)(uintptr_t)((__attribute__((address_space(3))) char*)smem);
 
-    issue_tile(smem, 0, kb, vb, rsb, 0, kv_end, w, lane, loff);
+    issue_tile(lds_base, 0, kb, vb, rsb, 0, kv_end, w, lane, loff);
 
     f16x8 qreg[16];   // Q[row][128 hh + 8 ks + 0..7]
     {
@@ -181,9 +236,13 @@ attn_prefill_kernel(const f16* __restrict__ q, int q_pitch, const f16* __restric
 #pragma unroll
         for (int ks = 0; ks < 16; ++ks) qreg[ks] = rvalid ? *(const f16x8*)(qrow + 8 * ks) : (f16x8)(0);
     }
+    // Wait for Q (and tile 0) here: left to the compiler, the wait for Q lands
+    // inside the tile loop as vmcnt(0) -- on every tile, and on the next tile's
+    // copy with it.
+    WAIT_VMCNT(0);
     f32x16 o[8];
 #pragma unroll
-    for (int mb = 0; mb < 8; ++mb) o[mb] = (f32x16)(0.f);
+    for (int mb = 0; mb < 8; ++mb) acc_zero(o[mb], (f16x8)(0));
     float m_run = -1e30f, l_run = 0.f;
 
     // K operand, k-step ks: row ql (and 32 + ql, +16 KiB) chunk 16 hh + ks,
@@ -209,12 +268,12 @@ attn_prefill_kernel(const f16* __restrict__ q, int q_pitch, const f16* __restric
     for (int j = 0; j < n_tiles; ++j) {
         const int st = j & 1;
         if (j + 1 < n_tiles) {
-            issue_tile(smem, st ^ 1, kb, vb, rsb, (j + 1) * PF_BK, kv_end, w, lane, loff);
+            issue_tile(lds_base, st ^ 1, kb, vb, rsb, (j + 1) * PF_BK, kv_end, w, lane, loff);
             WAIT_VMCNT(16);   // this tile's 16 copies done, the next tile's in flight
         } else {
             WAIT_VMCNT(0);
         }
-        lds_barrier();
+        tile_ready();
         const int kv0 = j * PF_BK;
         if (kv0 <= wqmax) {
             const uint32_t kst = koff + st * TILE_B;
@@ -252,8 +311,7 @@ attn_prefill_kernel(const f16* __restrict__ q, int q_pitch, const f16* __restric
                 const float corr = fast_exp2(m_run - m_new);
                 m_run = m_new;
                 l_run *= corr;
-#pragma unroll
-                for (int mb = 0; mb < 8; ++mb) o[mb] *= corr;
+                acc_scale(o, corr);
             }
             float psum = 0.f;
             f16x8 pk[4];
@@ -264,22 +322,20 @@ attn_prefill_kernel(const f16* __restrict__ q, int q_pitch, const f16* __restric
                 pk[rr >> 3][rr & 7] = (f16)p;
             }
             l_run += psum + lane_xor(psum, 32);
-            const uint32_t vt = lds_base + (uint32_t)(V_OFF + st * TILE_B);
-            uint32_t tb[8];
-#pragma unroll
-            for (int i = 0; i < 8; ++i) tb[i] = vt + troff[i];
-            pv_step<0, 0>(o, pk[0], tb);
-            pv_step<0, 1>(o, pk[0], tb);
-            pv_step<1, 0>(o, pk[1], tb);
-            pv_step<1, 1>(o, pk[1], tb);
-            pv_step<2, 0>(o, pk[2], tb);
-            pv_step<2, 1>(o, pk[2], tb);
-            pv_step<3, 0>(o, pk[3], tb);
-            pv_step<3, 1>(o, pk[3], tb);
+            const char* vt = smem + V_OFF + st * TILE_B;
+            pv_step<0, 0>(o, pk[0], vt, troff);
+            pv_step<0, 1>(o, pk[0], vt, troff);
+            pv_step<1, 0>(o, pk[1], vt, troff);
+            pv_step<1, 1>(o, pk[1], vt, troff);
+            pv_step<2, 0>(o, pk[2], vt, troff);
+            pv_step<2, 1>(o, pk[2], vt, troff);
+            pv_step<3, 0>(o, pk[3], vt, troff);
+            pv_step<3, 1>(o, pk[3], vt, troff);
         }
-        lds_barrier();   // this stage is refilled two tiles on
+        tile_done();   // this stage is refilled two tiles on
     }
 
+    acc_settle(o);
     if (rvalid) {
         const float inv = 1.f / l_run;
         f16* zrow = z + ((size_t)t * n_q_heads + h * G + g) * z_pitch + 4 * hh;
