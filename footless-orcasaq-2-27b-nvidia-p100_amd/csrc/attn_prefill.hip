@@ -278,13 +278,26 @@ attn_prefill_kernel(const f16* __restrict__ q, int q_pitch, const f16* __restric
         if (kv0 <= wqmax) {
             const uint32_t kst = koff + st * TILE_B;
             f32x16 s0 = (f32x16)(0.f), s1 = (f32x16)(0.f);
+            // K fragments read KPF k-steps ahead of their MFMAs
+            constexpr int KPF = 3;
+            f16x8 ka0[KPF], ka1[KPF];
+#pragma unroll
+            for (int ks = 0; ks < KPF; ++ks) {
+                lds_char* ka = (lds_char*)smem + (kst ^ (16 * ks));
+                ka0[ks] = *(lds_f16x8*)ka;
+                ka1[ks] = *(lds_f16x8*)(ka + 32 * ROW_B);
+            }
 #pragma unroll
             for (int ks = 0; ks < 16; ++ks) {
-                lds_char* ka = (lds_char*)smem + (kst ^ (16 * ks));
-                const f16x8 a0 = *(lds_f16x8*)ka;
-                const f16x8 a1 = *(lds_f16x8*)(ka + 32 * ROW_B);
+                const f16x8 a0 = ka0[ks % KPF], a1 = ka1[ks % KPF];
+                if (ks + KPF < 16) {
+                    lds_char* ka = (lds_char*)smem + (kst ^ (16 * (ks + KPF)));
+                    ka0[ks % KPF] = *(lds_f16x8*)ka;
+                    ka1[ks % KPF] = *(lds_f16x8*)(ka + 32 * ROW_B);
+                }
                 s0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, qreg[ks], s0, 0, 0, 0);
                 s1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, qreg[ks], s1, 0, 0, 0);
+                __builtin_amdgcn_sched_barrier(0);   // keep the reads ahead (the scheduler sinks them)
             }
             // raw scores; the causal mask only on tiles that cross the diagonal
             float sc[32];
