@@ -32,6 +32,13 @@ HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
 MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA, TFLOP/s
 METRIC = "attn/GDN decode µs/step + HBM GB/s %peak; prefill tokens/s + MFMA util"
 
+# HBM bytes one gdn_decode_kernel launch moves on MI355X, from two rocprofv3
+# --pmc passes over `bench.py --counters copy,gdn` (FETCH_SIZE, then
+# WRITE_SIZE), each scaled by what the same counter reads for a 256 MiB
+# device copy (FETCH_SIZE x2.0, WRITE_SIZE x1.0); summary and commands in
+# profiles/gdn_decode_B4_hbm_traffic.md. Re-measure when the kernel changes.
+GDN_DECODE_TRAFFIC_BYTES = 27_234_960
+
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
@@ -268,6 +275,62 @@ def cpu_baseline(budget_s=12.0):
                       f"fp32 on {os.cpu_count()} host cpus"}
 
 
+# ---------------------------------------------------------------------------
+# counter collection: workloads launched eagerly, untimed
+# ---------------------------------------------------------------------------
+
+def run_counter_workloads(torch, fl, names):
+    """A few eager launches of each named workload for rocprofv3 --pmc runs:
+    copy (a 256 MiB device copy, the scale reference for FETCH_SIZE /
+    WRITE_SIZE), gdn (config 1: 96 fused decode steps, 48 layer states
+    rotated), prefill8k (config 3 at 8k, 3 launches), decode100k (config 2
+    at 100k, B=4 T=3, 10 launches)."""
+    dev = torch.device("cuda:0")
+    for name in names:
+        log(f"counters: {name}")
+        if name == "copy":
+            src = torch.empty(64 << 20, dtype=torch.float32, device=dev).normal_()
+            dst = torch.empty_like(src)
+            for _ in range(3):
+                dst.copy_(src)
+            del src, dst
+        elif name == "gdn":
+            g = torch.Generator(device=dev).manual_seed(1)
+            L, row, nv = GDN_LAYERS, 10240, 48
+            S = torch.randn((L, B, nv, 128, 128), generator=g, device=dev) * 0.02
+            rings = torch.zeros((L, B, 2, row, 3), dtype=torch.float16, device=dev)
+            x = torch.randn((L, B, 1, row), generator=g, device=dev).half()
+            a = torch.randn((L, B, 1, nv), generator=g, device=dev)
+            b = torch.randn((L, B, 1, nv), generator=g, device=dev)
+            w = (torch.randn((L, row, 4), generator=g, device=dev) * 0.5).half()
+            A_log = torch.zeros((L, nv), device=dev)
+            dt_bias = torch.zeros((L, nv), device=dev)
+            y = torch.empty((L, B, 1, nv * 128), dtype=torch.float16, device=dev)
+            for i in range(2 * L):
+                l, ph = i % L, (i // L) & 1
+                fl.ops.gdn_decode(x[l], [S[l, j] for j in range(B)], a[l], b[l], A_log[l],
+                                  dt_bias[l], y[l], T=1, pos0s=[100 + i // L] * B,
+                                  conv_fused=True, conv_w=w[l],
+                                  cst_in=[rings[l, j, ph] for j in range(B)],
+                                  cst_out=[rings[l, j, ph ^ 1] for j in range(B)])
+            del S, rings
+        elif name == "prefill8k":
+            L = 8192
+            g = torch.Generator(device=dev).manual_seed(L)
+            q = (torch.randn((L, 24, 256), generator=g, device=dev) / 16).half()
+            kc = torch.randn((L, 4, 256), generator=g, device=dev).half()
+            vc = torch.randn((L, 4, 256), generator=g, device=dev).half()
+            for _ in range(3):
+                fl.ops.attention_prefill(q, kc, vc, pos0=0, scale=1.0)
+        elif name == "decode100k":
+            bench_attn_decode(torch, fl, 102400, iters=10)
+        else:
+            raise SystemExit(f"unknown counter workload {name!r}")
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+    log("counters: done")
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=1)
@@ -275,6 +338,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=48)
     ap.add_argument("--quick", action="store_true", help="primary line only, no extra configs")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--counters", default=None,
+                    help="comma list of workloads (copy,gdn,prefill8k,decode100k) to launch "
+                         "eagerly for rocprofv3 --pmc, then exit without timing")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported (this build runs "
@@ -289,6 +355,9 @@ def main():
     fl = ge.load_package()
     torch.cuda.init()
     log(f"bench: device {torch.cuda.get_device_name(0)}")
+    if args.counters:
+        run_counter_workloads(torch, fl, args.counters.split(","))
+        return
 
     log("bench: config 1 (GDN decode, B=4, 48 layer states rotated) ...")
     torch.cuda.synchronize()
@@ -331,7 +400,8 @@ def main():
                    "k_heads": 16, "v_heads": 48, "d_k": 128, "d_v": 128, "conv_width": 4,
                    "layer_states_rotated": GDN_LAYERS, "parallelism": "none (1 GPU)"},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+                     "traffic": GDN_DECODE_TRAFFIC_BYTES,
                      "bytes_per_launch": prim["bytes"]},
         "cpu_baseline": cpu,
         "extra": extra,

@@ -33,12 +33,13 @@ HIPCC_FLAGS = [
     f"-I{CSRC}",
 ]
 
-# Per-source extras. attn_prefill: MFMA accumulators in VGPRs, so the rare
-# online-softmax rescale of O is a plain multiply instead of making the
-# register allocator keep a VGPR copy of all 128 AGPR accumulators live
-# across the tile loop.
+# Per-source extras. attn_prefill: the compiler's MFMAs (the S = K Q^T
+# scores) accumulate in VGPRs, where the softmax reads them (the P V
+# accumulators are AGPRs held by inline asm); no NaNs and IEEE mode off, so
+# the score max is plain v_max / v_max3 without NaN-quieting canonicalisation
+# (scores are finite or -inf).
 FILE_FLAGS = {
-    "attn_prefill": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+    "attn_prefill": ["-mllvm", "-amdgpu-mfma-vgpr-form", "-fno-honor-nans", "-mno-amdgpu-ieee"],
 }
 
 

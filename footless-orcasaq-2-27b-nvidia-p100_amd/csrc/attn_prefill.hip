@@ -192,6 +192,14 @@ __device__ __forceinline__ void issue_tile(uint32_t lds_base, int st, const char
     }
 }
 
+// p as a wave-uniform (scalar) value: the copies take their row base in SGPRs
+__device__ __forceinline__ const char* uniform_ptr(const char* p) {
+    const uint64_t v = (uint64_t)(uintptr_t)p;
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return (const char*)(uintptr_t)(((uint64_t)hi << 32) | lo);
+}
+
 __global__ void __launch_bounds__(PF_THREADS)
 attn_prefill_kernel(const f16* __restrict__ q, int q_pitch, const f16* __restrict__ kc,
                     const f16* __restrict__ vc, f16* __restrict__ z, int z_pitch, int n_q_heads,
@@ -211,17 +219,20 @@ attn_prefill_kernel(const f16* __restrict__ q, int q_pitch, const f16* __restric
     const int t = rvalid ? row / G : 0;
     const int g = rvalid ? row - t * G : 0;
     const int qpos = rvalid ? pos0 + t : -1;
+    // Workgroup / wave scalars, marked uniform: the integer divisions are VALU
+    // code, and a VGPR-held bound would turn the copy issue into a divergent
+    // branch with its scalar base address in VGPRs.
     const int wfirst = R0 + 32 * w;
     const int wlast = min(wfirst + 31, RT - 1);
-    const int wqmax = wlast >= wfirst ? pos0 + wlast / G : -1;   // the wave's last query position
-    const int wqmin = pos0 + wfirst / G;                          // and its first
+    const int wqmax = __builtin_amdgcn_readfirstlane(wlast >= wfirst ? pos0 + wlast / G : -1);
+    const int wqmin = __builtin_amdgcn_readfirstlane(pos0 + wfirst / G);   // first query position
     const int blast = min(R0 + PF_BQ - 1, RT - 1);
-    const int kv_end = pos0 + blast / G + 1;                      // rows any query here sees
+    const int kv_end = __builtin_amdgcn_readfirstlane(pos0 + blast / G + 1);   // rows seen here
     const int n_tiles = (kv_end + PF_BK - 1) / PF_BK;
 
     const uint32_t rsb = (uint32_t)n_kv * ROW_B;   // bytes between cache rows
-    const char* kb = (const char*)(kc + (size_t)h * PF_HD);
-    const char* vb = (const char*)(vc + (size_t)h * PF_HD);
+    const char* kb = uniform_ptr((const char*)(kc + (size_t)h * PF_HD));
+    const char* vb = uniform_ptr((const char*)(vc + (size_t)h * PF_HD));
     uint32_t loff[8];
 #pragma unroll
     for (int n = 0; n < 8; ++n)
@@ -308,11 +319,14 @@ attn_prefill_kernel(const f16* __restrict__ q, int q_pitch, const f16* __restric
                     sc[16 + rr] = s1[rr];
                 }
             } else {
+                // score rr of s0 is kv row kv0 + 8 (rr / 4) + 4 hh + rr % 4 (s1:
+                // + 32); it is visible when that row <= qpos
+                const int lim = qpos - kv0 - 4 * hh;
 #pragma unroll
                 for (int rr = 0; rr < 16; ++rr) {
-                    const int kvr = kv0 + 8 * (rr >> 2) + 4 * hh + (rr & 3);
-                    sc[rr] = kvr <= qpos ? s0[rr] : -INFINITY;
-                    sc[16 + rr] = kvr + 32 <= qpos ? s1[rr] : -INFINITY;
+                    const int d = 8 * (rr >> 2) + (rr & 3);
+                    sc[rr] = d <= lim ? s0[rr] : -INFINITY;
+                    sc[16 + rr] = d + 32 <= lim ? s1[rr] : -INFINITY;
                 }
             }
             float mt = sc[0];
