@@ -37,7 +37,7 @@ METRIC = "attn/GDN decode µs/step + HBM GB/s %peak; prefill tokens/s + MFMA uti
 # WRITE_SIZE), each scaled by what the same counter reads for a 256 MiB
 # device copy (FETCH_SIZE x2.0, WRITE_SIZE x1.0); summary and commands in
 # profiles/gdn_decode_B4_hbm_traffic.md. Re-measure when the kernel changes.
-GDN_DECODE_TRAFFIC_BYTES = 27_234_960
+GDN_DECODE_TRAFFIC_BYTES = 27_234_791
 
 
 def log(*a):
@@ -331,6 +331,18 @@ def run_counter_workloads(torch, fl, names):
     log("counters: done")
 
 
+EXTRA_CONFIGS = {
+    "decode_verify_B1_T1_L4096": (bench_attn_decode, {"Lmax": 4096, "Bq": 1, "T": 1}),
+    "decode_verify_B4_T3_L8192": (bench_attn_decode, {"Lmax": 8192}),
+    "decode_verify_B4_T3_L32768": (bench_attn_decode, {"Lmax": 32768}),
+    "decode_verify_B4_T3_L102400": (bench_attn_decode, {"Lmax": 102400}),
+    "prefill_L2048": (bench_prefill, {"L": 2048}),
+    "prefill_L8192": (bench_prefill, {"L": 8192}),
+    "prefill_L32768": (bench_prefill, {"L": 32768}),
+    "gdn_chunked_L8192": (bench_chunked, {}),
+}
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=1)
@@ -338,6 +350,10 @@ def main():
     ap.add_argument("--warmup", type=int, default=48)
     ap.add_argument("--quick", action="store_true", help="primary line only, no extra configs")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--only", default=None,
+                    help="run one config by name (gdn_decode_B4, decode_verify_B1_T1_L4096, "
+                         "decode_verify_B4_T3_L{8192,32768,102400}, prefill_L{2048,8192,32768}, "
+                         "gdn_chunked_L8192) and print its result, not the contract line")
     ap.add_argument("--counters", default=None,
                     help="comma list of workloads (copy,gdn,prefill8k,decode100k) to launch "
                          "eagerly for rocprofv3 --pmc, then exit without timing")
@@ -358,6 +374,14 @@ def main():
     if args.counters:
         run_counter_workloads(torch, fl, args.counters.split(","))
         return
+    if args.only:
+        if args.only == "gdn_decode_B4":
+            r = bench_gdn_decode(torch, fl, args.steps, args.warmup)
+        else:
+            fn, kw = EXTRA_CONFIGS[args.only]
+            r = fn(torch, fl, **kw)
+        print(json.dumps({"config": args.only, **r}), flush=True)
+        return
 
     log("bench: config 1 (GDN decode, B=4, 48 layer states rotated) ...")
     torch.cuda.synchronize()
@@ -367,11 +391,7 @@ def main():
 
     extra = []
     if not args.quick:
-        for fn, kw in ((bench_attn_decode, {"Lmax": 4096, "Bq": 1, "T": 1}),
-                       (bench_attn_decode, {"Lmax": 8192}), (bench_attn_decode, {"Lmax": 32768}),
-                       (bench_attn_decode, {"Lmax": 102400}), (bench_prefill, {"L": 2048}),
-                       (bench_prefill, {"L": 8192}), (bench_prefill, {"L": 32768}),
-                       (bench_chunked, {})):
+        for fn, kw in EXTRA_CONFIGS.values():
             r = fn(torch, fl, **kw)
             log(f"bench: {r}")
             extra.append(r)
