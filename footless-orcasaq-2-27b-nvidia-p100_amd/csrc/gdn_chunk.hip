@@ -16,8 +16,9 @@
 //
 // Two launches: chunk_prep (every (chunk, v head) in parallel: Q K^T and K K^T
 // on MFMA, W and U by forward substitution in fp32, into the caller's
-// workspace), then chunk_state (one workgroup per (v head, 32 state rows),
-// sequential over the chunks with the rows in registers, fp32 throughout).
+// workspace), then chunk_state (one workgroup per (v head, 64 state rows),
+// sequential over the chunks with the state in MFMA accumulators; fp32 MFMA
+// (v_mfma_f32_16x16x4_f32) for the three products of a chunk).
 #include "fl_common.hpp"
 
 #pragma clang fp contract(off)
@@ -27,12 +28,12 @@ namespace {
 constexpr int CK_C = 64;       // tokens a chunk
 constexpr int CK_K = 128;      // key dim
 constexpr int CK_V = 128;      // value dim
-constexpr int CK_ROWS = 32;    // state rows a chunk_state workgroup
 constexpr int CK_KP = CK_K + 8;   // f16 pitch of staged K / Q rows
 constexpr int CK_AP = 68;      // f32 pitch of the A matrix rows
 
-// workspace block of one (chunk, v head): W [C][K], U [C][V], QKm [C][C], G [C]
-constexpr size_t CK_BLK = (size_t)CK_C * CK_K + (size_t)CK_C * CK_V + (size_t)CK_C * CK_C + CK_C;
+// workspace block of one (chunk, v head): W [C][K], U^T [V][C], QKm [C][C], then
+// G [C] (in-chunk prefix sums of log decay), e^{G} [C], e^{G_last - G} [C]
+constexpr size_t CK_BLK = (size_t)CK_C * CK_K + (size_t)CK_C * CK_V + (size_t)CK_C * CK_C + 3 * CK_C;
 
 __device__ __forceinline__ float safe_log(float d) { return logf(fmaxf(d, 1.17549435e-38f)); }
 
@@ -132,119 +133,222 @@ chunk_prep_kernel(const f16* __restrict__ q, const f16* __restrict__ k, const f1
             }
             x[i] = acc;
         }
-        float* dst = isW ? Wg : Ug;
+        if (isW) {
 #pragma unroll
-        for (int i = 0; i < CK_C; ++i) dst[(size_t)i * CK_K + col] = x[i];
+            for (int i = 0; i < CK_C; ++i) Wg[(size_t)i * CK_K + col] = x[i];
+        } else {   // U transposed: a v row's 64 tokens contiguous
+#pragma unroll
+            for (int i = 0; i < CK_C; i += 4)
+                *(f32x4*)(Ug + (size_t)col * CK_C + i) = (f32x4){x[i], x[i + 1], x[i + 2], x[i + 3]};
+        }
     }
-    if (tid < CK_C) Gg[tid] = sG[tid];
+    if (tid < CK_C) {
+        Gg[tid] = sG[tid];
+        Gg[CK_C + tid] = expf(sG[tid]);
+        Gg[2 * CK_C + tid] = expf(sG[CK_C - 1] - sG[tid]);
+    }
+}
+
+// The state pass. A workgroup of 4 waves owns 64 state rows (v) of one v
+// head, 16 a wave; a wave keeps its slice of S^T (128 k x 16 v) in 32 fp32
+// MFMA accumulators (block mb of 16 k rows, lane l: k = 16 mb + 4 (l/16) + r,
+// v = v0 + l%16 -- the D layout of v_mfma_f32_16x16x4_f32). Per chunk:
+//   A: P = W S^T, QS = Q S^T              [64 tok x 16 v], 256 MFMA
+//      Delta = U - P
+//   B: O = e^{g} o QS + QKm Delta         causal blocks only, 40 MFMA
+//   C: S^T = e^{g_C} S^T + Kd^T Delta     Kd^T[k][j] = e^{g_C - g_j} k_j[k], 128 MFMA
+// The k-step order of each product is permuted so that its B operand is an
+// accumulator register of the previous product: step (kq, r) takes k (or the
+// token) 16 kq + 4 (l/16) + r, which is register r of block kq. W, QKm, Q and
+// K are staged in LDS with row pitches that keep the operand reads on
+// distinct banks; Kd^T is read with ds_read_b64_tr_b16 from K's rows.
+constexpr int CS_ROWS = 64;          // state rows a workgroup
+constexpr int CS_WP = CK_K + 4;      // f32 pitch of staged W rows
+constexpr int CS_QKP = CK_C + 4;     // f32 pitch of staged QKm rows
+constexpr int CS_QP = CK_K + 8;      // f16 pitch of staged Q rows
+constexpr int CS_KP = CK_K + 16;     // f16 pitch of staged K rows
+constexpr int CS_OFF_QK = CK_C * CS_WP * 4;
+constexpr int CS_OFF_Q = CS_OFF_QK + CK_C * CS_QKP * 4;
+constexpr int CS_OFF_K = CS_OFF_Q + CK_C * CS_QP * 2;
+constexpr int CS_OFF_G = CS_OFF_K + CK_C * CS_KP * 2;
+constexpr int CS_LDS = CS_OFF_G + 3 * CK_C * 4;   // G, e^{G}, e^{G_last - G}
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+__device__ __forceinline__ f32x4 mfma4(float a, float b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
 __global__ void __launch_bounds__(256)
 chunk_state_kernel(const f16* __restrict__ q, const f16* __restrict__ k, float* __restrict__ S,
                    f16* __restrict__ y, int T, int n_vheads, int qk_stride, int y_stride,
                    float out_scale, int group, const float* __restrict__ work) {
-    __shared__ __attribute__((aligned(16))) float sW[CK_C][CK_K];
-    __shared__ __attribute__((aligned(16))) float sKf[CK_C][CK_K];
-    __shared__ __attribute__((aligned(16))) float sQf[CK_C][CK_K];
-    __shared__ __attribute__((aligned(16))) float sQK[CK_C][CK_C];
-    __shared__ float sU[CK_C][CK_ROWS];
-    __shared__ float sG[CK_C];
+    extern __shared__ __attribute__((aligned(16))) char smem[];
+    float* sW = (float*)smem;
+    float* sQK = (float*)(smem + CS_OFF_QK);
+    f16* sQ = (f16*)(smem + CS_OFF_Q);
+    f16* sK = (f16*)(smem + CS_OFF_K);
+    float* sG = (float*)(smem + CS_OFF_G);
 
     const int rb = blockIdx.x, hv = blockIdx.y, hk = hv / group;
-    const int tid = threadIdx.x, ri = tid >> 3, c0 = 4 * (tid & 7);
-    const int vi = rb * CK_ROWS + ri;
-    float* Srow = S + ((size_t)hv * CK_V + vi) * CK_K + c0;
-    float reg[16];
+    const int tid = threadIdx.x, l = tid & 63, w = tid >> 6;
+    const int m = l & 15, kk = l >> 4;
+    const int v0 = rb * CS_ROWS + 16 * w;
+    float* Sv = S + ((size_t)hv * CK_V + v0 + m) * CK_K + 4 * kk;   // S[v0 + m][4 kk ...]
+
+    f32x4 st[8];   // S^T block mb: rows k = 16 mb + 4 kk + r, column v0 + m
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const f32x4 v4 = *(const f32x4*)(Srow + 32 * j);
-        reg[4 * j] = v4[0]; reg[4 * j + 1] = v4[1]; reg[4 * j + 2] = v4[2]; reg[4 * j + 3] = v4[3];
-    }
-    const int n_chunks = (T + CK_C - 1) / CK_C;
-    for (int c = 0; c < n_chunks; ++c) {
+    for (int mb = 0; mb < 8; ++mb) st[mb] = *(const f32x4*)(Sv + 16 * mb);
+
+    // A chunk's operands are loaded into registers one chunk ahead (while the
+    // previous chunk computes) and written to LDS after its end barrier.
+    // Thread tid stages W rows i = tid / 32 + 8 j (f32x4 at column 4 (tid % 32)),
+    // QKm rows tid / 16 + 16 j, Q / K rows tid / 16 + 16 j (f16x8 at 8 (tid % 16)).
+    f32x4 pw[8], pqk[4];
+    f16x8 pq[4], pk[4];
+    float pg[3] = {0.f, 0.f, 0.f};
+    f32x4 pu[4];
+    auto prefetch = [&](int c) {
         const int t0 = c * CK_C;
         const int n = min(CK_C, T - t0);
         const float* blk = work + ((size_t)c * n_vheads + hv) * CK_BLK;
         const float* Wg = blk;
-        const float* Ug = Wg + CK_C * CK_K;
-        const float* QKg = Ug + CK_C * CK_V;
+        const float* UTg = Wg + CK_C * CK_K;
+        const float* QKg = UTg + CK_C * CK_V;
         const float* Gg = QKg + CK_C * CK_C;
-        __syncthreads();   // the previous chunk's reads are done
-        for (int idx = tid; idx < CK_C * CK_K / 4; idx += 256) {
-            const int i = idx >> 5, c4 = (idx & 31) * 4;
-            *(f32x4*)&sW[i][c4] = *(const f32x4*)(Wg + (size_t)i * CK_K + c4);
-            f16x4 kh = (f16x4)(0), qh = (f16x4)(0);
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            pw[j] = *(const f32x4*)(Wg + (size_t)((tid >> 5) + 8 * j) * CK_K + 4 * (tid & 31));
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int i = (tid >> 4) + 16 * j;
+            pqk[j] = *(const f32x4*)(QKg + (size_t)i * CK_C + 4 * (tid & 15));
+            pk[j] = pq[j] = (f16x8)(0);
             if (i < n) {
-                kh = *(const f16x4*)(k + (size_t)(t0 + i) * qk_stride + (size_t)hk * CK_K + c4);
-                qh = *(const f16x4*)(q + (size_t)(t0 + i) * qk_stride + (size_t)hk * CK_K + c4);
+                const size_t off = (size_t)(t0 + i) * qk_stride + (size_t)hk * CK_K + 8 * (tid & 15);
+                pk[j] = *(const f16x8*)(k + off);
+                pq[j] = *(const f16x8*)(q + off);
             }
-            *(f32x4*)&sKf[i][c4] = (f32x4){(float)kh[0], (float)kh[1], (float)kh[2], (float)kh[3]};
-            *(f32x4*)&sQf[i][c4] = (f32x4){(float)qh[0], (float)qh[1], (float)qh[2], (float)qh[3]};
         }
-        for (int idx = tid; idx < CK_C * CK_C / 4; idx += 256) {
-            const int i = idx >> 4, c4 = (idx & 15) * 4;
-            *(f32x4*)&sQK[i][c4] = *(const f32x4*)(QKg + (size_t)i * CK_C + c4);
+        if (tid < CK_C) {
+            pg[0] = Gg[tid];
+            pg[1] = Gg[CK_C + tid];
+            pg[2] = Gg[2 * CK_C + tid];
         }
-        for (int idx = tid; idx < CK_C * CK_ROWS; idx += 256) {
-            const int i = idx >> 5, r = idx & 31;
-            sU[i][r] = Ug[(size_t)i * CK_V + rb * CK_ROWS + r];
+#pragma unroll
+        for (int mb = 0; mb < 4; ++mb)
+            pu[mb] = *(const f32x4*)(UTg + (size_t)(v0 + m) * CK_C + 16 * mb + 4 * kk);
+    };
+    auto commit = [&]() {
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            *(f32x4*)&sW[((tid >> 5) + 8 * j) * CS_WP + 4 * (tid & 31)] = pw[j];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int i = (tid >> 4) + 16 * j;
+            *(f32x4*)&sQK[i * CS_QKP + 4 * (tid & 15)] = pqk[j];
+            *(f16x8*)&sK[i * CS_KP + 8 * (tid & 15)] = pk[j];
+            *(f16x8*)&sQ[i * CS_QP + 8 * (tid & 15)] = pq[j];
         }
-        if (tid < CK_C) sG[tid] = Gg[tid];
-        __syncthreads();
+        if (tid < CK_C) {
+            sG[tid] = pg[0];
+            sG[CK_C + tid] = pg[1];
+            sG[2 * CK_C + tid] = pg[2];
+        }
+    };
 
-        // Delta_i = U_i - W_i . S_row and (Q S0^T)_i, every lane of the row
-        float dl[CK_C];
-        float qs[CK_C];
+    const int n_chunks = (T + CK_C - 1) / CK_C;
+    prefetch(0);
+    commit();
+    for (int c = 0; c < n_chunks; ++c) {
+        const int t0 = c * CK_C;
+        const int n = min(CK_C, T - t0);
+        const f32x4 u[4] = {pu[0], pu[1], pu[2], pu[3]};   // U rows tok = 16 mb + 4 kk + r
+        __syncthreads();   // chunk c is in LDS
+        if (c + 1 < n_chunks) prefetch(c + 1);
+
+        // A: P = W S^T and QS = Q S^T
+        f32x4 p[4], qs[4];
 #pragma unroll
-        for (int i = 0; i < CK_C; ++i) {
-            float pw = 0.f, pq = 0.f;
+        for (int mb = 0; mb < 4; ++mb) p[mb] = qs[mb] = (f32x4)(0.f);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const f32x4 w4 = *(const f32x4*)&sW[i][c0 + 32 * j];
-                const f32x4 q4 = *(const f32x4*)&sQf[i][c0 + 32 * j];
+        for (int kq = 0; kq < 8; ++kq) {
+            f32x4 wf[4], qf[4];
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    pw = fmaf(w4[e], reg[4 * j + e], pw);
-                    pq = fmaf(q4[e], reg[4 * j + e], pq);
+            for (int mb = 0; mb < 4; ++mb) {
+                wf[mb] = *(const f32x4*)&sW[(16 * mb + m) * CS_WP + 16 * kq + 4 * kk];
+                const f16x4 qh = *(const f16x4*)&sQ[(16 * mb + m) * CS_QP + 16 * kq + 4 * kk];
+                qf[mb] = (f32x4){(float)qh[0], (float)qh[1], (float)qh[2], (float)qh[3]};
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+#pragma unroll
+                for (int mb = 0; mb < 4; ++mb) {
+                    p[mb] = mfma4(wf[mb][r], st[kq][r], p[mb]);
+                    qs[mb] = mfma4(qf[mb][r], st[kq][r], qs[mb]);
                 }
-            }
-            // sum over the row's 8 lanes (quad xor 1, xor 2, half-row mirror)
-            pw += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(pw), 0xB1, 0xF, 0xF, true));
-            pq += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(pq), 0xB1, 0xF, 0xF, true));
-            pw += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(pw), 0x4E, 0xF, 0xF, true));
-            pq += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(pq), 0x4E, 0xF, 0xF, true));
-            pw += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(pw), 0x141, 0xF, 0xF, true));
-            pq += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(pq), 0x141, 0xF, 0xF, true));
-            dl[i] = sU[i][ri] - pw;
-            qs[i] = pq;
         }
-        // outputs
+        f32x4 d[4];   // Delta rows tok = 16 mb + 4 kk + r, column v0 + m
 #pragma unroll
-        for (int i = 0; i < CK_C; ++i) {
-            float acc = expf(sG[i]) * qs[i];
+        for (int mb = 0; mb < 4; ++mb) d[mb] = u[mb] - p[mb];
+
+        // B: O = e^{g} o QS + QKm Delta (QKm is zero above the diagonal: blocks kq <= mb)
+        f32x4 o[4];
 #pragma unroll
-            for (int j = 0; j <= i; ++j) acc = fmaf(sQK[i][j], dl[j], acc);
-            if (c0 == 0 && i < n) y[(size_t)(t0 + i) * y_stride + (size_t)hv * CK_V + vi] = f16_sat(acc * out_scale);
-        }
-        // state: S = e^{g_C} S + sum_j Delta_j e^{g_C - g_j} k_j
-        const float gC = sG[CK_C - 1];
-        const float eC = expf(gC);
+        for (int mb = 0; mb < 4; ++mb) {
 #pragma unroll
-        for (int e = 0; e < 16; ++e) reg[e] = reg[e] * eC;
+            for (int r = 0; r < 4; ++r) o[mb][r] = sG[CK_C + 16 * mb + 4 * kk + r] * qs[mb][r];
 #pragma unroll
-        for (int j = 0; j < CK_C; ++j) {
-            const float coef = dl[j] * expf(gC - sG[j]);
+            for (int kq = 0; kq <= mb; ++kq) {
+                const f32x4 af = *(const f32x4*)&sQK[(16 * mb + m) * CS_QKP + 16 * kq + 4 * kk];
 #pragma unroll
-            for (int jj = 0; jj < 4; ++jj) {
-                const f32x4 k4 = *(const f32x4*)&sKf[j][c0 + 32 * jj];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) reg[4 * jj + e] = fmaf(coef, k4[e], reg[4 * jj + e]);
+                for (int r = 0; r < 4; ++r) o[mb] = mfma4(af[r], d[kq][r], o[mb]);
             }
         }
+#pragma unroll
+        for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int i = 16 * mb + 4 * kk + r;
+                if (i < n)
+                    y[(size_t)(t0 + i) * y_stride + (size_t)hv * CK_V + v0 + m] =
+                        f16_sat(o[mb][r] * out_scale);
+            }
+
+        // C: S^T = e^{g_C} S^T + Kd^T Delta
+        const float eC = sG[CK_C + CK_C - 1];
+        float dk[4][4];   // e^{g_C - g_tok}, tok = 16 kq + 4 kk + r
+#pragma unroll
+        for (int kq = 0; kq < 4; ++kq)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) dk[kq][r] = sG[2 * CK_C + 16 * kq + 4 * kk + r];
+        typedef __attribute__((address_space(3))) const char lds_char;
+#pragma unroll
+        for (int mb = 0; mb < 8; ++mb) st[mb] *= eC;
+#pragma unroll
+        for (int kq = 0; kq < 4; ++kq) {
+            // lane m of group kk receives K[16 kq + 4 kk + e][16 mb + m], e = 0..3
+            const int row = 16 * kq + 4 * kk + (m >> 2);
+            f32x4 ka[8];
+#pragma unroll
+            for (int mb = 0; mb < 8; ++mb) {
+                const s16x4 kt = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                    (lds_s16x4*)((lds_char*)sK + 2 * (row * CS_KP + 16 * mb + 4 * (m & 3))));
+                const f16x4 kh = __builtin_bit_cast(f16x4, kt);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) ka[mb][r] = (float)kh[r] * dk[kq][r];
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+#pragma unroll
+                for (int mb = 0; mb < 8; ++mb) st[mb] = mfma4(ka[mb][r], d[kq][r], st[mb]);
+        }
+        __syncthreads();   // chunk c's LDS reads are done
+        if (c + 1 < n_chunks) commit();
     }
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-        *(f32x4*)(Srow + 32 * j) = (f32x4){reg[4 * j], reg[4 * j + 1], reg[4 * j + 2], reg[4 * j + 3]};
+    for (int mb = 0; mb < 8; ++mb) *(f32x4*)(Sv + 16 * mb) = st[mb];
 }
 
 }  // namespace
@@ -281,7 +385,16 @@ int fl_gdn_prefill_chunked(const void* q, const void* k, const void* v, const fl
                        decay, T, n_vheads, qk_stride, v_stride, group, (float*)work);
     int rc = fl::check_launch("gdn_chunk_prep");
     if (rc) return rc;
-    hipLaunchKernelGGL(chunk_state_kernel, dim3(CK_V / CK_ROWS, n_vheads), dim3(256), 0,
+    static bool lds_attr_set = false;   // above the 64 KiB default of dynamic LDS
+    if (!lds_attr_set) {
+        if (hipFuncSetAttribute((const void*)chunk_state_kernel,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, CS_LDS) != hipSuccess) {
+            fl::set_error("gdn_chunk_state: cannot raise the dynamic LDS limit to %d bytes", CS_LDS);
+            return FL_ELAUNCH;
+        }
+        lds_attr_set = true;
+    }
+    hipLaunchKernelGGL(chunk_state_kernel, dim3(CK_V / CS_ROWS, n_vheads), dim3(256), CS_LDS,
                        (hipStream_t)stream, (const f16*)q, (const f16*)k, S, (f16*)y, T, n_vheads,
                        qk_stride, y_stride, out_scale, group, (const float*)work);
     return fl::check_launch("gdn_chunk_state");

@@ -71,7 +71,7 @@ def test_work_size_queries(fl):
     assert lib.fl_attn_decode_work_bytes(4, 3, 24, 256, 64) == 4 * 3 * 24 * 64 * (256 + 2) * 4
     n_chunks = (8192 + 63) // 64
     assert lib.fl_gdn_chunked_work_bytes(8192, 48, 128, 128, 64) == \
-        n_chunks * 48 * (64 * 128 * 2 + 64 * 64 + 64) * 4
+        n_chunks * 48 * (64 * 128 * 2 + 64 * 64 + 3 * 64) * 4
     assert lib.fl_gdn_chunked_work_bytes(8192, 48, 128, 128, 32) == 0
 
 
