@@ -208,6 +208,49 @@ def bench_prefill(torch, fl, L, iters=3):
 
 
 # ---------------------------------------------------------------------------
+# attention prep: q / k RMSNorm + partial RoPE + KV store (fused, one launch)
+# ---------------------------------------------------------------------------
+
+def attn_prep_bytes(T, n_q=24, n_kv=4, hd=256):
+    q = 2 * T * n_q * hd * 2            # q half of q|gate read + written
+    k = 2 * T * n_kv * hd * 2           # k read + written
+    v = T * n_kv * hd * 2
+    cache = 2 * T * n_kv * hd * 2       # k and v cache rows written
+    return q + k + v + cache + 2 * hd * 4
+
+
+def bench_attn_prep(torch, fl, T, iters=50):
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(T)
+    n_sets = max(1, -(-600_000_000 // attn_prep_bytes(T)))   # rotate > 256 MB MALL
+    n_sets = min(n_sets, 64)
+    sets = []
+    for _ in range(n_sets):
+        qg = torch.randn((T, 24, 512), generator=g, device=dev).half()
+        k = torch.randn((T, 4, 256), generator=g, device=dev).half()
+        v = torch.randn((T, 4, 256), generator=g, device=dev).half()
+        sets.append((qg, k, v))
+    wq = torch.randn(256, generator=g, device=dev) * 0.1
+    wk = torch.randn(256, generator=g, device=dev) * 0.1
+    max_pos = T + 4096
+    kc = torch.zeros((max_pos, 4, 256), dtype=torch.float16, device=dev)
+    vc = torch.zeros_like(kc)
+
+    def call(i):
+        qg, k, v = sets[i % n_sets]
+        fl.ops.attn_prep(qg, k, v, wq, wk, kc, vc, pos0=4096 - (i % 7))
+
+    gr = graph_of(torch, call, iters)
+    time_graph(torch, gr)
+    ms = time_graph(torch, gr, reps=3)
+    us = ms * 1e3 / iters
+    nbytes = attn_prep_bytes(T)
+    return {"config": f"attn_prep_T{T}", "us": round(us, 2),
+            "GBs": round(nbytes / (us * 1e-6) / 1e9, 1),
+            "hbm_frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 3)}
+
+
+# ---------------------------------------------------------------------------
 # config 4: chunked GDN prefill
 # ---------------------------------------------------------------------------
 
@@ -340,6 +383,8 @@ EXTRA_CONFIGS = {
     "prefill_L8192": (bench_prefill, {"L": 8192}),
     "prefill_L32768": (bench_prefill, {"L": 32768}),
     "gdn_chunked_L8192": (bench_chunked, {}),
+    "attn_prep_T1": (bench_attn_prep, {"T": 1}),
+    "attn_prep_T8192": (bench_attn_prep, {"T": 8192, "iters": 20}),
 }
 
 

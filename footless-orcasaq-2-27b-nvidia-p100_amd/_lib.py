@@ -28,6 +28,10 @@ SIGNATURES = {
     "fl_strerror": (ctypes.c_char_p, [_I]),
     "fl_last_error": (ctypes.c_char_p, []),
     "fl_kv_store": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P]),
+    "fl_rmsnorm1p": (_I, [_P, _P, _P, _I, _I, _I, _I, _F, _P]),
+    "fl_rope_partial": (_I, [_P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _F, _P]),
+    "fl_attn_prep": (_I, [_P, _I, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _F, _F,
+                          _P]),
     "fl_attention_split_gqa": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _F, _I,
                                     _I, _I, _P]),
     "fl_attention_merge": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _I, _I, _P]),

@@ -113,7 +113,7 @@ __device__ __forceinline__ void gather16(float (&dst)[16], const float* row, int
 }
 
 // ---------------------------------------------------------------------------
-// a8 / a9: conv
+// causal conv (decode / prefill rows, and verify rows with per-row states)
 // ---------------------------------------------------------------------------
 __global__ void conv1d_causal_kernel(const f16* __restrict__ x, const f16* __restrict__ w,
                                      const f16* __restrict__ st_in, f16* __restrict__ y,
@@ -185,7 +185,7 @@ __global__ void conv1d_causal_rows_kernel(const f16* __restrict__ x, const f16* 
 }
 
 // ---------------------------------------------------------------------------
-// a10: L2 norm, one 128-thread block a (row, token)
+// L2 norm, one 128-thread block a (row, token)
 // ---------------------------------------------------------------------------
 __global__ void l2norm_kernel(const f16* __restrict__ x, f16* __restrict__ y, int n, int rows,
                               int pitch, float eps, float scale) {
@@ -206,7 +206,7 @@ __global__ void l2norm_kernel(const f16* __restrict__ x, f16* __restrict__ y, in
 }
 
 // ---------------------------------------------------------------------------
-// a11: gates
+// gates
 // ---------------------------------------------------------------------------
 __global__ void gdn_scalars_kernel(const float* __restrict__ a, const float* __restrict__ b,
                                    const float* __restrict__ A_log,
@@ -222,7 +222,7 @@ __global__ void gdn_scalars_kernel(const float* __restrict__ a, const float* __r
 }
 
 // ---------------------------------------------------------------------------
-// a12: the delta rule over T tokens, 16 tokens of k / q / v / gates staged in
+// the delta rule over T tokens, 16 tokens of k / q / v / gates staged in
 // LDS at a time. grid (V / 32, n_vheads), block 256.
 // ---------------------------------------------------------------------------
 __global__ void __launch_bounds__(GR_THREADS)
@@ -276,7 +276,7 @@ gdn_scan_kernel(const f16* __restrict__ q, const f16* __restrict__ k, const f16*
 }
 
 // ---------------------------------------------------------------------------
-// a13: the fused decode / verify step of B sequences.
+// the fused decode / verify step of B sequences.
 // grid (V / 32, n_vheads, B), block 256.
 // ---------------------------------------------------------------------------
 struct GdnSeqs {

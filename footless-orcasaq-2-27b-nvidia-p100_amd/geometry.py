@@ -10,6 +10,10 @@ ATTN_SCALE = HEAD_DIM ** -0.5                           # runtime.py:83
 Q_PITCH = 2 * HEAD_DIM  # a head's row of the q|gate buffer: q(256) | gate(256) (kernels.cu:64-68)
 GATE_OFF = HEAD_DIM
 
+ROPE_DIM = 64           # partial rotary: the first 64 of 256 dims   runtime.py:81
+ROPE_THETA = 1e7        #                                 runtime.py:82
+NORM_EPS = 1e-6         # q / k RMSNorm (mean-space eps)   runtime.py:115
+
 GDN_K_HEADS = 16        #                                 runtime.py:86
 GDN_V_HEADS = 48        #                                 runtime.py:87
 GDN_K = 128             #                                 runtime.py:88

@@ -22,8 +22,8 @@ import torch
 
 from . import _lib
 from .geometry import (ATTN_SCALE, GATE_OFF, GDN_CHUNK, GDN_GROUP, GDN_K, GDN_K_HEADS, GDN_V,
-                       GDN_V_HEADS, HEAD_DIM, L2_EPS, N_HEADS, N_KV, Q_PITCH, Q_SCALE, QKV_ROWS,
-                       SPLIT_MAX, SPLIT_ROWS)
+                       GDN_V_HEADS, HEAD_DIM, L2_EPS, N_HEADS, N_KV, NORM_EPS, Q_PITCH, Q_SCALE,
+                       QKV_ROWS, ROPE_DIM, ROPE_THETA, SPLIT_MAX, SPLIT_ROWS)
 
 F16, F32 = torch.float16, torch.float32
 
@@ -73,6 +73,49 @@ def kv_store(k, v, kcache, vcache, *, layer: int = 0, pos0: int, T: int | None =
               _ptr(kcache, F16, "kcache", (layer + 1) * max_pos * row),
               _ptr(vcache, F16, "vcache", (layer + 1) * max_pos * row),
               layer, pos0, T, n_kv_heads, head_dim, max_pos, _stream())
+
+
+def rmsnorm1p(x, w, y=None, *, rows: int, pitch: int, T: int | None = None, n: int = HEAD_DIM,
+              eps: float = NORM_EPS):
+    """kernels.cu:241-272 (runtime.py:2797-2801): per-row Gemma RMSNorm of
+    [T, rows] rows `pitch` halves apart (q inside the q|gate buffer: rows =
+    n_q_heads, pitch = 512), weight w [n] fp32; y = x (in place) by default."""
+    T = x.shape[0] if T is None else T
+    y = x if y is None else y
+    span = T * rows * pitch
+    _lib.call("fl_rmsnorm1p", _ptr(x, F16, "x", span), _ptr(w, F32, "w", n),
+              _ptr(y, F16, "y", span), n, rows, pitch, T, float(eps), _stream())
+    return y
+
+
+def rope_partial(q, k, *, pos0: int, T: int | None = None, n_q_heads: int = N_HEADS,
+                 n_kv_heads: int = N_KV, head_dim: int = HEAD_DIM, rope_dim: int = ROPE_DIM,
+                 q_pitch: int = Q_PITCH, k_pitch: int = HEAD_DIM, theta: float = ROPE_THETA):
+    """kernels.cu:422-455 (runtime.py:2809-2812): partial NeoX RoPE in place on
+    q [T, n_q_heads, q_pitch] and k [T, n_kv_heads, k_pitch] fp16."""
+    T = q.shape[0] if T is None else T
+    _lib.call("fl_rope_partial", _ptr(q, F16, "q", T * n_q_heads * q_pitch),
+              _ptr(k, F16, "k", T * n_kv_heads * k_pitch), n_q_heads, n_kv_heads, head_dim,
+              rope_dim, q_pitch, k_pitch, pos0, T, float(theta), _stream())
+
+
+def attn_prep(qg, k, v, wq, wk, kcache, vcache, *, pos0: int, T: int | None = None,
+              layer: int = 0, n_q_heads: int = N_HEADS, n_kv_heads: int = N_KV,
+              head_dim: int = HEAD_DIM, q_pitch: int = Q_PITCH, max_pos: int | None = None,
+              rope_dim: int = ROPE_DIM, theta: float = ROPE_THETA, eps: float = NORM_EPS):
+    """runtime.py:2797-2815 in one launch: rmsnorm1p of q (inside qg) and k,
+    rope_partial of both (both rewritten in place), and the roped k and v
+    [T, n_kv, head_dim] stored at cache rows pos0 + t (kv_store)."""
+    T = qg.shape[0] if T is None else T
+    max_pos = kcache.shape[-3] if max_pos is None else max_pos
+    row = n_kv_heads * head_dim
+    _lib.call("fl_attn_prep", _ptr(qg, F16, "qg", T * n_q_heads * q_pitch), q_pitch,
+              _ptr(k, F16, "k", T * row), _ptr(v, F16, "v", T * row),
+              _ptr(wq, F32, "wq", head_dim), _ptr(wk, F32, "wk", head_dim),
+              _ptr(kcache, F16, "kcache", (layer + 1) * max_pos * row),
+              _ptr(vcache, F16, "vcache", (layer + 1) * max_pos * row), layer, n_q_heads,
+              n_kv_heads, head_dim, pos0, max_pos, T, rope_dim, float(theta), float(eps),
+              _stream())
 
 
 def attention_split_gqa(q, kcache, vcache, pacc, pm, pd, *, layer: int = 0,

@@ -40,7 +40,7 @@ const char* fl_strerror(int status);
 /* Detail of the last failure on the calling thread ("" if none). */
 const char* fl_last_error(void);
 
-/* ---------------------------------------------------------------- a4 ----
+/* ---- KV store -------------------------------------------------------------
  * kv_store: k, v [T][n_kv_heads][head_dim] f16 -> cache rows pos0 + t of a
  * position-addressable [layers][max_pos][n_kv_heads][head_dim] f16 cache.
  * Replaces kernels.cu:465-484 kv_store, launched at runtime.py:2813-2815.
@@ -49,7 +49,38 @@ int fl_kv_store(const void* k, const void* v, void* kcache, void* vcache, int la
                 int pos0, int T, int n_kv_heads, int head_dim, int max_pos,
                 fl_stream_t stream);
 
-/* ------------------------------------------------------------- a1 -------
+/* ---- attention prep ---------------------------------------------------------
+ * rmsnorm1p: per-row Gemma RMSNorm, y = f16(x * rsqrt(sum(x^2) / n + eps) *
+ * (1 + w[i])), rows [T][rows] at `pitch` f16 apart (q: rows = n_q_heads,
+ * pitch = 2 head_dim inside the q|gate buffer; k: rows = n_kv_heads, pitch =
+ * head_dim); x == y (in place) allowed. The sum of squares in the reference
+ * block reduction's order. Replaces kernels.cu:241-272 rmsnorm1p, launched at
+ * runtime.py:2797-2801 (via _rms, runtime.py:2747-2748). Supported: n == 256. */
+int fl_rmsnorm1p(const void* x, const float* w, void* y, int n, int rows, int pitch, int T,
+                 float eps, fl_stream_t stream);
+
+/* rope_partial: partial NeoX RoPE in place on q [T][n_q_heads][q_pitch] and
+ * k [T][n_kv_heads][k_pitch] f16 at positions pos0 + t: pairs (j, j +
+ * rope_dim / 2), j < rope_dim / 2, rotate by (pos0 + t) * theta^(-2j /
+ * rope_dim), frequency, angle and sincos in fp64; dims >= rope_dim untouched.
+ * Replaces kernels.cu:422-455 rope_partial, launched at runtime.py:2809-2812.
+ * Supported: head_dim == 256, rope_dim even, <= head_dim. */
+int fl_rope_partial(void* q, void* k, int n_q_heads, int n_kv_heads, int head_dim, int rope_dim,
+                    int q_pitch, int k_pitch, int pos0, int T, float theta, fl_stream_t stream);
+
+/* attn_prep: rmsnorm1p of q (inside qg, q_pitch) with wq and of k with wk,
+ * rope_partial of both, then the roped k and v rows [T][n_kv_heads][head_dim]
+ * stored at cache positions pos0 + t of `layer` -- the sequence
+ * runtime.py:2797-2815 launches (rmsnorm1p x2, rope_partial, kv_store) as one
+ * launch, the same values (the reference's own fused form is its int8-cache
+ * attn_prep_q8, kernels.cu:837-908, runtime.py:2922-2930). q and k are
+ * rewritten in place, as there. Supported: head_dim == 256. */
+int fl_attn_prep(void* qg, int q_pitch, void* k, const void* v, const float* wq, const float* wk,
+                 void* kcache, void* vcache, int layer, int n_q_heads, int n_kv_heads,
+                 int head_dim, int pos0, int max_pos, int T, int rope_dim, float theta, float eps,
+                 fl_stream_t stream);
+
+/* ---- decode attention: split partials -------------------------------------
  * attention_split_gqa for one sequence: split-K flash-decode partials of T
  * query tokens at positions pos0..pos0+T-1 (token t attends rows
  * [0, pos0 + t]), q [T][n_q_heads][q_pitch] f16 (q = first head_dim of a
@@ -69,7 +100,7 @@ int fl_attention_split_gqa(const void* q, const void* kcache, const void* vcache
                            float scale, int split_rows, int T, int split,
                            fl_stream_t stream);
 
-/* ------------------------------------------------------------ a2 + a3 ---
+/* ---- decode attention: merge + gate ---------------------------------------
  * attention_merge (+ attn_gate when gate != NULL): z[t][h][:] =
  * f16_sat(sum_s e_s acc_s / sum_s e_s d_s), e_s = exp(m_s - max m), then
  * z = f16_sat(z * sigmoid(gate[t][h][g_off + d])) with gate rows of g_pitch
@@ -84,7 +115,7 @@ int fl_attention_merge(const float* pacc, const float* pm, const float* pd, void
 int fl_attn_gate(void* z, const void* g, int n_heads, int head_dim, int z_pitch,
                  int g_pitch, int g_off, int T, fl_stream_t stream);
 
-/* ------------------------------------------------- a1 + a2 + a3 batched ---
+/* ---- decode attention, batched --------------------------------------------
  * The decode / MTP-verify attention of B sequences in two launches: the
  * split partials of every (sequence, kv head, split) and the gated merge.
  * qg [B][T][n_q_heads][q_pitch] f16, q at offset 0 of a head's row and the
@@ -103,7 +134,7 @@ int fl_attn_decode(const void* qg, int q_pitch, const void* const* kcache,
                    int split, const void* gate, int g_pitch, int g_off, void* z, int z_pitch,
                    void* work, size_t work_bytes, fl_stream_t stream);
 
-/* ------------------------------------------------------------ a5 + a6 ---
+/* ---- prefill attention ----------------------------------------------------
  * Causal GQA prefill attention of T tokens at pos0.. over one layer cache
  * [max_pos][n_kv_heads][head_dim] f16: query (t, h) attends rows
  * [0, pos0 + t] of kv head h / G, z [T][n_q_heads][z_pitch] f16.
@@ -118,7 +149,7 @@ int fl_attention_prefill(const void* q, int q_pitch, const void* k_new, const vo
                          int head_dim, int pos0, int max_pos, float scale, int T, void* z,
                          int z_pitch, fl_stream_t stream);
 
-/* ---------------------------------------------------------------- a8 ----
+/* ---- causal conv ----------------------------------------------------------
  * conv1d_causal over `dim` channels of rows x [T][row_stride] f16: E =
  * [st_in (width-1 frames, ZERO if pos0 == 0) | x], y[t][d] =
  * f16_sat(silu(sum_j w[d][j] E[t+j])), st_out = last width-1 frames of E.
@@ -133,14 +164,14 @@ int fl_conv1d_causal_rows(const void* x, const void* w, const void* st_in, void*
                           void* st1, void* st2, int dim, int T, int pos0, int row_stride,
                           fl_stream_t stream);
 
-/* ---------------------------------------------------------------- a10 ---
+/* ---- L2 norm --------------------------------------------------------------
  * l2norm_scaled: y = f16_sat((x / sqrt(sum x^2 + eps)) * scale) per row of n
  * (n <= 1024), rows [T][rows][pitch] f16.
  * Replaces kernels.cu:373-391, runtime.py:3070-3071. */
 int fl_l2norm_scaled(const void* x, void* y, int n, int rows, int pitch, float eps, float scale,
                      int T, fl_stream_t stream);
 
-/* ---------------------------------------------------------------- a11 ---
+/* ---- GDN gates ------------------------------------------------------------
  * gdn_scalars: beta = sigmoid(b), decay = exp(-exp(A_log[h]) *
  * softplus(a + dt_bias[h])), softplus threshold 20. a, b [T][stride] f32;
  * beta, decay [T][n_heads] f32. Replaces kernels.cu:1732-1748,
@@ -149,7 +180,7 @@ int fl_gdn_scalars(const float* a, const float* b, const float* A_log, const flo
                    float* beta, float* decay, int T, int n_heads, int a_stride, int b_stride,
                    fl_stream_t stream);
 
-/* ---------------------------------------------------------------- a12 ---
+/* ---- GDN recurrent scan ---------------------------------------------------
  * The gated delta rule over T tokens, S [n_vheads][V][K] f32 in place:
  *   S *= decay; m = S k; delta = beta (v - m); S += delta k^T;
  *   y = f16_sat((S q) * out_scale)
@@ -163,7 +194,7 @@ int fl_gdn_scan(const void* q, const void* k, const void* v, const float* beta,
                 int K, int V, int qk_stride, int v_stride, int y_stride, float out_scale,
                 int group, float* Ck, long long ck_step, fl_stream_t stream);
 
-/* ---------------------------------------------------------------- a13 ---
+/* ---- GDN fused decode / verify --------------------------------------------
  * The fused GDN decode / verify step of B sequences (T <= 3): the gates
  * (a11), the L2 norm of q and k (a10, eps l2eps, fp16-rounded, scale 1),
  * and the delta rule (a12) with checkpoints, in one launch. With
@@ -186,7 +217,7 @@ int fl_gdn_decode(const void* x, int x_stride, int conv_fused, const void* conv_
                   int n_vheads, int K, int V, float out_scale, float l2eps,
                   fl_stream_t stream);
 
-/* ---------------------------------------------------------------- a14 ---
+/* ---- GDN chunked prefill --------------------------------------------------
  * Chunked (WY / UT transform) GDN prefill: the same recurrence as
  * fl_gdn_scan over T tokens in chunks of `chunk` tokens, fp32 state carried
  * between chunks; S in place, y as fl_gdn_scan. NOT in the reference (the

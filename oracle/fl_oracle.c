@@ -144,6 +144,67 @@ static float tree_xor(const float* in, int n) {
 /* ======================================================================== */
 /* a4 kv_store -- kernels.cu:465-484                                         */
 /* ======================================================================== */
+/* ======================================================================== */
+/* attention prep: rmsnorm1p (kernels.cu:241-272), rope_partial (397-455)    */
+/* ======================================================================== */
+/* rmsnorm1p over rows of n = 256 (one element a thread of the reference's
+ * 256-thread block): y = f16_sat(x * inv * (1 + w)), inv = rsqrt(ss / n +
+ * eps) with ss = block_reduce_sum(fmaf(x, x, 0)) (kernels.cu:214-227): warp w
+ * sums elements 32w..32w+31 by the __shfl_down tree, then warp 0 sums the 8
+ * warp totals (its lanes 8..31 hold 0) by the same tree. The reference's
+ * rsqrtf is the fast-math reciprocal square root; 1 / sqrtf here. Rows are
+ * [T][rows] at `pitch` halves apart; x == y allowed. */
+ORC_API void orc_rmsnorm1p(const uint16_t* x, const float* w, uint16_t* y, int n, int rows,
+                           int pitch, int T, float eps) {
+    for (int t = 0; t < T; t++)
+        for (int r = 0; r < rows; r++) {
+            const uint16_t* xr = x + ((size_t)t * rows + r) * pitch;
+            uint16_t* yr = y + ((size_t)t * rows + r) * pitch;
+            float warp[32] = {0};
+            for (int wv = 0; wv < n / 32; wv++) {
+                float a[32];
+                for (int i = 0; i < 32; i++) {
+                    const float v = orc_h2f(xr[32 * wv + i]);
+                    a[i] = fmaf(v, v, 0.f);
+                }
+                warp[wv] = tree_down(a, 32);
+            }
+            const float ss = tree_down(warp, 32);
+            const float inv = 1.f / sqrtf(ss / (float)n + eps);
+            for (int i = 0; i < n; i++) yr[i] = orc_f16_sat(orc_h2f(xr[i]) * inv * (1.f + w[i]));
+        }
+}
+
+/* rope_partial: pairs (j, j + rope_dim / 2) of the first rope_dim dims of
+ * each q and k head rotate by pos * theta^(-2j / rope_dim); frequency, angle
+ * and sin / cos in double, rounded to float, the pair products in float on
+ * the fp16 values; dims >= rope_dim untouched. q [T][n_q_heads][q_pitch],
+ * k [T][n_kv_heads][k_pitch], in place, position pos0 + t. */
+static void rope_row(uint16_t* row, int rope_dim, int pos, double theta) {
+    const int half_r = rope_dim >> 1;
+    for (int j = 0; j < half_r; j++) {
+        const double invf = pow(theta, -2.0 * (double)j / (double)rope_dim);
+        const double ang = (double)pos * invf;
+        const float cf = (float)cos(ang);
+        const float sf = (float)sin(ang);
+        const float x0 = orc_h2f(row[j]);
+        const float x1 = orc_h2f(row[j + half_r]);
+        row[j] = orc_f16_sat(x0 * cf - x1 * sf);
+        row[j + half_r] = orc_f16_sat(x1 * cf + x0 * sf);
+    }
+}
+
+ORC_API void orc_rope_partial(uint16_t* q, uint16_t* k, int n_q_heads, int n_kv_heads,
+                              int rope_dim, int q_pitch, int k_pitch, int pos0, int T,
+                              double theta) {
+    for (int t = 0; t < T; t++) {
+        for (int h = 0; h < n_q_heads; h++)
+            rope_row(q + ((size_t)t * n_q_heads + h) * q_pitch, rope_dim, pos0 + t, theta);
+        for (int h = 0; h < n_kv_heads; h++)
+            rope_row(k + ((size_t)t * n_kv_heads + h) * k_pitch, rope_dim, pos0 + t, theta);
+    }
+}
+
 ORC_API void orc_kv_store(const uint16_t* k, const uint16_t* v, uint16_t* kcache,
                           uint16_t* vcache, int layer, int pos0, int n_kv_heads,
                           int head_dim, int max_pos, int T) {

@@ -51,6 +51,8 @@ def lib() -> ctypes.CDLL:
         L = ctypes.CDLL(str(_LIB_PATH))
         sigs = {
             "orc_kv_store": [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I],
+            "orc_rmsnorm1p": [_P, _P, _P, _I, _I, _I, _I, _F],
+            "orc_rope_partial": [_P, _P, _I, _I, _I, _I, _I, _I, _I, _D],
             "orc_attention_split": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _F, _I, _I, _I],
             "orc_attention_merge": [_P, _P, _P, _P, _I, _I, _I, _I, _I],
             "orc_attn_gate": [_P, _P, _I, _I, _I, _I, _I, _I],
@@ -112,6 +114,37 @@ def kv_store(k, v, kcache, vcache, layer, pos0, n_kv_heads, head_dim, max_pos, T
     k, v = _h(k), _h(v)
     lib().orc_kv_store(_p(k), _p(v), _p(kcache), _p(vcache), layer, pos0, n_kv_heads,
                        head_dim, max_pos, T)
+
+
+def rmsnorm1p(x, w, *, n=256, rows, pitch, T, eps=1e-6):
+    """kernels.cu:241-272 over [T][rows] rows `pitch` halves apart; returns a new
+    float16 array shaped like x (the elements past n of each pitch copied)."""
+    x = _h(x)
+    y = x.copy()
+    lib().orc_rmsnorm1p(_p(x), _p(_f(w)), _p(y), n, rows, pitch, T, eps)
+    return y
+
+
+def rope_partial(q, k, *, n_q_heads, n_kv_heads, rope_dim=64, q_pitch, k_pitch, pos0, T,
+                 theta=1e7):
+    """kernels.cu:422-455; returns new (q, k) float16 arrays."""
+    q, k = _h(q).copy(), _h(k).copy()
+    lib().orc_rope_partial(_p(q), _p(k), n_q_heads, n_kv_heads, rope_dim, q_pitch, k_pitch,
+                           pos0, T, float(theta))
+    return q, k
+
+
+def attn_prep(qg, k, v, wq, wk, kcache, vcache, *, pos0, T, n_q_heads=24, n_kv_heads=4,
+              head_dim=256, q_pitch=512, layer=0, max_pos, rope_dim=64, theta=1e7, eps=1e-6):
+    """The sequence runtime.py:2797-2815 launches: rmsnorm1p of q (inside qg)
+    and of k, rope_partial of both, kv_store of the roped k and v. Returns
+    (qg, k) as new arrays; kcache / vcache (float16) are updated in place."""
+    qn = rmsnorm1p(qg, wq, n=head_dim, rows=n_q_heads, pitch=q_pitch, T=T, eps=eps)
+    kn = rmsnorm1p(k, wk, n=head_dim, rows=n_kv_heads, pitch=head_dim, T=T, eps=eps)
+    qr, kr = rope_partial(qn, kn, n_q_heads=n_q_heads, n_kv_heads=n_kv_heads, rope_dim=rope_dim,
+                          q_pitch=q_pitch, k_pitch=head_dim, pos0=pos0, T=T, theta=theta)
+    kv_store(kr, v, kcache, vcache, layer, pos0, n_kv_heads, head_dim, max_pos, T)
+    return qr, kr
 
 
 def attention_split(q, kcache, vcache, layer, n_q_heads, n_kv_heads, head_dim, q_pitch,
