@@ -250,6 +250,31 @@ def bench_attn_prep(torch, fl, T, iters=50):
             "hbm_frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 3)}
 
 
+def bench_gdn_out_norm(torch, fl, T, iters=50):
+    """The GDN output RMSNormGated over T tokens x 48 v heads (HBM: o and z
+    read, y written)."""
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(T + 1)
+    nbytes = 3 * T * 48 * 128 * 2 + 128 * 4
+    n_sets = min(64, max(1, -(-600_000_000 // nbytes)))
+    sets = [(torch.randn((T, 48, 128), generator=g, device=dev).half(),
+             torch.randn((T, 48, 128), generator=g, device=dev).half()) for _ in range(n_sets)]
+    w = 1 + torch.randn(128, generator=g, device=dev) * 0.1
+    y = torch.empty((T, 48, 128), dtype=torch.float16, device=dev)
+
+    def call(i):
+        o, z = sets[i % n_sets]
+        fl.ops.rmsnorm_gated(o, z, w, y)
+
+    gr = graph_of(torch, call, iters)
+    time_graph(torch, gr)
+    ms = time_graph(torch, gr, reps=3)
+    us = ms * 1e3 / iters
+    return {"config": f"gdn_out_norm_T{T}", "us": round(us, 2),
+            "GBs": round(nbytes / (us * 1e-6) / 1e9, 1),
+            "hbm_frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 3)}
+
+
 # ---------------------------------------------------------------------------
 # config 4: chunked GDN prefill
 # ---------------------------------------------------------------------------
@@ -385,6 +410,8 @@ EXTRA_CONFIGS = {
     "gdn_chunked_L8192": (bench_chunked, {}),
     "attn_prep_T1": (bench_attn_prep, {"T": 1}),
     "attn_prep_T8192": (bench_attn_prep, {"T": 8192, "iters": 20}),
+    "gdn_out_norm_T4": (bench_gdn_out_norm, {"T": 4}),
+    "gdn_out_norm_T8192": (bench_gdn_out_norm, {"T": 8192, "iters": 20}),
 }
 
 

@@ -444,6 +444,45 @@ gdn_decode_kernel(const f16* __restrict__ x, int x_stride, int conv_fused,
     store_row16_nt(Srow, reg);
 }
 
+// The GDN output norm, RMSNormGated (kernels.cu:321-358, launched at
+// runtime.py:3063-3065 / 3109-3111): y = f16((o * rsqrt(mean(o^2) + eps) * w) *
+// silu(z)) -- plain gamma w (not 1 + w), mean-space eps, the norm over o alone
+// with the gate applied after it, one 128-long w for every v head. A wave a
+// row of 128: lane l holds o[2l], o[2l + 1] (one 4-byte load), so the
+// reference's warp w' (elements 32 w'..32 w' + 31) is lanes 16 w'..16 w' + 15
+// and its __shfl_down tree over offsets 16, 8, 4, 2, 1 is lane exchanges at
+// distance 8, 4, 2, 1 then the in-lane pair; the 4 warp sums combine as
+// block_reduce_sum does, (r0 + r2) + (r1 + r3).
+__global__ void __launch_bounds__(GR_THREADS)
+rmsnorm_gated_kernel(const f16* __restrict__ o, const f16* __restrict__ z,
+                     const float* __restrict__ w, f16* __restrict__ y, int rows, int pitch,
+                     int n_rows, float eps) {
+    const int lane = threadIdx.x & 63;
+    const int rid = blockIdx.x * (GR_THREADS / 64) + (threadIdx.x >> 6);
+    if (rid >= n_rows) return;   // whole wavefronts; no workgroup barrier
+    const int t = rid / rows, r = rid - t * rows;
+    const size_t base = ((size_t)t * rows + r) * pitch + 2 * lane;
+    typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+    const f16x2 ov = *(const f16x2*)(o + base);
+    const f16x2 zv = *(const f16x2*)(z + base);
+    const float x0 = (float)ov[0], x1 = (float)ov[1];
+    float s0 = fmaf(x0, x0, 0.f), s1 = fmaf(x1, x1, 0.f);
+#pragma unroll
+    for (int d = 8; d > 0; d >>= 1) {
+        s0 += lane_xor(s0, d);
+        s1 += lane_xor(s1, d);
+    }
+    const float ws = s0 + s1;   // lane 16 w': warp w''s total
+    auto at = [](float v, int src) {
+        return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), src));
+    };
+    const float ss = (at(ws, 0) + at(ws, 32)) + (at(ws, 16) + at(ws, 48));
+    const float inv = 1.f / sqrtf(ss / (float)GR_K + eps);
+    const f16x2 out = {f16_sat(x0 * inv * w[2 * lane] * silu_f((float)zv[0])),
+                       f16_sat(x1 * inv * w[2 * lane + 1] * silu_f((float)zv[1]))};
+    *(f16x2*)(y + base) = out;
+}
+
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 }  // namespace
@@ -554,6 +593,23 @@ int fl_gdn_decode(const void* x, int x_stride, int conv_fused, const void* conv_
                        y_stride, ck_step, T, n_kheads, n_vheads, V, out_scale, l2eps,
                        n_vheads / n_kheads);
     return fl::check_launch("gdn_decode");
+}
+
+
+int fl_rmsnorm_gated(const void* o, const void* z, const float* w, void* y, int n, int rows,
+                     int pitch, int T, float eps, fl_stream_t stream) {
+    FL_REQUIRE(o && z && w && y, "null pointer");
+    FL_REQUIRE(n == GR_K, "n must be 128 (the GDN v head dim)");
+    FL_REQUIRE(rows >= 1 && T >= 1 && pitch >= n && eps >= 0.f, "rows, T >= 1, pitch >= n");
+    FL_REQUIRE(pitch % 2 == 0 && ((uintptr_t)o & 3u) == 0 && ((uintptr_t)z & 3u) == 0 &&
+                   ((uintptr_t)y & 3u) == 0 && ((uintptr_t)w & 7u) == 0,
+               "pitch % 2, aligned o, z, y, w");
+    const long long n_rows = (long long)rows * T;
+    const int waves = GR_THREADS / 64;
+    hipLaunchKernelGGL(rmsnorm_gated_kernel, dim3((unsigned)((n_rows + waves - 1) / waves)),
+                       dim3(GR_THREADS), 0, (hipStream_t)stream, (const f16*)o, (const f16*)z, w,
+                       (f16*)y, rows, pitch, (int)n_rows, eps);
+    return fl::check_launch("rmsnorm_gated");
 }
 
 }  // extern "C"

@@ -23,6 +23,7 @@ CONV_WIDTH = 4          #                                 runtime.py:91
 QKV_ROWS = 10240        # q(2048) | k(2048) | v(6144)      runtime.py:92-94
 Q_SCALE = GDN_K ** -0.5                                 # runtime.py:101
 L2_EPS = 1e-6           #                                 runtime.py:116
+GDN_NORM_EPS = 1e-6     # GDN output RMSNormGated          runtime.py:113
 
 # Decode / verify split policy on MI355X. A token's split count is
 # clamp(seqlen / SPLIT_ROWS, 1, SPLIT_MAX) (the reference's per-token rule,

@@ -21,9 +21,9 @@ import ctypes
 import torch
 
 from . import _lib
-from .geometry import (ATTN_SCALE, GATE_OFF, GDN_CHUNK, GDN_GROUP, GDN_K, GDN_K_HEADS, GDN_V,
-                       GDN_V_HEADS, HEAD_DIM, L2_EPS, N_HEADS, N_KV, NORM_EPS, Q_PITCH, Q_SCALE,
-                       QKV_ROWS, ROPE_DIM, ROPE_THETA, SPLIT_MAX, SPLIT_ROWS)
+from .geometry import (ATTN_SCALE, GATE_OFF, GDN_CHUNK, GDN_GROUP, GDN_K, GDN_K_HEADS,
+                       GDN_NORM_EPS, GDN_V, GDN_V_HEADS, HEAD_DIM, L2_EPS, N_HEADS, N_KV, NORM_EPS,
+                       Q_PITCH, Q_SCALE, QKV_ROWS, ROPE_DIM, ROPE_THETA, SPLIT_MAX, SPLIT_ROWS)
 
 F16, F32 = torch.float16, torch.float32
 
@@ -254,6 +254,20 @@ def l2norm_scaled(x, y, *, n: int = GDN_K, rows: int, pitch: int = GDN_K, eps: f
     span = (T * rows - 1) * pitch + n
     _lib.call("fl_l2norm_scaled", _ptr(x, F16, "x", span), _ptr(y, F16, "y", span), n, rows,
               pitch, float(eps), float(scale), T, _stream())
+
+
+def rmsnorm_gated(o, z, w, y=None, *, T: int | None = None, rows: int = GDN_V_HEADS,
+                  n: int = GDN_V, pitch: int = GDN_V, eps: float = GDN_NORM_EPS):
+    """kernels.cu:335-358 (runtime.py:3063-3065): the GDN output norm
+    y = f16((o / rms(o) * w) * silu(z)) over [T, rows, pitch] fp16 rows, w [n]
+    fp32 (plain gamma). Returns y (new unless given)."""
+    T = o.shape[0] if T is None else T
+    span = T * rows * pitch
+    y = torch.empty_like(o) if y is None else y
+    _lib.call("fl_rmsnorm_gated", _ptr(o, F16, "o", span), _ptr(z, F16, "z", span),
+              _ptr(w, F32, "w", n), _ptr(y, F16, "y", span), n, rows, pitch, T, float(eps),
+              _stream())
+    return y
 
 
 def gdn_scalars(a, b, A_log, dt_bias, beta, decay, *, T: int, n_heads: int = GDN_V_HEADS,

@@ -217,6 +217,16 @@ int fl_gdn_decode(const void* x, int x_stride, int conv_fused, const void* conv_
                   int n_vheads, int K, int V, float out_scale, float l2eps,
                   fl_stream_t stream);
 
+/* ---- GDN output norm ----------------------------------------------------------
+ * rmsnorm_gated: y = f16((o * rsqrt(sum(o^2) / n + eps) * w) * silu(z)) over
+ * rows [T][rows] of `pitch` halves (o, z, y alike), w [n] f32 shared by every
+ * row -- plain gamma, the norm over o before the gate. silu's exp is the
+ * deterministic one the GDN kernels use. Replaces kernels.cu:335-358
+ * rmsnorm_gated, launched at runtime.py:3063-3065 and 3109-3111.
+ * Supported: n == 128. */
+int fl_rmsnorm_gated(const void* o, const void* z, const float* w, void* y, int n, int rows,
+                     int pitch, int T, float eps, fl_stream_t stream);
+
 /* ---- GDN chunked prefill --------------------------------------------------
  * Chunked (WY / UT transform) GDN prefill: the same recurrence as
  * fl_gdn_scan over T tokens in chunks of `chunk` tokens, fp32 state carried

@@ -205,6 +205,32 @@ ORC_API void orc_rope_partial(uint16_t* q, uint16_t* k, int n_q_heads, int n_kv_
     }
 }
 
+/* rmsnorm_gated (kernels.cu:321-358): y = f16_sat((o * inv * w) * silu(z)),
+ * inv = rsqrt(ss / n + eps), ss by block_reduce_sum over the reference's
+ * 128-thread block (4 warps of the __shfl_down tree, then warp 0 over the 4
+ * totals); plain gamma; silu with the deterministic exp (see orc_det_expf). */
+ORC_API void orc_rmsnorm_gated(const uint16_t* o, const uint16_t* z, const float* w, uint16_t* y,
+                               int n, int rows, int pitch, int T, float eps) {
+    for (int t = 0; t < T; t++)
+        for (int r = 0; r < rows; r++) {
+            const size_t base = ((size_t)t * rows + r) * pitch;
+            float warp[32] = {0};
+            for (int wv = 0; wv < n / 32; wv++) {
+                float a[32];
+                for (int i = 0; i < 32; i++) {
+                    const float v = orc_h2f(o[base + 32 * wv + i]);
+                    a[i] = fmaf(v, v, 0.f);
+                }
+                warp[wv] = tree_down(a, 32);
+            }
+            const float ss = tree_down(warp, 32);
+            const float inv = 1.f / sqrtf(ss / (float)n + eps);
+            for (int i = 0; i < n; i++)
+                y[base + i] = orc_f16_sat(orc_h2f(o[base + i]) * inv * w[i] *
+                                          silu_f(orc_h2f(z[base + i])));
+        }
+}
+
 ORC_API void orc_kv_store(const uint16_t* k, const uint16_t* v, uint16_t* kcache,
                           uint16_t* vcache, int layer, int pos0, int n_kv_heads,
                           int head_dim, int max_pos, int T) {

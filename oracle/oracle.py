@@ -53,6 +53,7 @@ def lib() -> ctypes.CDLL:
             "orc_kv_store": [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I],
             "orc_rmsnorm1p": [_P, _P, _P, _I, _I, _I, _I, _F],
             "orc_rope_partial": [_P, _P, _I, _I, _I, _I, _I, _I, _I, _D],
+            "orc_rmsnorm_gated": [_P, _P, _P, _P, _I, _I, _I, _I, _F],
             "orc_attention_split": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _F, _I, _I, _I],
             "orc_attention_merge": [_P, _P, _P, _P, _I, _I, _I, _I, _I],
             "orc_attn_gate": [_P, _P, _I, _I, _I, _I, _I, _I],
@@ -241,6 +242,14 @@ def l2norm_scaled(x, *, n, rows, pitch, eps, scale, T):
     x = _h(x)
     y = np.zeros_like(x)
     lib().orc_l2norm_scaled(_p(x), _p(y), n, rows, pitch, float(eps), float(scale), T)
+    return y
+
+
+def rmsnorm_gated(o, z, w, *, n=128, rows=48, pitch=128, T, eps=1e-6):
+    """kernels.cu:335-358 over [T][rows] rows of `pitch` halves; returns y."""
+    o, z = _h(o), _h(z)
+    y = np.zeros_like(o)
+    lib().orc_rmsnorm_gated(_p(o), _p(z), _p(_f(w)), _p(y), n, rows, pitch, T, eps)
     return y
 
 

@@ -230,3 +230,20 @@ def test_chunked_vs_recurrence(fl, dev, orc, T):
     assert rel_err(Sh, S_r) <= STATE_RTOL
     err, ok = close(y.cpu().numpy(), y_r, 2e-3, 1e-2)
     assert ok, f"T={T}: max|dy| {err}"
+
+
+@pytest.mark.parametrize("T", [1, 4, 1000])
+def test_rmsnorm_gated_vs_oracle(fl, dev, orc, rng, T):
+    """The GDN output norm through the C ABI: same operations and order as the
+    oracle (deterministic exp in silu), so bit for bit; the bar is 1 fp16 ulp."""
+    o = (rng.standard_normal((T, 48, 128)) * rng.uniform(0.01, 3)).astype(np.float16)
+    z = (rng.standard_normal((T, 48, 128)) * 2).astype(np.float16)
+    w = (1 + rng.standard_normal(128) * 0.2).astype(np.float32)
+    want = orc.rmsnorm_gated(o, z, w, T=T)
+    y = fl.ops.rmsnorm_gated(torch.from_numpy(o).to(dev), torch.from_numpy(z).to(dev),
+                             torch.from_numpy(w).to(dev))
+    torch.cuda.synchronize()
+    got = y.cpu().numpy()
+    d = np.abs(got.view(np.int16).astype(np.int32) - want.view(np.int16).astype(np.int32))
+    print(f"rmsnorm_gated T={T}: max {d.max()} ulp, {(d > 0).sum()} values differ")
+    assert d.max() <= 1

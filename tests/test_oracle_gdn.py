@@ -20,7 +20,7 @@ The reference ships no vectors; its kernel comments state what its
 import numpy as np
 import pytest
 
-from conftest import close
+from conftest import close, f16
 
 QS = 128 ** -0.5
 
@@ -280,3 +280,35 @@ def test_chunked_beta_zero_is_decay(orc, rng):
                     qk_stride=256, v_stride=768, out_scale=QS, group=3, chunk=64)
     want = S0.astype(np.float64) * np.prod(decay.astype(np.float64), axis=0)[:, None, None]
     assert np.abs(S - want).max() <= 1e-6 * np.abs(S0).max()
+
+
+# ---------------------------------------------------------------------------
+# rmsnorm_gated (kernels.cu:321-358): plain gamma, norm before the gate
+# ---------------------------------------------------------------------------
+
+def test_rmsnorm_gated_closed_form(orc, rng):
+    T, rows = 3, 48
+    o = f16(rng.standard_normal((T, rows, 128)) * 0.3)
+    z = f16(rng.standard_normal((T, rows, 128)) * 2)
+    w = (1 + rng.standard_normal(128) * 0.2).astype(np.float32)
+    y = orc.rmsnorm_gated(o, z, w, T=T).astype(np.float64)
+    of, zf = o.astype(np.float64), z.astype(np.float64)
+    silu = zf / (1 + np.exp(-zf))
+    want = of / np.sqrt((of ** 2).mean(-1, keepdims=True) + 1e-6) * w * silu
+    assert np.abs(y - want).max() <= 2e-3 * np.abs(want).max()
+    # (1 + w) instead of w, or the norm over o * silu(z), are far off
+    wrong_w = of / np.sqrt((of ** 2).mean(-1, keepdims=True) + 1e-6) * (1 + w) * silu
+    g = of * silu
+    wrong_gate = g / np.sqrt((g ** 2).mean(-1, keepdims=True) + 1e-6) * w
+    for wrong in (wrong_w, wrong_gate):
+        assert np.abs(wrong - want).max() > 0.1 * np.abs(want).max()
+
+
+def test_rmsnorm_gated_zero_gate_and_zero_row(orc):
+    o = np.ones((1, 2, 128), np.float16)
+    z = np.zeros((1, 2, 128), np.float16)          # silu(0) = 0
+    y = orc.rmsnorm_gated(o, z, np.ones(128, np.float32), rows=2, T=1)
+    assert not y.any()
+    o0 = np.zeros((1, 2, 128), np.float16)          # zero row: no NaN
+    y0 = orc.rmsnorm_gated(o0, np.ones((1, 2, 128), np.float16), np.ones(128, np.float32), rows=2, T=1)
+    assert np.isfinite(y0.astype(np.float32)).all() and not y0.any()
