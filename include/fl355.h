@@ -111,7 +111,7 @@ int fl_attention_merge(const float* pacc, const float* pm, const float* pd, void
                        int n_q_heads, int head_dim, int z_pitch, int T, int split,
                        const void* gate, int g_pitch, int g_off, fl_stream_t stream);
 
-/* a3 alone: z = f16_sat(z * sigmoid(g)), kernels.cu:1585-1600. */
+/* The output gate alone: z = f16_sat(z * sigmoid(g)), kernels.cu:1585-1600. */
 int fl_attn_gate(void* z, const void* g, int n_heads, int head_dim, int z_pitch,
                  int g_pitch, int g_off, int T, fl_stream_t stream);
 
@@ -139,7 +139,7 @@ int fl_attn_decode(const void* qg, int q_pitch, const void* const* kcache,
  * [max_pos][n_kv_heads][head_dim] f16: query (t, h) attends rows
  * [0, pos0 + t] of kv head h / G, z [T][n_q_heads][z_pitch] f16.
  * k_new / v_new [T][n_kv_heads][head_dim] f16, when not NULL, are first
- * stored into cache rows pos0.. (the fused kv_store, a4).
+ * stored into cache rows pos0.. (the fused kv_store).
  * Replaces kernels.cu:2768-2807 attention_prefill_fh (+ merge_fh) launched
  * by runtime.py:2943-2959 (and kv_store at runtime.py:2813-2815).
  * `scale` multiplies q.k (the reference passes sl2 = scale * log2 e).
@@ -158,7 +158,7 @@ int fl_attention_prefill(const void* q, int q_pitch, const void* k_new, const vo
 int fl_conv1d_causal(const void* x, const void* w, const void* st_in, void* y, void* st_out,
                      int dim, int T, int pos0, int row_stride, int width, fl_stream_t stream);
 
-/* a9 conv1d_causal_rows: T <= 3 verify rows, the state after row t into st_t
+/* conv1d_causal_rows: T <= 3 verify rows, the state after row t into st_t
  * (st0 may be st_in). Replaces kernels.cu:1686-1714, runtime.py:3021-3026. */
 int fl_conv1d_causal_rows(const void* x, const void* w, const void* st_in, void* y, void* st0,
                           void* st1, void* st2, int dim, int T, int pos0, int row_stride,
@@ -196,10 +196,10 @@ int fl_gdn_scan(const void* q, const void* k, const void* v, const float* beta,
 
 /* ---- GDN fused decode / verify --------------------------------------------
  * The fused GDN decode / verify step of B sequences (T <= 3): the gates
- * (a11), the L2 norm of q and k (a10, eps l2eps, fp16-rounded, scale 1),
- * and the delta rule (a12) with checkpoints, in one launch. With
+ * (gdn_scalars), the L2 norm of q and k (l2norm_scaled, eps l2eps, fp16-rounded, scale 1),
+ * and the delta rule (gdn_scan_rows) with checkpoints, in one launch. With
  * conv_fused = 1 (T == 1 only) x is the RAW q|k|v projection row and the
- * conv (a8, width 4) runs in the kernel from cst_in[b] into cst_out[b]
+ * conv (conv1d_causal, width 4) runs in the kernel from cst_in[b] into cst_out[b]
  * (distinct buffers); with conv_fused = 0 x is the conv output.
  * x [B][T][x_stride] f16 with q at channel 0, k at n_kheads*K, v at
  * 2*n_kheads*K; conv_w [x channels][4] f16; a, b [B][T][ab_stride] f32;
@@ -231,7 +231,7 @@ int fl_rmsnorm_gated(const void* o, const void* z, const float* w, void* y, int 
  * Chunked (WY / UT transform) GDN prefill: the same recurrence as
  * fl_gdn_scan over T tokens in chunks of `chunk` tokens, fp32 state carried
  * between chunks; S in place, y as fl_gdn_scan. NOT in the reference (the
- * reference runs a12 sequentially and names the chunked scan as undone,
+ * reference runs gdn_scan sequentially and names the chunked scan as undone,
  * kernels.cu:1788-1791); it replaces that call (runtime.py:3094-3100) for
  * prefill. work: caller scratch of fl_gdn_chunked_work_bytes(...) bytes (the
  * per-chunk W, U and decayed Q K^T of the WY form). chunk == 64,

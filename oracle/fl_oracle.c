@@ -142,7 +142,7 @@ static float tree_xor(const float* in, int n) {
 }
 
 /* ======================================================================== */
-/* a4 kv_store -- kernels.cu:465-484                                         */
+/* kv_store -- kernels.cu:465-484                                            */
 /* ======================================================================== */
 /* ======================================================================== */
 /* attention prep: rmsnorm1p (kernels.cu:241-272), rope_partial (397-455)    */
@@ -247,7 +247,7 @@ ORC_API void orc_kv_store(const uint16_t* k, const uint16_t* v, uint16_t* kcache
 }
 
 /* ======================================================================== */
-/* a1 attention_split / attention_split_gqa -- kernels.cu:522-680, 682-835   */
+/* attention_split / attention_split_gqa -- kernels.cu:522-680, 682-835      */
 /* ======================================================================== */
 /* The split a token asks for depends on its own seqlen only
  * (kernels.cu:535-544, 702-707): St = clamp(seqlen / split_rows, 1, split),
@@ -337,7 +337,7 @@ ORC_API void orc_attention_split(const uint16_t* q, const uint16_t* kcache,
 }
 
 /* ======================================================================== */
-/* a2 attention_merge -- kernels.cu:1398-1424 (+ a3 attn_gate 1585-1600)     */
+/* attention_merge -- kernels.cu:1398-1424 (+ attn_gate 1585-1600)          */
 /* ======================================================================== */
 ORC_API void orc_attention_merge(const float* pacc, const float* pm, const float* pd,
                                  uint16_t* z, int n_q_heads, int head_dim, int z_pitch,
@@ -373,7 +373,7 @@ ORC_API void orc_attn_gate(uint16_t* z, const uint16_t* g, int n_heads, int head
 }
 
 /* ======================================================================== */
-/* a5/a6 attention_prefill_fh (+ attention_merge_fh) -- kernels.cu:2461-2807 */
+/* attention_prefill_fh (+ attention_merge_fh) -- kernels.cu:2461-2807      */
 /* ======================================================================== */
 /* Causal GQA prefill: query (t, head) sees cache rows [0, pos0 + t]. Per
  * 64-row KV tile: fp32 scores (q . k) * sl2 with sl2 = scale * log2(e), the
@@ -531,7 +531,7 @@ ORC_API void orc_attention_exact_f64(const uint16_t* q, const uint16_t* kcache,
 }
 
 /* ======================================================================== */
-/* a8 conv1d_causal -- kernels.cu:1634-1679                                  */
+/* conv1d_causal -- kernels.cu:1634-1679                                     */
 /* ======================================================================== */
 /* E = [state(width-1) | x(T)], state read as ZERO when pos0 == 0;
  * y[t][d] = f16_sat(silu(sum_j w[d][j] * E[t + j])) (tap 0 oldest); the new
@@ -565,7 +565,7 @@ ORC_API void orc_conv1d_causal(const uint16_t* x, const uint16_t* w, const uint1
     }
 }
 
-/* a9 conv1d_causal_rows -- kernels.cu:1686-1714: row t is the T = 1 call at
+/* conv1d_causal_rows -- kernels.cu:1686-1714: row t is the T = 1 call at
  * pos0 + t from the state row t - 1 left, that state stored to st_t. */
 ORC_API void orc_conv1d_causal_rows(const uint16_t* x, const uint16_t* w, const uint16_t* st_in,
                                     uint16_t* y, uint16_t* st0, uint16_t* st1, uint16_t* st2,
@@ -592,7 +592,7 @@ ORC_API void orc_conv1d_causal_rows(const uint16_t* x, const uint16_t* w, const 
 }
 
 /* ======================================================================== */
-/* a10 l2norm_scaled -- kernels.cu:373-391                                   */
+/* l2norm_scaled -- kernels.cu:373-391                                      */
 /* ======================================================================== */
 /* y = f16_sat((x / sqrt(sum x^2 + eps)) * scale), SUM-space eps. The sum is
  * block_reduce_sum's order for the 128-thread launch (runtime.py:3070): per
@@ -618,7 +618,7 @@ ORC_API void orc_l2norm_scaled(const uint16_t* x, uint16_t* y, int n, int rows, 
 }
 
 /* ======================================================================== */
-/* a11 gdn_scalars -- kernels.cu:1732-1748                                   */
+/* gdn_scalars -- kernels.cu:1732-1748                                      */
 /* ======================================================================== */
 /* beta = sigmoid(b); decay = exp(-exp(A_log[h]) * softplus(a + dt_bias[h])),
  * softplus = log1p(exp(x)) for x <= 20, x above (threshold 20 exactly). */
@@ -635,7 +635,7 @@ ORC_API void orc_gdn_scalars(const float* a, const float* b, const float* A_log,
 }
 
 /* ======================================================================== */
-/* a12 gdn_scan / gdn_scan_rows -- kernels.cu:1794-1901, 2831-2914           */
+/* gdn_scan / gdn_scan_rows -- kernels.cu:1794-1901, 2831-2914              */
 /* ======================================================================== */
 /* Per token t, v-head hv (k/q head hv / group), S [V][K] fp32 in place:
  *   S *= decay_t; m = S.k_t; delta = beta_t (v_t - m); S += delta k_t^T;
@@ -714,7 +714,7 @@ ORC_API int orc_gdn_scan(const uint16_t* q, const uint16_t* k, const uint16_t* v
 }
 
 /* ======================================================================== */
-/* a13 gdn_scan_rows_f (+ gdn_conv1) -- kernels.cu:2916-3070                 */
+/* gdn_scan_rows_f (+ gdn_conv1) -- kernels.cu:2916-3070                    */
 /* ======================================================================== */
 /* The decode / verify step (T <= 3) with its producers folded in: the gates
  * of gdn_scalars, the q/k L2 norm (k by threads 0..127, q by 128..255: per
@@ -803,9 +803,9 @@ ORC_API int orc_gdn_decode(const uint16_t* q, const uint16_t* k, const uint16_t*
 }
 
 /* ======================================================================== */
-/* a14 chunked WY/UT scan -- NOT in the reference (kernels.cu:1788-1791     */
+/* chunked WY/UT scan -- NOT in the reference (kernels.cu:1788-1791         */
 /* names it as the undone prefill optimisation). Restated here in double    */
-/* from the recurrence a12 so the GPU chunked kernel has a second checker;   */
+/* from the recurrence gdn_scan so the GPU chunked kernel has a second checker; */
 /* the parity target stays orc_gdn_scan.                                     */
 /* ======================================================================== */
 /* Per chunk of C tokens with state S0 [V][K]: log-decay prefix sums
