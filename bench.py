@@ -144,29 +144,52 @@ def bench_gdn_decode(torch, fl, steps, warmup):
 # config 2: GQA decode + MTP verify; config 0
 # ---------------------------------------------------------------------------
 
-def bench_attn_decode(torch, fl, Lmax, Bq=4, T=3, iters=20, seed=0):
+def bench_attn_decode(torch, fl, Lmax, Bq=4, T=3, iters=20, seed=0, kv8=False, per_seq=False):
+    """kv8: int8 caches (fl_attn_decode_q8); per_seq: the reference's int8
+    launch shape instead -- attention_dec_q8 + the gated dec merge per sequence
+    (runtime.py:2907-2920, tmin 1 / smax 28)."""
     dev = torch.device("cuda:0")
     import numpy as np
 
     rng = np.random.default_rng(seed + Lmax)
     lens = [int(v) for v in rng.integers(int(np.ceil(0.9 * Lmax)), Lmax + 1, size=Bq)]
     g = torch.Generator(device=dev).manual_seed(seed)
-    kv_bytes = sum(lens) * 4 * 256 * 2 * 2
+    row = 4 * (256 + 16) if kv8 else 4 * 256 * 2          # bytes a position, K or V
+    kv_bytes = sum(lens) * row * 2
     n_sets = max(1, -(-600_000_000 // kv_bytes))     # rotate > 256 MB MALL
     sets = []
     for _ in range(n_sets):
         ks = [torch.randn((L, 4, 256), generator=g, device=dev).half() for L in lens]
         vs = [torch.randn((L, 4, 256), generator=g, device=dev).half() for L in lens]
+        if kv8:
+            k8 = [fl.ops.kv8_cache(L) for L in lens]
+            v8 = [fl.ops.kv8_cache(L) for L in lens]
+            for b, L in enumerate(lens):
+                fl.ops.kv_store_q8(ks[b], vs[b], k8[b], v8[b], pos0=0, max_pos=L)
+            torch.cuda.synchronize()
+            ks, vs = k8, v8
         sets.append((ks, vs))
     qg = torch.randn((Bq, T, 24, 512), generator=g, device=dev).half()
     qg[..., :256] *= 1 / 16
     z = torch.empty((Bq, T, 24, 256), dtype=torch.float16, device=dev)
     work = torch.empty(fl.ops.attn_decode_work_bytes(Bq, T), dtype=torch.uint8, device=dev)
     pos0 = [L - T for L in lens]
+    smax = fl.geometry.DEC_SMAX
+    pacc = torch.empty((T, 24, smax, 256), device=dev)
+    pm = torch.empty((T, 24, smax), device=dev)
+    pd = torch.empty_like(pm)
 
     def call(i):
         ks, vs = sets[i % n_sets]
-        fl.ops.attn_decode(qg, ks, vs, pos0, z=z, work=work)
+        if per_seq:
+            for b in range(Bq):
+                fl.ops.attention_dec_q8(qg[b], ks[b], vs[b], pacc, pm, pd, pos0=pos0[b],
+                                        max_pos=lens[b], T=T)
+                fl.ops.attention_dec_merge(pacc, pm, pd, z[b], pos0=pos0[b], T=T, gate=qg[b])
+        elif kv8:
+            fl.ops.attn_decode_q8(qg, ks, vs, pos0, lens, z=z, work=work)
+        else:
+            fl.ops.attn_decode(qg, ks, vs, pos0, z=z, work=work)
 
     gr = graph_of(torch, call, iters)
     time_graph(torch, gr)
@@ -174,7 +197,8 @@ def bench_attn_decode(torch, fl, Lmax, Bq=4, T=3, iters=20, seed=0):
     us = ms * 1e3 / iters
     nbytes = kv_bytes + Bq * T * 24 * 512 * 2 + Bq * T * 24 * 256 * 2
     flops = sum(4 * T * 24 * 256 * L for L in lens)
-    return {"config": f"decode_verify_B{Bq}_T{T}_L{Lmax}", "us_per_step": round(us, 2),
+    name = ("decode8_perseq" if per_seq else "decode8_verify" if kv8 else "decode_verify")
+    return {"config": f"{name}_B{Bq}_T{T}_L{Lmax}", "us_per_step": round(us, 2),
             "GBs": round(nbytes / (us * 1e-6) / 1e9, 1),
             "hbm_frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 3),
             "TFLOPs": round(flops / (us * 1e-6) / 1e12, 1), "lens": lens}
@@ -184,18 +208,26 @@ def bench_attn_decode(torch, fl, Lmax, Bq=4, T=3, iters=20, seed=0):
 # config 3: causal prefill attention
 # ---------------------------------------------------------------------------
 
-def bench_prefill(torch, fl, L, iters=3):
+def bench_prefill(torch, fl, L, iters=3, kv8=False):
+    """kv8: over an int8 cache (kv_store_q8 fused in front, as for fp16)."""
     dev = torch.device("cuda:0")
     g = torch.Generator(device=dev).manual_seed(L)
     q = (torch.randn((L, 24, 256), generator=g, device=dev) / 16).half()
     k = torch.randn((L, 4, 256), generator=g, device=dev).half()
     v = torch.randn((L, 4, 256), generator=g, device=dev).half()
-    kc = torch.zeros((L, 4, 256), dtype=torch.float16, device=dev)
-    vc = torch.zeros_like(kc)
+    if kv8:
+        kc, vc = fl.ops.kv8_cache(L), fl.ops.kv8_cache(L)
+    else:
+        kc = torch.zeros((L, 4, 256), dtype=torch.float16, device=dev)
+        vc = torch.zeros_like(kc)
     z = torch.empty((L, 24, 256), dtype=torch.float16, device=dev)
 
     def call(i):
-        fl.ops.attention_prefill(q, kc, vc, pos0=0, scale=1.0, z=z, k_new=k, v_new=v)
+        if kv8:
+            fl.ops.attention_prefill_q8(q, kc, vc, pos0=0, max_pos=L, scale=1.0, z=z, k_new=k,
+                                        v_new=v)
+        else:
+            fl.ops.attention_prefill(q, kc, vc, pos0=0, scale=1.0, z=z, k_new=k, v_new=v)
 
     gr = graph_of(torch, call, iters)
     time_graph(torch, gr)
@@ -203,7 +235,8 @@ def bench_prefill(torch, fl, L, iters=3):
     us = ms * 1e3 / iters
     flops = 4 * 24 * 256 * L * (L + 1) / 2
     tf = flops / (us * 1e-6) / 1e12
-    return {"config": f"prefill_L{L}", "us": round(us, 1), "tok_s": round(L / (us * 1e-6)),
+    return {"config": f"prefill{'8' if kv8 else ''}_L{L}", "us": round(us, 1),
+            "tok_s": round(L / (us * 1e-6)),
             "TFLOPs": round(tf, 1), "mfma_frac": round(tf / MFMA_F16_PEAK_TFLOPS, 3)}
 
 
@@ -407,6 +440,13 @@ EXTRA_CONFIGS = {
     "prefill_L2048": (bench_prefill, {"L": 2048}),
     "prefill_L8192": (bench_prefill, {"L": 8192}),
     "prefill_L32768": (bench_prefill, {"L": 32768}),
+    "decode8_verify_B4_T3_L8192": (bench_attn_decode, {"Lmax": 8192, "kv8": True}),
+    "decode8_verify_B4_T3_L32768": (bench_attn_decode, {"Lmax": 32768, "kv8": True}),
+    "decode8_verify_B4_T3_L102400": (bench_attn_decode, {"Lmax": 102400, "kv8": True}),
+    "decode8_perseq_B4_T3_L102400": (bench_attn_decode, {"Lmax": 102400, "kv8": True,
+                                                         "per_seq": True}),
+    "prefill8_L8192": (bench_prefill, {"L": 8192, "kv8": True}),
+    "prefill8_L32768": (bench_prefill, {"L": 32768, "kv8": True}),
     "gdn_chunked_L8192": (bench_chunked, {}),
     "attn_prep_T1": (bench_attn_prep, {"T": 1}),
     "attn_prep_T8192": (bench_attn_prep, {"T": 8192, "iters": 20}),
@@ -423,9 +463,9 @@ def main():
     ap.add_argument("--quick", action="store_true", help="primary line only, no extra configs")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", default=None,
-                    help="run one config by name (gdn_decode_B4, decode_verify_B1_T1_L4096, "
-                         "decode_verify_B4_T3_L{8192,32768,102400}, prefill_L{2048,8192,32768}, "
-                         "gdn_chunked_L8192) and print its result, not the contract line")
+                    help="run one config by name (gdn_decode_B4 or a key of EXTRA_CONFIGS: "
+                         + ", ".join(EXTRA_CONFIGS) + ") and print its result, not the "
+                         "contract line")
     ap.add_argument("--counters", default=None,
                     help="comma list of workloads (copy,gdn,prefill8k,decode100k) to launch "
                          "eagerly for rocprofv3 --pmc, then exit without timing")

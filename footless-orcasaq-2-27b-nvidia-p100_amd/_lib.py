@@ -41,6 +41,17 @@ SIGNATURES = {
                             _I, _P, _I, _P, _SZ, _P]),
     "fl_attention_prefill": (_I, [_P, _I, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _I, _P, _I,
                                   _P]),
+    "fl_kv_store_q8": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P]),
+    "fl_attn_prep_q8": (_I, [_P, _I, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _F,
+                             _F, _P]),
+    "fl_attention_split_gqa_q8": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _F,
+                                       _I, _I, _I, _P]),
+    "fl_attention_dec_q8": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _I, _I, _I, _P]),
+    "fl_attention_dec_merge": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P, _I, _I, _P]),
+    "fl_attn_decode_q8": (_I, [_P, _I, _PP, _PP, _IP, _IP, _I, _I, _I, _I, _I, _F, _I, _I, _P,
+                               _I, _I, _P, _I, _P, _SZ, _P]),
+    "fl_attention_prefill_q8": (_I, [_P, _I, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _I, _P,
+                                     _I, _P]),
     "fl_conv1d_causal": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P]),
     "fl_conv1d_causal_rows": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P]),
     "fl_l2norm_scaled": (_I, [_P, _P, _I, _I, _I, _F, _F, _I, _P]),

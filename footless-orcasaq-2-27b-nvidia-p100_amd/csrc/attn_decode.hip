@@ -7,6 +7,12 @@
 //   attention_split_gqa   682-835   split partials (m, d, acc), per-token split
 //   attention_merge       1387-1424 M = max m, z = sum e acc / sum e d, f16_sat
 //   attn_gate             1572-1600 z = f16_sat(z * sigmoid(gate))
+//   kv_store_q8           486-520   the int8 cache format (values, then fp16
+//                                   scales of 32-dim blocks)
+//   attention_split_gqa_q8 910-1047 the split partials over the int8 cache
+//   attention_dec_q8      1049-1335 int8 decode partials, 64-row tiles split
+//                                   by (tmin, smax), pm in log2 units
+//   attention_dec_merge   1336-1385 their merge (+ the gate), exp2
 //
 // Decode kernel design (one workgroup = one (sequence, kv head, split)):
 //   * The query rows of a kv head -- T tokens x G = 6 q heads, token-major,
@@ -27,6 +33,12 @@
 //     contiguous bytes of its row); V is loaded with 128-byte row segments per
 //     8 lanes and transposed into a per-wave LDS slice. The next tile's loads
 //     are issued before the current tile's math.
+//   * Over the int8 cache the same kernel runs on dequantized tiles: a lane
+//     loads its K / V bytes (half the fp16 bytes) and one dword of scales,
+//     and each value becomes fp16(byte * scale) in registers -- the
+//     reference's prefill dequantizes V the same way (kernels.cu:2500-2509);
+//     its decode keeps byte * scale in fp32, so scores and outputs differ
+//     from it by fp16 rounding, far below the int8 format's own error.
 //   * Tiles are 32-row aligned in absolute position and every tile a token's
 //     range does not cover is an exact no-op for that token (masked scores,
 //     p = 0, corr = 1), so a token's partial is the same bits whichever other
@@ -35,6 +47,7 @@
 #include "fl_common.hpp"
 
 #include <limits.h>
+#include <type_traits>
 
 namespace {
 
@@ -51,8 +64,10 @@ constexpr int VT_PITCH = 40;   // halves per d row of the transposed V slice (32
 #endif
 
 struct DecSeqs {
-    const f16* k[FL_MAX_SEQS];
+    const f16* k[FL_MAX_SEQS];    // int8 caches: the values, as bytes
     const f16* v[FL_MAX_SEQS];
+    const f16* ks[FL_MAX_SEQS];   // int8 caches: the scales (unused for fp16)
+    const f16* vs[FL_MAX_SEQS];
     int pos0[FL_MAX_SEQS];
 };
 
@@ -80,6 +95,30 @@ __host__ __device__ __forceinline__ void split_range(int seqlen, int s, int spli
     hi = t1 * DEC_TILE < seqlen ? t1 * DEC_TILE : seqlen;
 }
 
+// The int8 decode's rule (attention_dec_q8, kernels.cu:1107-1118): a token of
+// length len has nkt = ceil(len / 64) tiles of 64 rows, St = min(smax,
+// ceil(nkt / tmin)) splits, split s taking tiles [nkt s / St, nkt (s+1) / St).
+// Splits s >= St are not written (the merge reads the first St).
+__host__ __device__ __forceinline__ int dec_split_count(int len, int tmin, int smax) {
+    const int nkt = (len + 63) / 64;
+    const int st = (nkt + tmin - 1) / tmin;
+    return st > smax ? smax : st;
+}
+
+__host__ __device__ __forceinline__ void dec_split_range(int len, int s, int tmin, int smax,
+                                                         int& lo, int& hi) {
+    const int st = dec_split_count(len, tmin, smax);
+    if (s >= st) {
+        lo = 0;
+        hi = 0;
+        return;
+    }
+    const int nkt = (len + 63) / 64;
+    lo = (int)((long long)nkt * s / st) * 64;
+    const int e = (int)((long long)nkt * (s + 1) / st) * 64;
+    hi = e < len ? e : len;
+}
+
 // ---------------------------------------------------------------------------
 // kv_store: 16-byte copies, one lane per 8 halves of a (token, kv head) row.
 // ---------------------------------------------------------------------------
@@ -94,6 +133,21 @@ __global__ void kv_store_kernel(const uint4* __restrict__ k, const uint4* __rest
     vc[dst] = v[i];
 }
 
+// kv_store_q8: a wavefront a (token, kv head) row, 4 elements a lane.
+__global__ void __launch_bounds__(256)
+kv_store_q8_kernel(const f16* __restrict__ k, const f16* __restrict__ v, signed char* __restrict__ kc,
+                   signed char* __restrict__ vc, f16* __restrict__ ksc, f16* __restrict__ vsc,
+                   int pos0, int T, int n_kv) {
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);   // wave-uniform
+    if (row >= T * n_kv) return;
+    const int lane = threadIdx.x & 63;
+    const int t = row / n_kv, h = row - t * n_kv;
+    const size_t src = (size_t)row * DEC_HD + 4 * lane;
+    const size_t dst = (size_t)(pos0 + t) * n_kv + h;
+    q8_store_row(*(const f16x4*)(k + src), kc + dst * DEC_HD, ksc + dst * 8, lane);
+    q8_store_row(*(const f16x4*)(v + src), vc + dst * DEC_HD, vsc + dst * 8, lane);
+}
+
 // ---------------------------------------------------------------------------
 // split partials
 // ---------------------------------------------------------------------------
@@ -101,6 +155,71 @@ struct DecTileRegs {
     f16x8 k[4];   // K[row ql][64w + 32hh + 8ks + 0..7], ks = 0..3
     f16x8 v[4];   // V[row 4(l&7) + i][64w + 8(l>>3) + 0..7], i = 0..3
 };
+
+// One int8 tile in flight: the same elements as bytes, plus one dword of
+// scales a lane -- lane l < 32: row l's K scales of blocks 2w, 2w + 1 (this
+// wave's dims); lane l >= 32: row l - 32's V scales.
+struct DecTileQ8 {
+    u32x4 k[2];
+    u32x2 v[4];
+    uint32_t sc;
+};
+
+template <bool NT_V>
+__device__ __forceinline__ void dec_load_tile(DecTileQ8& r, const char* __restrict__ kbase,
+                                              const char* __restrict__ vbase,
+                                              const f16* __restrict__ ksb,
+                                              const f16* __restrict__ vsb, size_t row_stride,
+                                              int j, int uhi, int lane, int w) {
+    const int ql = lane & 31, hh = lane >> 5;
+    const int krow = j * DEC_TILE + ql;
+    if (krow < uhi) {
+        const u32x4* src = (const u32x4*)(kbase + (size_t)krow * row_stride + 64 * w + 32 * hh);
+        r.k[0] = src[0];
+        r.k[1] = src[1];
+        const f16* sb = hh ? vsb : ksb;
+        r.sc = *(const uint32_t*)(sb + (size_t)krow * (row_stride / 32) + 2 * w);
+    } else {
+        r.k[0] = r.k[1] = (u32x4)(0u);
+        r.sc = 0;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int vrow = j * DEC_TILE + 4 * (lane & 7) + i;
+        const u32x2* src = (const u32x2*)(vbase + (size_t)vrow * row_stride + 64 * w + 8 * (lane >> 3));
+        if (vrow < uhi)
+            r.v[i] = NT_V ? __builtin_nontemporal_load(src) : *src;
+        else
+            r.v[i] = (u32x2)(0u);
+    }
+}
+
+// The int8 tile as the fp16 tile the MFMAs read: fp16(byte * scale).
+__device__ __forceinline__ DecTileRegs dec_dequant(const DecTileQ8& q, int lane) {
+    const int ql = lane & 31, hh = lane >> 5;
+    DecTileRegs r;
+    const uint32_t kp = (uint32_t)__builtin_amdgcn_ds_bpermute(ql << 2, (int)q.sc);
+    const f16 ksh = __builtin_bit_cast(f16x2, kp)[hh];
+    const f16x2 ks2 = {ksh, ksh};
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+        const u32x4 b = q.k[ks >> 1];
+        const f16x4 lo = q8_deq4((ks & 1) ? b.z : b.x, ks2);
+        const f16x4 hi = q8_deq4((ks & 1) ? b.w : b.y, ks2);
+        r.k[ks] = (f16x8){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t vp =
+            (uint32_t)__builtin_amdgcn_ds_bpermute((32 + 4 * (lane & 7) + i) << 2, (int)q.sc);
+        const f16 vsh = __builtin_bit_cast(f16x2, vp)[hh];
+        const f16x2 vs2 = {vsh, vsh};
+        const f16x4 lo = q8_deq4(q.v[i].x, vs2);
+        const f16x4 hi = q8_deq4(q.v[i].y, vs2);
+        r.v[i] = (f16x8){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    }
+    return r;
+}
 
 template <bool NT_V>
 __device__ __forceinline__ void dec_load_tile(DecTileRegs& r, const f16* __restrict__ kbase,
@@ -127,7 +246,11 @@ __device__ __forceinline__ void dec_load_tile(DecTileRegs& r, const f16* __restr
     }
 }
 
-template <int NBUF, bool NT_V>
+// Q8: the caches are int8 (DecSeqs k / v the values, ks / vs the scales).
+// DEC: attention_dec_q8's split rule and partials -- (split, split_rows) are
+// (smax, tmin), pm in log2 units, no partial written for s >= St; otherwise
+// attention_split_gqa's -- pm in natural-log units, empty partials written.
+template <int NBUF, bool NT_V, bool Q8, bool DEC>
 __global__ void __launch_bounds__(DEC_THREADS)
 attn_decode_split_kernel(const f16* __restrict__ qg, DecSeqs seqs, float* __restrict__ pacc,
                          float* __restrict__ pm, float* __restrict__ pd, int n_q_heads,
@@ -141,15 +264,25 @@ attn_decode_split_kernel(const f16* __restrict__ qg, DecSeqs seqs, float* __rest
     const int G = n_q_heads / n_kv;
     const int R = T * G;
     const int pos0 = seqs.pos0[b];
-    const size_t row_stride = (size_t)n_kv * DEC_HD;
+    const size_t row_stride = (size_t)n_kv * DEC_HD;   // elements (bytes for int8)
     const f16* kbase = seqs.k[b] + (size_t)h * DEC_HD;
     const f16* vbase = seqs.v[b] + (size_t)h * DEC_HD;
+    const char* kbase8 = (const char*)seqs.k[b] + (size_t)h * DEC_HD;
+    const char* vbase8 = (const char*)seqs.v[b] + (size_t)h * DEC_HD;
+    const f16* ksb = Q8 ? seqs.ks[b] + (size_t)h * 8 : nullptr;
+    const f16* vsb = Q8 ? seqs.vs[b] + (size_t)h * 8 : nullptr;
+    auto range = [&](int len, int& lo, int& hi) {
+        if constexpr (DEC)
+            dec_split_range(len, s, split_rows, split, lo, hi);
+        else
+            split_range(len, s, split_rows, split, lo, hi);
+    };
 
     // the union of the launch's tokens' ranges for this split
     int ulo = INT_MAX, uhi = 0;
     for (int t = 0; t < T; ++t) {
         int lo, hi;
-        split_range(pos0 + t + 1, s, split_rows, split, lo, hi);
+        range(pos0 + t + 1, lo, hi);
         if (hi > lo) {
             ulo = lo < ulo ? lo : ulo;
             uhi = hi > uhi ? hi : uhi;
@@ -160,7 +293,7 @@ attn_decode_split_kernel(const f16* __restrict__ qg, DecSeqs seqs, float* __rest
     const int tq = qvalid ? ql / G : 0;
     const int gq = qvalid ? ql - tq * G : 0;
     int qlo = 0, qhi = 0;
-    if (qvalid) split_range(pos0 + tq + 1, s, split_rows, split, qlo, qhi);
+    if (qvalid) range(pos0 + tq + 1, qlo, qhi);
 
     f16x8 qreg[4];
     {
@@ -247,29 +380,37 @@ attn_decode_split_kernel(const f16* __restrict__ qg, DecSeqs seqs, float* __rest
         }
     };
 
+    typedef typename std::conditional<Q8, DecTileQ8, DecTileRegs>::type Raw;
+    auto load = [&](Raw& r, int j) {
+        if constexpr (Q8)
+            dec_load_tile<NT_V>(r, kbase8, vbase8, ksb, vsb, row_stride, j, uhi, lane, w);
+        else
+            dec_load_tile<NT_V>(r, kbase, vbase, row_stride, j, uhi, lane, w);
+    };
     if (uhi > ulo) {
         // NBUF register tile buffers: the loads of tile j + NBUF - 1 are issued
         // before the math of tile j
         const int j0 = ulo / DEC_TILE;
         const int j1 = (uhi + DEC_TILE - 1) / DEC_TILE;
-        DecTileRegs rbuf[NBUF];
+        Raw rbuf[NBUF];
 #pragma unroll
         for (int p = 0; p < NBUF - 1; ++p)
-            if (j0 + p < j1) dec_load_tile<NT_V>(rbuf[p], kbase, vbase, row_stride, j0 + p, uhi, lane, w);
+            if (j0 + p < j1) load(rbuf[p], j0 + p);
         for (int j = j0; j < j1; j += NBUF) {
 #pragma unroll
             for (int u = 0; u < NBUF; ++u) {
                 const int jj = j + u;
                 if (jj >= j1) break;
-                if (jj + NBUF - 1 < j1)
-                    dec_load_tile<NT_V>(rbuf[(u + NBUF - 1) % NBUF], kbase, vbase, row_stride,
-                                        jj + NBUF - 1, uhi, lane, w);
-                body(rbuf[u], jj);
+                if (jj + NBUF - 1 < j1) load(rbuf[(u + NBUF - 1) % NBUF], jj + NBUF - 1);
+                if constexpr (Q8)
+                    body(dec_dequant(rbuf[u], lane), jj);
+                else
+                    body(rbuf[u], jj);
             }
         }
     }
 
-    if (qvalid) {
+    if (qvalid && (!DEC || qhi > qlo)) {
         const size_t part = (((size_t)b * T + tq) * n_q_heads + h * G + gq) * split + s;
         float* dst = pacc + part * DEC_HD + 64 * w + 4 * hh;
 #pragma unroll
@@ -279,7 +420,10 @@ attn_decode_split_kernel(const f16* __restrict__ qg, DecSeqs seqs, float* __rest
                 (f32x4){o1[4 * r4], o1[4 * r4 + 1], o1[4 * r4 + 2], o1[4 * r4 + 3]};
         }
         if (w == 0 && hh == 0) {
-            pm[part] = l_run > 0.f ? m_run * FL_LN2 : -1e30f;
+            if constexpr (DEC)
+                pm[part] = m_run;
+            else
+                pm[part] = l_run > 0.f ? m_run * FL_LN2 : -1e30f;
             pd[part] = l_run;
         }
     }
@@ -310,6 +454,32 @@ __global__ void attn_merge_kernel(const float* __restrict__ pacc, const float* _
     z[((size_t)row * n_q_heads + head) * z_pitch + d] = zv;
 }
 
+// attention_dec_merge (kernels.cu:1336-1385): the first St partials of the
+// token (dec rule), exp2 weights, z = f16_sat(num / den), then the gate if
+// given. One block of 256 threads a (q head, token).
+__global__ void attn_dec_merge_kernel(const float* __restrict__ pacc, const float* __restrict__ pm,
+                                      const float* __restrict__ pd, f16* __restrict__ z,
+                                      const f16* __restrict__ gate, int n_q_heads, int z_pitch,
+                                      int g_pitch, int g_off, int pos0, int tmin, int smax) {
+    const int head = blockIdx.x, t = blockIdx.y, d = threadIdx.x;
+    const int st = dec_split_count(pos0 + t + 1, tmin, smax);
+    const size_t p0 = ((size_t)t * n_q_heads + head) * smax;
+    float M = -INFINITY;
+    for (int s = 0; s < st; ++s) M = fmaxf(M, pm[p0 + s]);
+    float num = 0.f, den = 0.f;
+    for (int s = 0; s < st; ++s) {
+        const float e = fast_exp2(pm[p0 + s] - M);
+        num = fmaf(e, pacc[(p0 + s) * DEC_HD + d], num);
+        den = fmaf(e, pd[p0 + s], den);
+    }
+    f16 zv = f16_sat(num / den);
+    if (gate != nullptr) {
+        const float g = (float)gate[((size_t)t * n_q_heads + head) * g_pitch + g_off + d];
+        zv = f16_sat((float)zv * sigmoid_f(g));
+    }
+    z[((size_t)t * n_q_heads + head) * z_pitch + d] = zv;
+}
+
 __global__ void attn_gate_kernel(f16* __restrict__ z, const f16* __restrict__ g, int n_heads,
                                  int head_dim, int z_pitch, int g_pitch, int g_off) {
     const int t = blockIdx.y;
@@ -324,14 +494,32 @@ __global__ void attn_gate_kernel(f16* __restrict__ z, const f16* __restrict__ g,
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
+#ifndef DEC_NBUF_Q8
+#define DEC_NBUF_Q8 3
+#endif
+
+// grid_split blocks a (sequence, kv head); `split` the partials' stride.
+template <bool Q8, bool DEC>
 int launch_split(const f16* qg, const DecSeqs& seqs, float* pacc, float* pm, float* pd, int B,
-                 int T, int n_q_heads, int n_kv, int q_pitch, int split, int split_rows,
-                 float scale, hipStream_t stream) {
-    dim3 grid(split, n_kv, B);
-    hipLaunchKernelGGL((attn_decode_split_kernel<DEC_NBUF, DEC_NT_V>), grid, dim3(DEC_THREADS), 0,
-                       stream, qg, seqs, pacc,
-                       pm, pd, n_q_heads, n_kv, q_pitch, T, split, split_rows, scale * FL_LOG2E);
+                 int T, int n_q_heads, int n_kv, int q_pitch, int grid_split, int split,
+                 int split_rows, float sl2, hipStream_t stream) {
+    dim3 grid(grid_split, n_kv, B);
+    constexpr int NBUF = Q8 ? DEC_NBUF_Q8 : DEC_NBUF;
+    hipLaunchKernelGGL((attn_decode_split_kernel<NBUF, DEC_NT_V, Q8, DEC>), grid, dim3(DEC_THREADS),
+                       0, stream, qg, seqs, pacc, pm, pd, n_q_heads, n_kv, q_pitch, T, split,
+                       split_rows, sl2);
     return fl::check_launch("attn_decode_split");
+}
+
+// sequence b over an int8 cache of capacity max_pos (scales after the values)
+void set_q8_seq(DecSeqs& seqs, int b, const void* kc, const void* vc, int max_pos, int n_kv,
+                int pos0) {
+    const size_t vals = (size_t)max_pos * n_kv * DEC_HD;
+    seqs.k[b] = (const f16*)kc;
+    seqs.v[b] = (const f16*)vc;
+    seqs.ks[b] = (const f16*)((const char*)kc + vals);
+    seqs.vs[b] = (const f16*)((const char*)vc + vals);
+    seqs.pos0[b] = pos0;
 }
 
 int check_decode_geometry(int T, int n_q_heads, int n_kv, int head_dim, int q_pitch, int split,
@@ -343,6 +531,54 @@ int check_decode_geometry(int T, int n_q_heads, int n_kv, int head_dim, int q_pi
     FL_REQUIRE(split >= 1 && split <= 65535, "split in [1, 65535]");
     FL_REQUIRE(split_rows >= DEC_TILE, "split_rows >= 32");
     return FL_OK;
+}
+
+template <bool Q8>
+int attn_decode_batched(const void* qg, int q_pitch, const void* const* kcache,
+                        const void* const* vcache, const int* pos0, const int* cap, int B, int T,
+                        int n_q_heads, int n_kv_heads, int head_dim, float scale, int split_rows,
+                        int split, const void* gate, int g_pitch, int g_off, void* z, int z_pitch,
+                        void* work, size_t work_bytes, fl_stream_t stream) {
+    int rc = check_decode_geometry(T, n_q_heads, n_kv_heads, head_dim, q_pitch, split, split_rows);
+    if (rc) return rc;
+    FL_REQUIRE(B >= 1 && B <= FL_MAX_SEQS, "1 <= B <= FL_MAX_SEQS");
+    FL_REQUIRE(qg && kcache && vcache && pos0 && cap && z && work, "null pointer");
+    FL_REQUIRE(z_pitch >= head_dim, "z_pitch >= head_dim");
+    FL_REQUIRE(gate == nullptr || g_off + head_dim <= g_pitch, "g_off + head_dim <= g_pitch");
+    FL_REQUIRE(aligned16(qg) && aligned16(work), "16-byte aligned qg / work");
+    if (work_bytes < fl_attn_decode_work_bytes(B, T, n_q_heads, head_dim, split)) {
+        fl::set_error("work: %zu bytes, fl_attn_decode_work_bytes asks %zu", work_bytes,
+                      fl_attn_decode_work_bytes(B, T, n_q_heads, head_dim, split));
+        return FL_ESCRATCH;
+    }
+    DecSeqs seqs = {};
+    int grid_split = 1;
+    for (int b = 0; b < B; ++b) {
+        FL_REQUIRE(kcache[b] && vcache[b], "null cache pointer");
+        FL_REQUIRE(aligned16(kcache[b]) && aligned16(vcache[b]), "16-byte aligned caches");
+        FL_REQUIRE(pos0[b] >= 0 && pos0[b] + T <= cap[b], "pos0[b] + T <= cap[b]");
+        if (Q8)
+            set_q8_seq(seqs, b, kcache[b], vcache[b], cap[b], n_kv_heads, pos0[b]);
+        else {
+            seqs.k[b] = (const f16*)kcache[b];
+            seqs.v[b] = (const f16*)vcache[b];
+            seqs.pos0[b] = pos0[b];
+        }
+        const int st = split_count(pos0[b] + T, split_rows, split);
+        grid_split = st > grid_split ? st : grid_split;
+    }
+    const size_t parts = (size_t)B * T * n_q_heads * grid_split;
+    float* pacc = (float*)work;
+    float* pm = pacc + parts * head_dim;
+    float* pd = pm + parts;
+    rc = launch_split<Q8, false>((const f16*)qg, seqs, pacc, pm, pd, B, T, n_q_heads, n_kv_heads,
+                                 q_pitch, grid_split, grid_split, split_rows, scale * FL_LOG2E,
+                                 (hipStream_t)stream);
+    if (rc) return rc;
+    hipLaunchKernelGGL(attn_merge_kernel, dim3(n_q_heads, B * T), dim3(head_dim), 0,
+                       (hipStream_t)stream, pacc, pm, pd, (f16*)z, (const f16*)gate, n_q_heads,
+                       head_dim, z_pitch, g_pitch, g_off, grid_split);
+    return fl::check_launch("attn_merge");
 }
 
 }  // namespace
@@ -382,8 +618,77 @@ int fl_attention_split_gqa(const void* q, const void* kcache, const void* vcache
     seqs.k[0] = (const f16*)kcache + off;
     seqs.v[0] = (const f16*)vcache + off;
     seqs.pos0[0] = pos0;
-    return launch_split((const f16*)q, seqs, pacc, pm, pd, 1, T, n_q_heads, n_kv_heads, q_pitch,
-                        split, split_rows, scale, (hipStream_t)stream);
+    return launch_split<false, false>((const f16*)q, seqs, pacc, pm, pd, 1, T, n_q_heads,
+                                      n_kv_heads, q_pitch, split, split, split_rows,
+                                      scale * FL_LOG2E, (hipStream_t)stream);
+}
+
+int fl_attention_split_gqa_q8(const void* q, const void* kcache, const void* vcache, float* pacc,
+                              float* pm, float* pd, int layer, int n_q_heads, int n_kv_heads,
+                              int head_dim, int q_pitch, int pos0, int max_pos, float scale,
+                              int split_rows, int T, int split, fl_stream_t stream) {
+    int rc = check_decode_geometry(T, n_q_heads, n_kv_heads, head_dim, q_pitch, split, split_rows);
+    if (rc) return rc;
+    FL_REQUIRE(q && kcache && vcache && pacc && pm && pd, "null pointer");
+    FL_REQUIRE(layer == 0, "an int8 cache is one buffer a layer: layer must be 0");
+    FL_REQUIRE(pos0 >= 0 && pos0 + T <= max_pos, "pos0 + T <= max_pos");
+    FL_REQUIRE(aligned16(q) && aligned16(kcache) && aligned16(vcache) && aligned16(pacc),
+               "16-byte aligned buffers");
+    DecSeqs seqs = {};
+    set_q8_seq(seqs, 0, kcache, vcache, max_pos, n_kv_heads, pos0);
+    return launch_split<true, false>((const f16*)q, seqs, pacc, pm, pd, 1, T, n_q_heads,
+                                     n_kv_heads, q_pitch, split, split, split_rows,
+                                     scale * FL_LOG2E, (hipStream_t)stream);
+}
+
+int fl_attention_dec_q8(const void* q, const void* kcache, const void* vcache, float* pacc,
+                        float* pm, float* pd, int n_q_heads, int n_kv_heads, int q_pitch, int pos0,
+                        int max_pos, float sl2, int tmin, int smax, int T, fl_stream_t stream) {
+    int rc = check_decode_geometry(T, n_q_heads, n_kv_heads, DEC_HD, q_pitch, smax, DEC_TILE);
+    if (rc) return rc;
+    FL_REQUIRE(q && kcache && vcache && pacc && pm && pd, "null pointer");
+    FL_REQUIRE(tmin >= 1, "tmin >= 1");
+    FL_REQUIRE(pos0 >= 0 && pos0 + T <= max_pos, "pos0 + T <= max_pos");
+    FL_REQUIRE(aligned16(q) && aligned16(kcache) && aligned16(vcache) && aligned16(pacc),
+               "16-byte aligned buffers");
+    DecSeqs seqs = {};
+    set_q8_seq(seqs, 0, kcache, vcache, max_pos, n_kv_heads, pos0);
+    // the last token is the longest: its split count is the widest
+    const int grid_split = dec_split_count(pos0 + T, tmin, smax);
+    return launch_split<true, true>((const f16*)q, seqs, pacc, pm, pd, 1, T, n_q_heads, n_kv_heads,
+                                    q_pitch, grid_split, smax, tmin, sl2, (hipStream_t)stream);
+}
+
+int fl_attention_dec_merge(const float* pacc, const float* pm, const float* pd, void* z,
+                           int n_q_heads, int z_pitch, int pos0, int tmin, int smax, int T,
+                           const void* gate, int g_pitch, int g_off, fl_stream_t stream) {
+    FL_REQUIRE(pacc && pm && pd && z, "null pointer");
+    FL_REQUIRE(n_q_heads >= 1 && T >= 1 && pos0 >= 0, "n_q_heads, T >= 1, pos0 >= 0");
+    FL_REQUIRE(tmin >= 1 && smax >= 1 && z_pitch >= DEC_HD, "tmin, smax >= 1, z_pitch >= 256");
+    FL_REQUIRE(gate == nullptr || g_off + DEC_HD <= g_pitch, "g_off + 256 <= g_pitch");
+    hipLaunchKernelGGL(attn_dec_merge_kernel, dim3(n_q_heads, T), dim3(DEC_HD), 0,
+                       (hipStream_t)stream, pacc, pm, pd, (f16*)z, (const f16*)gate, n_q_heads,
+                       z_pitch, g_pitch, g_off, pos0, tmin, smax);
+    return fl::check_launch("attn_dec_merge");
+}
+
+int fl_kv_store_q8(const void* k, const void* v, void* kcache, void* vcache, int layer, int pos0,
+                   int T, int n_kv_heads, int head_dim, int max_pos, fl_stream_t stream) {
+    FL_REQUIRE(k && v && kcache && vcache, "null pointer");
+    FL_REQUIRE(layer == 0, "an int8 cache is one buffer a layer: layer must be 0");
+    FL_REQUIRE(head_dim == DEC_HD, "head_dim must be 256");
+    FL_REQUIRE(T >= 0 && pos0 >= 0 && n_kv_heads > 0 && pos0 + T <= max_pos, "pos0 + T <= max_pos");
+    FL_REQUIRE(((uintptr_t)k & 7u) == 0 && ((uintptr_t)v & 7u) == 0 &&
+                   ((uintptr_t)kcache & 3u) == 0 && ((uintptr_t)vcache & 3u) == 0,
+               "8-byte aligned k, v; 4-byte aligned caches");
+    if (T == 0) return FL_OK;
+    const size_t vals = (size_t)max_pos * n_kv_heads * DEC_HD;
+    const int rows = T * n_kv_heads;
+    hipLaunchKernelGGL(kv_store_q8_kernel, dim3((rows + 3) / 4), dim3(256), 0, (hipStream_t)stream,
+                       (const f16*)k, (const f16*)v, (signed char*)kcache, (signed char*)vcache,
+                       (f16*)((char*)kcache + vals), (f16*)((char*)vcache + vals), pos0, T,
+                       n_kv_heads);
+    return fl::check_launch("kv_store_q8");
 }
 
 int fl_attention_merge(const float* pacc, const float* pm, const float* pd, void* z,
@@ -423,41 +728,19 @@ int fl_attn_decode(const void* qg, int q_pitch, const void* const* kcache,
                    int n_q_heads, int n_kv_heads, int head_dim, float scale, int split_rows,
                    int split, const void* gate, int g_pitch, int g_off, void* z, int z_pitch,
                    void* work, size_t work_bytes, fl_stream_t stream) {
-    int rc = check_decode_geometry(T, n_q_heads, n_kv_heads, head_dim, q_pitch, split, split_rows);
-    if (rc) return rc;
-    FL_REQUIRE(B >= 1 && B <= FL_MAX_SEQS, "1 <= B <= FL_MAX_SEQS");
-    FL_REQUIRE(qg && kcache && vcache && pos0 && cap && z && work, "null pointer");
-    FL_REQUIRE(z_pitch >= head_dim, "z_pitch >= head_dim");
-    FL_REQUIRE(gate == nullptr || g_off + head_dim <= g_pitch, "g_off + head_dim <= g_pitch");
-    FL_REQUIRE(aligned16(qg) && aligned16(work), "16-byte aligned qg / work");
-    if (work_bytes < fl_attn_decode_work_bytes(B, T, n_q_heads, head_dim, split)) {
-        fl::set_error("work: %zu bytes, fl_attn_decode_work_bytes asks %zu", work_bytes,
-                      fl_attn_decode_work_bytes(B, T, n_q_heads, head_dim, split));
-        return FL_ESCRATCH;
-    }
-    DecSeqs seqs = {};
-    int grid_split = 1;
-    for (int b = 0; b < B; ++b) {
-        FL_REQUIRE(kcache[b] && vcache[b], "null cache pointer");
-        FL_REQUIRE(aligned16(kcache[b]) && aligned16(vcache[b]), "16-byte aligned caches");
-        FL_REQUIRE(pos0[b] >= 0 && pos0[b] + T <= cap[b], "pos0[b] + T <= cap[b]");
-        seqs.k[b] = (const f16*)kcache[b];
-        seqs.v[b] = (const f16*)vcache[b];
-        seqs.pos0[b] = pos0[b];
-        const int st = split_count(pos0[b] + T, split_rows, split);
-        grid_split = st > grid_split ? st : grid_split;
-    }
-    const size_t parts = (size_t)B * T * n_q_heads * grid_split;
-    float* pacc = (float*)work;
-    float* pm = pacc + parts * head_dim;
-    float* pd = pm + parts;
-    rc = launch_split((const f16*)qg, seqs, pacc, pm, pd, B, T, n_q_heads, n_kv_heads, q_pitch,
-                      grid_split, split_rows, scale, (hipStream_t)stream);
-    if (rc) return rc;
-    hipLaunchKernelGGL(attn_merge_kernel, dim3(n_q_heads, B * T), dim3(head_dim), 0,
-                       (hipStream_t)stream, pacc, pm, pd, (f16*)z, (const f16*)gate, n_q_heads,
-                       head_dim, z_pitch, g_pitch, g_off, grid_split);
-    return fl::check_launch("attn_merge");
+    return attn_decode_batched<false>(qg, q_pitch, kcache, vcache, pos0, cap, B, T, n_q_heads,
+                                      n_kv_heads, head_dim, scale, split_rows, split, gate,
+                                      g_pitch, g_off, z, z_pitch, work, work_bytes, stream);
+}
+
+int fl_attn_decode_q8(const void* qg, int q_pitch, const void* const* kcache,
+                      const void* const* vcache, const int* pos0, const int* cap, int B, int T,
+                      int n_q_heads, int n_kv_heads, int head_dim, float scale, int split_rows,
+                      int split, const void* gate, int g_pitch, int g_off, void* z, int z_pitch,
+                      void* work, size_t work_bytes, fl_stream_t stream) {
+    return attn_decode_batched<true>(qg, q_pitch, kcache, vcache, pos0, cap, B, T, n_q_heads,
+                                     n_kv_heads, head_dim, scale, split_rows, split, gate,
+                                     g_pitch, g_off, z, z_pitch, work, work_bytes, stream);
 }
 
 }  // extern "C"

@@ -27,6 +27,14 @@
 // operand is read with ds_read_b64_tr_b16: in each 16-lane group, lane j
 // points at row kb + j/4, columns n0 + 4 (j%4)..+3 of the tile, and lane i
 // receives V[kb..kb+3][n0 + i] -- four kv rows of one output dim.
+//
+// Over the int8 cache (attention_prefill_fh_q8, kernels.cu:2778-2786) the
+// tiles reach LDS through registers instead: each thread loads 64 bytes of a
+// K row and of a V row of the next tile (and their two block scales) while
+// the current tile is computed, then writes them as fp16(byte * scale) into
+// the other stage, in the same swizzled layout, so the compute is the fp16
+// kernel's. The reference dequantizes V the same way; its K stays fp32
+// (byte * scale exact), here it is rounded to fp16 once.
 #include "fl_common.hpp"
 
 namespace {
@@ -200,9 +208,26 @@ __device__ __forceinline__ const char* uniform_ptr(const char* p) {
     return (const char*)(uintptr_t)(((uint64_t)hi << 32) | lo);
 }
 
+// One int8 tile row quarter in flight: thread tid holds bytes 64 (tid % 4) ..
+// + 63 of K and V row tid / 4 and the two scales of those 64 dims.
+struct PfRawQ8 {
+    u32x4 k[4], v[4];
+    uint32_t ks, vs;
+};
+
+// 8 bytes (two dwords) to 8 halves fp16(byte * s)
+__device__ __forceinline__ f16x8 deq8(uint32_t a, uint32_t b, f16 s) {
+    const f16x2 s2 = {s, s};
+    const f16x4 lo = q8_deq4(a, s2), hi = q8_deq4(b, s2);
+    return (f16x8){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
+
+// Q8: kc / vc are int8 values, ksc / vsc their scales (unused for fp16).
+template <bool Q8>
 __global__ void __launch_bounds__(PF_THREADS)
-attn_prefill_kernel(const f16* __restrict__ q, int q_pitch, const f16* __restrict__ kc,
-                    const f16* __restrict__ vc, f16* __restrict__ z, int z_pitch, int n_q_heads,
+attn_prefill_kernel(const f16* __restrict__ q, int q_pitch, const void* __restrict__ kc,
+                    const void* __restrict__ vc, const f16* __restrict__ ksc,
+                    const f16* __restrict__ vsc, f16* __restrict__ z, int z_pitch, int n_q_heads,
                     int n_kv, int pos0, int T, float sl2, int n_row_tiles) {
     extern __shared__ __attribute__((aligned(16))) char smem[];
 
@@ -231,15 +256,52 @@ attn_prefill_kernel(const f16* __restrict__ q, int q_pitch, const f16* __restric
     const int n_tiles = (kv_end + PF_BK - 1) / PF_BK;
 
     const uint32_t rsb = (uint32_t)n_kv * ROW_B;   // bytes between cache rows
-    const char* kb = uniform_ptr((const char*)(kc + (size_t)h * PF_HD));
-    const char* vb = uniform_ptr((const char*)(vc + (size_t)h * PF_HD));
+    const char* kb = uniform_ptr((const char*)((const f16*)kc + (size_t)h * PF_HD));
+    const char* vb = uniform_ptr((const char*)((const f16*)vc + (size_t)h * PF_HD));
     uint32_t loff[8];
 #pragma unroll
     for (int n = 0; n < 8; ++n)
         loff[n] = (lane >> 5) * rsb + 16 * ((lane & 31) ^ sw(2 * n + (lane >> 5)));
     const uint32_t lds_base = (uint32_t)(uintptr_t)((__attribute__((address_space(3))) char*)smem);
 
-    issue_tile(lds_base, 0, kb, vb, rsb, 0, kv_end, w, lane, loff);
+    // int8 staging: this thread's row and quarter of a tile
+    const int qr = tid >> 2, qc = tid & 3;
+    const char* kb8 = (const char*)kc + (size_t)h * PF_HD + 64 * qc;
+    const char* vb8 = (const char*)vc + (size_t)h * PF_HD + 64 * qc;
+    const size_t rs8 = (size_t)n_kv * PF_HD;   // bytes between int8 rows
+    PfRawQ8 raw;
+    // rows past kv_end read row kv_end - 1 (in bounds; masked, p = 0)
+    auto q8_load = [&](int kv0) {
+        const int kv = min(kv0 + qr, kv_end - 1);
+        const u32x4* ks = (const u32x4*)(kb8 + (size_t)kv * rs8);
+        const u32x4* vs = (const u32x4*)(vb8 + (size_t)kv * rs8);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            raw.k[i] = ks[i];
+            raw.v[i] = __builtin_nontemporal_load(vs + i);
+        }
+        const size_t so = ((size_t)kv * n_kv + h) * 8 + 2 * qc;
+        raw.ks = *(const uint32_t*)(ksc + so);
+        raw.vs = *(const uint32_t*)(vsc + so);
+    };
+    // into LDS stage st: chunk 8 qc + i of row qr at (8 qc + i) ^ sw(qr)
+    auto q8_store = [&](int st) {
+        char* kd = smem + st * TILE_B + qr * ROW_B;
+        const f16x2 ks2 = __builtin_bit_cast(f16x2, raw.ks), vs2 = __builtin_bit_cast(f16x2, raw.vs);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int off = 16 * ((8 * qc + i) ^ sw(qr));
+            const u32x4 kw = raw.k[i >> 1], vw = raw.v[i >> 1];
+            *(f16x8*)(kd + off) = (i & 1) ? deq8(kw.z, kw.w, ks2[i >> 2]) : deq8(kw.x, kw.y, ks2[i >> 2]);
+            *(f16x8*)(kd + V_OFF + off) =
+                (i & 1) ? deq8(vw.z, vw.w, vs2[i >> 2]) : deq8(vw.x, vw.y, vs2[i >> 2]);
+        }
+    };
+
+    if constexpr (Q8)
+        q8_load(0);
+    else
+        issue_tile(lds_base, 0, kb, vb, rsb, 0, kv_end, w, lane, loff);
 
     f16x8 qreg[16];   // Q[row][128 hh + 8 ks + 0..7]
     {
@@ -251,6 +313,10 @@ attn_prefill_kernel(const f16* __restrict__ q, int q_pitch, const f16* __restric
     // inside the tile loop as vmcnt(0) -- on every tile, and on the next tile's
     // copy with it.
     WAIT_VMCNT(0);
+    if constexpr (Q8) {
+        q8_store(0);
+        tile_done();
+    }
     f32x16 o[8];
 #pragma unroll
     for (int mb = 0; mb < 8; ++mb) acc_zero(o[mb], (f16x8)(0));
@@ -278,13 +344,17 @@ attn_prefill_kernel(const f16* __restrict__ q, int q_pitch, const f16* __restric
     typedef __attribute__((address_space(3))) const char lds_char;
     for (int j = 0; j < n_tiles; ++j) {
         const int st = j & 1;
-        if (j + 1 < n_tiles) {
-            issue_tile(lds_base, st ^ 1, kb, vb, rsb, (j + 1) * PF_BK, kv_end, w, lane, loff);
-            WAIT_VMCNT(16);   // this tile's 16 copies done, the next tile's in flight
+        if constexpr (Q8) {
+            if (j + 1 < n_tiles) q8_load((j + 1) * PF_BK);   // in registers during the math
         } else {
-            WAIT_VMCNT(0);
+            if (j + 1 < n_tiles) {
+                issue_tile(lds_base, st ^ 1, kb, vb, rsb, (j + 1) * PF_BK, kv_end, w, lane, loff);
+                WAIT_VMCNT(16);   // this tile's 16 copies done, the next tile's in flight
+            } else {
+                WAIT_VMCNT(0);
+            }
+            tile_ready();
         }
-        tile_ready();
         const int kv0 = j * PF_BK;
         if (kv0 <= wqmax) {
             const uint32_t kst = koff + st * TILE_B;
@@ -359,6 +429,10 @@ attn_prefill_kernel(const f16* __restrict__ q, int q_pitch, const f16* __restric
             pv_step<3, 0>(o, pk[3], vt, troff);
             pv_step<3, 1>(o, pk[3], vt, troff);
         }
+        if constexpr (Q8) {
+            // the other stage's last readers passed the previous barrier
+            if (j + 1 < n_tiles) q8_store(st ^ 1);
+        }
         tile_done();   // this stage is refilled two tiles on
     }
 
@@ -378,31 +452,31 @@ attn_prefill_kernel(const f16* __restrict__ q, int q_pitch, const f16* __restric
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
-}  // namespace
-
-extern "C" int fl_attention_prefill(const void* q, int q_pitch, const void* k_new,
-                                    const void* v_new, void* kcache, void* vcache, int layer,
-                                    int n_q_heads, int n_kv_heads, int head_dim, int pos0,
-                                    int max_pos, float scale, int T, void* z, int z_pitch,
-                                    fl_stream_t stream) {
+template <bool Q8>
+int prefill(const void* q, int q_pitch, const void* k_new, const void* v_new, void* kcache,
+            void* vcache, int layer, int n_q_heads, int n_kv_heads, int head_dim, int pos0,
+            int max_pos, float scale, int T, void* z, int z_pitch, fl_stream_t stream) {
     FL_REQUIRE(q && kcache && vcache && z, "null pointer");
     FL_REQUIRE(head_dim == PF_HD, "head_dim must be 256");
     FL_REQUIRE(n_kv_heads > 0 && n_q_heads > 0 && n_q_heads % n_kv_heads == 0,
                "n_q_heads % n_kv_heads");
     FL_REQUIRE(T >= 1 && pos0 >= 0 && layer >= 0 && pos0 + T <= max_pos, "pos0 + T <= max_pos");
+    FL_REQUIRE(!Q8 || layer == 0, "an int8 cache is one buffer a layer: layer must be 0");
     FL_REQUIRE(q_pitch >= head_dim && q_pitch % 8 == 0 && z_pitch >= head_dim && z_pitch % 4 == 0,
                "q_pitch, z_pitch");
     FL_REQUIRE((k_new == nullptr) == (v_new == nullptr), "k_new and v_new together");
     FL_REQUIRE(aligned16(q) && aligned16(kcache) && aligned16(vcache) && ((uintptr_t)z & 7u) == 0,
                "aligned buffers");
     if (k_new != nullptr) {
-        const int rc = fl_kv_store(k_new, v_new, kcache, vcache, layer, pos0, T, n_kv_heads,
-                                   head_dim, max_pos, stream);
+        const int rc = Q8 ? fl_kv_store_q8(k_new, v_new, kcache, vcache, layer, pos0, T,
+                                           n_kv_heads, head_dim, max_pos, stream)
+                          : fl_kv_store(k_new, v_new, kcache, vcache, layer, pos0, T, n_kv_heads,
+                                        head_dim, max_pos, stream);
         if (rc) return rc;
     }
     static bool lds_attr_set = false;   // 128 KiB of dynamic LDS is above the default limit
     if (!lds_attr_set) {
-        if (hipFuncSetAttribute((const void*)attn_prefill_kernel,
+        if (hipFuncSetAttribute((const void*)attn_prefill_kernel<Q8>,
                                 hipFuncAttributeMaxDynamicSharedMemorySize, LDS_B) !=
             hipSuccess) {
             fl::set_error("attn_prefill: cannot raise the dynamic LDS limit to %d bytes",
@@ -411,13 +485,46 @@ extern "C" int fl_attention_prefill(const void* q, int q_pitch, const void* k_ne
         }
         lds_attr_set = true;
     }
-    const size_t off = (size_t)layer * max_pos * n_kv_heads * head_dim;
+    const void* kc;
+    const void* vc;
+    const f16* ksc = nullptr;
+    const f16* vsc = nullptr;
+    if (Q8) {
+        const size_t vals = (size_t)max_pos * n_kv_heads * head_dim;   // scales follow
+        kc = kcache;
+        vc = vcache;
+        ksc = (const f16*)((const char*)kcache + vals);
+        vsc = (const f16*)((const char*)vcache + vals);
+    } else {
+        const size_t off = (size_t)layer * max_pos * n_kv_heads * head_dim;
+        kc = (const f16*)kcache + off;
+        vc = (const f16*)vcache + off;
+    }
     const int rows = T * (n_q_heads / n_kv_heads);
     const int n_row_tiles = (rows + PF_BQ - 1) / PF_BQ;
-    hipLaunchKernelGGL(attn_prefill_kernel, dim3(n_row_tiles, n_kv_heads), dim3(PF_THREADS),
-                       LDS_B,
-                       (hipStream_t)stream, (const f16*)q, q_pitch, (const f16*)kcache + off,
-                       (const f16*)vcache + off, (f16*)z, z_pitch, n_q_heads, n_kv_heads, pos0, T,
-                       scale * FL_LOG2E, n_row_tiles);
+    hipLaunchKernelGGL(attn_prefill_kernel<Q8>, dim3(n_row_tiles, n_kv_heads), dim3(PF_THREADS),
+                       LDS_B, (hipStream_t)stream, (const f16*)q, q_pitch, kc, vc, ksc, vsc,
+                       (f16*)z, z_pitch, n_q_heads, n_kv_heads, pos0, T, scale * FL_LOG2E,
+                       n_row_tiles);
     return fl::check_launch("attn_prefill");
+}
+
+}  // namespace
+
+extern "C" int fl_attention_prefill(const void* q, int q_pitch, const void* k_new,
+                                    const void* v_new, void* kcache, void* vcache, int layer,
+                                    int n_q_heads, int n_kv_heads, int head_dim, int pos0,
+                                    int max_pos, float scale, int T, void* z, int z_pitch,
+                                    fl_stream_t stream) {
+    return prefill<false>(q, q_pitch, k_new, v_new, kcache, vcache, layer, n_q_heads, n_kv_heads,
+                          head_dim, pos0, max_pos, scale, T, z, z_pitch, stream);
+}
+
+extern "C" int fl_attention_prefill_q8(const void* q, int q_pitch, const void* k_new,
+                                       const void* v_new, void* kcache, void* vcache, int layer,
+                                       int n_q_heads, int n_kv_heads, int head_dim, int pos0,
+                                       int max_pos, float scale, int T, void* z, int z_pitch,
+                                       fl_stream_t stream) {
+    return prefill<true>(q, q_pitch, k_new, v_new, kcache, vcache, layer, n_q_heads, n_kv_heads,
+                         head_dim, pos0, max_pos, scale, T, z, z_pitch, stream);
 }

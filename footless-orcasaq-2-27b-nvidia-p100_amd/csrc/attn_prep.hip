@@ -13,8 +13,8 @@
 //     touched.
 //   kv_store (kernels.cu:457-484): the roped k row and the v row to position
 //     pos0 + t of the layer's cache.
-// attn_prep_q8 (kernels.cu:837-908) is the reference's fused form for its int8
-// cache; this is the fused form for the fp16 cache the hot path uses.
+//   attn_prep_q8 (kernels.cu:837-908): the same fused, with kv_store_q8's int8
+//     store (kernels.cu:486-520) in place of kv_store.
 //
 // One workgroup a (token, group of 4 RPW heads), a wavefront RPW rows (all
 // loaded before any is processed). The rotation's cos / sin depend only on
@@ -37,24 +37,19 @@ constexpr int PR_HD = 256;
 constexpr int PR_WAVES = 4;
 constexpr int PR_MAXPAIRS = PR_HD / 2;
 
-__device__ __forceinline__ float dpp_xor1(float v) {
-    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, true));
-}
-__device__ __forceinline__ float dpp_xor2(float v) {
-    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, true));
-}
-
-// flags: bit 0 norm, bit 1 rope, bit 2 KV store (k rows and their v rows);
-// RPW rows a wavefront
+// flags: bit 0 norm, bit 1 rope, bit 2 KV store (k rows and their v rows),
+// bit 3 the store in the int8 format (caches of capacity max_pos); RPW rows a
+// wavefront
 template <int FLAGS, int RPW>
 __global__ void __launch_bounds__(64 * PR_WAVES)
 attn_prep_kernel(const f16* q, f16* qo, int q_pitch, f16* k, int k_pitch,
                  const f16* __restrict__ v, const float* __restrict__ wq,
-                 const float* __restrict__ wk, f16* __restrict__ kc, f16* __restrict__ vc,
-                 int n_q_heads, int n_kv_heads, int pos0, int rope_dim, double theta, float eps) {
+                 const float* __restrict__ wk, void* __restrict__ kc, void* __restrict__ vc,
+                 int n_q_heads, int n_kv_heads, int pos0, int max_pos, int rope_dim, double theta,
+                 float eps) {
     __shared__ float scs[PR_MAXPAIRS], ssn[PR_MAXPAIRS];
     __shared__ __attribute__((aligned(16))) f16 srow[PR_WAVES][PR_HD];
-    constexpr bool NORM = FLAGS & 1, ROPE = FLAGS & 2, STORE = FLAGS & 4;
+    constexpr bool NORM = FLAGS & 1, ROPE = FLAGS & 2, STORE = FLAGS & 4, Q8 = FLAGS & 8;
     const int t = blockIdx.x, hd0 = blockIdx.y * PR_WAVES * RPW;
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int pos = pos0 + t;
@@ -138,9 +133,18 @@ attn_prep_kernel(const f16* q, f16* qo, int q_pitch, f16* k, int k_pitch,
         }
         if (NORM || ROPE) *(f16x4*)(orow + 4 * lane) = y;
         if (STORE && !is_q) {
-            const size_t crow = ((size_t)pos * n_kv_heads + h) * PR_HD + 4 * lane;
-            *(f16x4*)(kc + crow) = y;
-            *(f16x4*)(vc + crow) = *(const f16x4*)(v + ((size_t)t * n_kv_heads + h) * PR_HD + 4 * lane);
+            const f16x4 vin = *(const f16x4*)(v + ((size_t)t * n_kv_heads + h) * PR_HD + 4 * lane);
+            const size_t crow = (size_t)pos * n_kv_heads + h;
+            if constexpr (Q8) {
+                const size_t vals = (size_t)max_pos * n_kv_heads * PR_HD;   // scales follow
+                q8_store_row(y, (signed char*)kc + crow * PR_HD,
+                             (f16*)((signed char*)kc + vals) + crow * 8, lane);
+                q8_store_row(vin, (signed char*)vc + crow * PR_HD,
+                             (f16*)((signed char*)vc + vals) + crow * 8, lane);
+            } else {
+                *(f16x4*)((f16*)kc + crow * PR_HD + 4 * lane) = y;
+                *(f16x4*)((f16*)vc + crow * PR_HD + 4 * lane) = vin;
+            }
         }
     }
 }
@@ -151,26 +155,44 @@ attn_prep_kernel(const f16* q, f16* qo, int q_pitch, f16* k, int k_pitch,
 // 7 rows a wave 97 us, the fp64 sincos per workgroup being the difference).
 template <int FLAGS>
 int launch_prep(const f16* q, f16* qo, int q_pitch, f16* k, int k_pitch, const f16* v,
-                const float* wq, const float* wk, f16* kc, f16* vc, int n_q_heads, int n_kv_heads,
-                int pos0, int T, int rope_dim, float theta, float eps, fl_stream_t stream) {
+                const float* wq, const float* wk, void* kc, void* vc, int n_q_heads, int n_kv_heads,
+                int pos0, int max_pos, int T, int rope_dim, float theta, float eps,
+                fl_stream_t stream) {
     const int heads = n_q_heads + n_kv_heads;
     if (T < 256) {
         hipLaunchKernelGGL((attn_prep_kernel<FLAGS, 1>),
                            dim3(T, (heads + PR_WAVES - 1) / PR_WAVES), dim3(64 * PR_WAVES), 0,
                            (hipStream_t)stream, q, qo, q_pitch, k, k_pitch, v, wq, wk, kc, vc,
-                           n_q_heads, n_kv_heads, pos0, rope_dim, (double)theta, eps);
+                           n_q_heads, n_kv_heads, pos0, max_pos, rope_dim, (double)theta, eps);
     } else {
         hipLaunchKernelGGL((attn_prep_kernel<FLAGS, 7>),
                            dim3(T, (heads + 7 * PR_WAVES - 1) / (7 * PR_WAVES)),
                            dim3(64 * PR_WAVES), 0, (hipStream_t)stream, q, qo, q_pitch, k,
-                           k_pitch, v, wq, wk, kc, vc, n_q_heads, n_kv_heads, pos0, rope_dim,
-                           (double)theta, eps);
+                           k_pitch, v, wq, wk, kc, vc, n_q_heads, n_kv_heads, pos0, max_pos,
+                           rope_dim, (double)theta, eps);
     }
     return fl::check_launch("attn_prep");
 }
 
 
 bool al(const void* p, unsigned a) { return ((uintptr_t)p & (a - 1)) == 0; }
+
+int check_prep(const void* qg, const void* k, const void* v, const float* wq, const float* wk,
+               const void* kcache, const void* vcache, int q_pitch, int n_q_heads,
+               int n_kv_heads, int head_dim, int pos0, int max_pos, int T, int rope_dim,
+               float eps) {
+    FL_REQUIRE(qg && k && v && wq && wk && kcache && vcache, "null pointer");
+    FL_REQUIRE(head_dim == PR_HD, "head_dim must be 256");
+    FL_REQUIRE(rope_dim > 0 && rope_dim <= head_dim && (rope_dim & 1) == 0,
+               "0 < rope_dim <= head_dim, even");
+    FL_REQUIRE(n_q_heads >= 1 && n_kv_heads >= 1 && n_q_heads % n_kv_heads == 0,
+               "n_q_heads % n_kv_heads");
+    FL_REQUIRE(T >= 1 && pos0 >= 0 && pos0 + T <= max_pos, "pos0 + T <= max_pos");
+    FL_REQUIRE(q_pitch >= head_dim && eps >= 0.f, "q_pitch >= head_dim");
+    FL_REQUIRE(q_pitch % 4 == 0 && al(qg, 8) && al(k, 8) && al(v, 8) && al(wq, 16) && al(wk, 16),
+               "q_pitch % 4, aligned qg, k, v, weights");
+    return FL_OK;
+}
 
 }  // namespace
 
@@ -184,7 +206,7 @@ int fl_rmsnorm1p(const void* x, const float* w, void* y, int n, int rows, int pi
     FL_REQUIRE(pitch % 4 == 0 && al(x, 8) && al(y, 8) && al(w, 16), "pitch % 4, aligned x, y, w");
     // the rows of one tensor run as the kernel's "q" heads, none as "k"
     return launch_prep<1>((const f16*)x, (f16*)y, pitch, nullptr, 0, nullptr, w, nullptr, nullptr,
-                          nullptr, rows, 0, 0, T, 0, 0.f, eps, stream);
+                          nullptr, rows, 0, 0, 0, T, 0, 0.f, eps, stream);
 }
 
 int fl_rope_partial(void* q, void* k, int n_q_heads, int n_kv_heads, int head_dim, int rope_dim,
@@ -198,29 +220,36 @@ int fl_rope_partial(void* q, void* k, int n_q_heads, int n_kv_heads, int head_di
     FL_REQUIRE(q_pitch >= head_dim && k_pitch >= head_dim, "pitches");
     FL_REQUIRE(q_pitch % 4 == 0 && k_pitch % 4 == 0 && al(q, 8) && al(k, 8), "pitch % 4, aligned q, k");
     return launch_prep<2>((const f16*)q, (f16*)q, q_pitch, (f16*)k, k_pitch, nullptr, nullptr,
-                          nullptr, nullptr, nullptr, n_q_heads, n_kv_heads, pos0, T, rope_dim, theta,
-                          0.f, stream);
+                          nullptr, nullptr, nullptr, n_q_heads, n_kv_heads, pos0, 0, T, rope_dim,
+                          theta, 0.f, stream);
 }
 
 int fl_attn_prep(void* qg, int q_pitch, void* k, const void* v, const float* wq, const float* wk,
                  void* kcache, void* vcache, int layer, int n_q_heads, int n_kv_heads,
                  int head_dim, int pos0, int max_pos, int T, int rope_dim, float theta, float eps,
                  fl_stream_t stream) {
-    FL_REQUIRE(qg && k && v && wq && wk && kcache && vcache, "null pointer");
-    FL_REQUIRE(head_dim == PR_HD, "head_dim must be 256");
-    FL_REQUIRE(rope_dim > 0 && rope_dim <= head_dim && (rope_dim & 1) == 0,
-               "0 < rope_dim <= head_dim, even");
-    FL_REQUIRE(n_q_heads >= 1 && n_kv_heads >= 1 && n_q_heads % n_kv_heads == 0,
-               "n_q_heads % n_kv_heads");
-    FL_REQUIRE(T >= 1 && pos0 >= 0 && layer >= 0 && pos0 + T <= max_pos, "pos0 + T <= max_pos");
-    FL_REQUIRE(q_pitch >= head_dim && eps >= 0.f, "q_pitch >= head_dim");
-    FL_REQUIRE(q_pitch % 4 == 0 && al(qg, 8) && al(k, 8) && al(v, 8) && al(kcache, 8) &&
-                   al(vcache, 8) && al(wq, 16) && al(wk, 16),
-               "q_pitch % 4, aligned qg, k, v, caches, weights");
+    int rc = check_prep(qg, k, v, wq, wk, kcache, vcache, q_pitch, n_q_heads, n_kv_heads,
+                        head_dim, pos0, max_pos, T, rope_dim, eps);
+    if (rc) return rc;
+    FL_REQUIRE(layer >= 0 && al(kcache, 8) && al(vcache, 8), "layer >= 0, 8-byte aligned caches");
     const size_t off = (size_t)layer * max_pos * n_kv_heads * head_dim;
     return launch_prep<7>((const f16*)qg, (f16*)qg, q_pitch, (f16*)k, head_dim, (const f16*)v, wq, wk,
-                          (f16*)kcache + off, (f16*)vcache + off, n_q_heads, n_kv_heads, pos0, T,
-                          rope_dim, theta, eps, stream);
+                          (f16*)kcache + off, (f16*)vcache + off, n_q_heads, n_kv_heads, pos0,
+                          max_pos, T, rope_dim, theta, eps, stream);
+}
+
+int fl_attn_prep_q8(void* qg, int q_pitch, void* k, const void* v, const float* wq,
+                    const float* wk, void* kcache, void* vcache, int layer, int n_q_heads,
+                    int n_kv_heads, int head_dim, int pos0, int max_pos, int T, int rope_dim,
+                    float theta, float eps, fl_stream_t stream) {
+    int rc = check_prep(qg, k, v, wq, wk, kcache, vcache, q_pitch, n_q_heads, n_kv_heads,
+                        head_dim, pos0, max_pos, T, rope_dim, eps);
+    if (rc) return rc;
+    FL_REQUIRE(layer == 0, "an int8 cache is one buffer a layer: layer must be 0");
+    FL_REQUIRE(al(kcache, 4) && al(vcache, 4), "4-byte aligned caches");
+    return launch_prep<15>((const f16*)qg, (f16*)qg, q_pitch, (f16*)k, head_dim, (const f16*)v, wq,
+                           wk, kcache, vcache, n_q_heads, n_kv_heads, pos0, max_pos, T, rope_dim,
+                           theta, eps, stream);
 }
 
 }  // extern "C"

@@ -13,6 +13,8 @@ typedef f16 f16x4 __attribute__((ext_vector_type(4)));
 typedef f16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 #define FL_LOG2E 1.4426950408889634f
 #define FL_LN2 0.6931471805599453f
@@ -62,6 +64,63 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 __device__ __forceinline__ float lane_xor(float v, int mask) {
     const int lane = __lane_id();
     return __int_as_float(__builtin_amdgcn_ds_bpermute((lane ^ mask) << 2, __float_as_int(v)));
+}
+
+// Lane exchanges at distance 1 and 2 inside each group of 4 lanes (DPP quad
+// permutes, no LDS).
+__device__ __forceinline__ float dpp_xor1(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, true));
+}
+__device__ __forceinline__ float dpp_xor2(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, true));
+}
+
+// ---------------------------------------------------------------------------
+// int8 KV cache format (kernels.cu:486-520): one buffer a layer of capacity
+// max_pos, values [max_pos][n_kv][256] int8, then the scales
+// [max_pos][n_kv][8] fp16 at byte max_pos * n_kv * 256. A 32-dim block shares
+// the fp16 scale absmax / 127 and stores rint(x / scale) in [-127, 127]
+// (0 where the scale is 0).
+// ---------------------------------------------------------------------------
+constexpr int Q8_BLOCK = 32;
+
+__device__ __forceinline__ f16 q8_scale(float absmax) { return (f16)(absmax / 127.0f); }
+
+__device__ __forceinline__ int q8_value(float x, float scale) {
+    return scale > 0.f ? (int)fminf(fmaxf(rintf(x / scale), -127.f), 127.f) : 0;
+}
+
+// One 256-wide row held 4 consecutive elements a lane (lane l: dims 4l..4l+3,
+// so a 32-dim block is 8 lanes) stored in the int8 format: its 256 values at
+// `vals`, its 8 scales at `scales`. The block max is exact in any order.
+__device__ __forceinline__ void q8_store_row(f16x4 y, signed char* vals, f16* scales, int lane) {
+    float a = fmaxf(fmaxf(fabsf((float)y[0]), fabsf((float)y[1])),
+                    fmaxf(fabsf((float)y[2]), fabsf((float)y[3])));
+    a = fmaxf(a, lane_xor(a, 4));
+    a = fmaxf(a, dpp_xor2(a));
+    a = fmaxf(a, dpp_xor1(a));
+    const f16 sh = q8_scale(a);
+    const float sc = (float)sh;
+    uint32_t packed = 0;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) packed |= (uint32_t)(q8_value((float)y[c], sc) & 0xff) << (8 * c);
+    *(uint32_t*)(vals + 4 * lane) = packed;
+    if ((lane & 7) == 0) scales[lane >> 3] = sh;
+}
+
+typedef f16 f16x2 __attribute__((ext_vector_type(2)));
+
+// Four int8 (one dword, byte 0 first) to fp16(byte * s): each byte is made an
+// exact fp16 by placing (byte + 128) in the mantissa of 1024 (0x64XX is
+// 1024 + XX) and subtracting 1152; the product with the scale rounds once.
+__device__ __forceinline__ f16x4 q8_deq4(uint32_t b, f16x2 s2) {
+    const uint32_t u = b ^ 0x80808080u;
+    const uint32_t lo = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);
+    const uint32_t hi = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);
+    const f16x2 off = {(f16)1152.f, (f16)1152.f};
+    const f16x2 a = (__builtin_bit_cast(f16x2, lo) - off) * s2;
+    const f16x2 c = (__builtin_bit_cast(f16x2, hi) - off) * s2;
+    return (f16x4){a[0], a[1], c[0], c[1]};
 }
 
 // ---------------------------------------------------------------------------

@@ -39,3 +39,20 @@ SPLIT_MAX = 64
 SPLIT_T_MAX = 4
 
 GDN_CHUNK = 64
+
+# The int8 KV cache (runtime.py:117-129): per position and kv head, 256 int8
+# values and 8 fp16 block scales; a buffer of capacity max_pos holds all the
+# values first, then all the scales.
+KV8_BLOCK = 32
+KV8_ROW = HEAD_DIM + 2 * (HEAD_DIM // KV8_BLOCK)   # bytes a position and kv head
+# attention_dec_q8's split policy as the reference runtime sets it
+# (runtime.py:219-220): at least DEC_TMIN 64-row tiles a split, at most
+# DEC_SMAX splits.
+DEC_TMIN = 1
+DEC_SMAX = 28
+LOG2E = 1.4426950408889634
+
+
+def kv8_nbytes(max_pos: int, n_kv_heads: int = N_KV, head_dim: int = HEAD_DIM) -> int:
+    """Bytes of one layer's int8 K (or V) buffer of capacity max_pos."""
+    return max_pos * n_kv_heads * (head_dim + 2 * (head_dim // KV8_BLOCK))

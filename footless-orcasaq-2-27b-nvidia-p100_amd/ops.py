@@ -21,11 +21,12 @@ import ctypes
 import torch
 
 from . import _lib
-from .geometry import (ATTN_SCALE, GATE_OFF, GDN_CHUNK, GDN_GROUP, GDN_K, GDN_K_HEADS,
-                       GDN_NORM_EPS, GDN_V, GDN_V_HEADS, HEAD_DIM, L2_EPS, N_HEADS, N_KV, NORM_EPS,
-                       Q_PITCH, Q_SCALE, QKV_ROWS, ROPE_DIM, ROPE_THETA, SPLIT_MAX, SPLIT_ROWS)
+from .geometry import (ATTN_SCALE, DEC_SMAX, DEC_TMIN, GATE_OFF, GDN_CHUNK, GDN_GROUP, GDN_K,
+                       GDN_K_HEADS, GDN_NORM_EPS, GDN_V, GDN_V_HEADS, HEAD_DIM, L2_EPS, LOG2E,
+                       N_HEADS, N_KV, NORM_EPS, Q_PITCH, Q_SCALE, QKV_ROWS, ROPE_DIM, ROPE_THETA,
+                       SPLIT_MAX, SPLIT_ROWS, kv8_nbytes)
 
-F16, F32 = torch.float16, torch.float32
+F16, F32, I8 = torch.float16, torch.float32, torch.int8
 
 
 def _stream():
@@ -219,6 +220,142 @@ def attention_prefill(q, kcache, vcache, *, pos0: int, T: int | None = None, z=N
               _ptr(kcache, F16, "kcache", (layer + 1) * max_pos * row),
               _ptr(vcache, F16, "vcache", (layer + 1) * max_pos * row), layer, n_q_heads,
               n_kv_heads, head_dim, pos0, max_pos, float(scale), T,
+              _ptr(z, F16, "z", T * n_q_heads * z.shape[-1]), z.shape[-1], _stream())
+    return z
+
+
+# ---------------------------------------------------------------------------
+# int8 KV cache (kernels.cu:486-520's format): one flat int8 buffer a layer
+# and K / V of kv8_nbytes(max_pos) bytes -- the values [max_pos, n_kv, 256],
+# then the fp16 scales [max_pos, n_kv, 8]. A flat buffer carries no shape, so
+# these take max_pos explicitly.
+# ---------------------------------------------------------------------------
+
+def kv8_cache(max_pos: int, n_kv_heads: int = N_KV, head_dim: int = HEAD_DIM, device="cuda"):
+    """A zeroed int8 cache buffer of capacity max_pos."""
+    return torch.zeros(kv8_nbytes(max_pos, n_kv_heads, head_dim), dtype=I8, device=device)
+
+
+def _kv8(c, name, max_pos, n_kv_heads, head_dim):
+    _contig(c, name)
+    return _ptr(c, I8, name, kv8_nbytes(max_pos, n_kv_heads, head_dim))
+
+
+def kv_store_q8(k, v, kcache, vcache, *, pos0: int, max_pos: int, T: int | None = None,
+                n_kv_heads: int = N_KV, head_dim: int = HEAD_DIM):
+    """kernels.cu:486-520 (runtime.py:2813-2815 with KV8): k, v [T, n_kv,
+    head_dim] fp16 quantized into positions pos0.. of the int8 buffers."""
+    T = k.shape[0] if T is None else T
+    row = n_kv_heads * head_dim
+    _contig(k, "k"), _contig(v, "v")
+    _lib.call("fl_kv_store_q8", _ptr(k, F16, "k", T * row), _ptr(v, F16, "v", T * row),
+              _kv8(kcache, "kcache", max_pos, n_kv_heads, head_dim),
+              _kv8(vcache, "vcache", max_pos, n_kv_heads, head_dim), 0, pos0, T, n_kv_heads,
+              head_dim, max_pos, _stream())
+
+
+def attn_prep_q8(qg, k, v, wq, wk, kcache, vcache, *, pos0: int, max_pos: int,
+                 T: int | None = None, n_q_heads: int = N_HEADS, n_kv_heads: int = N_KV,
+                 head_dim: int = HEAD_DIM, q_pitch: int = Q_PITCH, rope_dim: int = ROPE_DIM,
+                 theta: float = ROPE_THETA, eps: float = NORM_EPS):
+    """attn_prep_q8 (kernels.cu:837-908, runtime.py:2922-2930): attn_prep with
+    the int8 store."""
+    T = qg.shape[0] if T is None else T
+    row = n_kv_heads * head_dim
+    _lib.call("fl_attn_prep_q8", _ptr(qg, F16, "qg", T * n_q_heads * q_pitch), q_pitch,
+              _ptr(k, F16, "k", T * row), _ptr(v, F16, "v", T * row),
+              _ptr(wq, F32, "wq", head_dim), _ptr(wk, F32, "wk", head_dim),
+              _kv8(kcache, "kcache", max_pos, n_kv_heads, head_dim),
+              _kv8(vcache, "vcache", max_pos, n_kv_heads, head_dim), 0, n_q_heads, n_kv_heads,
+              head_dim, pos0, max_pos, T, rope_dim, float(theta), float(eps), _stream())
+
+
+def attention_split_gqa_q8(q, kcache, vcache, pacc, pm, pd, *, pos0: int, max_pos: int, T: int,
+                           n_q_heads: int = N_HEADS, n_kv_heads: int = N_KV,
+                           head_dim: int = HEAD_DIM, q_pitch: int = Q_PITCH,
+                           scale: float = ATTN_SCALE, split_rows: int = SPLIT_ROWS,
+                           split: int = SPLIT_MAX):
+    """kernels.cu:910-1047: attention_split_gqa's partials over an int8 cache."""
+    parts = T * n_q_heads * split
+    _lib.call("fl_attention_split_gqa_q8", _ptr(q, F16, "q", T * n_q_heads * q_pitch),
+              _kv8(kcache, "kcache", max_pos, n_kv_heads, head_dim),
+              _kv8(vcache, "vcache", max_pos, n_kv_heads, head_dim),
+              _ptr(pacc, F32, "pacc", parts * head_dim), _ptr(pm, F32, "pm", parts),
+              _ptr(pd, F32, "pd", parts), 0, n_q_heads, n_kv_heads, head_dim, q_pitch, pos0,
+              max_pos, float(scale), split_rows, T, split, _stream())
+
+
+def attention_dec_q8(q, kcache, vcache, pacc, pm, pd, *, pos0: int, max_pos: int, T: int,
+                     n_q_heads: int = N_HEADS, n_kv_heads: int = N_KV, q_pitch: int = Q_PITCH,
+                     sl2: float = ATTN_SCALE * LOG2E, tmin: int = DEC_TMIN,
+                     smax: int = DEC_SMAX):
+    """kernels.cu:1049-1335 (runtime.py:2907-2916): int8 decode partials of T
+    tokens -- pacc [T, n_q_heads, smax, 256], pm (log2 units) / pd [T,
+    n_q_heads, smax]; only each token's first St splits are written."""
+    parts = T * n_q_heads * smax
+    _lib.call("fl_attention_dec_q8", _ptr(q, F16, "q", T * n_q_heads * q_pitch),
+              _kv8(kcache, "kcache", max_pos, n_kv_heads, HEAD_DIM),
+              _kv8(vcache, "vcache", max_pos, n_kv_heads, HEAD_DIM),
+              _ptr(pacc, F32, "pacc", parts * HEAD_DIM), _ptr(pm, F32, "pm", parts),
+              _ptr(pd, F32, "pd", parts), n_q_heads, n_kv_heads, q_pitch, pos0, max_pos,
+              float(sl2), tmin, smax, T, _stream())
+
+
+def attention_dec_merge(pacc, pm, pd, z, *, pos0: int, T: int, n_q_heads: int = N_HEADS,
+                        z_pitch: int = HEAD_DIM, tmin: int = DEC_TMIN, smax: int = DEC_SMAX,
+                        gate=None, g_pitch: int = Q_PITCH, g_off: int = GATE_OFF):
+    """kernels.cu:1336-1385 (runtime.py:2917-2920): the merge of
+    attention_dec_q8's partials, with the sigmoid gate when `gate` is given."""
+    parts = T * n_q_heads * smax
+    _lib.call("fl_attention_dec_merge", _ptr(pacc, F32, "pacc", parts * HEAD_DIM),
+              _ptr(pm, F32, "pm", parts), _ptr(pd, F32, "pd", parts),
+              _ptr(z, F16, "z", T * n_q_heads * z_pitch), n_q_heads, z_pitch, pos0, tmin, smax,
+              T, _ptr(gate, F16, "gate", T * n_q_heads * g_pitch), g_pitch, g_off, _stream())
+
+
+def attn_decode_q8(qg, kcaches, vcaches, pos0s, caps, *, z=None, gate: bool = True,
+                   n_kv_heads: int = N_KV, scale: float = ATTN_SCALE,
+                   split_rows: int = SPLIT_ROWS, split: int = SPLIT_MAX, work=None):
+    """attn_decode over int8 caches: kcaches / vcaches per-sequence int8 buffers
+    of capacities caps. Returns z [B, T, n_q_heads, 256] fp16."""
+    B, T, n_q_heads, q_pitch = qg.shape
+    _contig(qg, "qg")
+    if z is None:
+        z = torch.empty((B, T, n_q_heads, HEAD_DIM), dtype=F16, device=qg.device)
+    need = attn_decode_work_bytes(B, T, n_q_heads, HEAD_DIM, split)
+    if work is None:
+        work = torch.empty(need, dtype=torch.uint8, device=qg.device)
+    if not (len(kcaches) == len(vcaches) == len(pos0s) == len(caps) == B):
+        raise ValueError("one cache pair, pos0 and capacity per sequence")
+    for b in range(B):
+        _kv8(kcaches[b], "kcache", caps[b], n_kv_heads, HEAD_DIM)
+        _kv8(vcaches[b], "vcache", caps[b], n_kv_heads, HEAD_DIM)
+    _lib.call("fl_attn_decode_q8", _ptr(qg, F16, "qg", B * T * n_q_heads * q_pitch), q_pitch,
+              _lib.ptr_array([c.data_ptr() for c in kcaches]),
+              _lib.ptr_array([c.data_ptr() for c in vcaches]), _lib.int_array(pos0s),
+              _lib.int_array(caps), B, T, n_q_heads, n_kv_heads, HEAD_DIM, float(scale),
+              split_rows, split, qg.data_ptr() if gate else None, q_pitch, GATE_OFF if gate else 0,
+              _ptr(z, F16, "z", B * T * n_q_heads * HEAD_DIM), z.shape[-1],
+              _ptr(work, torch.uint8, "work", need), work.numel(), _stream())
+    return z
+
+
+def attention_prefill_q8(q, kcache, vcache, *, pos0: int, max_pos: int, T: int | None = None,
+                         z=None, k_new=None, v_new=None, n_q_heads: int = N_HEADS,
+                         n_kv_heads: int = N_KV, q_pitch: int | None = None,
+                         scale: float = ATTN_SCALE):
+    """attention_prefill_fh_q8 (kernels.cu:2778-2786) over an int8 cache, with
+    kv_store_q8 of k_new / v_new fused in front when given."""
+    T = q.shape[0] if T is None else T
+    q_pitch = q.shape[-1] if q_pitch is None else q_pitch
+    row = n_kv_heads * HEAD_DIM
+    if z is None:
+        z = torch.empty((T, n_q_heads, HEAD_DIM), dtype=F16, device=q.device)
+    _lib.call("fl_attention_prefill_q8", _ptr(q, F16, "q", T * n_q_heads * q_pitch), q_pitch,
+              _ptr(k_new, F16, "k_new", T * row), _ptr(v_new, F16, "v_new", T * row),
+              _kv8(kcache, "kcache", max_pos, n_kv_heads, HEAD_DIM),
+              _kv8(vcache, "vcache", max_pos, n_kv_heads, HEAD_DIM), 0, n_q_heads, n_kv_heads,
+              HEAD_DIM, pos0, max_pos, float(scale), T,
               _ptr(z, F16, "z", T * n_q_heads * z.shape[-1]), z.shape[-1], _stream())
     return z
 

@@ -149,6 +149,81 @@ int fl_attention_prefill(const void* q, int q_pitch, const void* k_new, const vo
                          int head_dim, int pos0, int max_pos, float scale, int T, void* z,
                          int z_pitch, fl_stream_t stream);
 
+/* ---- int8 KV cache --------------------------------------------------------
+ * The reference's int8 cache format (kernels.cu:486-520, runtime.py:119-132),
+ * one buffer a layer and K / V: for capacity max_pos, the values
+ * [max_pos][n_kv_heads][256] int8, then the scales [max_pos][n_kv_heads][8]
+ * f16 at byte max_pos * n_kv_heads * 256 (256 + 16 bytes a position and kv
+ * head; 1088 for the model's 4 kv heads). A 32-dim block shares the scale
+ * f16(absmax / 127) and stores rint(x / scale) clamped to [-127, 127], 0 where
+ * the scale is 0. `layer` must be 0 (one buffer a layer), head_dim 256.
+ * The attention entry points read fp16(byte * scale) -- one rounding of the
+ * product, where the reference's decode kept it in fp32. */
+
+/* kv_store_q8: k, v [T][n_kv_heads][256] f16 into positions pos0 + t.
+ * Replaces kernels.cu:486-520 kv_store_q8, launched at runtime.py:2813-2815,
+ * 2895-2897, 3247-3249. Differs: pos0 + T > max_pos is FL_EINVAL. */
+int fl_kv_store_q8(const void* k, const void* v, void* kcache, void* vcache, int layer,
+                   int pos0, int T, int n_kv_heads, int head_dim, int max_pos,
+                   fl_stream_t stream);
+
+/* attn_prep_q8: fl_attn_prep with the int8 store -- q / k norms, rope and
+ * kv_store_q8 in one launch, the same values as the separate steps.
+ * Replaces kernels.cu:837-908 attn_prep_q8, launched at runtime.py:2922-2930. */
+int fl_attn_prep_q8(void* qg, int q_pitch, void* k, const void* v, const float* wq,
+                    const float* wk, void* kcache, void* vcache, int layer, int n_q_heads,
+                    int n_kv_heads, int head_dim, int pos0, int max_pos, int T, int rope_dim,
+                    float theta, float eps, fl_stream_t stream);
+
+/* attention_split_gqa_q8: fl_attention_split_gqa over an int8 cache (the same
+ * split rule and partials). Replaces kernels.cu:910-1047, launched at
+ * runtime.py:2832-2837 with KV8. */
+int fl_attention_split_gqa_q8(const void* q, const void* kcache, const void* vcache,
+                              float* pacc, float* pm, float* pd, int layer, int n_q_heads,
+                              int n_kv_heads, int head_dim, int q_pitch, int pos0, int max_pos,
+                              float scale, int split_rows, int T, int split,
+                              fl_stream_t stream);
+
+/* attention_dec_q8: decode partials of T tokens at pos0.. over an int8 cache.
+ * Token t (length len = pos0 + t + 1) has nkt = ceil(len / 64) tiles of 64
+ * rows and St = min(smax, ceil(nkt / tmin)) splits; split s covers tiles
+ * [nkt*s/St, nkt*(s+1)/St). Writes pacc [T][n_q_heads][smax][256] f32,
+ * pm / pd [T][n_q_heads][smax] f32 for s < St only, pm in log2 units
+ * (sl2 = scale * log2 e multiplies q.k). Each token's partials equal the
+ * T = 1 call's at its position, bit for bit.
+ * Replaces kernels.cu:1049-1335 attention_dec_q8, runtime.py:2907-2916.
+ * Supported: head_dim 256, T * n_q_heads / n_kv_heads <= 32. */
+int fl_attention_dec_q8(const void* q, const void* kcache, const void* vcache, float* pacc,
+                        float* pm, float* pd, int n_q_heads, int n_kv_heads, int q_pitch,
+                        int pos0, int max_pos, float sl2, int tmin, int smax, int T,
+                        fl_stream_t stream);
+
+/* attention_dec_merge (+ gate when gate != NULL): z = f16_sat(sum_s 2^(m_s -
+ * M) acc_s / sum_s 2^(m_s - M) d_s) over token t's first St partials, then
+ * z = f16_sat(z * sigmoid(gate[t][h][g_off + d])). z [T][n_q_heads][z_pitch].
+ * Replaces kernels.cu:1336-1385 attention_dec_merge / _gate,
+ * runtime.py:2917-2920. */
+int fl_attention_dec_merge(const float* pacc, const float* pm, const float* pd, void* z,
+                           int n_q_heads, int z_pitch, int pos0, int tmin, int smax, int T,
+                           const void* gate, int g_pitch, int g_off, fl_stream_t stream);
+
+/* fl_attn_decode over int8 caches of capacities cap[b] (same arguments, work
+ * from fl_attn_decode_work_bytes). Replaces the per-sequence _attn_dec loop of
+ * runtime.py:2865-2878 (the batched _step_rows path, runtime.py:1784-1860). */
+int fl_attn_decode_q8(const void* qg, int q_pitch, const void* const* kcache,
+                      const void* const* vcache, const int* pos0, const int* cap, int B, int T,
+                      int n_q_heads, int n_kv_heads, int head_dim, float scale, int split_rows,
+                      int split, const void* gate, int g_pitch, int g_off, void* z, int z_pitch,
+                      void* work, size_t work_bytes, fl_stream_t stream);
+
+/* fl_attention_prefill over an int8 cache (k_new / v_new, when given, are
+ * stored first with kv_store_q8). Replaces kernels.cu:2778-2786
+ * attention_prefill_fh_q8 (+ merge_fh), launched by runtime.py:2943-2959. */
+int fl_attention_prefill_q8(const void* q, int q_pitch, const void* k_new, const void* v_new,
+                            void* kcache, void* vcache, int layer, int n_q_heads,
+                            int n_kv_heads, int head_dim, int pos0, int max_pos, float scale,
+                            int T, void* z, int z_pitch, fl_stream_t stream);
+
 /* ---- causal conv ----------------------------------------------------------
  * conv1d_causal over `dim` channels of rows x [T][row_stride] f16: E =
  * [st_in (width-1 frames, ZERO if pos0 == 0) | x], y[t][d] =

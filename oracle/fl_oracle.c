@@ -142,9 +142,6 @@ static float tree_xor(const float* in, int n) {
 }
 
 /* ======================================================================== */
-/* kv_store -- kernels.cu:465-484                                            */
-/* ======================================================================== */
-/* ======================================================================== */
 /* attention prep: rmsnorm1p (kernels.cu:241-272), rope_partial (397-455)    */
 /* ======================================================================== */
 /* rmsnorm1p over rows of n = 256 (one element a thread of the reference's
@@ -231,6 +228,9 @@ ORC_API void orc_rmsnorm_gated(const uint16_t* o, const uint16_t* z, const float
         }
 }
 
+/* ======================================================================== */
+/* kv_store -- kernels.cu:465-484                                            */
+/* ======================================================================== */
 ORC_API void orc_kv_store(const uint16_t* k, const uint16_t* v, uint16_t* kcache,
                           uint16_t* vcache, int layer, int pos0, int n_kv_heads,
                           int head_dim, int max_pos, int T) {
@@ -421,11 +421,12 @@ static uint16_t hfma16(uint16_t a, uint16_t b, uint16_t c) {
     return d2h_exact(s, err);
 }
 
-ORC_API void orc_attention_prefill(const uint16_t* q, const uint16_t* kcache,
-                                   const uint16_t* vcache, uint16_t* z, int layer,
-                                   int n_q_heads, int n_kv_heads, int head_dim, int q_pitch,
-                                   int z_pitch, int pos0, int max_pos, float scale, int T,
-                                   int pv_fp16) {
+/* The prefill over K given as float rows (the fp16 K widened exactly, or the
+ * int8 K dequantized exactly) and V as fp16 rows, both [rows][n_kv_heads]
+ * [head_dim] from the layer's first position. */
+static void prefill_core(const uint16_t* q, const float* kf, const uint16_t* vh, uint16_t* z,
+                         int n_q_heads, int n_kv_heads, int head_dim, int q_pitch, int z_pitch,
+                         int pos0, float scale, int T, int pv_fp16) {
     const int G = n_q_heads / n_kv_heads;
     const long long kv_stride = (long long)n_kv_heads * head_dim;
     const float sl2 = scale * 1.4426950408889634f;
@@ -435,8 +436,8 @@ ORC_API void orc_attention_prefill(const uint16_t* q, const uint16_t* kcache,
             float o[1024], ot[1024], s[64];
             uint16_t oh[1024];
             const int hkv = head / G;
-            const uint16_t* kb = kcache + (long long)layer * max_pos * kv_stride + (long long)hkv * head_dim;
-            const uint16_t* vb = vcache + (long long)layer * max_pos * kv_stride + (long long)hkv * head_dim;
+            const float* kb = kf + (long long)hkv * head_dim;
+            const uint16_t* vb = vh + (long long)hkv * head_dim;
             const uint16_t* qr = q + ((size_t)t * n_q_heads + head) * q_pitch;
             const int qpos = pos0 + t;
             float mrow = -1e30f, lrow = 0.f;
@@ -446,9 +447,9 @@ ORC_API void orc_attention_prefill(const uint16_t* q, const uint16_t* kcache,
                 for (int j = 0; j < 64; j++) {
                     const int kv = kv0 + j;
                     if (kv <= qpos) {
-                        const uint16_t* kr = kb + (long long)kv * kv_stride;
+                        const float* kr = kb + (long long)kv * kv_stride;
                         float acc = 0.f;
-                        for (int d = 0; d < head_dim; d++) acc = fmaf(orc_h2f(qr[d]), orc_h2f(kr[d]), acc);
+                        for (int d = 0; d < head_dim; d++) acc = fmaf(orc_h2f(qr[d]), kr[d], acc);
                         s[j] = acc * sl2;
                     } else {
                         s[j] = -1e30f;
@@ -492,6 +493,21 @@ ORC_API void orc_attention_prefill(const uint16_t* q, const uint16_t* kcache,
         }
 }
 
+ORC_API void orc_attention_prefill(const uint16_t* q, const uint16_t* kcache,
+                                   const uint16_t* vcache, uint16_t* z, int layer,
+                                   int n_q_heads, int n_kv_heads, int head_dim, int q_pitch,
+                                   int z_pitch, int pos0, int max_pos, float scale, int T,
+                                   int pv_fp16) {
+    const long long kv_stride = (long long)n_kv_heads * head_dim;
+    const long long n = (long long)(pos0 + T) * kv_stride;
+    const uint16_t* kb = kcache + (long long)layer * max_pos * kv_stride;
+    float* kf = (float*)malloc(sizeof(float) * (size_t)n);
+    for (long long i = 0; i < n; i++) kf[i] = orc_h2f(kb[i]);
+    prefill_core(q, kf, vcache + (long long)layer * max_pos * kv_stride, z, n_q_heads,
+                 n_kv_heads, head_dim, q_pitch, z_pitch, pos0, scale, T, pv_fp16);
+    free(kf);
+}
+
 /* Exact causal GQA softmax attention in double: the closed form every fp32
  * attention restatement above is pinned against. out [T][n_q_heads][head_dim]
  * double. Query (t, head) sees rows [0, pos0 + t] of kv head head / G. */
@@ -524,6 +540,245 @@ ORC_API void orc_attention_exact_f64(const uint16_t* q, const uint16_t* kcache,
             for (int d = 0; d < head_dim; d++) {
                 double a = 0.0;
                 for (int r = 0; r < n; r++) a += sc[r] * (double)orc_h2f(vb[(long long)r * kv_stride + d]);
+                orow[d] = a / den;
+            }
+            free(sc);
+        }
+}
+
+/* ======================================================================== */
+/* int8 KV cache -- kv_store_q8 kernels.cu:486-520, attention_dec_q8        */
+/* 1049-1335, attention_dec_merge 1336-1385, attention_prefill_fh_q8        */
+/* 2778-2786 (staging 2500-2509, 2585-2620)                                  */
+/* ======================================================================== */
+/* The format: one buffer a layer of capacity max_pos, values
+ * [max_pos][n_kv_heads][head_dim] int8, then fp16 scales
+ * [max_pos][n_kv_heads][head_dim / 32] at byte max_pos * n_kv_heads *
+ * head_dim. A 32-dim block's scale is f16(absmax / 127); a value stores
+ * rint(x / scale) clamped to [-127, 127], 0 where the scale is 0. */
+static inline const uint16_t* q8_scales(const int8_t* cache, int max_pos, int n_kv, int hd) {
+    return (const uint16_t*)(cache + (long long)max_pos * n_kv * hd);
+}
+
+ORC_API void orc_kv_store_q8(const uint16_t* k, const uint16_t* v, int8_t* kcache,
+                             int8_t* vcache, int pos0, int n_kv_heads, int head_dim,
+                             int max_pos, int T) {
+    const long long stride = (long long)n_kv_heads * head_dim;
+    const int nsb = head_dim / 32;
+    for (int t = 0; t < T; t++) {
+        const int pos = pos0 + t;
+        if (pos >= max_pos) continue;
+        for (int h = 0; h < n_kv_heads; h++)
+            for (int which = 0; which < 2; which++) {
+                const uint16_t* src = (which ? v : k) + ((size_t)t * n_kv_heads + h) * head_dim;
+                int8_t* cache = which ? vcache : kcache;
+                uint16_t* sc = (uint16_t*)(cache + (long long)max_pos * stride);
+                for (int b = 0; b < nsb; b++) {
+                    float a = 0.f;
+                    for (int i = 0; i < 32; i++) a = fmaxf(a, fabsf(orc_h2f(src[32 * b + i])));
+                    const uint16_t sh = orc_f2h(a / 127.0f);
+                    const float scale = orc_h2f(sh);
+                    for (int i = 0; i < 32; i++) {
+                        const float x = orc_h2f(src[32 * b + i]);
+                        const float qv = scale > 0.f ? fminf(fmaxf(rintf(x / scale), -127.f), 127.f) : 0.f;
+                        cache[(long long)pos * stride + (long long)h * head_dim + 32 * b + i] = (int8_t)(int)qv;
+                    }
+                    sc[((long long)pos * n_kv_heads + h) * nsb + b] = sh;
+                }
+            }
+    }
+}
+
+/* attention_dec_q8's split rule (kernels.cu:1107-1118) */
+static void dec_split(int len, int s, int tmin, int smax, int* lo, int* hi) {
+    const int nkt = (len + 63) / 64;
+    int st = (nkt + tmin - 1) / tmin;
+    st = st > smax ? smax : st;
+    *lo = s < st ? (int)((long long)nkt * s / st) : 0;
+    *hi = s < st ? (int)((long long)nkt * (s + 1) / st) : 0;
+}
+
+ORC_API int orc_dec_split_count(int len, int tmin, int smax) {
+    const int nkt = (len + 63) / 64;
+    const int st = (nkt + tmin - 1) / tmin;
+    return st > smax ? smax : st;
+}
+
+/* attention_dec_q8 (G = 6, head_dim 256), one (token, q head, split) at a
+ * time in the reference's arithmetic order: q staged as fp32 q * sl2; a
+ * row's score = sum over the 8 parts of (fmaf chain over the part's 32 dims
+ * of q * byte) * scale, the parts added as the xor-1/2/4 butterfly; masked
+ * rows -inf; per 64-row tile the max, c = exp2(m - m_new) (1 if both -inf),
+ * p = exp2(x - m_new), the tile sum as the reference's lane / warp tree
+ * (rows rp and rp + 32 of thread rp, then 4 rp's a warp, then the 8 warp
+ * sums pairwise); O += P V by 4 row slots (rows slot + 4i, V = byte * scale in
+ * fp32), the slots summed in order at the end. pm in log2 units. Partials
+ * s >= St are not written. */
+ORC_API void orc_attention_dec_q8(const uint16_t* q, const int8_t* kcache, const int8_t* vcache,
+                                  float* pacc, float* pm, float* pd, int n_q_heads,
+                                  int n_kv_heads, int q_pitch, int pos0, int max_pos, float sl2,
+                                  int tmin, int smax, int T) {
+    const int G = n_q_heads / n_kv_heads;
+    const long long kvs = (long long)n_kv_heads * 256;
+    const uint16_t* ksc = q8_scales(kcache, max_pos, n_kv_heads, 256);
+    const uint16_t* vsc = q8_scales(vcache, max_pos, n_kv_heads, 256);
+    #pragma omp parallel for collapse(2) schedule(dynamic)
+    for (int t = 0; t < T; t++)
+        for (int head = 0; head < n_q_heads; head++) {
+            const int hkv = head / G;
+            const int len = pos0 + t + 1, qpos = pos0 + t;
+            float qs[256];
+            const uint16_t* qr = q + ((size_t)t * n_q_heads + head) * q_pitch;
+            for (int d = 0; d < 256; d++) qs[d] = orc_h2f(qr[d]) * sl2;
+            for (int s = 0; s < smax; s++) {
+                int tlo, thi;
+                dec_split(len, s, tmin, smax, &tlo, &thi);
+                if (thi <= tlo) continue;
+                float m = -INFINITY, dp = 0.f;
+                static __thread float acc[4][256];
+                memset(acc, 0, sizeof(acc));
+                for (int tile = tlo; tile < thi; tile++) {
+                    float x[64];
+                    float mt = -INFINITY;
+                    for (int i = 0; i < 64; i++) {
+                        const int row = tile * 64 + i;
+                        if (row > qpos) { x[i] = -INFINITY; continue; }
+                        const int8_t* kr = kcache + (long long)row * kvs + (long long)hkv * 256;
+                        float v[8];
+                        for (int part = 0; part < 8; part++) {
+                            float sa = 0.f;
+                            for (int d = 0; d < 32; d++)
+                                sa = fmaf(qs[32 * part + d], (float)kr[32 * part + d], sa);
+                            v[part] = sa * orc_h2f(ksc[((long long)row * n_kv_heads + hkv) * 8 + part]);
+                        }
+                        x[i] = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
+                        mt = fmaxf(mt, x[i]);
+                    }
+                    const float mn = fmaxf(m, mt);
+                    const float c = mn == -INFINITY ? 1.f : exp2f(m - mn);
+                    m = mn;
+                    for (int sl = 0; sl < 4; sl++)
+                        for (int d = 0; d < 256; d++) acc[sl][d] *= c;
+                    float p[64];
+                    for (int i = 0; i < 64; i++) p[i] = x[i] == -INFINITY ? 0.f : exp2f(x[i] - mn);
+                    float srp[32], wsum[8];
+                    for (int rp = 0; rp < 32; rp++) srp[rp] = p[rp] + p[rp + 32];
+                    for (int w = 0; w < 8; w++)
+                        wsum[w] = (srp[4 * w] + srp[4 * w + 1]) + (srp[4 * w + 2] + srp[4 * w + 3]);
+                    const float tsum = ((wsum[0] + wsum[1]) + (wsum[2] + wsum[3])) +
+                                       ((wsum[4] + wsum[5]) + (wsum[6] + wsum[7]));
+                    dp = fmaf(dp, c, tsum);
+                    for (int sl = 0; sl < 4; sl++)
+                        for (int i = 0; i < 16; i++) {
+                            const int row = tile * 64 + sl + 4 * i;
+                            if (p[sl + 4 * i] == 0.f) {
+                                /* the reference still adds p * v = +0 (v finite) */
+                                continue;
+                            }
+                            const int8_t* vr = vcache + (long long)row * kvs + (long long)hkv * 256;
+                            for (int d = 0; d < 256; d++) {
+                                const float vs = orc_h2f(vsc[((long long)row * n_kv_heads + hkv) * 8 + d / 32]);
+                                acc[sl][d] = fmaf(p[sl + 4 * i], (float)vr[d] * vs, acc[sl][d]);
+                            }
+                        }
+                }
+                const size_t pi = ((size_t)t * n_q_heads + head) * smax + s;
+                for (int d = 0; d < 256; d++)
+                    pacc[pi * 256 + d] = ((acc[0][d] + acc[1][d]) + acc[2][d]) + acc[3][d];
+                pm[pi] = m;
+                pd[pi] = dp;
+            }
+        }
+}
+
+/* attention_dec_merge (+ _gate when g != NULL) */
+ORC_API void orc_attention_dec_merge(const float* pacc, const float* pm, const float* pd,
+                                     uint16_t* z, int n_q_heads, int z_pitch, int pos0, int tmin,
+                                     int smax, int T, const uint16_t* g, int g_pitch, int g_off) {
+    for (int t = 0; t < T; t++)
+        for (int head = 0; head < n_q_heads; head++) {
+            const int st = orc_dec_split_count(pos0 + t + 1, tmin, smax);
+            const size_t p0 = ((size_t)t * n_q_heads + head) * smax;
+            float M = -INFINITY;
+            for (int s = 0; s < st; s++) M = fmaxf(M, pm[p0 + s]);
+            for (int d = 0; d < 256; d++) {
+                float num = 0.f, den = 0.f;
+                for (int s = 0; s < st; s++) {
+                    const float e = exp2f(pm[p0 + s] - M);
+                    num = fmaf(e, pacc[(p0 + s) * 256 + d], num);
+                    den = fmaf(e, pd[p0 + s], den);
+                }
+                uint16_t o = orc_f16_sat(num / den);
+                if (g) {
+                    const float gv = orc_h2f(g[((size_t)t * n_q_heads + head) * g_pitch + g_off + d]);
+                    o = orc_f16_sat(orc_h2f(o) * sigmoid_f(gv));
+                }
+                z[((size_t)t * n_q_heads + head) * z_pitch + d] = o;
+            }
+        }
+}
+
+/* attention_prefill_fh_q8: K dequantized exactly in fp32 (byte * scale,
+ * kernels.cu:2585-2590), V as fp16(byte * scale), one rounding
+ * (kernels.cu:2500-2509, 2615-2620), then the fp16 prefill's arithmetic. */
+ORC_API void orc_attention_prefill_q8(const uint16_t* q, const int8_t* kcache,
+                                      const int8_t* vcache, uint16_t* z, int n_q_heads,
+                                      int n_kv_heads, int head_dim, int q_pitch, int z_pitch,
+                                      int pos0, int max_pos, float scale, int T, int pv_fp16) {
+    const long long kvs = (long long)n_kv_heads * head_dim;
+    const long long n = (long long)(pos0 + T) * kvs;
+    const uint16_t* ksc = q8_scales(kcache, max_pos, n_kv_heads, head_dim);
+    const uint16_t* vsc = q8_scales(vcache, max_pos, n_kv_heads, head_dim);
+    float* kf = (float*)malloc(sizeof(float) * (size_t)n);
+    uint16_t* vh = (uint16_t*)malloc(sizeof(uint16_t) * (size_t)n);
+    for (long long i = 0; i < n; i++) {
+        const long long blk = i / 32;   /* (row, head, block): the scales' index */
+        kf[i] = (float)kcache[i] * orc_h2f(ksc[blk]);
+        vh[i] = orc_f2h((float)vcache[i] * orc_h2f(vsc[blk]));
+    }
+    prefill_core(q, kf, vh, z, n_q_heads, n_kv_heads, head_dim, q_pitch, z_pitch, pos0, scale,
+                 T, pv_fp16);
+    free(kf);
+    free(vh);
+}
+
+/* Exact causal GQA softmax attention in double over an int8 cache, the
+ * values dequantized exactly (byte * scale): the closed form the int8
+ * restatements are pinned against. */
+ORC_API void orc_attention_exact_f64_q8(const uint16_t* q, const int8_t* kcache,
+                                        const int8_t* vcache, double* out, int n_q_heads,
+                                        int n_kv_heads, int head_dim, int q_pitch, int pos0,
+                                        int max_pos, double scale, int T) {
+    const int G = n_q_heads / n_kv_heads;
+    const long long kvs = (long long)n_kv_heads * head_dim;
+    const uint16_t* ksc = q8_scales(kcache, max_pos, n_kv_heads, head_dim);
+    const uint16_t* vsc = q8_scales(vcache, max_pos, n_kv_heads, head_dim);
+    #pragma omp parallel for collapse(2) schedule(dynamic)
+    for (int t = 0; t < T; t++)
+        for (int head = 0; head < n_q_heads; head++) {
+            const int hkv = head / G;
+            const int n = pos0 + t + 1;
+            const uint16_t* qr = q + ((size_t)t * n_q_heads + head) * q_pitch;
+            double* sc = (double*)malloc(sizeof(double) * n);
+            double mx = -1e300;
+            for (int r = 0; r < n; r++) {
+                const long long base = (long long)r * kvs + (long long)hkv * head_dim;
+                double a = 0.0;
+                for (int d = 0; d < head_dim; d++)
+                    a += (double)orc_h2f(qr[d]) * (double)kcache[base + d] *
+                         (double)orc_h2f(ksc[(base + d) / 32]);
+                sc[r] = a * scale;
+                if (sc[r] > mx) mx = sc[r];
+            }
+            double den = 0.0;
+            for (int r = 0; r < n; r++) { sc[r] = exp(sc[r] - mx); den += sc[r]; }
+            double* orow = out + ((size_t)t * n_q_heads + head) * head_dim;
+            for (int d = 0; d < head_dim; d++) {
+                double a = 0.0;
+                for (int r = 0; r < n; r++) {
+                    const long long i = (long long)r * kvs + (long long)hkv * head_dim + d;
+                    a += sc[r] * (double)vcache[i] * (double)orc_h2f(vsc[i / 32]);
+                }
                 orow[d] = a / den;
             }
             free(sc);

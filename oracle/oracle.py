@@ -59,6 +59,11 @@ def lib() -> ctypes.CDLL:
             "orc_attn_gate": [_P, _P, _I, _I, _I, _I, _I, _I],
             "orc_attention_prefill": [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _F, _I, _I],
             "orc_attention_exact_f64": [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _D, _I],
+            "orc_kv_store_q8": [_P, _P, _P, _P, _I, _I, _I, _I, _I],
+            "orc_attention_dec_q8": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _I, _I, _I],
+            "orc_attention_dec_merge": [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P, _I, _I],
+            "orc_attention_prefill_q8": [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _F, _I, _I],
+            "orc_attention_exact_f64_q8": [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _D, _I],
             "orc_conv1d_causal": [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I],
             "orc_conv1d_causal_rows": [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I],
             "orc_l2norm_scaled": [_P, _P, _I, _I, _I, _F, _F, _I],
@@ -72,6 +77,8 @@ def lib() -> ctypes.CDLL:
             fn = getattr(L, name)
             fn.argtypes = args
             fn.restype = _I if name in ("orc_gdn_scan", "orc_gdn_decode", "orc_gdn_chunked") else None
+        L.orc_dec_split_count.argtypes = [_I, _I, _I]
+        L.orc_dec_split_count.restype = _I
         L.orc_f16_sat.argtypes = [_F]
         L.orc_f16_sat.restype = ctypes.c_uint16
         L.orc_det_expf.argtypes = [_F]
@@ -210,6 +217,110 @@ def attention_exact(q, kcache, vcache, *, layer=0, n_q_heads=24, n_kv_heads=4, h
     out = np.zeros((T, n_q_heads, head_dim), np.float64)
     lib().orc_attention_exact_f64(_p(q), _p(kcache), _p(vcache), _p(out), layer, n_q_heads,
                                   n_kv_heads, head_dim, q_pitch, pos0, max_pos, float(scale), T)
+    return out
+
+
+# --------------------------------------------------------------------------
+# int8 KV cache
+# --------------------------------------------------------------------------
+
+def kv8_buffer(max_pos, n_kv_heads=4, head_dim=256):
+    """An empty int8 cache buffer of capacity max_pos: values, then fp16 scales
+    (kernels.cu:486-490), as flat int8."""
+    return np.zeros(max_pos * n_kv_heads * (head_dim + 2 * head_dim // 32), np.int8)
+
+
+def kv8_split(buf, max_pos, n_kv_heads=4, head_dim=256):
+    """(values [max_pos, n_kv, head_dim] int8, scales [max_pos, n_kv, head_dim/32]
+    float16) views of an int8 cache buffer."""
+    nv = max_pos * n_kv_heads * head_dim
+    vals = buf[:nv].reshape(max_pos, n_kv_heads, head_dim)
+    scales = buf[nv:].view(np.float16).reshape(max_pos, n_kv_heads, head_dim // 32)
+    return vals, scales
+
+
+def kv_store_q8(k, v, kcache, vcache, pos0, max_pos, T, n_kv_heads=4, head_dim=256):
+    """kernels.cu:486-520. Updates the int8 buffers kcache / vcache in place."""
+    k, v = _h(k), _h(v)
+    assert kcache.dtype == np.int8 and vcache.dtype == np.int8
+    lib().orc_kv_store_q8(_p(k), _p(v), _p(kcache), _p(vcache), pos0, n_kv_heads, head_dim,
+                          max_pos, T)
+
+
+def attn_prep_q8(qg, k, v, wq, wk, kcache, vcache, *, pos0, T, max_pos, n_q_heads=24,
+                 n_kv_heads=4, head_dim=256, q_pitch=512, rope_dim=64, theta=1e7, eps=1e-6):
+    """attn_prep_q8 (kernels.cu:837-908): rmsnorm1p, rope_partial, kv_store_q8.
+    Returns (qg, k) as new arrays; the int8 buffers are updated in place."""
+    qn = rmsnorm1p(qg, wq, n=head_dim, rows=n_q_heads, pitch=q_pitch, T=T, eps=eps)
+    kn = rmsnorm1p(k, wk, n=head_dim, rows=n_kv_heads, pitch=head_dim, T=T, eps=eps)
+    qr, kr = rope_partial(qn, kn, n_q_heads=n_q_heads, n_kv_heads=n_kv_heads, rope_dim=rope_dim,
+                          q_pitch=q_pitch, k_pitch=head_dim, pos0=pos0, T=T, theta=theta)
+    kv_store_q8(kr, v, kcache, vcache, pos0, max_pos, T, n_kv_heads, head_dim)
+    return qr, kr
+
+
+def dec_split_count(length, tmin, smax):
+    return lib().orc_dec_split_count(length, tmin, smax)
+
+
+def attention_dec_q8(q, kcache, vcache, *, pos0, max_pos, sl2, tmin=1, smax=28, T,
+                     n_q_heads=24, n_kv_heads=4, q_pitch=512):
+    """kernels.cu:1049-1335. Returns (pacc [T,H,smax,256], pm, pd); partials the
+    reference does not write stay NaN."""
+    q = _h(q)
+    pacc = np.full((T, n_q_heads, smax, 256), np.nan, np.float32)
+    pm = np.full((T, n_q_heads, smax), np.nan, np.float32)
+    pd = np.full((T, n_q_heads, smax), np.nan, np.float32)
+    lib().orc_attention_dec_q8(_p(q), _p(kcache), _p(vcache), _p(pacc), _p(pm), _p(pd),
+                               n_q_heads, n_kv_heads, q_pitch, pos0, max_pos, float(sl2), tmin,
+                               smax, T)
+    return pacc, pm, pd
+
+
+def attention_dec_merge(pacc, pm, pd, *, pos0, tmin=1, smax=28, T, n_q_heads=24, gate=None,
+                        g_pitch=512, g_off=256):
+    """kernels.cu:1336-1385 (the _gate form when gate is given). Returns z
+    [T, n_q_heads, 256] float16."""
+    z = np.zeros((T, n_q_heads, 256), np.float16)
+    g = None if gate is None else _h(gate)
+    lib().orc_attention_dec_merge(_p(_f(pacc)), _p(_f(pm)), _p(_f(pd)), _p(z), n_q_heads, 256,
+                                  pos0, tmin, smax, T, _p(g), g_pitch, g_off)
+    return z
+
+
+def attention_decode_q8(qg, kcache, vcache, pos0, *, max_pos, scale, tmin=1, smax=28,
+                        n_q_heads=24, n_kv_heads=4, q_pitch=512, gate=True, g_off=256):
+    """_attn_dec with the gate (runtime.py:2907-2920): attention_dec_q8 then
+    attention_dec_merge_gate over one sequence's int8 cache. Returns z
+    [T, n_q_heads, 256] float16."""
+    qg = _h(qg)
+    T = qg.shape[0]
+    pacc, pm, pd = attention_dec_q8(qg, kcache, vcache, pos0=pos0, max_pos=max_pos,
+                                    sl2=scale * 1.4426950408889634, tmin=tmin, smax=smax, T=T,
+                                    n_q_heads=n_q_heads, n_kv_heads=n_kv_heads, q_pitch=q_pitch)
+    return attention_dec_merge(pacc, pm, pd, pos0=pos0, tmin=tmin, smax=smax, T=T,
+                               n_q_heads=n_q_heads, gate=qg if gate else None, g_pitch=q_pitch,
+                               g_off=g_off)
+
+
+def attention_prefill_q8(q, kcache, vcache, *, n_q_heads=24, n_kv_heads=4, head_dim=256,
+                         q_pitch, pos0, max_pos, scale, T, pv_fp16=False):
+    """kernels.cu:2778-2786 (KV split 1). Returns z [T, n_q_heads, head_dim] float16."""
+    q = _h(q)
+    z = np.zeros((T, n_q_heads, head_dim), np.float16)
+    lib().orc_attention_prefill_q8(_p(q), _p(kcache), _p(vcache), _p(z), n_q_heads, n_kv_heads,
+                                   head_dim, q_pitch, head_dim, pos0, max_pos, float(scale), T,
+                                   1 if pv_fp16 else 0)
+    return z
+
+
+def attention_exact_q8(q, kcache, vcache, *, n_q_heads=24, n_kv_heads=4, head_dim=256, q_pitch,
+                       pos0, max_pos, scale, T):
+    """Closed form over an int8 cache (values dequantized exactly), float64."""
+    q = _h(q)
+    out = np.zeros((T, n_q_heads, head_dim), np.float64)
+    lib().orc_attention_exact_f64_q8(_p(q), _p(kcache), _p(vcache), _p(out), n_q_heads,
+                                     n_kv_heads, head_dim, q_pitch, pos0, max_pos, float(scale), T)
     return out
 
 

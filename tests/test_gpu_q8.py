@@ -1,0 +1,244 @@
+"""GPU parity of the int8 KV cache path against the CPU oracle.
+
+Bar: the int8 store (values and scales) bit-exact, in kv_store_q8 and in the
+fused attn_prep_q8; attention outputs within max-abs 2e-3 / rel 1e-2 of the
+oracle (the kernels read fp16(byte * scale) where the reference's decode
+keeps the product in fp32 -- one fp16 rounding, far below both this bar and
+the int8 format's own error). Properties: a verify row equals the T = 1 call
+at its position bit for bit; a batched call equals single calls bit for bit;
+attention_dec_q8 leaves the partials of splits s >= St unwritten.
+"""
+import numpy as np
+import pytest
+import torch
+
+from conftest import close, f16, rand_qg
+from test_oracle_q8 import LOG2E, rand_kv
+
+pytestmark = pytest.mark.gpu
+
+SCALE = 256 ** -0.5
+ATOL, RTOL = 2e-3, 1e-2
+
+
+def to_dev(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def oracle_cache(orc, rng, L, max_pos):
+    """(k, v fp16 rows, int8 buffers holding them at positions 0..L-1)."""
+    k, v = rand_kv(rng, L, lo=-1.5, hi=0.5), rand_kv(rng, L, lo=-1.5, hi=0.5)
+    kc8, vc8 = orc.kv8_buffer(max_pos), orc.kv8_buffer(max_pos)
+    if L:
+        orc.kv_store_q8(k, v, kc8, vc8, 0, max_pos, L)
+    return k, v, kc8, vc8
+
+
+@pytest.mark.parametrize("T,pos0", [(1, 0), (37, 200), (1000, 5)])
+def test_kv_store_q8_bit_exact(fl, dev, orc, rng, T, pos0):
+    max_pos = pos0 + T + 3
+    k, v = rand_kv(rng, T), rand_kv(rng, T)
+    k[0, 0, :32] = 0
+    k[0, 1, :32] = f16(np.r_[127.0, -126.0, 2.5, 3.5, -4.5, 0.5, -0.5, 1.5, np.zeros(24)])
+    kc8, vc8 = orc.kv8_buffer(max_pos), orc.kv8_buffer(max_pos)
+    orc.kv_store_q8(k, v, kc8, vc8, pos0, max_pos, T)
+    kd, vd = fl.ops.kv8_cache(max_pos), fl.ops.kv8_cache(max_pos)
+    fl.ops.kv_store_q8(to_dev(k, dev), to_dev(v, dev), kd, vd, pos0=pos0, max_pos=max_pos)
+    torch.cuda.synchronize()
+    assert np.array_equal(kd.cpu().numpy(), kc8) and np.array_equal(vd.cpu().numpy(), vc8)
+
+
+@pytest.mark.parametrize("T,pos0", [(1, 4095), (3, 100), (2048, 0)])
+def test_attn_prep_q8_vs_oracle_and_unfused(fl, dev, orc, rng, T, pos0):
+    max_pos = pos0 + T + 5
+    qg = f16(rng.standard_normal((T, 24, 512)))
+    k = f16(rng.standard_normal((T, 4, 256)) * 3)
+    v = f16(rng.standard_normal((T, 4, 256)))
+    wq = (rng.standard_normal(256) * 0.2).astype(np.float32)
+    wk = (rng.standard_normal(256) * 0.2).astype(np.float32)
+    kc8, vc8 = orc.kv8_buffer(max_pos), orc.kv8_buffer(max_pos)
+    wq_o, wk_o = orc.attn_prep_q8(qg, k, v, wq, wk, kc8, vc8, pos0=pos0, T=T, max_pos=max_pos)
+    qd, kd, vd = to_dev(qg, dev), to_dev(k, dev), to_dev(v, dev)
+    wqd, wkd = to_dev(wq, dev), to_dev(wk, dev)
+    kcd, vcd = fl.ops.kv8_cache(max_pos), fl.ops.kv8_cache(max_pos)
+    fl.ops.attn_prep_q8(qd, kd, vd, wqd, wkd, kcd, vcd, pos0=pos0, max_pos=max_pos)
+    # unfused: rmsnorm1p x2, rope_partial, kv_store_q8
+    qu, ku = to_dev(qg, dev), to_dev(k, dev)
+    kcu, vcu = fl.ops.kv8_cache(max_pos), fl.ops.kv8_cache(max_pos)
+    fl.ops.rmsnorm1p(qu, wqd, rows=24, pitch=512)
+    fl.ops.rmsnorm1p(ku, wkd, rows=4, pitch=256)
+    fl.ops.rope_partial(qu, ku, pos0=pos0)
+    fl.ops.kv_store_q8(ku, vd, kcu, vcu, pos0=pos0, max_pos=max_pos)
+    torch.cuda.synchronize()
+    gq, gk, gkc, gvc = (t.cpu().numpy() for t in (qd, kd, kcd, vcd))
+    assert np.array_equal(gq, qu.cpu().numpy()) and np.array_equal(gk, ku.cpu().numpy())
+    assert np.array_equal(gkc, kcu.cpu().numpy()) and np.array_equal(gvc, vcu.cpu().numpy())
+    assert np.array_equal(gq, wq_o) and np.array_equal(gk, wk_o)
+    assert np.array_equal(gkc, kc8) and np.array_equal(gvc, vc8)
+
+
+@pytest.mark.parametrize("L,T,tmin,smax", [(1, 1, 1, 28), (2, 2, 1, 28), (63, 1, 1, 28),
+                                           (64, 1, 1, 28), (65, 3, 1, 28), (1000, 3, 1, 28),
+                                           (4096, 1, 1, 28), (5000, 2, 2, 5), (3000, 4, 1, 64)])
+def test_dec_q8_and_merge_vs_oracle(fl, dev, orc, rng, L, T, tmin, smax):
+    max_pos = L + 7
+    _, _, kc8, vc8 = oracle_cache(orc, rng, L, max_pos)
+    qg = rand_qg(rng, T)
+    pos0 = L - T
+    kd, vd, qd = to_dev(kc8, dev), to_dev(vc8, dev), to_dev(qg, dev)
+    pacc = torch.full((T, 24, smax, 256), float("nan"), device=dev)
+    pm = torch.full((T, 24, smax), float("nan"), device=dev)
+    pd = torch.full_like(pm, float("nan"))
+    z = torch.empty((T, 24, 256), dtype=torch.float16, device=dev)
+    fl.ops.attention_dec_q8(qd, kd, vd, pacc, pm, pd, pos0=pos0, max_pos=max_pos, T=T,
+                            tmin=tmin, smax=smax)
+    fl.ops.attention_dec_merge(pacc, pm, pd, z, pos0=pos0, T=T, tmin=tmin, smax=smax, gate=qd)
+    torch.cuda.synchronize()
+    opa, opm, opd = orc.attention_dec_q8(qg, kc8, vc8, pos0=pos0, max_pos=max_pos,
+                                         sl2=SCALE * LOG2E, tmin=tmin, smax=smax, T=T)
+    want = orc.attention_dec_merge(opa, opm, opd, pos0=pos0, tmin=tmin, smax=smax, T=T, gate=qg)
+    err, ok = close(z.cpu().numpy(), want, ATOL, RTOL)
+    assert ok, f"L={L} T={T}: max|err| {err}"
+    gpm, gpd = pm.cpu().numpy(), pd.cpu().numpy()
+    for t in range(T):
+        st = orc.dec_split_count(pos0 + t + 1, tmin, smax)
+        assert np.isnan(gpm[t, :, st:]).all() and np.isnan(gpd[t, :, st:]).all()
+        e1, ok1 = close(gpm[t, :, :st], opm[t, :, :st], 1e-3, 1e-3)      # log2 units
+        e2, ok2 = close(gpd[t, :, :st], opd[t, :, :st], 0, 5e-3)
+        assert ok1 and ok2, (t, e1, e2)
+
+
+def test_dec_q8_verify_rows_equal_t1_calls_bit_exact(fl, dev, orc, rng):
+    L, T = 40000, 4
+    _, _, kc8, vc8 = oracle_cache(orc, rng, L, L)
+    qg = rand_qg(rng, T)
+    kd, vd = to_dev(kc8, dev), to_dev(vc8, dev)
+    pos0 = L - T
+
+    def run(q, p0, n):
+        pacc = torch.zeros((n, 24, 28, 256), device=dev)
+        pm = torch.zeros((n, 24, 28), device=dev)
+        pd = torch.zeros_like(pm)
+        z = torch.empty((n, 24, 256), dtype=torch.float16, device=dev)
+        qd = to_dev(q, dev)
+        fl.ops.attention_dec_q8(qd, kd, vd, pacc, pm, pd, pos0=p0, max_pos=L, T=n)
+        fl.ops.attention_dec_merge(pacc, pm, pd, z, pos0=p0, T=n, gate=qd)
+        return z
+
+    zv = run(qg, pos0, T)
+    for t in range(T):
+        assert torch.equal(zv[t], run(qg[t:t + 1], pos0 + t, 1)[0]), t
+    # the batched int8 decode (the other split rule) gives the same rows bit for bit
+    zb = fl.ops.attn_decode_q8(to_dev(qg[None], dev), [kd], [vd], [pos0], [L])
+    for t in range(T):
+        z1 = fl.ops.attn_decode_q8(to_dev(qg[None, t:t + 1], dev), [kd], [vd], [pos0 + t], [L])
+        assert torch.equal(zb[0, t], z1[0, 0]), t
+
+
+def test_decode_q8_batched_vs_single_and_oracle(fl, dev, orc, rng):
+    lens = [3000, 17, 9000, 1]
+    caps = [L + 64 for L in lens]
+    caches = [oracle_cache(orc, rng, L, c) for L, c in zip(lens, caps)]
+    qg = np.stack([rand_qg(rng, 1) for _ in lens])
+    ks = [to_dev(c[2], dev) for c in caches]
+    vs = [to_dev(c[3], dev) for c in caches]
+    pos0s = [L - 1 for L in lens]
+    zb = fl.ops.attn_decode_q8(to_dev(qg, dev), ks, vs, pos0s, caps)
+    torch.cuda.synchronize()
+    for b, L in enumerate(lens):
+        z1 = fl.ops.attn_decode_q8(to_dev(qg[b:b + 1], dev), [ks[b]], [vs[b]], [L - 1], [caps[b]])
+        assert torch.equal(zb[b], z1[0]), b
+        want = orc.attention_decode_q8(qg[b], caches[b][2], caches[b][3], L - 1, max_pos=caps[b],
+                                       scale=SCALE)
+        err, ok = close(zb[b].cpu().numpy(), want, ATOL, RTOL)
+        assert ok, f"seq {b} L={L}: {err}"
+
+
+def test_decode_q8_config2_vs_oracle(fl, dev, orc):
+    """Config 2's shape at 8k: B = 4, T = 3 verify rows over int8 caches."""
+    rng = np.random.default_rng(8192)
+    B, T, Lmax = 4, 3, 8192
+    lens = rng.integers(int(0.9 * Lmax), Lmax + 1, size=B)
+    caches = [oracle_cache(orc, rng, int(L), int(L)) for L in lens]
+    qg = np.stack([rand_qg(rng, T) for _ in range(B)])
+    pos0s = [int(L) - T for L in lens]
+    z = fl.ops.attn_decode_q8(to_dev(qg, dev), [to_dev(c[2], dev) for c in caches],
+                              [to_dev(c[3], dev) for c in caches], pos0s, [int(L) for L in lens])
+    torch.cuda.synchronize()
+    zh = z.cpu().numpy()
+    for b in range(B):
+        want = orc.attention_decode_q8(qg[b], caches[b][2], caches[b][3], pos0s[b],
+                                       max_pos=int(lens[b]), scale=SCALE)
+        err, ok = close(zh[b], want, ATOL, RTOL)
+        assert ok, f"seq {b}: {err}"
+
+
+def test_decode_q8_tracks_fp16_decode(fl, dev, orc, rng):
+    """The int8 cache's output stays within the format's quantization error of
+    the fp16 cache's over the same rows (a sanity bound, not the parity bar)."""
+    L = 6000
+    k, v, kc8, vc8 = oracle_cache(orc, rng, L, L)
+    qg = rand_qg(rng, 2)
+    z8 = fl.ops.attn_decode_q8(to_dev(qg[None], dev), [to_dev(kc8, dev)], [to_dev(vc8, dev)],
+                               [L - 2], [L])
+    z16 = fl.ops.attn_decode(to_dev(qg[None], dev), [to_dev(k, dev)], [to_dev(v, dev)], [L - 2])
+    err, ok = close(z8.cpu().numpy(), z16.cpu().numpy().astype(np.float64), 2e-2, 5e-2)
+    assert ok, err
+
+
+def test_q8_rejects_bad_geometry(fl, dev, rng):
+    kd, vd = fl.ops.kv8_cache(64), fl.ops.kv8_cache(64)
+    k = torch.zeros((2, 4, 256), dtype=torch.float16, device=dev)
+    with pytest.raises(ValueError):                       # pos0 + T beyond the capacity
+        fl.ops.kv_store_q8(k, k, kd, vd, pos0=63, max_pos=64)
+    lib = fl._lib.lib()
+    # layer != 0: an int8 cache is one buffer a layer (nothing is launched)
+    assert lib.fl_kv_store_q8(k.data_ptr(), k.data_ptr(), kd.data_ptr(), vd.data_ptr(), 1, 0, 2,
+                              4, 256, 64, None) == 1
+    qg = to_dev(rand_qg(rng, 6), dev)                     # 6 tokens x 6 heads > 32 columns
+    p = torch.zeros(6 * 24 * 28 * 256, device=dev)
+    with pytest.raises(ValueError):
+        fl.ops.attention_dec_q8(qg, kd, vd, p, p, p, pos0=10, max_pos=64, T=6)
+    with pytest.raises(ValueError):                       # a buffer smaller than its capacity says
+        fl.ops.attention_prefill_q8(to_dev(rand_qg(rng, 1), dev), kd, vd, pos0=0, max_pos=65)
+
+
+@pytest.mark.parametrize("T,pos0", [(1, 0), (13, 0), (40, 3), (300, 0), (129, 1000), (2048, 0)])
+def test_prefill_q8_vs_oracle(fl, dev, orc, rng, T, pos0):
+    L = pos0 + T
+    k, v, kc8, vc8 = oracle_cache(orc, rng, L, L)
+    qg = rand_qg(rng, T)
+    # the new rows arrive through the fused kv_store_q8; older rows are already cached
+    kd, vd = fl.ops.kv8_cache(L), fl.ops.kv8_cache(L)
+    if pos0:
+        fl.ops.kv_store_q8(to_dev(k[:pos0], dev), to_dev(v[:pos0], dev), kd, vd, pos0=0, max_pos=L)
+    z = fl.ops.attention_prefill_q8(to_dev(qg, dev), kd, vd, pos0=pos0, max_pos=L,
+                                    k_new=to_dev(k[pos0:], dev), v_new=to_dev(v[pos0:], dev))
+    torch.cuda.synchronize()
+    assert np.array_equal(kd.cpu().numpy(), kc8) and np.array_equal(vd.cpu().numpy(), vc8)
+    want = orc.attention_prefill_q8(qg, kc8, vc8, q_pitch=512, pos0=pos0, max_pos=L, scale=SCALE,
+                                    T=T)
+    err, ok = close(z.cpu().numpy(), want, ATOL, RTOL)
+    assert ok, f"T={T} pos0={pos0}: max|err| {err}"
+
+
+@pytest.mark.parametrize("L", [8192])
+def test_prefill_q8_config3_sampled_rows(fl, dev, orc, L):
+    """Config 3's shape over an int8 cache: sampled rows against the float64
+    closed form over the dequantized cache, every row finite."""
+    rng = np.random.default_rng(L)
+    k, v, kc8, vc8 = oracle_cache(orc, rng, L, L)
+    qg = rand_qg(rng, L)
+    q = np.ascontiguousarray(qg[..., :256])
+    kd, vd = fl.ops.kv8_cache(L), fl.ops.kv8_cache(L)
+    z = fl.ops.attention_prefill_q8(to_dev(q, dev), kd, vd, pos0=0, max_pos=L, scale=1.0,
+                                    k_new=to_dev(k, dev), v_new=to_dev(v, dev))
+    torch.cuda.synchronize()
+    zh = z.cpu().numpy()
+    assert np.isfinite(zh.astype(np.float32)).all()
+    for t in sorted({0, 1, 63, 64, 127, L // 2 + 5, L - 2, L - 1,
+                     *rng.integers(0, L, 4).tolist()}):
+        want = orc.attention_exact_q8(q[t:t + 1], kc8, vc8, q_pitch=256, pos0=t, max_pos=L,
+                                      scale=1.0, T=1)
+        err, ok = close(zh[t:t + 1], want, ATOL, RTOL)
+        assert ok, f"L={L} row {t}: max|err| {err}"
