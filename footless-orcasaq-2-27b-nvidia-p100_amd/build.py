@@ -37,9 +37,11 @@ HIPCC_FLAGS = [
 # scores) accumulate in VGPRs, where the softmax reads them (the P V
 # accumulators are AGPRs held by inline asm); no NaNs and IEEE mode off, so
 # the score max is plain v_max / v_max3 without NaN-quieting canonicalisation
-# (scores are finite or -inf).
+# (scores are finite or -inf). attn_decode: its accumulators (scores read by the
+# softmax, O rescaled in place) in VGPRs as well.
 FILE_FLAGS = {
     "attn_prefill": ["-mllvm", "-amdgpu-mfma-vgpr-form", "-fno-honor-nans", "-mno-amdgpu-ieee"],
+    "attn_decode": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
 }
 
 

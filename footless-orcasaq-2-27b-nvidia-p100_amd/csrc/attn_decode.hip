@@ -56,6 +56,7 @@ constexpr int DEC_HD = 256;
 constexpr int DEC_WAVES = 4;
 constexpr int DEC_THREADS = 64 * DEC_WAVES;
 constexpr int VT_PITCH = 40;   // halves per d row of the transposed V slice (32 + 8 pad)
+constexpr float RESCALE_LOG2 = 8.f;
 #ifndef DEC_NBUF
 #define DEC_NBUF 2                // register tile buffers (prefetch depth + 1)
 #endif
@@ -172,25 +173,18 @@ __device__ __forceinline__ void dec_load_tile(DecTileQ8& r, const char* __restri
                                               const f16* __restrict__ vsb, size_t row_stride,
                                               int j, int uhi, int lane, int w) {
     const int ql = lane & 31, hh = lane >> 5;
-    const int krow = j * DEC_TILE + ql;
-    if (krow < uhi) {
-        const u32x4* src = (const u32x4*)(kbase + (size_t)krow * row_stride + 64 * w + 32 * hh);
-        r.k[0] = src[0];
-        r.k[1] = src[1];
-        const f16* sb = hh ? vsb : ksb;
-        r.sc = *(const uint32_t*)(sb + (size_t)krow * (row_stride / 32) + 2 * w);
-    } else {
-        r.k[0] = r.k[1] = (u32x4)(0u);
-        r.sc = 0;
-    }
+    const uint32_t rs = (uint32_t)row_stride;   // bytes between rows; caches < 2 GiB
+    const uint32_t krow = (uint32_t)min(j * DEC_TILE + ql, uhi - 1);
+    const u32x4* src = (const u32x4*)(kbase + (krow * rs + 64 * w + 32 * hh));
+    r.k[0] = src[0];
+    r.k[1] = src[1];
+    const char* sb = (const char*)(hh ? vsb : ksb);
+    r.sc = *(const uint32_t*)(sb + (krow * (rs / 16) + 4 * w));
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const int vrow = j * DEC_TILE + 4 * (lane & 7) + i;
-        const u32x2* src = (const u32x2*)(vbase + (size_t)vrow * row_stride + 64 * w + 8 * (lane >> 3));
-        if (vrow < uhi)
-            r.v[i] = NT_V ? __builtin_nontemporal_load(src) : *src;
-        else
-            r.v[i] = (u32x2)(0u);
+        const uint32_t vrow = (uint32_t)min(j * DEC_TILE + 4 * (lane & 7) + i, uhi - 1);
+        const u32x2* vsrc = (const u32x2*)(vbase + (vrow * rs + 64 * w + 8 * (lane >> 3)));
+        r.v[i] = NT_V ? __builtin_nontemporal_load(vsrc) : *vsrc;
     }
 }
 
@@ -226,24 +220,25 @@ __device__ __forceinline__ void dec_load_tile(DecTileRegs& r, const f16* __restr
                                               const f16* __restrict__ vbase, size_t row_stride,
                                               int j, int uhi, int lane, int w) {
     const int ql = lane & 31, hh = lane >> 5;
-    const int krow = j * DEC_TILE + ql;
-    if (krow < uhi) {
-        const f16x8* src = (const f16x8*)(kbase + (size_t)krow * row_stride + 64 * w + 32 * hh);
+    const uint32_t rs = (uint32_t)row_stride * 2;   // bytes between rows; caches < 2 GiB
+    const char* kb = (const char*)kbase;
+    const char* vb = (const char*)vbase;
+    const uint32_t krow = (uint32_t)min(j * DEC_TILE + ql, uhi - 1);
+    const f16x8* src = (const f16x8*)(kb + (krow * rs + 2 * (64 * w + 32 * hh)));
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) r.k[ks] = src[ks];
-    } else {
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) r.k[ks] = (f16x8)(0);
-    }
+    for (int ks = 0; ks < 4; ++ks) r.k[ks] = src[ks];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const int vrow = j * DEC_TILE + 4 * (lane & 7) + i;
-        const f16x8* src = (const f16x8*)(vbase + (size_t)vrow * row_stride + 64 * w + 8 * (lane >> 3));
-        if (vrow < uhi)
-            r.v[i] = NT_V ? __builtin_nontemporal_load(src) : *src;
-        else
-            r.v[i] = (f16x8)(0);
+        const uint32_t vrow = (uint32_t)min(j * DEC_TILE + 4 * (lane & 7) + i, uhi - 1);
+        const f16x8* vsrc = (const f16x8*)(vb + (vrow * rs + 2 * (64 * w + 8 * (lane >> 3))));
+        r.v[i] = NT_V ? __builtin_nontemporal_load(vsrc) : *vsrc;
     }
+}
+
+// Workgroup barrier after this wave's LDS writes, without the vmcnt drain of
+// __syncthreads(): the next tiles' loads stay in flight across it.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
 // Q8: the caches are int8 (DecSeqs k / v the values, ks / vs the scales).
@@ -322,7 +317,7 @@ attn_decode_split_kernel(const f16* __restrict__ qg, DecSeqs seqs, float* __rest
             const f16x4 col = {r.v[0][e], r.v[1][e], r.v[2][e], r.v[3][e]};
             *(f16x4*)&s_vt[w][8 * (lane >> 3) + e][4 * (lane & 7)] = col;
         }
-        __syncthreads();
+        lds_barrier();
         // full scores, summed in wave order
         float sc[16];
 #pragma unroll
@@ -335,32 +330,46 @@ attn_decode_split_kernel(const f16* __restrict__ qg, DecSeqs seqs, float* __rest
             sc[4 * r4 + 2] = t4[2];
             sc[4 * r4 + 3] = t4[3];
         }
-        // online softmax of this lane's column over the tile's 32 rows
-        float mt = -INFINITY;
+        // online softmax of this lane's column over the tile's 32 rows. The
+        // range mask only runs when some column's range ends inside the tile.
+        const int r0 = j * DEC_TILE;
+        const bool inside = !qvalid || (r0 >= qlo && r0 + DEC_TILE <= qhi);
+        if (!__all(inside)) {
 #pragma unroll
-        for (int rr = 0; rr < 16; ++rr) {
-            const int row = j * DEC_TILE + 8 * (rr >> 2) + 4 * hh + (rr & 3);
-            const bool ok = row >= qlo && row < qhi;
-            sc[rr] = ok ? sc[rr] * sl2 : -INFINITY;
-            mt = fmaxf(mt, sc[rr]);
+            for (int rr = 0; rr < 16; ++rr) {
+                const int row = r0 + 8 * (rr >> 2) + 4 * hh + (rr & 3);
+                sc[rr] = (row >= qlo && row < qhi) ? sc[rr] : -INFINITY;
+            }
         }
-        mt = fmaxf(mt, lane_xor(mt, 32));
-        const float m_new = fmaxf(m_run, mt);
-        const float corr = fast_exp2(m_run - m_new);
+        float mt = sc[0];
+#pragma unroll
+        for (int rr = 1; rr < 16; ++rr) mt = fmaxf(mt, sc[rr]);
+        mt = fmaxf(mt, lane_xor(mt, 32)) * sl2;
+        // A column's running max moves only when the tile's max exceeds it by
+        // more than RESCALE_LOG2: p <= 2^RESCALE_LOG2 stays exact in fp16 range
+        // and O / l are rescaled on few tiles. The decision is the column's own
+        // (corr = 1 exactly for the others), so a token's values do not depend
+        // on the other tokens in the launch.
+        const bool grow = mt > m_run + RESCALE_LOG2;
+        if (__any(grow)) {
+            const float m_new = grow ? mt : m_run;
+            const float corr = fast_exp2(m_run - m_new);
+            m_run = m_new;
+            l_run *= corr;
+            o0 *= corr;
+            o1 *= corr;
+        }
         float psum = 0.f;
         f16x8 pk0, pk1;
 #pragma unroll
         for (int rr = 0; rr < 16; ++rr) {
-            const float p = fast_exp2(sc[rr] - m_new);
+            const float p = fast_exp2(fmaf(sc[rr], sl2, -m_run));
             psum += p;
             if (rr < 8) pk0[rr] = (f16)p;
             else pk1[rr - 8] = (f16)p;
         }
         psum += lane_xor(psum, 32);
-        l_run = l_run * corr + psum;
-        m_run = m_new;
-        o0 *= corr;
-        o1 *= corr;
+        l_run += psum;
         // O^T += V^T P^T over the tile's two 16-row k-steps
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
@@ -389,23 +398,27 @@ attn_decode_split_kernel(const f16* __restrict__ qg, DecSeqs seqs, float* __rest
     };
     if (uhi > ulo) {
         // NBUF register tile buffers: the loads of tile j + NBUF - 1 are issued
-        // before the math of tile j
+        // before the math of tile j. Every load is issued unconditionally (rows
+        // and tiles clamped into the range: a row past uhi reads row uhi - 1,
+        // masked to p = 0; a tile past the end re-reads the last one), so the
+        // compiler's wait before tile j's math counts exactly the loads of the
+        // tiles behind it instead of draining them all.
         const int j0 = ulo / DEC_TILE;
         const int j1 = (uhi + DEC_TILE - 1) / DEC_TILE;
         Raw rbuf[NBUF];
 #pragma unroll
-        for (int p = 0; p < NBUF - 1; ++p)
-            if (j0 + p < j1) load(rbuf[p], j0 + p);
+        for (int p = 0; p < NBUF - 1; ++p) load(rbuf[p], min(j0 + p, j1 - 1));
         for (int j = j0; j < j1; j += NBUF) {
 #pragma unroll
             for (int u = 0; u < NBUF; ++u) {
                 const int jj = j + u;
-                if (jj >= j1) break;
-                if (jj + NBUF - 1 < j1) load(rbuf[(u + NBUF - 1) % NBUF], jj + NBUF - 1);
-                if constexpr (Q8)
-                    body(dec_dequant(rbuf[u], lane), jj);
-                else
-                    body(rbuf[u], jj);
+                load(rbuf[(u + NBUF - 1) % NBUF], min(jj + NBUF - 1, j1 - 1));
+                if (jj < j1) {
+                    if constexpr (Q8)
+                        body(dec_dequant(rbuf[u], lane), jj);
+                    else
+                        body(rbuf[u], jj);
+                }
             }
         }
     }
@@ -522,6 +535,12 @@ void set_q8_seq(DecSeqs& seqs, int b, const void* kc, const void* vc, int max_po
     seqs.pos0[b] = pos0;
 }
 
+// The kernels address a cache row with a 32-bit byte offset from the layer's
+// (or sequence's) base.
+bool cache_fits(int max_pos, int n_kv, int bytes_per_elem) {
+    return (uint64_t)max_pos * n_kv * DEC_HD * bytes_per_elem < (1ull << 31);
+}
+
 int check_decode_geometry(int T, int n_q_heads, int n_kv, int head_dim, int q_pitch, int split,
                           int split_rows) {
     FL_REQUIRE(head_dim == DEC_HD, "head_dim must be 256");
@@ -557,6 +576,7 @@ int attn_decode_batched(const void* qg, int q_pitch, const void* const* kcache,
         FL_REQUIRE(kcache[b] && vcache[b], "null cache pointer");
         FL_REQUIRE(aligned16(kcache[b]) && aligned16(vcache[b]), "16-byte aligned caches");
         FL_REQUIRE(pos0[b] >= 0 && pos0[b] + T <= cap[b], "pos0[b] + T <= cap[b]");
+        FL_REQUIRE(cache_fits(cap[b], n_kv_heads, Q8 ? 1 : 2), "a cache of at most 2 GiB");
         if (Q8)
             set_q8_seq(seqs, b, kcache[b], vcache[b], cap[b], n_kv_heads, pos0[b]);
         else {
@@ -611,6 +631,7 @@ int fl_attention_split_gqa(const void* q, const void* kcache, const void* vcache
     if (rc) return rc;
     FL_REQUIRE(q && kcache && vcache && pacc && pm && pd, "null pointer");
     FL_REQUIRE(pos0 >= 0 && layer >= 0 && pos0 + T <= max_pos, "pos0 + T <= max_pos");
+    FL_REQUIRE(cache_fits(max_pos, n_kv_heads, 2), "a layer cache of at most 2 GiB");
     FL_REQUIRE(aligned16(q) && aligned16(kcache) && aligned16(vcache) && aligned16(pacc),
                "16-byte aligned buffers");
     DecSeqs seqs = {};
@@ -632,6 +653,7 @@ int fl_attention_split_gqa_q8(const void* q, const void* kcache, const void* vca
     FL_REQUIRE(q && kcache && vcache && pacc && pm && pd, "null pointer");
     FL_REQUIRE(layer == 0, "an int8 cache is one buffer a layer: layer must be 0");
     FL_REQUIRE(pos0 >= 0 && pos0 + T <= max_pos, "pos0 + T <= max_pos");
+    FL_REQUIRE(cache_fits(max_pos, n_kv_heads, 1), "a cache of at most 2 GiB");
     FL_REQUIRE(aligned16(q) && aligned16(kcache) && aligned16(vcache) && aligned16(pacc),
                "16-byte aligned buffers");
     DecSeqs seqs = {};
@@ -649,6 +671,7 @@ int fl_attention_dec_q8(const void* q, const void* kcache, const void* vcache, f
     FL_REQUIRE(q && kcache && vcache && pacc && pm && pd, "null pointer");
     FL_REQUIRE(tmin >= 1, "tmin >= 1");
     FL_REQUIRE(pos0 >= 0 && pos0 + T <= max_pos, "pos0 + T <= max_pos");
+    FL_REQUIRE(cache_fits(max_pos, n_kv_heads, 1), "a cache of at most 2 GiB");
     FL_REQUIRE(aligned16(q) && aligned16(kcache) && aligned16(vcache) && aligned16(pacc),
                "16-byte aligned buffers");
     DecSeqs seqs = {};
