@@ -443,28 +443,95 @@ attn_decode_split_kernel(const f16* __restrict__ qg, DecSeqs seqs, float* __rest
 }
 
 // ---------------------------------------------------------------------------
-// merge (+ gate): one block of head_dim threads per (row, q head)
+// merge (+ gate): attention_merge (kernels.cu:1387-1424) with attn_gate
+// (kernels.cu:1572-1600) fused. M = max_s m_s, z = f16_sat(sum_s e_s acc_s /
+// sum_s e_s d_s), e_s = e^(m_s - M), then z = f16_sat(z * sigmoid(g)).
+// One block of 256 threads a (row, q head). Thread tid owns the float4 of
+// dims 4c..4c+3 (c = tid % C, C = head_dim / 4) for the splits s = j, j + J,
+// ... (j = tid / C, J = 256 / C), eight partials in flight; the J group sums
+// are added in j order through LDS. Empty partials (m = -1e30, d = 0, acc =
+// 0) contribute exact zeros, so the result does not depend on how many
+// empty splits follow a token's own.
 // ---------------------------------------------------------------------------
-__global__ void attn_merge_kernel(const float* __restrict__ pacc, const float* __restrict__ pm,
-                                  const float* __restrict__ pd, f16* __restrict__ z,
-                                  const f16* __restrict__ gate, int n_q_heads, int head_dim,
-                                  int z_pitch, int g_pitch, int g_off, int split) {
-    const int head = blockIdx.x, row = blockIdx.y, d = threadIdx.x;
+constexpr int MG_THREADS = 256;
+
+__global__ void __launch_bounds__(MG_THREADS)
+attn_merge_kernel(const float* __restrict__ pacc, const float* __restrict__ pm,
+                  const float* __restrict__ pd, f16* __restrict__ z,
+                  const f16* __restrict__ gate, int n_q_heads, int head_dim, int z_pitch,
+                  int g_pitch, int g_off, int split) {
+    __shared__ f32x4 s_num[MG_THREADS];
+    __shared__ float s_den[MG_THREADS];
+    __shared__ float s_max[MG_THREADS / 64];
+    const int head = blockIdx.x, row = blockIdx.y, tid = threadIdx.x;
+    const int C = head_dim >> 2, J = MG_THREADS / C;
+    const int c = tid % C, j = tid / C;
     const size_t p0 = ((size_t)row * n_q_heads + head) * split;
+    const float* pmr = pm + p0;
+    const float* pdr = pd + p0;
+
     float M = -1e30f;
-    for (int s = 0; s < split; ++s) M = fmaxf(M, pm[p0 + s]);
-    float num = 0.f, den = 0.f;
-    for (int s = 0; s < split; ++s) {
-        const float e = fast_exp2((pm[p0 + s] - M) * FL_LOG2E);
-        num = fmaf(e, pacc[(p0 + s) * head_dim + d], num);
-        den = fmaf(e, pd[p0 + s], den);
+    for (int s = tid; s < split; s += MG_THREADS) M = fmaxf(M, pmr[s]);
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) M = fmaxf(M, lane_xor(M, d));
+    if ((tid & 63) == 0) s_max[tid >> 6] = M;
+    __syncthreads();
+    M = fmaxf(fmaxf(s_max[0], s_max[1]), fmaxf(s_max[2], s_max[3]));
+
+    f32x4 num = (f32x4)(0.f);
+    float den = 0.f;
+    if (j < J) {
+        const f32x4* acc = (const f32x4*)(pacc + p0 * head_dim) + c;
+        auto add = [&](float m, float dv, const f32x4& a) {
+            const float e = fast_exp2((m - M) * FL_LOG2E);
+            num[0] = fmaf(e, a[0], num[0]);
+            num[1] = fmaf(e, a[1], num[1]);
+            num[2] = fmaf(e, a[2], num[2]);
+            num[3] = fmaf(e, a[3], num[3]);
+            den = fmaf(e, dv, den);
+        };
+        int s = j;
+        for (; s + 7 * J < split; s += 8 * J) {
+            float mv[8], dv[8];
+            f32x4 av[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                mv[u] = pmr[s + u * J];
+                dv[u] = pdr[s + u * J];
+                av[u] = acc[(size_t)(s + u * J) * C];
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) add(mv[u], dv[u], av[u]);
+        }
+        for (; s < split; s += J) add(pmr[s], pdr[s], acc[(size_t)s * C]);
     }
-    f16 zv = f16_sat(num * (1.f / den));
-    if (gate != nullptr) {
-        const float g = (float)gate[((size_t)row * n_q_heads + head) * g_pitch + g_off + d];
-        zv = f16_sat((float)zv * sigmoid_f(g));
+    s_num[tid] = num;
+    s_den[tid] = den;
+    __syncthreads();
+    if (tid < C) {
+        f32x4 n = s_num[tid];
+        float dsum = s_den[tid];
+        for (int jj = 1; jj < J; ++jj) {
+            const f32x4 o = s_num[jj * C + tid];
+            n[0] += o[0];
+            n[1] += o[1];
+            n[2] += o[2];
+            n[3] += o[3];
+            dsum += s_den[jj * C + tid];
+        }
+        const float inv = 1.f / dsum;
+        const size_t rh = (size_t)row * n_q_heads + head;
+        f16* zr = z + rh * z_pitch + 4 * tid;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            f16 zv = f16_sat(n[e] * inv);
+            if (gate != nullptr) {
+                const float g = (float)gate[rh * g_pitch + g_off + 4 * tid + e];
+                zv = f16_sat((float)zv * sigmoid_f(g));
+            }
+            zr[e] = zv;
+        }
     }
-    z[((size_t)row * n_q_heads + head) * z_pitch + d] = zv;
 }
 
 // attention_dec_merge (kernels.cu:1336-1385): the first St partials of the
@@ -595,7 +662,7 @@ int attn_decode_batched(const void* qg, int q_pitch, const void* const* kcache,
                                  q_pitch, grid_split, grid_split, split_rows, scale * FL_LOG2E,
                                  (hipStream_t)stream);
     if (rc) return rc;
-    hipLaunchKernelGGL(attn_merge_kernel, dim3(n_q_heads, B * T), dim3(head_dim), 0,
+    hipLaunchKernelGGL(attn_merge_kernel, dim3(n_q_heads, B * T), dim3(MG_THREADS), 0,
                        (hipStream_t)stream, pacc, pm, pd, (f16*)z, (const f16*)gate, n_q_heads,
                        head_dim, z_pitch, g_pitch, g_off, grid_split);
     return fl::check_launch("attn_merge");
@@ -718,10 +785,13 @@ int fl_attention_merge(const float* pacc, const float* pm, const float* pd, void
                        int n_q_heads, int head_dim, int z_pitch, int T, int split,
                        const void* gate, int g_pitch, int g_off, fl_stream_t stream) {
     FL_REQUIRE(pacc && pm && pd && z, "null pointer");
-    FL_REQUIRE(head_dim >= 1 && head_dim <= 1024 && z_pitch >= head_dim, "head_dim, z_pitch");
+    FL_REQUIRE(head_dim >= 4 && head_dim <= 4 * MG_THREADS && head_dim % 4 == 0 &&
+                   z_pitch >= head_dim,
+               "head_dim a multiple of 4 in [4, 1024], z_pitch >= head_dim");
     FL_REQUIRE(T >= 1 && split >= 1 && n_q_heads >= 1, "T, split, n_q_heads >= 1");
     FL_REQUIRE(gate == nullptr || g_off + head_dim <= g_pitch, "g_off + head_dim <= g_pitch");
-    hipLaunchKernelGGL(attn_merge_kernel, dim3(n_q_heads, T), dim3(head_dim), 0,
+    FL_REQUIRE(aligned16(pacc), "16-byte aligned pacc");
+    hipLaunchKernelGGL(attn_merge_kernel, dim3(n_q_heads, T), dim3(MG_THREADS), 0,
                        (hipStream_t)stream, pacc, pm, pd, (f16*)z, (const f16*)gate, n_q_heads,
                        head_dim, z_pitch, g_pitch, g_off, split);
     return fl::check_launch("attn_merge");

@@ -104,7 +104,8 @@ int fl_attention_split_gqa(const void* q, const void* kcache, const void* vcache
  * attention_merge (+ attn_gate when gate != NULL): z[t][h][:] =
  * f16_sat(sum_s e_s acc_s / sum_s e_s d_s), e_s = exp(m_s - max m), then
  * z = f16_sat(z * sigmoid(gate[t][h][g_off + d])) with gate rows of g_pitch
- * per head. z is written at z_pitch per head.
+ * per head. z is written at z_pitch per head. head_dim is a multiple of 4
+ * up to 1024; pacc is 16-byte aligned.
  * Replaces kernels.cu:1398-1424 (runtime.py:2844-2846) and kernels.cu:
  * 1585-1600 (runtime.py:2860-2862); the fused form of kernels.cu:1342-1385. */
 int fl_attention_merge(const float* pacc, const float* pm, const float* pd, void* z,
