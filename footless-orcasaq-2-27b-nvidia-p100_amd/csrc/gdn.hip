@@ -305,48 +305,75 @@ __device__ __forceinline__ void store_row16_nt(float* dst, const float (&reg)[16
                                     (f32x4*)(dst + 32 * j));
 }
 
+// warp32_tree's value at lanes 0 and 32 (other lanes: partial sums) without
+// LDS-pipe exchanges but the first: lane i pairs with i + 16 (ds_swizzle,
+// i ^ 16 within each 32 lanes), then with i + 8, 4, 2, 1 inside its 16-lane
+// row (DPP row_shl, a VALU operand modifier). At lanes 0 and 32 these are the
+// pairs of the xor tree (x ^ d == x + d there), added in the same order.
+template <int D>
+__device__ __forceinline__ float dpp_shl(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x100 + D, 0xF, 0xF, true));
+}
+__device__ __forceinline__ float warp32_tree_lane0(float v) {
+    v += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401F));
+    v += dpp_shl<8>(v);
+    v += dpp_shl<4>(v);
+    v += dpp_shl<2>(v);
+    v += dpp_shl<1>(v);
+    return v;
+}
+
 // Sum of squares of a 128-wide row held two per lane (lane l: x[l], x[l+64])
 // in the reference's order: 32-lane trees give r0 (x[0..31], lane 0), r1
 // (x[32..63], lane 32), r2 (x[64..95], lane 0), r3 (x[96..127], lane 32);
 // the total is (r0 + r2) + (r1 + r3) (kernels.cu:214-227 over 4 warps).
 __device__ __forceinline__ float sumsq128(float lo, float hi) {
-    const float a = warp32_tree(lo * lo) + warp32_tree(hi * hi);   // lane 0: r0+r2, lane 32: r1+r3
+    const float a = warp32_tree_lane0(lo * lo) + warp32_tree_lane0(hi * hi);   // lane 0: r0+r2, lane 32: r1+r3
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a), 0)) +
            __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a), 32));
 }
 
-// conv1_ch split in two so the loads can be issued ahead of the state's.
+// conv1_ch split in two so the loads can be issued ahead of the state's: the
+// raw fp16 values are kept until conv1_apply, after the state loads are
+// issued, so no wait for them lands in front of those loads.
 struct ConvIn {
-    float s0, s1, s2, xv;
+    f16 h0, h1, h2, x;
     f16x4 w;
 };
 
+// The ring is read unconditionally (the buffer is always there) and zeroed
+// by a select in conv1_apply when pos0 == 0: a load under a branch would be
+// waited for inside the branch, one HBM round trip after another.
 __device__ __forceinline__ ConvIn conv1_load(const f16* __restrict__ x, const f16* __restrict__ w,
-                                             const f16* __restrict__ st_in, int d, int pos0) {
+                                             const f16* __restrict__ st_in, int d) {
     ConvIn c;
     const f16* st = st_in + (size_t)d * 3;
-    c.s0 = pos0 > 0 ? (float)st[0] : 0.f;
-    c.s1 = pos0 > 0 ? (float)st[1] : 0.f;
-    c.s2 = pos0 > 0 ? (float)st[2] : 0.f;
-    c.xv = (float)x[d];
+    c.h0 = st[0];
+    c.h1 = st[1];
+    c.h2 = st[2];
+    c.x = x[d];
     c.w = *(const f16x4*)(w + (size_t)d * 4);
     return c;
 }
 
 // conv1d_causal at T = 1 for channel d (width 4, kernels.cu:1634-1679 /
-// 2916-2941): the fp16-rounded silu output; the new state (s1, s2, x) into
-// st_out when given.
-__device__ __forceinline__ float conv1_apply(const ConvIn& c, f16* st_out, int d) {
+// 2916-2941; the history is zero when pos0 == 0): the fp16-rounded silu
+// output; the new state (s1, s2, x) into st_out when given.
+__device__ __forceinline__ float conv1_apply(const ConvIn& c, bool hist, f16* st_out, int d) {
+    const float s0 = hist ? (float)c.h0 : 0.f;
+    const float s1 = hist ? (float)c.h1 : 0.f;
+    const float s2 = hist ? (float)c.h2 : 0.f;
+    const float xv = (float)c.x;
     float acc = 0.f;
-    acc = fmaf((float)c.w[0], c.s0, acc);
-    acc = fmaf((float)c.w[1], c.s1, acc);
-    acc = fmaf((float)c.w[2], c.s2, acc);
-    acc = fmaf((float)c.w[3], c.xv, acc);
+    acc = fmaf((float)c.w[0], s0, acc);
+    acc = fmaf((float)c.w[1], s1, acc);
+    acc = fmaf((float)c.w[2], s2, acc);
+    acc = fmaf((float)c.w[3], xv, acc);
     if (st_out != nullptr) {
         f16* so = st_out + (size_t)d * 3;
-        so[0] = f16_sat(c.s1);
-        so[1] = f16_sat(c.s2);
-        so[2] = f16_sat(c.xv);
+        so[0] = f16_sat(s1);
+        so[1] = f16_sat(s2);
+        so[2] = f16_sat(xv);
     }
     return (float)f16_sat(silu_f(acc));
 }
@@ -357,13 +384,16 @@ __device__ __forceinline__ float conv1_apply(const ConvIn& c, f16* st_out, int d
 // threads 0-127, q: 128-255) -- the one workgroup barrier -- then every wave
 // forms both L2 norms itself with in-wave reductions in the reference's
 // order, normalises the 256 values into its own LDS slice and runs the delta
-// rule on its 8 rows. Token 0's conv / gate inputs are issued before the
-// state's loads so the prologue computes while the state streams in; the
-// state is read and written with non-temporal loads / stores (once a step).
+// rule on its 8 rows. (Measured and not kept: two rows a thread, and the
+// norm's partial sums shared through LDS with a second barrier -- both
+// slower.) Token 0's conv / gate inputs are issued before the state's loads
+// so the prologue computes while the state streams in; the state is read and
+// written with non-temporal loads / stores (once a step).
+template <bool CONV>
 __global__ void __launch_bounds__(GR_THREADS)
-gdn_decode_kernel(const f16* __restrict__ x, int x_stride, int conv_fused,
-                  const f16* __restrict__ conv_w, GdnSeqs seqs, const float* __restrict__ ga,
-                  const float* __restrict__ gb, int ab_stride, const float* __restrict__ A_log,
+gdn_decode_kernel(const f16* __restrict__ x, int x_stride, const f16* __restrict__ conv_w,
+                  GdnSeqs seqs, const float* __restrict__ ga, const float* __restrict__ gb,
+                  int ab_stride, const float* __restrict__ A_log,
                   const float* __restrict__ dt_bias, f16* __restrict__ y, int y_stride,
                   long long ck_step, int T, int n_kheads, int n_vheads, int V, float out_scale,
                   float l2eps, int group) {
@@ -385,37 +415,32 @@ gdn_decode_kernel(const f16* __restrict__ x, int x_stride, int conv_fused,
     const float ga0 = ga[(size_t)b * T * ab_stride + hv], gb0 = gb[(size_t)b * T * ab_stride + hv];
     ConvIn cq, cv;
     const f16* x0 = x + (size_t)b * T * x_stride;
-    if (conv_fused) {
-        cq = conv1_load(x0, conv_w, seqs.cst_in[b], ch, pos0);
-        cv = conv1_load(x0, conv_w, seqs.cst_in[b], ch_v, pos0);
+    if constexpr (CONV) {
+        cq = conv1_load(x0, conv_w, seqs.cst_in[b], ch);
+        cv = conv1_load(x0, conv_w, seqs.cst_in[b], ch_v);
     } else {
-        cq.xv = (float)x0[ch];
-        cv.xv = (float)x0[ch_v];
+        cq.x = x0[ch];
+        cv.x = x0[ch_v];
     }
     __builtin_amdgcn_sched_barrier(0);
     float reg[16];
     load_row16_nt(reg, Srow);
     __builtin_amdgcn_sched_barrier(0);
     const float al = expf(A);
-    for (int t = 0; t < T; ++t) {
+    // one token; token 0 is peeled so that nothing of its conversions is
+    // hoisted in front of the state loads
+    auto token = [&](int t, float a_t, float b_t) {
         const size_t bt_row = (size_t)b * T + t;
-        if (t > 0) {   // verify rows: the conv output of row t (conv_fused is T == 1 only)
-            const f16* xr = x + bt_row * x_stride;
-            cq.xv = (float)xr[ch];
-            cv.xv = (float)xr[ch_v];
-        }
-        const float a_t = t == 0 ? ga0 : ga[bt_row * ab_stride + hv];
-        const float b_t = t == 0 ? gb0 : gb[bt_row * ab_stride + hv];
         const float bt = sigmoid_f(b_t);
         const float dt = expf(-al * softplus20(a_t + dtb));
         float xv, vt;
-        if (conv_fused) {
+        if constexpr (CONV) {
             const bool own = (hv % group) == 0 && rb == 0;   // one workgroup stores q / k state
-            xv = conv1_apply(cq, own ? seqs.cst_out[b] : nullptr, ch);
-            vt = conv1_apply(cv, c0 == 0 ? seqs.cst_out[b] : nullptr, ch_v);
+            xv = conv1_apply(cq, pos0 > 0, own ? seqs.cst_out[b] : nullptr, ch);
+            vt = conv1_apply(cv, pos0 > 0, c0 == 0 ? seqs.cst_out[b] : nullptr, ch_v);
         } else {
-            xv = cq.xv;
-            vt = cv.xv;
+            xv = (float)cq.x;
+            vt = (float)cv.x;
         }
         sraw[tid] = xv;
         __syncthreads();
@@ -439,7 +464,15 @@ gdn_decode_kernel(const f16* __restrict__ x, int x_stride, int conv_fused,
         if (c0 == 0) y[bt_row * y_stride + (size_t)hv * V + vi] = f16_sat(o * out_scale);
         if (Ck != nullptr && t < T - 1)
             store_row16_nt(Ck + (size_t)t * ck_step + ((size_t)hv * V + vi) * GR_K + c0, reg);
-        if (t + 1 < T) __syncthreads();   // sraw is rewritten by the next token
+    };
+    token(0, ga0, gb0);
+    for (int t = 1; t < T; ++t) {   // verify rows (conv_fused is T == 1 only)
+        __syncthreads();   // sraw is rewritten by this token
+        const size_t bt_row = (size_t)b * T + t;
+        const f16* xr = x + bt_row * x_stride;
+        cq.x = xr[ch];
+        cv.x = xr[ch_v];
+        token(t, ga[bt_row * ab_stride + hv], gb[bt_row * ab_stride + hv]);
     }
     store_row16_nt(Srow, reg);
 }
@@ -587,11 +620,17 @@ int fl_gdn_decode(const void* x, int x_stride, int conv_fused, const void* conv_
             seqs.Ck[i] = Ck[i];
         }
     }
-    hipLaunchKernelGGL(gdn_decode_kernel, dim3(V / GR_ROWS, n_vheads, B), dim3(GR_THREADS), 0,
-                       (hipStream_t)stream, (const f16*)x, x_stride, conv_fused,
-                       (const f16*)conv_w, seqs, a, b, ab_stride, A_log, dt_bias, (f16*)y,
-                       y_stride, ck_step, T, n_kheads, n_vheads, V, out_scale, l2eps,
-                       n_vheads / n_kheads);
+    const dim3 grid(V / GR_ROWS, n_vheads, B);
+    if (conv_fused)
+        hipLaunchKernelGGL(gdn_decode_kernel<true>, grid, dim3(GR_THREADS), 0, (hipStream_t)stream,
+                           (const f16*)x, x_stride, (const f16*)conv_w, seqs, a, b, ab_stride,
+                           A_log, dt_bias, (f16*)y, y_stride, ck_step, T, n_kheads, n_vheads, V,
+                           out_scale, l2eps, n_vheads / n_kheads);
+    else
+        hipLaunchKernelGGL(gdn_decode_kernel<false>, grid, dim3(GR_THREADS), 0,
+                           (hipStream_t)stream, (const f16*)x, x_stride, (const f16*)conv_w, seqs,
+                           a, b, ab_stride, A_log, dt_bias, (f16*)y, y_stride, ck_step, T,
+                           n_kheads, n_vheads, V, out_scale, l2eps, n_vheads / n_kheads);
     return fl::check_launch("gdn_decode");
 }
 

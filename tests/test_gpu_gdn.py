@@ -170,6 +170,41 @@ def test_config1_decode_1024_steps_vs_oracle(fl, dev, orc):
     assert worst_y <= 2e-3
 
 
+@pytest.mark.parametrize("T", [1, 3])
+def test_fused_decode_equals_unfused_bit_exact(fl, dev, rng, T):
+    """The fused decode (norms, gates and delta rule in one launch) against the
+    unfused launches on the GPU -- l2norm_scaled, gdn_scalars, gdn_scan -- on
+    the same conv output: y and the state bit for bit. The unfused l2norm adds
+    the sums of squares in the reference's block_reduce_sum order, so this
+    pins the fused kernel's in-wave norm to that order."""
+    B = 2
+    c = (rng.standard_normal((B, T, ROW)) * 2).astype(np.float16)
+    c[1, 0, 2048:2176] = 0                                   # a zero k row
+    a = rng.standard_normal((B, T, NV)).astype(np.float32)
+    bb = rng.standard_normal((B, T, NV)).astype(np.float32)
+    A_log = (rng.standard_normal(NV) * 0.3).astype(np.float32)
+    dt = (rng.standard_normal(NV) * 0.3).astype(np.float32)
+    S0 = (rng.standard_normal((B, NV, 128, 128)) * 0.02).astype(np.float32)
+    Sf = [to_dev(S0[i], dev) for i in range(B)]
+    yf = fl.ops.gdn_decode(to_dev(c, dev), Sf, to_dev(a, dev), to_dev(bb, dev), to_dev(A_log, dev),
+                           to_dev(dt, dev), T=T, pos0s=[7] * B)
+    for i in range(B):
+        cd = to_dev(c[i], dev)
+        ln = cd.clone()
+        for t in range(T):
+            fl.ops.l2norm_scaled(cd[t], ln[t], rows=32, T=1)
+        beta = torch.empty((T, NV), dtype=torch.float32, device=dev)
+        decay = torch.empty_like(beta)
+        fl.ops.gdn_scalars(to_dev(a[i], dev), to_dev(bb[i], dev), to_dev(A_log, dev),
+                           to_dev(dt, dev), beta, decay, T=T)
+        Su = to_dev(S0[i], dev)
+        yu = torch.empty((T, NV * 128), dtype=torch.float16, device=dev)
+        fl.ops.gdn_scan(ln[:, :2048], ln[:, 2048:4096], ln[:, 4096:], beta, decay, Su, yu, T=T)
+        torch.cuda.synchronize()
+        assert torch.equal(yf[i], yu), f"seq {i}: y differs"
+        assert torch.equal(Sf[i], Su), f"seq {i}: state differs"
+
+
 def test_verify_t3_checkpoints_and_rollback(fl, dev, orc, rng):
     """MTP verify (runtime.py:3017-3053): conv rows then the fused scan with
     checkpoints; each checkpoint equals the state after that many T=1 steps."""
