@@ -344,7 +344,7 @@ attn_decode_split_kernel(const f16* __restrict__ qg, DecSeqs seqs, float* __rest
         float mt = sc[0];
 #pragma unroll
         for (int rr = 1; rr < 16; ++rr) mt = fmaxf(mt, sc[rr]);
-        mt = fmaxf(mt, lane_xor(mt, 32)) * sl2;
+        mt = pair32_max(mt) * sl2;
         // A column's running max moves only when the tile's max exceeds it by
         // more than RESCALE_LOG2: p <= 2^RESCALE_LOG2 stays exact in fp16 range
         // and O / l are rescaled on few tiles. The decision is the column's own
@@ -368,8 +368,7 @@ attn_decode_split_kernel(const f16* __restrict__ qg, DecSeqs seqs, float* __rest
             if (rr < 8) pk0[rr] = (f16)p;
             else pk1[rr - 8] = (f16)p;
         }
-        psum += lane_xor(psum, 32);
-        l_run += psum;
+        l_run += pair32_sum(psum);
         // O^T += V^T P^T over the tile's two 16-row k-steps
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {

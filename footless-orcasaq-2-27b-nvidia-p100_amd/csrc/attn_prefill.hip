@@ -402,7 +402,7 @@ attn_prefill_kernel(const f16* __restrict__ q, int q_pitch, const void* __restri
             float mt = sc[0];
 #pragma unroll
             for (int rr = 1; rr < 32; ++rr) mt = fmaxf(mt, sc[rr]);
-            mt = fmaxf(mt, lane_xor(mt, 32)) * sl2;
+            mt = pair32_max(mt) * sl2;
             if (__any(mt > m_run + RESCALE_LOG2)) {   // always on a wave's first tile, rarely after
                 const float m_new = fmaxf(m_run, mt);
                 const float corr = fast_exp2(m_run - m_new);
@@ -418,7 +418,7 @@ attn_prefill_kernel(const f16* __restrict__ q, int q_pitch, const void* __restri
                 psum += p;
                 pk[rr >> 3][rr & 7] = (f16)p;
             }
-            l_run += psum + lane_xor(psum, 32);
+            l_run += pair32_sum(psum);
             const char* vt = smem + V_OFF + st * TILE_B;
             pv_step<0, 0>(o, pk[0], vt, troff);
             pv_step<0, 1>(o, pk[0], vt, troff);
@@ -450,6 +450,287 @@ attn_prefill_kernel(const f16* __restrict__ q, int q_pitch, const void* __restri
     }
 }
 
+// One HBM -> LDS copy of 16 bytes a lane to LDS dst + IMM (+ 16 lane). m0 is
+// set inside the asm from a wave-uniform base and an immediate, so the
+// compiler keeps no per-copy LDS addresses in SGPRs (it would otherwise hoist
+// all of them out of the tile loop); the asm declares m0 as its output.
+template <int IMM>
+__device__ __forceinline__ void copy16_at(const char* sbase, uint32_t voff, uint32_t dst) {
+    uint32_t m0v;
+    asm volatile("s_add_u32 m0, %3, %4\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
+                 : "={m0}"(m0v)
+                 : "v"(voff), "s"(sbase), "s"(dst), "i"(IMM));
+}
+
+// ---------------------------------------------------------------------------
+// fp16 cache, long prompts: 64 query rows a wave. A workgroup owns 256 rows
+// (4 waves x 64) of one kv head and walks the causal KV range in 32-row
+// tiles. Per wave and tile the 64 rows are two 32-column MFMA blocks (nb = 0,
+// 1) that share every K and V fragment read from LDS:
+//   S^T (32 kv x 64 rows) = K Q^T      16 k-steps x 2 MFMA 32x32x16 (one
+//                                       K fragment per k-step, Q in
+//                                       registers)
+//   online softmax per query column     as attn_prefill_kernel, per block
+//   O^T (256 d x 64 rows) += V^T P^T    8 dim blocks x 2 k-steps x 2 MFMA
+//                                       (one V^T fragment per pair)
+// so a wave reads 32 KiB of K and V from LDS per 64 MFMAs (attn_prefill_
+// kernel: 64 KiB) and the workgroup copies 32 KiB from HBM per 256 x 32 query
+// x key pairs (there: 64 KiB per 128 x 64). O^T is 256 AGPRs (all of them),
+// Q^T 128 VGPRs. Tiles are copied HBM -> LDS by global_load_lds, R64_DIST
+// tiles ahead of the one computed, into R64_NST = R64_DIST + 1 stages of 32
+// KiB (K | V), with the swizzle of attn_prefill_kernel. Same arithmetic as
+// attn_prefill_kernel (fp32 scores, exp2 with the scale folded in, the
+// lazy rescale, P rounded to fp16); 32-row tiles move the rescale points,
+// so the two kernels agree to rounding, not bit for bit.
+// ---------------------------------------------------------------------------
+constexpr int R64_BQ = 256;                 // rows a workgroup
+constexpr int R64_BK = 32;                  // kv rows a tile
+constexpr int R64_TILE = R64_BK * ROW_B;    // 16 KiB: K (or V) of a tile
+constexpr int R64_STAGE = 2 * R64_TILE;     // K | V
+constexpr int R64_DIST = 3;                 // tiles copied ahead
+constexpr int R64_NST = R64_DIST + 1;
+constexpr int R64_LDS = R64_NST * R64_STAGE;   // 128 KiB
+constexpr int R64_COPIES = 8;               // copy instructions a wave a tile (4 K + 4 V)
+#ifndef R64_MIN_WGS
+#define R64_MIN_WGS 512                     // the r64 kernel from this many workgroups up
+#endif
+
+// Copy tile kv0 (K and V, 32 rows each) into the stage at dst: wave w copies
+// rows 8 w .. 8 w + 7, two a copy instruction (as issue_rows: loff[n] = this
+// lane's source offset from row 8 w, row 2 n + lane / 32, swizzled chunk).
+__device__ __forceinline__ void r64_issue(uint32_t dst, const char* kb, const char* vb,
+                                          uint32_t rsb, int kv0, int kv_end, int w, int lane,
+                                          const uint32_t (&loff)[4]) {
+    const uint32_t d0 = __builtin_amdgcn_readfirstlane(dst + 8 * w * ROW_B);
+    if (kv0 + R64_BK <= kv_end) {
+        const size_t ro = (size_t)(kv0 + 8 * w) * rsb;
+        const char* kr = kb + ro;
+        const char* vr = vb + ro;
+        copy16_at<0 * ROW_B>(kr, loff[0], d0);
+        copy16_at<2 * ROW_B>(kr, loff[1], d0);
+        copy16_at<4 * ROW_B>(kr, loff[2], d0);
+        copy16_at<6 * ROW_B>(kr, loff[3], d0);
+        copy16_at<R64_TILE + 0 * ROW_B>(vr, loff[0], d0);
+        copy16_at<R64_TILE + 2 * ROW_B>(vr, loff[1], d0);
+        copy16_at<R64_TILE + 4 * ROW_B>(vr, loff[2], d0);
+        copy16_at<R64_TILE + 6 * ROW_B>(vr, loff[3], d0);
+    } else {
+        uint32_t vo[4];
+#pragma unroll
+        for (int n = 0; n < 4; ++n) {
+            const int r = 8 * w + 2 * n + (lane >> 5);
+            const int c = (lane & 31) ^ sw(r);
+            vo[n] = (uint32_t)min(kv0 + r, kv_end - 1) * rsb + 16 * c;
+        }
+        copy16_at<0 * ROW_B>(kb, vo[0], d0);
+        copy16_at<2 * ROW_B>(kb, vo[1], d0);
+        copy16_at<4 * ROW_B>(kb, vo[2], d0);
+        copy16_at<6 * ROW_B>(kb, vo[3], d0);
+        copy16_at<R64_TILE + 0 * ROW_B>(vb, vo[0], d0);
+        copy16_at<R64_TILE + 2 * ROW_B>(vb, vo[1], d0);
+        copy16_at<R64_TILE + 4 * ROW_B>(vb, vo[2], d0);
+        copy16_at<R64_TILE + 6 * ROW_B>(vb, vo[3], d0);
+    }
+}
+
+// Softmax of one 32-column block of a tile (one query column per lane pair,
+// 16 of its 32 scores a lane): the masked scores (diag: the tile crosses this
+// wave's diagonal; score r is kv row 8 (r / 4) + 4 hh + r % 4 of the tile,
+// kept when that is <= lim), the running max / sum update with the lazy
+// rescale of this block's O^T, and P in fp16 (pk[kq] = scores 8 kq .. + 7,
+// the B operand of the PV k-step kq).
+__device__ __forceinline__ void r64_softmax(f32x16& s, bool diag, int lim, float sl2,
+                                            float& m_run, float& l_run, f32x16 (&o)[8],
+                                            f16x8 (&pk)[2]) {
+    if (diag) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s[r] = 8 * (r >> 2) + (r & 3) <= lim ? s[r] : -INFINITY;
+    }
+    float mt = s[0];
+#pragma unroll
+    for (int r = 1; r < 16; ++r) mt = fmaxf(mt, s[r]);
+    mt = pair32_max(mt) * sl2;
+    if (__any(mt > m_run + RESCALE_LOG2)) {   // always on a wave's first tile, rarely after
+        const float m_new = fmaxf(m_run, mt);
+        const float corr = fast_exp2(m_run - m_new);
+        m_run = m_new;
+        l_run *= corr;
+        acc_scale(o, corr);
+    }
+    float psum = 0.f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const float p = fast_exp2(fmaf(s[r], sl2, -m_run));
+        psum += p;
+        pk[r >> 3][r & 7] = (f16)p;
+    }
+    l_run += pair32_sum(psum);
+}
+
+// The 8 V^T fragments (ds_read_b64_tr_b16) of PV step n: k-step kq = n / 2
+// (kv rows 16 kq ..), dim blocks 4 (n % 2) .. + 3; b: this lane's offsets
+// (the troff of attn_prefill_kernel).
+__device__ __forceinline__ void r64_vfrags(s16x4 (&vb)[8], const char* vt,
+                                           const uint32_t (&b)[8], int n) {
+    const int imm = 16 * ROW_B * (n >> 1) + 256 * (n & 1);
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+        vb[i] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vt + b[i] + imm));
+}
+
+__global__ void __launch_bounds__(PF_THREADS)
+attn_prefill_r64_kernel(const f16* __restrict__ q, int q_pitch, const f16* __restrict__ kc,
+                        const f16* __restrict__ vc, f16* __restrict__ z, int z_pitch,
+                        int n_q_heads, int n_kv, int pos0, int T, float sl2, int n_row_tiles) {
+    extern __shared__ __attribute__((aligned(16))) char smem[];
+
+    const int tile = n_row_tiles - 1 - (int)blockIdx.x;   // heaviest first
+    const int h = blockIdx.y;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int ql = lane & 31, hh = lane >> 5;
+    const int G = n_q_heads / n_kv;
+    const int RT = T * G;
+    const int R0 = tile * R64_BQ;
+    // this lane's two query rows (columns of the two MFMA blocks)
+    int row[2], t[2], g[2], qpos[2];
+    bool rvalid[2];
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) {
+        row[nb] = R0 + 64 * w + 32 * nb + ql;
+        rvalid[nb] = row[nb] < RT;
+        t[nb] = rvalid[nb] ? row[nb] / G : 0;
+        g[nb] = rvalid[nb] ? row[nb] - t[nb] * G : 0;
+        qpos[nb] = rvalid[nb] ? pos0 + t[nb] : -1;
+    }
+    const int wfirst = R0 + 64 * w;
+    const int wlast = min(wfirst + 63, RT - 1);
+    const int wqmax = __builtin_amdgcn_readfirstlane(wlast >= wfirst ? pos0 + wlast / G : -1);
+    const int wqmin = __builtin_amdgcn_readfirstlane(pos0 + wfirst / G);
+    const int blast = min(R0 + R64_BQ - 1, RT - 1);
+    const int kv_end = __builtin_amdgcn_readfirstlane(pos0 + blast / G + 1);
+    const int n_tiles = (kv_end + R64_BK - 1) / R64_BK;
+
+    const uint32_t rsb = (uint32_t)n_kv * ROW_B;
+    const char* kb = uniform_ptr((const char*)(kc + (size_t)h * PF_HD));
+    const char* vb = uniform_ptr((const char*)(vc + (size_t)h * PF_HD));
+    uint32_t loff[4];
+#pragma unroll
+    for (int n = 0; n < 4; ++n) {
+        const int r = 2 * n + (lane >> 5);   // row from 8 w
+        loff[n] = r * rsb + 16 * ((lane & 31) ^ sw(8 * w + r));
+    }
+    const uint32_t lds_base = (uint32_t)(uintptr_t)((__attribute__((address_space(3))) char*)smem);
+
+#pragma unroll
+    for (int d = 0; d < R64_DIST; ++d)
+        if (d < n_tiles) r64_issue(lds_base + d * R64_STAGE, kb, vb, rsb, d * R64_BK, kv_end, w, lane, loff);
+
+    f16x8 qreg[2][16];   // Q[row nb][128 hh + 8 ks + 0..7]
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) {
+        const f16* qrow = q + ((size_t)t[nb] * n_q_heads + h * G + g[nb]) * q_pitch + 128 * hh;
+#pragma unroll
+        for (int ks = 0; ks < 16; ++ks)
+            qreg[nb][ks] = rvalid[nb] ? *(const f16x8*)(qrow + 8 * ks) : (f16x8)(0);
+    }
+    WAIT_VMCNT(0);   // Q and the first tiles: the wait left to the compiler lands in the loop
+
+    f32x16 o[2][8];
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+        for (int mb = 0; mb < 8; ++mb) acc_zero(o[nb][mb], (f16x8)(0));
+    float m_run[2] = {-1e30f, -1e30f}, l_run[2] = {0.f, 0.f};
+
+    // K operand of k-step ks: tile row ql, chunk 16 hh + ks, at 16 hh + (ks ^ sw(ql))
+    const uint32_t koff = ql * ROW_B + 256 * hh + 16 * sw(ql);
+    const int tr_r = (lane & 15) >> 2;
+    const int tr_d = 16 * ((lane & 31) >> 4) + 4 * (lane & 3);
+    uint32_t troff[8];
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2)
+            troff[2 * u + s2] = (4 * hh + tr_r + 8 * s2) * ROW_B + 64 * (u ^ tr_r) +
+                                16 * ((tr_d >> 3) ^ (hh + 2 * s2)) + 2 * (tr_d & 7);
+
+    typedef __attribute__((address_space(3))) const f16x8 lds_f16x8;
+    typedef __attribute__((address_space(3))) const char lds_char;
+    int st = 0;   // stage of tile j
+    for (int j = 0; j < n_tiles; ++j) {
+        // tile j landed: the copies of the min(DIST - 1, n_tiles - 1 - j)
+        // tiles issued after it may still be in flight
+        const int ahead = min(R64_DIST - 1, n_tiles - 1 - j);
+        if (ahead >= 2) WAIT_VMCNT(2 * R64_COPIES);
+        else if (ahead == 1) WAIT_VMCNT(R64_COPIES);
+        else WAIT_VMCNT(0);
+        tile_done();   // every wave is past tile j - 1: its stage can be refilled
+        if (j + R64_DIST < n_tiles) {
+            const int sn = st == 0 ? R64_NST - 1 : st - 1;   // (j + DIST) % NST == (j - 1) % NST
+            r64_issue(lds_base + sn * R64_STAGE, kb, vb, rsb, (j + R64_DIST) * R64_BK, kv_end, w,
+                      lane, loff);
+        }
+        const int kv0 = j * R64_BK;
+        if (kv0 <= wqmax) {
+            const uint32_t kst = koff + st * R64_STAGE;
+            f32x16 s[2] = {(f32x16)(0.f), (f32x16)(0.f)};
+            constexpr int KPF = 3;   // K fragments read KPF k-steps ahead of their MFMAs
+            f16x8 ka[KPF];
+#pragma unroll
+            for (int ks = 0; ks < KPF; ++ks) ka[ks] = *(lds_f16x8*)((lds_char*)smem + (kst ^ (16 * ks)));
+#pragma unroll
+            for (int ks = 0; ks < 16; ++ks) {
+                const f16x8 a = ka[ks % KPF];
+                if (ks + KPF < 16)
+                    ka[ks % KPF] = *(lds_f16x8*)((lds_char*)smem + (kst ^ (16 * (ks + KPF))));
+                s[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qreg[0][ks], s[0], 0, 0, 0);
+                s[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qreg[1][ks], s[1], 0, 0, 0);
+                __builtin_amdgcn_sched_barrier(0);   // keep the reads ahead
+            }
+            const bool diag = kv0 + R64_BK - 1 > wqmin;   // wave-uniform
+            f16x8 pk[2][2];
+            r64_softmax(s[0], diag, qpos[0] - kv0 - 4 * hh, sl2, m_run[0], l_run[0], o[0], pk[0]);
+            r64_softmax(s[1], diag, qpos[1] - kv0 - 4 * hh, sl2, m_run[1], l_run[1], o[1], pk[1]);
+            // O^T += V^T P^T: 4 steps (kq, dim half) of 4 fragments x 2 blocks,
+            // the next step's fragments read under this step's MFMAs
+            const char* vt = smem + st * R64_STAGE + R64_TILE;
+            s16x4 vf[2][8];
+            r64_vfrags(vf[0], vt, troff, 0);
+#pragma unroll
+            for (int n = 0; n < 4; ++n) {
+                if (n + 1 < 4) r64_vfrags(vf[(n + 1) & 1], vt, troff, n + 1);
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const f16x4 lf = __builtin_bit_cast(f16x4, vf[n & 1][2 * u]);
+                    const f16x4 hf = __builtin_bit_cast(f16x4, vf[n & 1][2 * u + 1]);
+                    const f16x8 av = {lf[0], lf[1], lf[2], lf[3], hf[0], hf[1], hf[2], hf[3]};
+                    acc_mfma(o[0][4 * (n & 1) + u], av, pk[0][n >> 1]);
+                    acc_mfma(o[1][4 * (n & 1) + u], av, pk[1][n >> 1]);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+        st = st == R64_NST - 1 ? 0 : st + 1;
+    }
+
+    acc_settle(o[0]);
+    acc_settle(o[1]);
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) {
+        if (!rvalid[nb]) continue;
+        const float inv = 1.f / l_run[nb];
+        f16* zrow = z + ((size_t)t[nb] * n_q_heads + h * G + g[nb]) * z_pitch + 4 * hh;
+#pragma unroll
+        for (int mb = 0; mb < 8; ++mb)
+#pragma unroll
+            for (int r4 = 0; r4 < 4; ++r4)
+                *(f16x4*)(zrow + 32 * mb + 8 * r4) = (f16x4){
+                    f16_sat(o[nb][mb][4 * r4] * inv), f16_sat(o[nb][mb][4 * r4 + 1] * inv),
+                    f16_sat(o[nb][mb][4 * r4 + 2] * inv), f16_sat(o[nb][mb][4 * r4 + 3] * inv)};
+    }
+}
+
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 template <bool Q8>
@@ -478,7 +759,10 @@ int prefill(const void* q, int q_pitch, const void* k_new, const void* v_new, vo
     if (!lds_attr_set) {
         if (hipFuncSetAttribute((const void*)attn_prefill_kernel<Q8>,
                                 hipFuncAttributeMaxDynamicSharedMemorySize, LDS_B) !=
-            hipSuccess) {
+                hipSuccess ||
+            (!Q8 && hipFuncSetAttribute((const void*)attn_prefill_r64_kernel,
+                                        hipFuncAttributeMaxDynamicSharedMemorySize,
+                                        R64_LDS) != hipSuccess)) {
             fl::set_error("attn_prefill: cannot raise the dynamic LDS limit to %d bytes",
                           LDS_B);
             return FL_ELAUNCH;
@@ -501,6 +785,16 @@ int prefill(const void* q, int q_pitch, const void* k_new, const void* v_new, vo
         vc = (const f16*)vcache + off;
     }
     const int rows = T * (n_q_heads / n_kv_heads);
+    // 64 rows a wave once there are enough 256-row workgroups to fill the
+    // chip twice over; below that the 128-row workgroups keep more CUs busy
+    const int r64_tiles = (rows + R64_BQ - 1) / R64_BQ;
+    if (!Q8 && r64_tiles * n_kv_heads >= R64_MIN_WGS) {
+        hipLaunchKernelGGL(attn_prefill_r64_kernel, dim3(r64_tiles, n_kv_heads), dim3(PF_THREADS),
+                           R64_LDS, (hipStream_t)stream, (const f16*)q, q_pitch,
+                           (const f16*)kc, (const f16*)vc, (f16*)z, z_pitch, n_q_heads,
+                           n_kv_heads, pos0, T, scale * FL_LOG2E, r64_tiles);
+        return fl::check_launch("attn_prefill_r64");
+    }
     const int n_row_tiles = (rows + PF_BQ - 1) / PF_BQ;
     hipLaunchKernelGGL(attn_prefill_kernel<Q8>, dim3(n_row_tiles, n_kv_heads), dim3(PF_THREADS),
                        LDS_B, (hipStream_t)stream, (const f16*)q, q_pitch, kc, vc, ksc, vsc,

@@ -66,6 +66,23 @@ __device__ __forceinline__ float lane_xor(float v, int mask) {
     return __int_as_float(__builtin_amdgcn_ds_bpermute((lane ^ mask) << 2, __float_as_int(v)));
 }
 
+// max / sum of v over the lane pair (l, l ^ 32) on every lane, with one
+// v_permlane32_swap (gfx950, a VALU operation) instead of an LDS-pipe lane
+// exchange: with both operands v it returns (v[0..31], v[0..31]) and
+// (v[32..63], v[32..63]), so lane l gets v[l % 32] and v[l % 32 + 32];
+// max and + are symmetric, the result equals v op lane_xor(v, 32) bit for
+// bit.
+__device__ __forceinline__ float pair32_max(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                    false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float pair32_sum(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                    false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 // Lane exchanges at distance 1 and 2 inside each group of 4 lanes (DPP quad
 // permutes, no LDS).
 __device__ __forceinline__ float dpp_xor1(float v) {

@@ -306,16 +306,20 @@ __device__ __forceinline__ void store_row16_nt(float* dst, const float (&reg)[16
 }
 
 // warp32_tree's value at lanes 0 and 32 (other lanes: partial sums) without
-// LDS-pipe exchanges but the first: lane i pairs with i + 16 (ds_swizzle,
-// i ^ 16 within each 32 lanes), then with i + 8, 4, 2, 1 inside its 16-lane
-// row (DPP row_shl, a VALU operand modifier). At lanes 0 and 32 these are the
-// pairs of the xor tree (x ^ d == x + d there), added in the same order.
+// LDS-pipe exchanges: lane i pairs with i + 16 (v_permlane16_swap, gfx950:
+// with both operands v it returns rows (0, 0, 2, 2) and (1, 1, 3, 3) of v, so
+// their sum at lane i of rows 0 and 2 is v[i] + v[i + 16]), then with i + 8,
+// 4, 2, 1 inside its 16-lane row (DPP row_shl, a VALU operand modifier). At
+// lanes 0 and 32 these are the pairs of the xor tree (x ^ d == x + d there),
+// added in the same order.
 template <int D>
 __device__ __forceinline__ float dpp_shl(float v) {
     return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x100 + D, 0xF, 0xF, true));
 }
 __device__ __forceinline__ float warp32_tree_lane0(float v) {
-    v += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401F));
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                    false);
+    v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
     v += dpp_shl<8>(v);
     v += dpp_shl<4>(v);
     v += dpp_shl<2>(v);

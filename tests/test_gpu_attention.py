@@ -202,3 +202,31 @@ def test_prefill_config3_sampled_rows(fl, dev, orc, L):
                                    scale=1.0, T=1)
         err, ok = close(zh[t:t + 1], want, ATOL, RTOL)
         assert ok, f"L={L} row {t}: max|err| {err}"
+
+
+@pytest.mark.parametrize("T,pos0,ramp", [(6000, 0, False), (5800, 700, True)])
+def test_prefill_long_sampled_rows(fl, dev, orc, T, pos0, ramp):
+    """Prompts long enough for the 64-rows-a-wave prefill kernel (at least 512
+    workgroups of 256 (token, head) rows): a ragged last workgroup, pos0 > 0,
+    and (ramp) scores that climb along the sequence so the lazy O / l rescale
+    runs on later tiles; sampled rows against the float64 closed form."""
+    L = pos0 + T
+    rng = np.random.default_rng(T)
+    kc, vc = rand_cache(rng, L)
+    qg = rand_qg(rng, T)
+    if ramp:
+        pos = np.arange(L)
+        kc = (kc.astype(np.float32) * 0.25 + (0.12 * (pos % 384))[:, None, None]).astype(np.float16)
+        qg[..., :256] = (1 / 16 + 0.01 * rng.standard_normal((T, 24, 256))).astype(np.float16)
+    kd = torch.from_numpy(kc).to(dev)
+    vd = torch.from_numpy(vc).to(dev)
+    z = fl.ops.attention_prefill(to_dev(qg, dev), kd, vd, pos0=pos0)
+    torch.cuda.synchronize()
+    zh = z.cpu().numpy()
+    assert np.isfinite(zh.astype(np.float32)).all()
+    for t in sorted({0, 1, 5, 42, 43, 255, 256, T // 2, T - 43, T - 2, T - 1,
+                     *rng.integers(0, T, 5).tolist()}):
+        want = orc.attention_exact(qg[t:t + 1], kc, vc, q_pitch=512, pos0=pos0 + t, max_pos=L,
+                                   scale=SCALE, T=1)
+        err, ok = close(zh[t:t + 1], want, ATOL, RTOL)
+        assert ok, f"T={T} pos0={pos0} row {t}: max|err| {err}"
