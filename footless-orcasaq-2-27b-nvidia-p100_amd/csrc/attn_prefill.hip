@@ -487,13 +487,15 @@ constexpr int R64_BQ = 256;                 // rows a workgroup
 constexpr int R64_BK = 32;                  // kv rows a tile
 constexpr int R64_TILE = R64_BK * ROW_B;    // 16 KiB: K (or V) of a tile
 constexpr int R64_STAGE = 2 * R64_TILE;     // K | V
-constexpr int R64_DIST = 3;                 // tiles copied ahead
+// Tiles copied ahead and K fragments read ahead: 2, 3 and 4 tiles and 2, 3
+// and 4 k-steps measured the same within noise at 8k and 32k.
+constexpr int R64_DIST = 3;
+constexpr int R64_KPF = 3;
 constexpr int R64_NST = R64_DIST + 1;
-constexpr int R64_LDS = R64_NST * R64_STAGE;   // 128 KiB
+constexpr int R64_LDS = R64_NST * R64_STAGE;   // 128 KiB at R64_DIST 3
+static_assert(R64_LDS <= 160 * 1024, "R64_DIST: LDS <= 160 KiB");
 constexpr int R64_COPIES = 8;               // copy instructions a wave a tile (4 K + 4 V)
-#ifndef R64_MIN_WGS
-#define R64_MIN_WGS 512                     // the r64 kernel from this many workgroups up
-#endif
+constexpr int R64_MIN_WGS = 512;            // the r64 kernel from this many workgroups up
 
 // Copy tile kv0 (K and V, 32 rows each) into the stage at dst: wave w copies
 // rows 8 w .. 8 w + 7, two a copy instruction (as issue_rows: loff[n] = this
@@ -662,7 +664,8 @@ attn_prefill_r64_kernel(const f16* __restrict__ q, int q_pitch, const f16* __res
         // tile j landed: the copies of the min(DIST - 1, n_tiles - 1 - j)
         // tiles issued after it may still be in flight
         const int ahead = min(R64_DIST - 1, n_tiles - 1 - j);
-        if (ahead >= 2) WAIT_VMCNT(2 * R64_COPIES);
+        if (ahead >= 3) WAIT_VMCNT(3 * R64_COPIES);
+        else if (ahead == 2) WAIT_VMCNT(2 * R64_COPIES);
         else if (ahead == 1) WAIT_VMCNT(R64_COPIES);
         else WAIT_VMCNT(0);
         tile_done();   // every wave is past tile j - 1: its stage can be refilled
@@ -675,7 +678,7 @@ attn_prefill_r64_kernel(const f16* __restrict__ q, int q_pitch, const f16* __res
         if (kv0 <= wqmax) {
             const uint32_t kst = koff + st * R64_STAGE;
             f32x16 s[2] = {(f32x16)(0.f), (f32x16)(0.f)};
-            constexpr int KPF = 3;   // K fragments read KPF k-steps ahead of their MFMAs
+            constexpr int KPF = R64_KPF;
             f16x8 ka[KPF];
 #pragma unroll
             for (int ks = 0; ks < KPF; ++ks) ka[ks] = *(lds_f16x8*)((lds_char*)smem + (kst ^ (16 * ks)));
