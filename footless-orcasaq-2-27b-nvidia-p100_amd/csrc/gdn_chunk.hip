@@ -16,9 +16,10 @@
 //
 // Two launches: chunk_prep (every (chunk, v head) in parallel: Q K^T and K K^T
 // on MFMA, W and U by forward substitution in fp32, into the caller's
-// workspace), then chunk_state (one workgroup per (v head, 64 state rows),
-// sequential over the chunks with the state in MFMA accumulators; fp32 MFMA
-// (v_mfma_f32_16x16x4_f32) for the three products of a chunk).
+// workspace), then chunk_state (one workgroup per (v head, 16 state rows),
+// sequential over the chunks with the state in MFMA accumulators spread over
+// four waves; fp32 MFMA (v_mfma_f32_16x16x4_f32) for the three products of a
+// chunk).
 #include "fl_common.hpp"
 
 #pragma clang fp contract(off)
@@ -149,30 +150,6 @@ chunk_prep_kernel(const f16* __restrict__ q, const f16* __restrict__ k, const f1
     }
 }
 
-// The state pass. A workgroup of 4 waves owns 64 state rows (v) of one v
-// head, 16 a wave; a wave keeps its slice of S^T (128 k x 16 v) in 32 fp32
-// MFMA accumulators (block mb of 16 k rows, lane l: k = 16 mb + 4 (l/16) + r,
-// v = v0 + l%16 -- the D layout of v_mfma_f32_16x16x4_f32). Per chunk:
-//   A: P = W S^T, QS = Q S^T              [64 tok x 16 v], 256 MFMA
-//      Delta = U - P
-//   B: O = e^{g} o QS + QKm Delta         causal blocks only, 40 MFMA
-//   C: S^T = e^{g_C} S^T + Kd^T Delta     Kd^T[k][j] = e^{g_C - g_j} k_j[k], 128 MFMA
-// The k-step order of each product is permuted so that its B operand is an
-// accumulator register of the previous product: step (kq, r) takes k (or the
-// token) 16 kq + 4 (l/16) + r, which is register r of block kq. W, QKm, Q and
-// K are staged in LDS with row pitches that keep the operand reads on
-// distinct banks; Kd^T is read with ds_read_b64_tr_b16 from K's rows.
-constexpr int CS_ROWS = 64;          // state rows a workgroup
-constexpr int CS_WP = CK_K + 4;      // f32 pitch of staged W rows
-constexpr int CS_QKP = CK_C + 4;     // f32 pitch of staged QKm rows
-constexpr int CS_QP = CK_K + 8;      // f16 pitch of staged Q rows
-constexpr int CS_KP = CK_K + 16;     // f16 pitch of staged K rows
-constexpr int CS_OFF_QK = CK_C * CS_WP * 4;
-constexpr int CS_OFF_Q = CS_OFF_QK + CK_C * CS_QKP * 4;
-constexpr int CS_OFF_K = CS_OFF_Q + CK_C * CS_QP * 2;
-constexpr int CS_OFF_G = CS_OFF_K + CK_C * CS_KP * 2;
-constexpr int CS_LDS = CS_OFF_G + 3 * CK_C * 4;   // G, e^{G}, e^{G_last - G}
-
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 
@@ -180,175 +157,198 @@ __device__ __forceinline__ f32x4 mfma4(float a, float b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
-__global__ void __launch_bounds__(256)
+// The state pass, with the state's k columns split over the 4 waves of a
+// workgroup (four waves on each sequential chain, a quarter of its MFMAs
+// each). A workgroup owns 16 state rows (v) of one v head; wave w the k
+// range [32 w, 32 w + 32) of them, as two 16 x 16 blocks of S^T in the D
+// layout of v_mfma_f32_16x16x4_f32 (block kb, lane l: k = 32 w + 16 kb +
+// 4 (l / 16) + r, v = v0 + l % 16). Per chunk:
+//   A: the wave's partials P_w = W[:, k_w] S^T[k_w, :] and QS_w = Q[:, k_w]
+//      S^T[k_w, :] (64 tokens x 16 v, 64 MFMA) into LDS; one barrier;
+//      every wave adds the four partials of P in wave order: Delta = U - P
+//   B: wave w's token block of O = e^{g} o QS + QKm Delta (QS summed the
+//      same way), the causal blocks only
+//   C: its k range of S^T = e^{g_C} S^T + Kd^T Delta (32 MFMA; Kd^T read
+//      from this wave's K slice in LDS with ds_read_b64_tr_b16)
+// Every operand is read by one wave only (W, Q and K by k range, QKm by
+// token block; U and the decay factors by all four), straight from the
+// workspace into registers: W and Q of the next chunk are requested after
+// phase A, the rest after phase C, so each load has half a chunk to land.
+// The partial buffers alternate between chunks (one barrier a chunk).
+constexpr int CS_ROWS = 16;                       // state rows (v) a workgroup
+constexpr int CS_PART = 2 * 4 * 4 * 64;           // f32x4 of one parity: [wave][P | QS][mb][lane]
+constexpr int CS_KSLICE = 64 * 64;                // bytes of one wave's K slice (64 tok x 32 k f16)
+constexpr int CS_LDS = 2 * CS_PART * 16 + 4 * CS_KSLICE;   // 64 KiB + 16 KiB
+
+__global__ void __launch_bounds__(256, 2)   // two workgroups a CU: <= 256 registers a lane
 chunk_state_kernel(const f16* __restrict__ q, const f16* __restrict__ k, float* __restrict__ S,
                    f16* __restrict__ y, int T, int n_vheads, int qk_stride, int y_stride,
                    float out_scale, int group, const float* __restrict__ work) {
     extern __shared__ __attribute__((aligned(16))) char smem[];
-    float* sW = (float*)smem;
-    float* sQK = (float*)(smem + CS_OFF_QK);
-    f16* sQ = (f16*)(smem + CS_OFF_Q);
-    f16* sK = (f16*)(smem + CS_OFF_K);
-    float* sG = (float*)(smem + CS_OFF_G);
-
-    const int rb = blockIdx.x, hv = blockIdx.y, hk = hv / group;
-    const int tid = threadIdx.x, l = tid & 63, w = tid >> 6;
+    f32x4* part = (f32x4*)smem;
+    // grid (v heads, row blocks): the workgroups of a v head, which read the
+    // same W / QKm / K of every chunk, are dispatched n_vheads apart and so,
+    // with n_vheads a multiple of 8 (48 here), land on one XCD (dispatch goes
+    // round robin over the 8) and share its L2
+    const int hv = blockIdx.x, rb = blockIdx.y, hk = hv / group;
+    const int tid = threadIdx.x, l = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int m = l & 15, kk = l >> 4;
-    const int v0 = rb * CS_ROWS + 16 * w;
-    float* Sv = S + ((size_t)hv * CK_V + v0 + m) * CK_K + 4 * kk;   // S[v0 + m][4 kk ...]
+    const int v0 = rb * CS_ROWS, k0 = 32 * w;
+    char* ksl = smem + 2 * CS_PART * 16 + w * CS_KSLICE;   // this wave's K slice
+    typedef __attribute__((address_space(3))) const char lds_char;
+    const uint32_t ksl_lds = (uint32_t)(uintptr_t)((__attribute__((address_space(3))) char*)ksl);
 
-    f32x4 st[8];   // S^T block mb: rows k = 16 mb + 4 kk + r, column v0 + m
+    float* Sv = S + ((size_t)hv * CK_V + v0 + m) * CK_K + k0 + 4 * kk;   // S[v0 + m][k0 + 4 kk ..]
+    f32x4 st[2];
 #pragma unroll
-    for (int mb = 0; mb < 8; ++mb) st[mb] = *(const f32x4*)(Sv + 16 * mb);
+    for (int kb = 0; kb < 2; ++kb) st[kb] = *(const f32x4*)(Sv + 16 * kb);
 
-    // A chunk's operands are loaded into registers one chunk ahead (while the
-    // previous chunk computes) and written to LDS after its end barrier.
-    // Thread tid stages W rows i = tid / 32 + 8 j (f32x4 at column 4 (tid % 32)),
-    // QKm rows tid / 16 + 16 j, Q / K rows tid / 16 + 16 j (f16x8 at 8 (tid % 16)).
-    f32x4 pw[8], pqk[4];
-    f16x8 pq[4], pk[4];
-    float pg[3] = {0.f, 0.f, 0.f};
-    f32x4 pu[4];
-    auto prefetch = [&](int c) {
+    // operands of a chunk
+    f32x4 wf[4][2];    // W[16 mb + m][k0 + 16 kq + 4 kk ..]
+    f16x4 qf[4][2];    // Q[t0 + 16 mb + m][k0 + 16 kq + 4 kk ..]
+    f32x4 qkm[4];      // QKm[16 w + m][16 kq + 4 kk ..]
+    f32x4 u[4];        // U^T[v0 + m][16 mb + 4 kk ..]
+    f32x4 dk[4];       // e^{g_C - g}[16 kq + 4 kk ..]
+    f32x4 eg;          // e^{g}[16 w + 4 kk ..]
+    float eC;          // e^{g_C}
+    f16x8 kv[4];       // K slice staging: 16-byte chunk l + 64 j of the wave's [64 tok][32 k]
+    auto blk_of = [&](int c) { return work + ((size_t)c * n_vheads + hv) * CK_BLK; };
+    auto load_wq = [&](int c) {
         const int t0 = c * CK_C;
         const int n = min(CK_C, T - t0);
-        const float* blk = work + ((size_t)c * n_vheads + hv) * CK_BLK;
-        const float* Wg = blk;
+        const float* Wg = blk_of(c);
+#pragma unroll
+        for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+            for (int kq = 0; kq < 2; ++kq) {
+                wf[mb][kq] = *(const f32x4*)(Wg + (size_t)(16 * mb + m) * CK_K + k0 + 16 * kq + 4 * kk);
+                const int i = 16 * mb + m;
+                qf[mb][kq] = i < n ? *(const f16x4*)(q + (size_t)(t0 + i) * qk_stride +
+                                                     (size_t)hk * CK_K + k0 + 16 * kq + 4 * kk)
+                                   : (f16x4)(0);
+            }
+    };
+    auto load_rest = [&](int c) {
+        const int t0 = c * CK_C;
+        const int n = min(CK_C, T - t0);
+        const float* Wg = blk_of(c);
         const float* UTg = Wg + CK_C * CK_K;
         const float* QKg = UTg + CK_C * CK_V;
         const float* Gg = QKg + CK_C * CK_C;
 #pragma unroll
-        for (int j = 0; j < 8; ++j)
-            pw[j] = *(const f32x4*)(Wg + (size_t)((tid >> 5) + 8 * j) * CK_K + 4 * (tid & 31));
+        for (int j = 0; j < 4; ++j) {
+            qkm[j] = *(const f32x4*)(QKg + (size_t)(16 * w + m) * CK_C + 16 * j + 4 * kk);
+            u[j] = *(const f32x4*)(UTg + (size_t)(v0 + m) * CK_C + 16 * j + 4 * kk);
+            dk[j] = *(const f32x4*)(Gg + 2 * CK_C + 16 * j + 4 * kk);
+        }
+        eg = *(const f32x4*)(Gg + CK_C + 16 * w + 4 * kk);
+        eC = Gg[2 * CK_C - 1];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const int i = (tid >> 4) + 16 * j;
-            pqk[j] = *(const f32x4*)(QKg + (size_t)i * CK_C + 4 * (tid & 15));
-            pk[j] = pq[j] = (f16x8)(0);
-            if (i < n) {
-                const size_t off = (size_t)(t0 + i) * qk_stride + (size_t)hk * CK_K + 8 * (tid & 15);
-                pk[j] = *(const f16x8*)(k + off);
-                pq[j] = *(const f16x8*)(q + off);
-            }
+            const int idx = l + 64 * j, row = idx >> 2, c16 = idx & 3;
+            kv[j] = row < n ? *(const f16x8*)(k + (size_t)(t0 + row) * qk_stride +
+                                              (size_t)hk * CK_K + k0 + 8 * c16)
+                            : (f16x8)(0);
         }
-        if (tid < CK_C) {
-            pg[0] = Gg[tid];
-            pg[1] = Gg[CK_C + tid];
-            pg[2] = Gg[2 * CK_C + tid];
-        }
-#pragma unroll
-        for (int mb = 0; mb < 4; ++mb)
-            pu[mb] = *(const f32x4*)(UTg + (size_t)(v0 + m) * CK_C + 16 * mb + 4 * kk);
     };
-    auto commit = [&]() {
-#pragma unroll
-        for (int j = 0; j < 8; ++j)
-            *(f32x4*)&sW[((tid >> 5) + 8 * j) * CS_WP + 4 * (tid & 31)] = pw[j];
+    // the K slice into LDS: row r's 32-byte half kb at kb ^ ((r / 4) % 2), so
+    // the transposed reads of phase C hit 16 distinct 32-byte bank groups
+    auto stage_k = [&]() {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const int i = (tid >> 4) + 16 * j;
-            *(f32x4*)&sQK[i * CS_QKP + 4 * (tid & 15)] = pqk[j];
-            *(f16x8*)&sK[i * CS_KP + 8 * (tid & 15)] = pk[j];
-            *(f16x8*)&sQ[i * CS_QP + 8 * (tid & 15)] = pq[j];
-        }
-        if (tid < CK_C) {
-            sG[tid] = pg[0];
-            sG[CK_C + tid] = pg[1];
-            sG[2 * CK_C + tid] = pg[2];
+            const int idx = l + 64 * j, row = idx >> 2, c16 = idx & 3;
+            const int pos = row * 64 + 32 * ((c16 >> 1) ^ ((row >> 2) & 1)) + 16 * (c16 & 1);
+            *(f16x8*)(ksl + pos) = kv[j];
         }
     };
 
     const int n_chunks = (T + CK_C - 1) / CK_C;
-    prefetch(0);
-    commit();
+    load_wq(0);
+    load_rest(0);
     for (int c = 0; c < n_chunks; ++c) {
         const int t0 = c * CK_C;
         const int n = min(CK_C, T - t0);
-        const f32x4 u[4] = {pu[0], pu[1], pu[2], pu[3]};   // U rows tok = 16 mb + 4 kk + r
-        __syncthreads();   // chunk c is in LDS
-        if (c + 1 < n_chunks) prefetch(c + 1);
+        const int par = c & 1;
 
-        // A: P = W S^T and QS = Q S^T
+        // A: this wave's partials of P = W S^T and QS = Q S^T
         f32x4 p[4], qs[4];
 #pragma unroll
         for (int mb = 0; mb < 4; ++mb) p[mb] = qs[mb] = (f32x4)(0.f);
 #pragma unroll
-        for (int kq = 0; kq < 8; ++kq) {
-            f32x4 wf[4], qf[4];
-#pragma unroll
-            for (int mb = 0; mb < 4; ++mb) {
-                wf[mb] = *(const f32x4*)&sW[(16 * mb + m) * CS_WP + 16 * kq + 4 * kk];
-                const f16x4 qh = *(const f16x4*)&sQ[(16 * mb + m) * CS_QP + 16 * kq + 4 * kk];
-                qf[mb] = (f32x4){(float)qh[0], (float)qh[1], (float)qh[2], (float)qh[3]};
-            }
+        for (int kq = 0; kq < 2; ++kq)
 #pragma unroll
             for (int r = 0; r < 4; ++r)
 #pragma unroll
                 for (int mb = 0; mb < 4; ++mb) {
-                    p[mb] = mfma4(wf[mb][r], st[kq][r], p[mb]);
-                    qs[mb] = mfma4(qf[mb][r], st[kq][r], qs[mb]);
+                    p[mb] = mfma4(wf[mb][kq][r], st[kq][r], p[mb]);
+                    qs[mb] = mfma4((float)qf[mb][kq][r], st[kq][r], qs[mb]);
                 }
-        }
-        f32x4 d[4];   // Delta rows tok = 16 mb + 4 kk + r, column v0 + m
-#pragma unroll
-        for (int mb = 0; mb < 4; ++mb) d[mb] = u[mb] - p[mb];
-
-        // B: O = e^{g} o QS + QKm Delta (QKm is zero above the diagonal: blocks kq <= mb)
-        f32x4 o[4];
+        if (c + 1 < n_chunks) load_wq(c + 1);
+        f32x4* mine = part + par * (CS_PART) + w * (2 * 4 * 64);
 #pragma unroll
         for (int mb = 0; mb < 4; ++mb) {
-#pragma unroll
-            for (int r = 0; r < 4; ++r) o[mb][r] = sG[CK_C + 16 * mb + 4 * kk + r] * qs[mb][r];
-#pragma unroll
-            for (int kq = 0; kq <= mb; ++kq) {
-                const f32x4 af = *(const f32x4*)&sQK[(16 * mb + m) * CS_QKP + 16 * kq + 4 * kk];
-#pragma unroll
-                for (int r = 0; r < 4; ++r) o[mb] = mfma4(af[r], d[kq][r], o[mb]);
-            }
+            mine[mb * 64 + l] = p[mb];
+            mine[4 * 64 + mb * 64 + l] = qs[mb];
         }
+        stage_k();   // this wave's own region: its reads of the previous slice came before
+        __syncthreads();
+        const f32x4* all = part + par * (CS_PART);
+        f32x4 d[4];   // Delta rows tok = 16 mb + 4 kk + r, column v0 + m
 #pragma unroll
-        for (int mb = 0; mb < 4; ++mb)
+        for (int mb = 0; mb < 4; ++mb) {
+            f32x4 s = all[mb * 64 + l];
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int i = 16 * mb + 4 * kk + r;
-                if (i < n)
-                    y[(size_t)(t0 + i) * y_stride + (size_t)hv * CK_V + v0 + m] =
-                        f16_sat(o[mb][r] * out_scale);
-            }
+            for (int ww = 1; ww < 4; ++ww) s += all[ww * (2 * 4 * 64) + mb * 64 + l];
+            d[mb] = u[mb] - s;
+        }
+        f32x4 qsw = all[4 * 64 + w * 64 + l];   // this wave's token block of QS
+#pragma unroll
+        for (int ww = 1; ww < 4; ++ww) qsw += all[ww * (2 * 4 * 64) + 4 * 64 + w * 64 + l];
 
-        // C: S^T = e^{g_C} S^T + Kd^T Delta
-        const float eC = sG[CK_C + CK_C - 1];
-        float dk[4][4];   // e^{g_C - g_tok}, tok = 16 kq + 4 kk + r
+        // B: O for tokens 16 w .. 16 w + 15
+        f32x4 o;
 #pragma unroll
-        for (int kq = 0; kq < 4; ++kq)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) dk[kq][r] = sG[2 * CK_C + 16 * kq + 4 * kk + r];
-        typedef __attribute__((address_space(3))) const char lds_char;
-#pragma unroll
-        for (int mb = 0; mb < 8; ++mb) st[mb] *= eC;
+        for (int r = 0; r < 4; ++r) o[r] = eg[r] * qsw[r];
 #pragma unroll
         for (int kq = 0; kq < 4; ++kq) {
-            // lane m of group kk receives K[16 kq + 4 kk + e][16 mb + m], e = 0..3
-            const int row = 16 * kq + 4 * kk + (m >> 2);
-            f32x4 ka[8];
+            if (kq > w) break;   // QKm is zero above the diagonal
 #pragma unroll
-            for (int mb = 0; mb < 8; ++mb) {
+            for (int r = 0; r < 4; ++r) o = mfma4(qkm[kq][r], d[kq][r], o);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int i = 16 * w + 4 * kk + r;
+            if (i < n)
+                y[(size_t)(t0 + i) * y_stride + (size_t)hv * CK_V + v0 + m] = f16_sat(o[r] * out_scale);
+        }
+
+        // C: S^T = e^{g_C} S^T + Kd^T Delta over this wave's k range
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) st[kb] *= eC;
+#pragma unroll
+        for (int kq = 0; kq < 4; ++kq) {
+            // lane m of group kk receives K[16 kq + 4 kk + e][k0 + 16 kb + m], e = 0..3
+            const int row = 16 * kq + 4 * kk + (m >> 2);
+            f32x4 ka[2];
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+                const int pos = row * 64 + 32 * (kb ^ ((row >> 2) & 1)) + 8 * (m & 3);
                 const s16x4 kt = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                    (lds_s16x4*)((lds_char*)sK + 2 * (row * CS_KP + 16 * mb + 4 * (m & 3))));
+                    (lds_s16x4*)((lds_char*)(uintptr_t)ksl_lds + pos));
                 const f16x4 kh = __builtin_bit_cast(f16x4, kt);
 #pragma unroll
-                for (int r = 0; r < 4; ++r) ka[mb][r] = (float)kh[r] * dk[kq][r];
+                for (int r = 0; r < 4; ++r) ka[kb][r] = (float)kh[r] * dk[kq][r];
             }
 #pragma unroll
             for (int r = 0; r < 4; ++r)
 #pragma unroll
-                for (int mb = 0; mb < 8; ++mb) st[mb] = mfma4(ka[mb][r], d[kq][r], st[mb]);
+                for (int kb = 0; kb < 2; ++kb) st[kb] = mfma4(ka[kb][r], d[kq][r], st[kb]);
         }
-        __syncthreads();   // chunk c's LDS reads are done
-        if (c + 1 < n_chunks) commit();
+        if (c + 1 < n_chunks) load_rest(c + 1);
     }
 #pragma unroll
-    for (int mb = 0; mb < 8; ++mb) *(f32x4*)(Sv + 16 * mb) = st[mb];
+    for (int kb = 0; kb < 2; ++kb) *(f32x4*)(Sv + 16 * kb) = st[kb];
 }
 
 }  // namespace
@@ -394,7 +394,7 @@ int fl_gdn_prefill_chunked(const void* q, const void* k, const void* v, const fl
         }
         lds_attr_set = true;
     }
-    hipLaunchKernelGGL(chunk_state_kernel, dim3(CK_V / CS_ROWS, n_vheads), dim3(256), CS_LDS,
+    hipLaunchKernelGGL(chunk_state_kernel, dim3(n_vheads, CK_V / CS_ROWS), dim3(256), CS_LDS,
                        (hipStream_t)stream, (const f16*)q, (const f16*)k, S, (f16*)y, T, n_vheads,
                        qk_stride, y_stride, out_scale, group, (const float*)work);
     return fl::check_launch("gdn_chunk_state");
