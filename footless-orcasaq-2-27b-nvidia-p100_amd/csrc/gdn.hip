@@ -36,7 +36,35 @@ __device__ __forceinline__ float row8_sum(float v) {
     return v;
 }
 
-__device__ __forceinline__ float softplus20(float x) { return x <= 20.f ? log1pf(expf(x)) : x; }
+// e^x built as the reference's __expf builds it: 2^(x log2 e) on the
+// transcendental unit (v_exp_f32, 1 ulp).
+__device__ __forceinline__ float hw_expf(float x) { return __builtin_amdgcn_exp2f(x * 1.44269504f); }
+
+// log1p(e) for e >= 0 from the hardware log2 (v_log_f32) with Goldberg's
+// correction: u = 1 + e is rounded, and log(u) * e / (u - 1) cancels that
+// rounding (log1p(e) = e to working precision where u == 1).
+__device__ __forceinline__ float log1p_pos(float e) {
+    const float u = 1.f + e, d = u - 1.f;
+    return d == 0.f ? e : __builtin_amdgcn_logf(u) * 0.693147181f * (e * __builtin_amdgcn_rcpf(d));
+}
+
+// The gates (kernels.cu:1732-1748): beta = sigmoid(b) with a correctly
+// rounded divide, decay = exp(-e^A softplus(a + dt_bias)), softplus =
+// log1p(e^x) up to x = 20 and x above. The exponentials and the log run on the
+// transcendental unit; against the fp64 values the worst error is ~1e-7 on
+// beta and ~4e-7 on decay, inside the reference's own (4.6e-7 and 5.6e-6
+// relative, kernels.cu:139), with a dozen dependent instructions instead of
+// three libm calls in series. The conv's silu takes the same exponential, as
+// the reference's does (silu_f, kernels.cu:234): x / (1 + e^-x), correctly
+// rounded divide; its fp16-rounded output can differ from a libm-exp silu by
+// one fp16 ulp where the fp32 value sits within an ulp or two of a rounding
+// boundary.
+__device__ __forceinline__ float conv_silu(float x) { return x / (1.f + hw_expf(-x)); }
+__device__ __forceinline__ float gdn_beta(float b) { return 1.f / (1.f + hw_expf(-b)); }
+__device__ __forceinline__ float gdn_decay(float a_dt, float A) {
+    const float sp = a_dt <= 20.f ? log1p_pos(hw_expf(a_dt)) : a_dt;
+    return hw_expf(-hw_expf(A) * sp);
+}
 
 // Sum of squares over a 128-thread row in the reference's order (kernels.cu:
 // 214-227, block_reduce_sum over 4 warps of 32): a tree inside each 32-lane
@@ -135,7 +163,7 @@ __global__ void conv1d_causal_kernel(const f16* __restrict__ x, const f16* __res
         }
         acc = fmaf((float)w[(size_t)d * width + j], e, acc);
     }
-    y[(size_t)t * row_stride + d] = f16_sat(silu_f(acc));
+    y[(size_t)t * row_stride + d] = f16_sat(conv_silu(acc));
     if (t == T - 1) {
         f16* so = st_out + (size_t)d * sl;
         for (int k = 0; k < sl; ++k) {
@@ -173,7 +201,7 @@ __global__ void conv1d_causal_rows_kernel(const f16* __restrict__ x, const f16* 
         acc = fmaf(wv[1], e[1], acc);
         acc = fmaf(wv[2], e[2], acc);
         acc = fmaf(wv[3], xt, acc);
-        y[(size_t)t * row_stride + d] = f16_sat(silu_f(acc));
+        y[(size_t)t * row_stride + d] = f16_sat(conv_silu(acc));
         e[0] = e[1];
         e[1] = e[2];
         e[2] = (float)f16_sat(xt);
@@ -216,9 +244,8 @@ __global__ void gdn_scalars_kernel(const float* __restrict__ a, const float* __r
     const int t = blockIdx.y;
     const int h = blockIdx.x * blockDim.x + threadIdx.x;
     if (h >= n_heads) return;
-    beta[(size_t)t * n_heads + h] = sigmoid_f(b[(size_t)t * b_stride + h]);
-    const float sp = softplus20(a[(size_t)t * a_stride + h] + dt_bias[h]);
-    decay[(size_t)t * n_heads + h] = expf(-expf(A_log[h]) * sp);
+    beta[(size_t)t * n_heads + h] = gdn_beta(b[(size_t)t * b_stride + h]);
+    decay[(size_t)t * n_heads + h] = gdn_decay(a[(size_t)t * a_stride + h] + dt_bias[h], A_log[h]);
 }
 
 // ---------------------------------------------------------------------------
@@ -337,6 +364,14 @@ __device__ __forceinline__ float sumsq128(float lo, float hi) {
            __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a), 32));
 }
 
+// 0, in a VGPR the compiler cannot see through: an index plus this makes a
+// uniform load a vector load
+__device__ __forceinline__ int opaque_zero() {
+    int z;
+    asm volatile("v_mov_b32 %0, 0" : "=v"(z));
+    return z;
+}
+
 // conv1_ch split in two so the loads can be issued ahead of the state's: the
 // raw fp16 values are kept until conv1_apply, after the state loads are
 // issued, so no wait for them lands in front of those loads.
@@ -379,20 +414,25 @@ __device__ __forceinline__ float conv1_apply(const ConvIn& c, bool hist, f16* st
         so[1] = f16_sat(s2);
         so[2] = f16_sat(xv);
     }
-    return (float)f16_sat(silu_f(acc));
+    return (float)f16_sat(conv_silu(acc));
 }
 
 // The decode / verify step: a workgroup of 4 wavefronts owns 32 state rows
 // of one v head (8 lanes a row, 8 rows a wave). Per token every thread
 // convolves (or reads) one q / k channel of the row's k head into LDS (k:
-// threads 0-127, q: 128-255) -- the one workgroup barrier -- then every wave
-// forms both L2 norms itself with in-wave reductions in the reference's
-// order, normalises the 256 values into its own LDS slice and runs the delta
-// rule on its 8 rows. (Measured and not kept: two rows a thread, and the
-// norm's partial sums shared through LDS with a second barrier -- both
-// slower.) Token 0's conv / gate inputs are issued before the state's loads
-// so the prologue computes while the state streams in; the state is read and
-// written with non-temporal loads / stores (once a step).
+// threads 0-127, q: 128-255) and one of the 32 rows' v channels; one wave
+// keeps the v values, another forms the two gates -- barrier -- waves 0 / 1
+// form k's L2 norm and waves 2 / 3 q's (in-wave reductions in the reference's
+// order), each normalising a quarter of the 256 values into LDS -- barrier --
+// and every wave runs the delta rule on its 8 rows. The kernel is a chain of
+// short dependent steps between the state's load and its store, so the
+// per-wave instruction count on that chain is what was cut: the gates (now a
+// dozen transcendental-unit instructions) and the v convolution once a
+// workgroup instead of once a wave, the norms split four ways. (Measured and
+// not kept: two rows a thread.) Token 0's conv / gate inputs are issued
+// before the state's loads so the prologue computes while the state streams
+// in; the state is read and written with non-temporal loads / stores (once a
+// step).
 template <bool CONV>
 __global__ void __launch_bounds__(GR_THREADS)
 gdn_decode_kernel(const f16* __restrict__ x, int x_stride, const f16* __restrict__ conv_w,
@@ -402,68 +442,106 @@ gdn_decode_kernel(const f16* __restrict__ x, int x_stride, const f16* __restrict
                   long long ck_step, int T, int n_kheads, int n_vheads, int V, float out_scale,
                   float l2eps, int group) {
     __shared__ __attribute__((aligned(16))) float sraw[2 * GR_K];          // k | q, raw
-    __shared__ __attribute__((aligned(16))) float snorm[4][2][GR_K];       // per wave: k | q
+    __shared__ __attribute__((aligned(16))) float snorm[2 * GR_K];         // k | q, normalised
+    __shared__ float sv[GR_ROWS];   // the rows' v values
+    __shared__ float sg[2];         // beta, decay
     const int rb = blockIdx.x, hv = blockIdx.y, b = blockIdx.z;
+    // this sequence's kernel-argument values in one scalar round, ahead of
+    // every vector load (each later scalar load would be one more round trip
+    // on the way to the state stores)
+    float* const Sb = seqs.S[b];
+    const f16* const cst_in = seqs.cst_in[b];
+    f16* const cst_out = seqs.cst_out[b];
+    float* const Ck = seqs.Ck[b];
+    const int pos0 = seqs.pos0[b];
+    asm volatile("" ::"s"(Sb), "s"(cst_in), "s"(cst_out), "s"(Ck), "s"(pos0), "s"(x), "s"(conv_w),
+                 "s"(ga), "s"(gb), "s"(A_log), "s"(dt_bias), "s"(x_stride), "s"(ab_stride), "s"(T),
+                 "s"(n_kheads), "s"(V), "s"(group), "s"(y), "s"(y_stride), "s"(out_scale),
+                 "s"(l2eps), "s"(ck_step));
+    __builtin_amdgcn_sched_barrier(0);
     const int hk = hv / group;
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int ri = tid >> 3, c0 = 4 * (tid & 7);
     const int vi = rb * GR_ROWS + ri;
-    float* Srow = seqs.S[b] + ((size_t)hv * V + vi) * GR_K + c0;
-    float* Ck = seqs.Ck[b];
-    const int pos0 = seqs.pos0[b];
+    float* Srow = Sb + ((size_t)hv * V + vi) * GR_K + c0;
     const int half_ = tid >> 7, i = tid & 127;
     const int ch = (half_ ? hk * GR_K : n_kheads * GR_K + hk * GR_K) + i;   // q | k channel
-    const int ch_v = 2 * n_kheads * GR_K + hv * V + vi;
-    // token 0's inputs first, then the state: the prologue runs while S streams in
-    const float dtb = dt_bias[hv], A = A_log[hv];
-    const float ga0 = ga[(size_t)b * T * ab_stride + hv], gb0 = gb[(size_t)b * T * ab_stride + hv];
+    // the per-head gates and the 32 rows' v channels are formed once a
+    // workgroup, by one wave each (which two varies with the block, spreading
+    // that work over the SIMDs), and handed over at the barrier
+    const int gw = (rb + hv + b) & 3, vw = gw ^ 2;
+    const int ch_v = 2 * n_kheads * GR_K + hv * V + rb * GR_ROWS + (lane & 31);
+    // token 0's inputs first, then the state: the prologue runs while S streams
+    // in. The per-head gate inputs are uniform but read with vector loads (an
+    // opaque zero in the index): they then queue in order ahead of the state
+    // loads, where a scalar load's wait (lgkmcnt, out of order) would also
+    // wait for every kernel-argument load issued after it.
     ConvIn cq, cv;
     const f16* x0 = x + (size_t)b * T * x_stride;
     if constexpr (CONV) {
-        cq = conv1_load(x0, conv_w, seqs.cst_in[b], ch);
-        cv = conv1_load(x0, conv_w, seqs.cst_in[b], ch_v);
+        cq = conv1_load(x0, conv_w, cst_in, ch);
+        cv = conv1_load(x0, conv_w, cst_in, ch_v);
     } else {
         cq.x = x0[ch];
         cv.x = x0[ch_v];
     }
+    const int vz = opaque_zero();
+    const float dtb = dt_bias[hv + vz], A = A_log[hv + vz];
+    const size_t ab0 = (size_t)b * T * ab_stride + hv + vz;
+    const float ga0 = ga[ab0], gb0 = gb[ab0];
+    // The state loads wait ~512 clocks behind the small loads above. The grid's
+    // 768 workgroups (B = 4) are dispatched over ~0.3 us; issued at once, the
+    // first workgroups' state reads (16 KiB each) queue ahead of the later
+    // ones' conv inputs, which head the chain to every store. Measured over
+    // s_sleep 4..16 at B = 4: 8 and 9 best (6.45 -> 6.25 us a step). Small
+    // grids do not wait.
+    if (gridDim.x * gridDim.y * gridDim.z >= 512) __builtin_amdgcn_s_sleep(8);
     __builtin_amdgcn_sched_barrier(0);
     float reg[16];
     load_row16_nt(reg, Srow);
     __builtin_amdgcn_sched_barrier(0);
-    const float al = expf(A);
     // one token; token 0 is peeled so that nothing of its conversions is
     // hoisted in front of the state loads
     auto token = [&](int t, float a_t, float b_t) {
         const size_t bt_row = (size_t)b * T + t;
-        const float bt = sigmoid_f(b_t);
-        const float dt = expf(-al * softplus20(a_t + dtb));
-        float xv, vt;
+        // every wave convolves a v channel beside its q / k one (independent
+        // chains, interleaved); wave vw keeps them
+        const bool vkeep = w == vw && lane < GR_ROWS;
+        float xv, v_;
         if constexpr (CONV) {
             const bool own = (hv % group) == 0 && rb == 0;   // one workgroup stores q / k state
-            xv = conv1_apply(cq, pos0 > 0, own ? seqs.cst_out[b] : nullptr, ch);
-            vt = conv1_apply(cv, pos0 > 0, c0 == 0 ? seqs.cst_out[b] : nullptr, ch_v);
+            xv = conv1_apply(cq, pos0 > 0, own ? cst_out : nullptr, ch);
+            v_ = conv1_apply(cv, pos0 > 0, vkeep ? cst_out : nullptr, ch_v);
         } else {
             xv = (float)cq.x;
-            vt = (float)cv.x;
+            v_ = (float)cv.x;
         }
         sraw[tid] = xv;
+        if (vkeep) sv[lane] = v_;
+        if (w == gw) {
+            const float bt_ = gdn_beta(b_t);
+            const float dt_ = gdn_decay(a_t + dtb, A);
+            if (lane == 0) {
+                sg[0] = bt_;
+                sg[1] = dt_;
+            }
+        }
         __syncthreads();
-        // both norms in this wave, the reference's order
-        const float k_lo = sraw[lane], k_hi = sraw[lane + 64];
-        const float q_lo = sraw[GR_K + lane], q_hi = sraw[GR_K + lane + 64];
-        const float den_k = sqrtf(sumsq128(k_lo, k_hi) + l2eps);
-        const float den_q = sqrtf(sumsq128(q_lo, q_hi) + l2eps);
-        float* sn = &snorm[w][0][0];
-        sn[lane] = (float)f16_sat(k_lo / den_k);
-        sn[lane + 64] = (float)f16_sat(k_hi / den_k);
-        sn[GR_K + lane] = (float)f16_sat(q_lo / den_q);
-        sn[GR_K + lane + 64] = (float)f16_sat(q_hi / den_q);
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        const float vt = sv[ri], bt = sg[0], dt = sg[1];
+        // the norms, the reference's order: waves 0 / 1 form k's (each
+        // normalising one half of it), waves 2 / 3 q's; a second barrier
+        const int nq = w >> 1, nh = w & 1;
+        const float n_lo = sraw[nq * GR_K + lane], n_hi = sraw[nq * GR_K + lane + 64];
+        const float den = sqrtf(sumsq128(n_lo, n_hi) + l2eps);
+        snorm[nq * GR_K + nh * 64 + lane] = (float)f16_sat((nh ? n_hi : n_lo) / den);
+        __syncthreads();
         float kk[16], qq[16];
-        gather16(kk, sn, c0);
-        gather16(qq, sn + GR_K, c0);
+        gather16(kk, snorm, c0);
+        gather16(qq, snorm + GR_K, c0);
+        // nothing of the delta rule (its S *= decay first) above this point:
+        // the state's wait would otherwise land inside the norms
+        __builtin_amdgcn_sched_barrier(0);
         const float o = delta_rule_token(reg, kk, qq, vt, bt, dt);
         if (c0 == 0) y[bt_row * y_stride + (size_t)hv * V + vi] = f16_sat(o * out_scale);
         if (Ck != nullptr && t < T - 1)
@@ -471,12 +549,12 @@ gdn_decode_kernel(const f16* __restrict__ x, int x_stride, const f16* __restrict
     };
     token(0, ga0, gb0);
     for (int t = 1; t < T; ++t) {   // verify rows (conv_fused is T == 1 only)
-        __syncthreads();   // sraw is rewritten by this token
+        __syncthreads();   // sraw, sv and sg are rewritten by this token
         const size_t bt_row = (size_t)b * T + t;
         const f16* xr = x + bt_row * x_stride;
         cq.x = xr[ch];
         cv.x = xr[ch_v];
-        token(t, ga[bt_row * ab_stride + hv], gb[bt_row * ab_stride + hv]);
+        token(t, ga[bt_row * ab_stride + hv + vz], gb[bt_row * ab_stride + hv + vz]);
     }
     store_row16_nt(Srow, reg);
 }
