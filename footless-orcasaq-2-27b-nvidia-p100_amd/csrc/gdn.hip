@@ -397,8 +397,8 @@ __device__ __forceinline__ ConvIn conv1_load(const f16* __restrict__ x, const f1
 
 // conv1d_causal at T = 1 for channel d (width 4, kernels.cu:1634-1679 /
 // 2916-2941; the history is zero when pos0 == 0): the fp16-rounded silu
-// output; the new state (s1, s2, x) into st_out when given.
-__device__ __forceinline__ float conv1_apply(const ConvIn& c, bool hist, f16* st_out, int d) {
+// output.
+__device__ __forceinline__ float conv1_apply(const ConvIn& c, bool hist) {
     const float s0 = hist ? (float)c.h0 : 0.f;
     const float s1 = hist ? (float)c.h1 : 0.f;
     const float s2 = hist ? (float)c.h2 : 0.f;
@@ -408,13 +408,18 @@ __device__ __forceinline__ float conv1_apply(const ConvIn& c, bool hist, f16* st
     acc = fmaf((float)c.w[1], s1, acc);
     acc = fmaf((float)c.w[2], s2, acc);
     acc = fmaf((float)c.w[3], xv, acc);
-    if (st_out != nullptr) {
-        f16* so = st_out + (size_t)d * 3;
-        so[0] = f16_sat(s1);
-        so[1] = f16_sat(s2);
-        so[2] = f16_sat(xv);
-    }
     return (float)f16_sat(conv_silu(acc));
+}
+
+// ... and its new state (s1, s2, x) into the ring. Stored at the kernel's
+// end: vector memory operations complete in order for the wait counter, so
+// a store issued behind the state's loads would make every later wait (the
+// barrier's for the gate loads included) wait for those loads too.
+__device__ __forceinline__ void conv1_ring_store(const ConvIn& c, bool hist, f16* st_out, int d) {
+    f16* so = st_out + (size_t)d * 3;
+    so[0] = f16_sat(hist ? (float)c.h1 : 0.f);
+    so[1] = f16_sat(hist ? (float)c.h2 : 0.f);
+    so[2] = f16_sat((float)c.x);
 }
 
 // The decode / verify step: a workgroup of 4 wavefronts owns 32 state rows
@@ -471,6 +476,7 @@ gdn_decode_kernel(const f16* __restrict__ x, int x_stride, const f16* __restrict
     // workgroup, by one wave each (which two varies with the block, spreading
     // that work over the SIMDs), and handed over at the barrier
     const int gw = (rb + hv + b) & 3, vw = gw ^ 2;
+    const bool vkeep = w == vw && lane < GR_ROWS;
     const int ch_v = 2 * n_kheads * GR_K + hv * V + rb * GR_ROWS + (lane & 31);
     // token 0's inputs first, then the state: the prologue runs while S streams
     // in. The per-head gate inputs are uniform but read with vector loads (an
@@ -507,12 +513,10 @@ gdn_decode_kernel(const f16* __restrict__ x, int x_stride, const f16* __restrict
         const size_t bt_row = (size_t)b * T + t;
         // every wave convolves a v channel beside its q / k one (independent
         // chains, interleaved); wave vw keeps them
-        const bool vkeep = w == vw && lane < GR_ROWS;
         float xv, v_;
         if constexpr (CONV) {
-            const bool own = (hv % group) == 0 && rb == 0;   // one workgroup stores q / k state
-            xv = conv1_apply(cq, pos0 > 0, own ? cst_out : nullptr, ch);
-            v_ = conv1_apply(cv, pos0 > 0, vkeep ? cst_out : nullptr, ch_v);
+            xv = conv1_apply(cq, pos0 > 0);
+            v_ = conv1_apply(cv, pos0 > 0);
         } else {
             xv = (float)cq.x;
             v_ = (float)cv.x;
@@ -557,6 +561,11 @@ gdn_decode_kernel(const f16* __restrict__ x, int x_stride, const f16* __restrict
         token(t, ga[bt_row * ab_stride + hv + vz], gb[bt_row * ab_stride + hv + vz]);
     }
     store_row16_nt(Srow, reg);
+    if constexpr (CONV) {   // T == 1
+        if ((hv % group) == 0 && rb == 0)   // one workgroup stores the q / k channels' ring
+            conv1_ring_store(cq, pos0 > 0, cst_out, ch);
+        if (vkeep) conv1_ring_store(cv, pos0 > 0, cst_out, ch_v);
+    }
 }
 
 // The GDN output norm, RMSNormGated (kernels.cu:321-358, launched at
