@@ -80,12 +80,13 @@ __device__ __forceinline__ float warp32_tree(float v) {
 }
 
 // One token of the delta rule on a lane's 16 columns (`reg`), with k and q
-// (fp32 values of fp16 numbers) at columns c0 + 32j + 0..3. Returns the row's
-// output o = S_new . q (identical in the 8 lanes of the row). The dots run in
-// two chains (even / odd register) summed, then over the row's lanes -- the
-// reference's gdn_scan_rows order (kernels.cu:2866-2905).
-__device__ __forceinline__ float delta_rule_token(float (&reg)[16], const float* kk,
-                                                  const float* qq, float vt, float bt, float dt) {
+// (fp32 values of fp16 numbers) at columns c0 + 32j + 0..3: delta_update
+// updates the state, delta_out returns the row's output o = S_new . q
+// (identical in the 8 lanes of the row). The dots run in two chains (even /
+// odd register) summed, then over the row's lanes -- the reference's
+// gdn_scan_rows order (kernels.cu:2866-2905).
+__device__ __forceinline__ void delta_update(float (&reg)[16], const float* kk, float vt, float bt,
+                                             float dt) {
     float m0 = 0.f, m1 = 0.f;
 #pragma unroll
     for (int c = 0; c < 16; c += 2) {
@@ -96,19 +97,24 @@ __device__ __forceinline__ float delta_rule_token(float (&reg)[16], const float*
     }
     const float m = row8_sum(m0 + m1);
     const float delta = bt * (vt - m);
+#pragma unroll
+    for (int c = 0; c < 16; ++c) reg[c] = fmaf(delta, kk[c], reg[c]);
+}
+
+__device__ __forceinline__ float delta_out(const float (&reg)[16], const float* qq) {
     float o0 = 0.f, o1 = 0.f;
 #pragma unroll
-    for (int c = 0; c < 16; c += 4) {
-        reg[c] = fmaf(delta, kk[c], reg[c]);
-        reg[c + 1] = fmaf(delta, kk[c + 1], reg[c + 1]);
-        reg[c + 2] = fmaf(delta, kk[c + 2], reg[c + 2]);
-        reg[c + 3] = fmaf(delta, kk[c + 3], reg[c + 3]);
+    for (int c = 0; c < 16; c += 2) {
         o0 = fmaf(reg[c], qq[c], o0);
         o1 = fmaf(reg[c + 1], qq[c + 1], o1);
-        o0 = fmaf(reg[c + 2], qq[c + 2], o0);
-        o1 = fmaf(reg[c + 3], qq[c + 3], o1);
     }
     return row8_sum(o0 + o1);
+}
+
+__device__ __forceinline__ float delta_rule_token(float (&reg)[16], const float* kk,
+                                                  const float* qq, float vt, float bt, float dt) {
+    delta_update(reg, kk, vt, bt, dt);
+    return delta_out(reg, qq);
 }
 
 __device__ __forceinline__ void load_row16(float (&reg)[16], const float* src) {
@@ -354,16 +360,6 @@ __device__ __forceinline__ float warp32_tree_lane0(float v) {
     return v;
 }
 
-// Sum of squares of a 128-wide row held two per lane (lane l: x[l], x[l+64])
-// in the reference's order: 32-lane trees give r0 (x[0..31], lane 0), r1
-// (x[32..63], lane 32), r2 (x[64..95], lane 0), r3 (x[96..127], lane 32);
-// the total is (r0 + r2) + (r1 + r3) (kernels.cu:214-227 over 4 warps).
-__device__ __forceinline__ float sumsq128(float lo, float hi) {
-    const float a = warp32_tree_lane0(lo * lo) + warp32_tree_lane0(hi * hi);   // lane 0: r0+r2, lane 32: r1+r3
-    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a), 0)) +
-           __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a), 32));
-}
-
 // 0, in a VGPR the compiler cannot see through: an index plus this makes a
 // uniform load a vector load
 __device__ __forceinline__ int opaque_zero() {
@@ -424,20 +420,21 @@ __device__ __forceinline__ void conv1_ring_store(const ConvIn& c, bool hist, f16
 
 // The decode / verify step: a workgroup of 4 wavefronts owns 32 state rows
 // of one v head (8 lanes a row, 8 rows a wave). Per token every thread
-// convolves (or reads) one q / k channel of the row's k head into LDS (k:
-// threads 0-127, q: 128-255) and one of the 32 rows' v channels; one wave
-// keeps the v values, another forms the two gates -- barrier -- waves 0 / 1
-// form k's L2 norm and waves 2 / 3 q's (in-wave reductions in the reference's
-// order), each normalising a quarter of the 256 values into LDS -- barrier --
+// convolves (or reads) one q / k channel of the row's k head (k: threads
+// 0-127, q: 128-255) and one of the 32 rows' v channels, and each wave sums
+// the squares of its 64 q / k values as two 32-lane trees (the reference's
+// warp sums); one wave keeps the v values, another forms the two gates --
+// barrier -- every thread normalises its own channel into LDS -- barrier --
 // and every wave runs the delta rule on its 8 rows. The kernel is a chain of
 // short dependent steps between the state's load and its store, so the
-// per-wave instruction count on that chain is what was cut: the gates (now a
-// dozen transcendental-unit instructions) and the v convolution once a
-// workgroup instead of once a wave, the norms split four ways. (Measured and
-// not kept: two rows a thread.) Token 0's conv / gate inputs are issued
-// before the state's loads so the prologue computes while the state streams
-// in; the state is read and written with non-temporal loads / stores (once a
-// step).
+// per-wave instruction count on that chain is what was cut: the gates (a
+// dozen transcendental-unit instructions) and the v values once a workgroup
+// instead of once a wave, the norm's trees ahead of the first barrier. The
+// state is stored as soon as it is updated, before the output's reduction.
+// (Measured and not kept: two rows a thread.) Token 0's conv / gate inputs
+// are issued before the state's loads so the prologue computes while the
+// state streams in; the state is read and written with non-temporal loads /
+// stores (once a step).
 template <bool CONV>
 __global__ void __launch_bounds__(GR_THREADS)
 gdn_decode_kernel(const f16* __restrict__ x, int x_stride, const f16* __restrict__ conv_w,
@@ -446,7 +443,7 @@ gdn_decode_kernel(const f16* __restrict__ x, int x_stride, const f16* __restrict
                   const float* __restrict__ dt_bias, f16* __restrict__ y, int y_stride,
                   long long ck_step, int T, int n_kheads, int n_vheads, int V, float out_scale,
                   float l2eps, int group) {
-    __shared__ __attribute__((aligned(16))) float sraw[2 * GR_K];          // k | q, raw
+    __shared__ __attribute__((aligned(16))) float ssq[8];   // k's, q's 32-channel sums of squares
     __shared__ __attribute__((aligned(16))) float snorm[2 * GR_K];         // k | q, normalised
     __shared__ float sv[GR_ROWS];   // the rows' v values
     __shared__ float sg[2];         // beta, decay
@@ -521,7 +518,11 @@ gdn_decode_kernel(const f16* __restrict__ x, int x_stride, const f16* __restrict
             xv = (float)cq.x;
             v_ = (float)cv.x;
         }
-        sraw[tid] = xv;
+        // the sums of squares of this wave's 64 values as two 32-lane trees:
+        // lanes 0 and 32 hold the reference's warp sums r0, r1 (wave 0) and
+        // r2, r3 (wave 1) of k, the same of q in waves 2 and 3
+        const float tr = warp32_tree_lane0(xv * xv);
+        if ((lane & 31) == 0) ssq[tid >> 5] = tr;
         if (vkeep) sv[lane] = v_;
         if (w == gw) {
             const float bt_ = gdn_beta(b_t);
@@ -533,12 +534,12 @@ gdn_decode_kernel(const f16* __restrict__ x, int x_stride, const f16* __restrict
         }
         __syncthreads();
         const float vt = sv[ri], bt = sg[0], dt = sg[1];
-        // the norms, the reference's order: waves 0 / 1 form k's (each
-        // normalising one half of it), waves 2 / 3 q's; a second barrier
-        const int nq = w >> 1, nh = w & 1;
-        const float n_lo = sraw[nq * GR_K + lane], n_hi = sraw[nq * GR_K + lane + 64];
-        const float den = sqrtf(sumsq128(n_lo, n_hi) + l2eps);
-        snorm[nq * GR_K + nh * 64 + lane] = (float)f16_sat((nh ? n_hi : n_lo) / den);
+        // the norms, the reference's order (r0 + r2) + (r1 + r3): every thread
+        // normalises its own channel (snorm is [k | q] as the channels are
+        // laid over the threads); a second barrier
+        const f32x4 r = *(const f32x4*)&ssq[4 * (w >> 1)];
+        const float den = sqrtf(((r[0] + r[2]) + (r[1] + r[3])) + l2eps);
+        snorm[tid] = (float)f16_sat(xv / den);
         __syncthreads();
         float kk[16], qq[16];
         gather16(kk, snorm, c0);
@@ -546,21 +547,24 @@ gdn_decode_kernel(const f16* __restrict__ x, int x_stride, const f16* __restrict
         // nothing of the delta rule (its S *= decay first) above this point:
         // the state's wait would otherwise land inside the norms
         __builtin_amdgcn_sched_barrier(0);
-        const float o = delta_rule_token(reg, kk, qq, vt, bt, dt);
-        if (c0 == 0) y[bt_row * y_stride + (size_t)hv * V + vi] = f16_sat(o * out_scale);
-        if (Ck != nullptr && t < T - 1)
+        delta_update(reg, kk, vt, bt, dt);
+        // the state (or its checkpoint) leaves ahead of the output's reduction
+        if (t == T - 1)
+            store_row16_nt(Srow, reg);
+        else if (Ck != nullptr)
             store_row16_nt(Ck + (size_t)t * ck_step + ((size_t)hv * V + vi) * GR_K + c0, reg);
+        const float o = delta_out(reg, qq);
+        if (c0 == 0) y[bt_row * y_stride + (size_t)hv * V + vi] = f16_sat(o * out_scale);
     };
     token(0, ga0, gb0);
     for (int t = 1; t < T; ++t) {   // verify rows (conv_fused is T == 1 only)
-        __syncthreads();   // sraw, sv and sg are rewritten by this token
+        __syncthreads();   // ssq, sv and sg are rewritten by this token
         const size_t bt_row = (size_t)b * T + t;
         const f16* xr = x + bt_row * x_stride;
         cq.x = xr[ch];
         cv.x = xr[ch_v];
         token(t, ga[bt_row * ab_stride + hv + vz], gb[bt_row * ab_stride + hv + vz]);
     }
-    store_row16_nt(Srow, reg);
     if constexpr (CONV) {   // T == 1
         if ((hv % group) == 0 && rb == 0)   // one workgroup stores the q / k channels' ring
             conv1_ring_store(cq, pos0 > 0, cst_out, ch);
