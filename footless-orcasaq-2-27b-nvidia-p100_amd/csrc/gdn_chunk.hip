@@ -45,7 +45,7 @@ chunk_prep_kernel(const f16* __restrict__ q, const f16* __restrict__ k, const f1
     __shared__ __attribute__((aligned(16))) f16 sK[CK_C][CK_KP];
     __shared__ __attribute__((aligned(16))) f16 sQ[CK_C][CK_KP];
     __shared__ __attribute__((aligned(16))) float sA[CK_C][CK_AP];
-    __shared__ float sG[CK_C], sB[CK_C];
+    __shared__ float sG[CK_C], sB[CK_C], sEG[CK_C];
 
     const int c = blockIdx.x, hv = blockIdx.y, hk = hv / group;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
@@ -58,30 +58,53 @@ chunk_prep_kernel(const f16* __restrict__ q, const f16* __restrict__ k, const f1
     float* QKg = Ug + CK_C * CK_V;
     float* Gg = QKg + CK_C * CK_C;
 
-    // stage K, Q (padding rows zero)
-    for (int idx = tid; idx < CK_C * (CK_K / 8); idx += 256) {
-        const int i = idx >> 4, c8 = (idx & 15) * 8;
-        f16x8 kv8 = (f16x8)(0), qv8 = (f16x8)(0);
-        if (i < n) {
-            kv8 = *(const f16x8*)(k + (size_t)(t0 + i) * qk_stride + (size_t)hk * CK_K + c8);
-            qv8 = *(const f16x8*)(q + (size_t)(t0 + i) * qk_stride + (size_t)hk * CK_K + c8);
-        }
-        *(f16x8*)&sK[i][c8] = kv8;
-        *(f16x8*)&sQ[i][c8] = qv8;
+    // Every global load of the chunk is issued up front and unconditionally,
+    // rows clamped to the chunk's last token, past-the-end rows then zeroed
+    // by a select: a load under a branch is waited for inside it, one HBM
+    // round trip after another.
+    // K, Q (4 rows x 16 B a thread), the gates, and this thread's v column
+    // (U threads, tid >= 128: column tid - 128, every token)
+    f16x8 kv8[4], qv8[4];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+        const int idx = tid + 256 * m, i = idx >> 4, c8 = (idx & 15) * 8;
+        const size_t off = (size_t)(t0 + min(i, n - 1)) * qk_stride + (size_t)hk * CK_K + c8;
+        kv8[m] = *(const f16x8*)(k + off);
+        qv8[m] = *(const f16x8*)(q + off);
+    }
+    const int tg = min(tid & (CK_C - 1), n - 1);
+    const float dec = decay[(size_t)(t0 + tg) * n_vheads + hv];
+    const float bet = beta[(size_t)(t0 + tg) * n_vheads + hv];
+    const bool isW = tid < CK_K;
+    const int col = isW ? tid : tid - CK_K;
+    f16 vcol[CK_C];
+#pragma unroll
+    for (int i = 0; i < CK_C; ++i)
+        vcol[i] = v[(size_t)(t0 + min(i, n - 1)) * v_stride + (size_t)hv * CK_V + col];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+        const int idx = tid + 256 * m, i = idx >> 4, c8 = (idx & 15) * 8;
+        *(f16x8*)&sK[i][c8] = i < n ? kv8[m] : (f16x8)(0);
+        *(f16x8*)&sQ[i][c8] = i < n ? qv8[m] : (f16x8)(0);
     }
     if (tid < CK_C) {
-        sG[tid] = tid < n ? safe_log(decay[(size_t)(t0 + tid) * n_vheads + hv]) : 0.f;
-        sB[tid] = tid < n ? beta[(size_t)(t0 + tid) * n_vheads + hv] : 0.f;
+        sG[tid] = tid < n ? safe_log(dec) : 0.f;
+        sB[tid] = tid < n ? bet : 0.f;
     }
     __syncthreads();
-    if (tid == 0) {
+    if (tid == 0) {   // the in-chunk prefix sums of log decay, in token order
+        float g[CK_C];
+#pragma unroll
+        for (int i = 0; i < CK_C; ++i) g[i] = sG[i];
         float a = 0.f;
+#pragma unroll
         for (int i = 0; i < CK_C; ++i) {
-            a += sG[i];
+            a += g[i];
             sG[i] = a;
         }
     }
     __syncthreads();
+    if (tid < CK_C) sEG[tid] = expf(sG[tid]);   // read after the next barrier
 
     // K K^T and Q K^T: wave w takes the 32x32 block (bi, bj)
     {
@@ -107,21 +130,12 @@ chunk_prep_kernel(const f16* __restrict__ q, const f16* __restrict__ k, const f1
     __syncthreads();
 
     // forward substitution: thread c < 128 solves column c of W, c >= 128 of U
+    // (sB and the staged K rows are zero past the chunk end; v by select)
     {
-        const bool isW = tid < CK_K;
-        const int col = isW ? tid : tid - CK_K;
         float x[CK_C];
 #pragma unroll
-        for (int i = 0; i < CK_C; ++i) {
-            float rhs = 0.f;
-            if (i < n) {
-                if (isW)
-                    rhs = sB[i] * expf(sG[i]) * (float)sK[i][col];
-                else
-                    rhs = sB[i] * (float)v[(size_t)(t0 + i) * v_stride + (size_t)hv * CK_V + col];
-            }
-            x[i] = rhs;
-        }
+        for (int i = 0; i < CK_C; ++i)
+            x[i] = isW ? sB[i] * sEG[i] * (float)sK[i][col] : (i < n ? sB[i] * (float)vcol[i] : 0.f);
 #pragma unroll
         for (int i = 1; i < CK_C; ++i) {
             float acc = x[i];
@@ -145,7 +159,7 @@ chunk_prep_kernel(const f16* __restrict__ q, const f16* __restrict__ k, const f1
     }
     if (tid < CK_C) {
         Gg[tid] = sG[tid];
-        Gg[CK_C + tid] = expf(sG[tid]);
+        Gg[CK_C + tid] = sEG[tid];
         Gg[2 * CK_C + tid] = expf(sG[CK_C - 1] - sG[tid]);
     }
 }
