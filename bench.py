@@ -37,7 +37,7 @@ METRIC = "attn/GDN decode µs/step + HBM GB/s %peak; prefill tokens/s + MFMA uti
 # WRITE_SIZE), each scaled by what the same counter reads for a 256 MiB
 # device copy (FETCH_SIZE x2.0, WRITE_SIZE x1.0); summary and commands in
 # profiles/gdn_decode_B4_hbm_traffic.md. Re-measure when the kernel changes.
-GDN_DECODE_TRAFFIC_BYTES = 27_262_773
+GDN_DECODE_TRAFFIC_BYTES = 27_221_660
 
 
 def log(*a):
