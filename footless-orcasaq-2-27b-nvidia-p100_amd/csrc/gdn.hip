@@ -54,12 +54,10 @@ __device__ __forceinline__ float log1p_pos(float e) {
 // transcendental unit; against the fp64 values the worst error is ~1e-7 on
 // beta and ~4e-7 on decay, inside the reference's own (4.6e-7 and 5.6e-6
 // relative, kernels.cu:139), with a dozen dependent instructions instead of
-// three libm calls in series. The conv's silu takes the same exponential, as
-// the reference's does (silu_f, kernels.cu:234): x / (1 + e^-x), correctly
-// rounded divide; its fp16-rounded output can differ from a libm-exp silu by
-// one fp16 ulp where the fp32 value sits within an ulp or two of a rounding
-// boundary.
-__device__ __forceinline__ float conv_silu(float x) { return x / (1.f + hw_expf(-x)); }
+// three libm calls in series. (The conv's silu keeps det_expf: its output is
+// rounded to fp16, and with the transcendental unit's exponential an fp16
+// flip now and then moved config 1's state after 1024 steps from 4e-8 to 4e-5
+// of the oracle's, within the 1e-4 bar but too close to it.)
 __device__ __forceinline__ float gdn_beta(float b) { return 1.f / (1.f + hw_expf(-b)); }
 __device__ __forceinline__ float gdn_decay(float a_dt, float A) {
     const float sp = a_dt <= 20.f ? log1p_pos(hw_expf(a_dt)) : a_dt;
@@ -169,7 +167,7 @@ __global__ void conv1d_causal_kernel(const f16* __restrict__ x, const f16* __res
         }
         acc = fmaf((float)w[(size_t)d * width + j], e, acc);
     }
-    y[(size_t)t * row_stride + d] = f16_sat(conv_silu(acc));
+    y[(size_t)t * row_stride + d] = f16_sat(silu_f(acc));
     if (t == T - 1) {
         f16* so = st_out + (size_t)d * sl;
         for (int k = 0; k < sl; ++k) {
@@ -207,7 +205,7 @@ __global__ void conv1d_causal_rows_kernel(const f16* __restrict__ x, const f16* 
         acc = fmaf(wv[1], e[1], acc);
         acc = fmaf(wv[2], e[2], acc);
         acc = fmaf(wv[3], xt, acc);
-        y[(size_t)t * row_stride + d] = f16_sat(conv_silu(acc));
+        y[(size_t)t * row_stride + d] = f16_sat(silu_f(acc));
         e[0] = e[1];
         e[1] = e[2];
         e[2] = (float)f16_sat(xt);
@@ -404,7 +402,7 @@ __device__ __forceinline__ float conv1_apply(const ConvIn& c, bool hist) {
     acc = fmaf((float)c.w[1], s1, acc);
     acc = fmaf((float)c.w[2], s2, acc);
     acc = fmaf((float)c.w[3], xv, acc);
-    return (float)f16_sat(conv_silu(acc));
+    return (float)f16_sat(silu_f(acc));
 }
 
 // ... and its new state (s1, s2, x) into the ring. Stored at the kernel's
