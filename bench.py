@@ -308,6 +308,43 @@ def bench_gdn_out_norm(torch, fl, T, iters=50):
             "hbm_frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 3)}
 
 
+def bench_gdn_verify(torch, fl, T=3, steps=256, warmup=16):
+    """The GDN step of an MTP verify (runtime.py:3040-3053, gdn_scan_rows_f):
+    B = 4 sequences, T = 3 conv'd rows each, the state updated over the three
+    tokens with the checkpoints after the first two; 48 layer states rotated
+    as in config 1. HBM: state read + written, two checkpoints written, the
+    rows / gates / y."""
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(7)
+    L, row, nv = GDN_LAYERS, 10240, 48
+    S = torch.randn((L, B, nv, 128, 128), generator=g, device=dev) * 0.02
+    ck = torch.empty((B, T - 1, nv, 128, 128), device=dev)
+    x = torch.randn((L, B, T, row), generator=g, device=dev).half()
+    a = torch.randn((L, B, T, nv), generator=g, device=dev)
+    b = torch.randn((L, B, T, nv), generator=g, device=dev)
+    A_log = torch.zeros((L, nv), device=dev)
+    dt_bias = torch.zeros((L, nv), device=dev)
+    y = torch.empty((L, B, T, nv * 128), dtype=torch.float16, device=dev)
+    state = nv * 128 * 128 * 4
+
+    def step(i):
+        l = i % L
+        fl.ops.gdn_decode(x[l], [S[l, j] for j in range(B)], a[l], b[l], A_log[l], dt_bias[l],
+                          y[l], T=T, pos0s=[100 + i // L] * B, ck=[ck[j] for j in range(B)],
+                          ck_step=nv * 128 * 128)
+
+    gw = graph_of(torch, step, warmup)
+    gt = graph_of(torch, lambda i: step(warmup + i), steps)
+    time_graph(torch, gw)
+    ms = time_graph(torch, gt)
+    us = ms * 1e3 / steps
+    nbytes = B * (2 * state + (T - 1) * state + T * row * 2 + 2 * T * nv * 4 + T * nv * 128 * 2) \
+        + 2 * nv * 4
+    return {"config": f"gdn_verify_B{B}_T{T}", "us_per_step": round(us, 2),
+            "GBs": round(nbytes / (us * 1e-6) / 1e9, 1),
+            "hbm_frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 3)}
+
+
 # ---------------------------------------------------------------------------
 # config 4: chunked GDN prefill
 # ---------------------------------------------------------------------------
@@ -448,6 +485,7 @@ EXTRA_CONFIGS = {
     "prefill8_L8192": (bench_prefill, {"L": 8192, "kv8": True}),
     "prefill8_L32768": (bench_prefill, {"L": 32768, "kv8": True}),
     "gdn_chunked_L8192": (bench_chunked, {}),
+    "gdn_verify_B4_T3": (bench_gdn_verify, {}),
     "attn_prep_T1": (bench_attn_prep, {"T": 1}),
     "attn_prep_T8192": (bench_attn_prep, {"T": 8192, "iters": 20}),
     "gdn_out_norm_T4": (bench_gdn_out_norm, {"T": 4}),
