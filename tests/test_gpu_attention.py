@@ -204,6 +204,39 @@ def test_prefill_config3_sampled_rows(fl, dev, orc, L):
         assert ok, f"L={L} row {t}: max|err| {err}"
 
 
+@pytest.mark.parametrize("n_kv,G,T", [(8, 3, 300), (1, 24, 256), (1, 24, 300), (3, 8, 200),
+                                       (8, 3, 5600), (2, 12, 5632), (2, 12, 5600)])
+def test_prefill_kv_head_counts(fl, dev, orc, n_kv, G, T):
+    """Other kv-head counts and GQA group sizes, on both prefill kernels and
+    both workgroup orders (row tiles spread over the XCDs by kv head when the
+    head count divides 8 and the tiles split evenly, the plain grid order
+    otherwise): every row against the oracle for the short prompts, sampled
+    rows against the float64 closed form for the long ones."""
+    n_q = n_kv * G
+    rng = np.random.default_rng(1000 * n_kv + T)
+    kc = rng.standard_normal((T, n_kv, 256)).astype(np.float16)
+    vc = rng.standard_normal((T, n_kv, 256)).astype(np.float16)
+    q = (rng.standard_normal((T, n_q, 256)) / 16).astype(np.float16)
+    kd = torch.zeros((T, n_kv, 256), dtype=torch.float16, device=dev)
+    vd = torch.zeros_like(kd)
+    z = fl.ops.attention_prefill(to_dev(q, dev), kd, vd, pos0=0, scale=1.0, n_q_heads=n_q,
+                                 n_kv_heads=n_kv, k_new=to_dev(kc, dev), v_new=to_dev(vc, dev))
+    torch.cuda.synchronize()
+    zh = z.cpu().numpy()
+    assert np.isfinite(zh.astype(np.float32)).all()
+    if T <= 512:
+        want = orc.attention_prefill(q, kc, vc, n_q_heads=n_q, n_kv_heads=n_kv, q_pitch=256,
+                                     pos0=0, max_pos=T, scale=1.0, T=T)
+        err, ok = close(zh, want, ATOL, RTOL)
+        assert ok, f"n_kv={n_kv} T={T}: max|err| {err}"
+        return
+    for t in sorted({0, 1, 85, 86, T // 2, T - 2, T - 1, *rng.integers(0, T, 4).tolist()}):
+        want = orc.attention_exact(q[t:t + 1], kc, vc, n_q_heads=n_q, n_kv_heads=n_kv,
+                                   q_pitch=256, pos0=t, max_pos=T, scale=1.0, T=1)
+        err, ok = close(zh[t:t + 1], want, ATOL, RTOL)
+        assert ok, f"n_kv={n_kv} T={T} row {t}: max|err| {err}"
+
+
 @pytest.mark.parametrize("T,pos0,ramp", [(6000, 0, False), (5800, 700, True)])
 def test_prefill_long_sampled_rows(fl, dev, orc, T, pos0, ramp):
     """Prompts long enough for the 64-rows-a-wave prefill kernel (at least 512
