@@ -514,7 +514,11 @@ constexpr int R64_NST = R64_DIST + 1;
 constexpr int R64_LDS = R64_NST * R64_STAGE;   // 128 KiB at R64_DIST 3
 static_assert(R64_LDS <= 160 * 1024, "R64_DIST: LDS <= 160 KiB");
 constexpr int R64_COPIES = 8;               // copy instructions a wave a tile (4 K + 4 V)
-constexpr int R64_MIN_WGS = 512;            // the r64 kernel from this many workgroups up
+// the r64 kernel from this many workgroups up (T >= 4096 at 24 / 4 heads).
+// Same-box A/B, r64 against the 128-row kernel: 192 workgroups (T = 2048)
+// 156 against 100 us, 384 (T = 4096) 289-299 against 297-315 us, 480 (T =
+// 5120) 378 against 410-422 us.
+constexpr int R64_MIN_WGS = 384;
 
 // Copy tile kv0 (K and V, 32 rows each) into the stage at dst: wave w copies
 // rows 8 w .. 8 w + 7, two a copy instruction (as issue_rows: loff[n] = this
