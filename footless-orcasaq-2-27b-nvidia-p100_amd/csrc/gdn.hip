@@ -609,6 +609,78 @@ rmsnorm_gated_kernel(const f16* __restrict__ o, const f16* __restrict__ z,
     *(f16x2*)(y + base) = out;
 }
 
+// The same norm, 16-byte aligned rows: 16 lanes a row (lane j of the row holds
+// o[8 j .. 8 j + 7], one 16-byte load), 4 rows a wave per pass and GR_PASSES
+// passes (all loads issued first), so a wave carries 4 GR_PASSES rows.
+// The reference's warp w' is lanes 4 w' .. 4 w' + 3 of the row; its
+// __shfl_down tree over offsets 16, 8, 4, 2, 1 is lane exchanges at distance
+// 2 and 1 (butterflies: a + b == b + a, so every lane holds the tree's lane-0
+// sum bit for bit) then the in-lane pairs (i, i + 4), (i, i + 2), (0, 1); the
+// warp sums combine as (r0 + r2) + (r1 + r3) by exchanges at distance 8, 4.
+// Passes a wave: 1, 2 and 4 measured alike at T = 8192 (48 rows a token,
+// 74 us against 111 us for a wave a row), 1 best at T = 1024 (11.4 / 12.7 /
+// 14.2 us against 15.5).
+constexpr int GR_PASSES = 1;
+// the 16-lanes-a-row kernel from this many rows up: below, a wave a row keeps
+// more waves on a decode step's few rows (T = 4, 192 rows: 2.0 us, against
+// 3.7 us at 8 rows a wave)
+constexpr long long GR_ROWS_MIN = 8192;
+// v of lane l ^ 1 / l ^ 2 (DPP quad permutes [1 0 3 2] / [2 3 0 1])
+__device__ __forceinline__ float dpp_xor1(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float dpp_xor2(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));
+}
+__global__ void __launch_bounds__(GR_THREADS)
+rmsnorm_gated_rows_kernel(const f16* __restrict__ o, const f16* __restrict__ z,
+                          const float* __restrict__ w, f16* __restrict__ y, int rows, int pitch,
+                          int n_rows, float eps) {
+    const int lane = threadIdx.x & 63, j = lane & 15;
+    const int wave = blockIdx.x * (GR_THREADS / 64) + (threadIdx.x >> 6);
+    typedef _Float16 f16x8v __attribute__((ext_vector_type(8)));
+    f16x8v ov[GR_PASSES], zv[GR_PASSES];
+    size_t base[GR_PASSES];
+    bool ok[GR_PASSES];
+#pragma unroll
+    for (int p = 0; p < GR_PASSES; ++p) {
+        const int rid = (wave * GR_PASSES + p) * 4 + (lane >> 4);
+        ok[p] = rid < n_rows;
+        const int rr = ok[p] ? rid : n_rows - 1;
+        const int t = rr / rows, r = rr - t * rows;
+        base[p] = ((size_t)t * rows + r) * pitch + 8 * j;
+        ov[p] = *(const f16x8v*)(o + base[p]);
+        zv[p] = *(const f16x8v*)(z + base[p]);
+    }
+    const f32x4 w0 = *(const f32x4*)(w + 8 * j), w1 = *(const f32x4*)(w + 8 * j + 4);
+    const float wv[8] = {w0[0], w0[1], w0[2], w0[3], w1[0], w1[1], w1[2], w1[3]};
+#pragma unroll
+    for (int p = 0; p < GR_PASSES; ++p) {
+        float x[8], sq[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            x[i] = (float)ov[p][i];
+            sq[i] = x[i] * x[i];
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) sq[i] += dpp_xor2(sq[i]);   // offset 16
+#pragma unroll
+        for (int i = 0; i < 8; ++i) sq[i] += dpp_xor1(sq[i]);   // offset 8
+        float t4[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) t4[i] = sq[i] + sq[i + 4];        // offset 4
+        const float t2a = t4[0] + t4[2], t2b = t4[1] + t4[3];         // offset 2
+        float ss = t2a + t2b;                                          // offset 1: warp sum
+        ss += lane_xor(ss, 8);                                         // r0 + r2, r1 + r3
+        ss += lane_xor(ss, 4);                                         // (r0 + r2) + (r1 + r3)
+        const float inv = 1.f / sqrtf(ss / (float)GR_K + eps);
+        f16x8v out;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) out[i] = f16_sat(x[i] * inv * wv[i] * silu_f((float)zv[p][i]));
+        if (ok[p]) *(f16x8v*)(y + base[p]) = out;
+    }
+}
+
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 }  // namespace
@@ -738,6 +810,14 @@ int fl_rmsnorm_gated(const void* o, const void* z, const float* w, void* y, int 
                "pitch % 2, aligned o, z, y, w");
     const long long n_rows = (long long)rows * T;
     const int waves = GR_THREADS / 64;
+    if (n_rows >= GR_ROWS_MIN && pitch % 8 == 0 && aligned16(o) && aligned16(z) && aligned16(y) &&
+        aligned16(w)) {
+        const long long rows_wg = 4LL * GR_PASSES * waves;
+        hipLaunchKernelGGL(rmsnorm_gated_rows_kernel, dim3((unsigned)((n_rows + rows_wg - 1) / rows_wg)),
+                           dim3(GR_THREADS), 0, (hipStream_t)stream, (const f16*)o, (const f16*)z, w,
+                           (f16*)y, rows, pitch, (int)n_rows, eps);
+        return fl::check_launch("rmsnorm_gated");
+    }
     hipLaunchKernelGGL(rmsnorm_gated_kernel, dim3((unsigned)((n_rows + waves - 1) / waves)),
                        dim3(GR_THREADS), 0, (hipStream_t)stream, (const f16*)o, (const f16*)z, w,
                        (f16*)y, rows, pitch, (int)n_rows, eps);

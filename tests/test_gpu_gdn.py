@@ -267,6 +267,33 @@ def test_chunked_vs_recurrence(fl, dev, orc, T):
     assert ok, f"T={T}: max|dy| {err}"
 
 
+@pytest.mark.parametrize("T,rows", [(1, 48), (3, 5), (7, 48)])
+def test_rmsnorm_gated_row_layouts(fl, dev, orc, rng, T, rows):
+    """Rows 16-byte aligned (pitch 136: 16 lanes a row, 8 rows a wave) and
+    not (pitch 130: a wave a row) give the same bits, and the oracle's; row
+    counts that leave a wave's last rows empty."""
+    o = (rng.standard_normal((T, rows, 128)) * 0.7).astype(np.float16)
+    z = (rng.standard_normal((T, rows, 128)) * 2).astype(np.float16)
+    w = (1 + rng.standard_normal(128) * 0.2).astype(np.float32)
+    want = orc.rmsnorm_gated(o, z, w, rows=rows, T=T)
+    wd = torch.from_numpy(w).to(dev)
+    outs = []
+    for pitch in (136, 130):
+        op = np.zeros((T, rows, pitch), np.float16)
+        zp = np.zeros((T, rows, pitch), np.float16)
+        op[..., :128], zp[..., :128] = o, z
+        y = torch.full((T, rows, pitch), 7.0, dtype=torch.float16, device=dev)
+        fl.ops.rmsnorm_gated(torch.from_numpy(op).to(dev), torch.from_numpy(zp).to(dev), wd, y,
+                             T=T, rows=rows, pitch=pitch)
+        torch.cuda.synchronize()
+        yh = y.cpu().numpy()
+        assert (yh[..., 128:] == 7.0).all(), f"pitch {pitch}: wrote past the row"
+        outs.append(yh[..., :128])
+    assert np.array_equal(outs[0].view(np.int16), outs[1].view(np.int16))
+    d = np.abs(outs[0].view(np.int16).astype(np.int32) - want.view(np.int16).astype(np.int32))
+    assert d.max() <= 1, f"max {d.max()} ulp"
+
+
 @pytest.mark.parametrize("T", [1, 4, 1000])
 def test_rmsnorm_gated_vs_oracle(fl, dev, orc, rng, T):
     """The GDN output norm through the C ABI: same operations and order as the
