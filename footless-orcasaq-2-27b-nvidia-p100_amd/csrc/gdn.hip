@@ -11,12 +11,12 @@
 //   gdn_scan_rows_f      2943-3070  the fused decode / verify step
 //
 // State layout: S [n_vheads][V rows][K cols] fp32, a head is 64 KiB. The
-// delta-rule kernels give a workgroup 32 rows of one head (8 lanes a row,
-// 16 columns a lane = four float4 at columns c0 + 32j, c0 = 4 (lane % 8)),
-// so each 8-lane group reads a row's 128 contiguous bytes per load and the
-// row's dot products reduce inside the group with DPP (quad_perm xor 1,
-// xor 2, then the half-row mirror). The state of the workgroup's rows stays
-// in registers for the whole call: loaded once, stored once.
+// delta-rule kernels give a state row 8 lanes (16 columns a lane = four
+// float4 at columns c0 + 32j, c0 = 4 (lane % 8)), so each 8-lane group reads
+// a row's 128 contiguous bytes per load and the row's dot products reduce
+// inside the group with DPP (quad_perm xor 1, xor 2, then the half-row
+// mirror); a wavefront holds 8 rows. The rows' state stays in registers for
+// the whole call: loaded once, stored once.
 #include "fl_common.hpp"
 
 #pragma clang fp contract(off)
@@ -26,7 +26,6 @@ namespace {
 constexpr int GR_ROWS = 32;       // state rows a workgroup
 constexpr int GR_THREADS = 256;   // 8 lanes a row
 constexpr int GR_K = 128;
-constexpr int GR_TC = 16;         // tokens staged a time by the scan
 
 // Sum over the 8 lanes of a row group; every lane gets the same bits.
 __device__ __forceinline__ float row8_sum(float v) {
@@ -145,74 +144,177 @@ __device__ __forceinline__ void gather16(float (&dst)[16], const float* row, int
 }
 
 // ---------------------------------------------------------------------------
-// causal conv (decode / prefill rows, and verify rows with per-row states)
+// Causal conv over a run of tokens (a8) and a verify's rows (a9): one
+// "sliding window" kernel. A lane owns CPL adjacent channels -- 8 (one
+// 16-byte load of a token's row, one 16-byte store of y) when the layout
+// allows it, else 1 -- and a block of CONV_TB consecutive tokens. It requests
+// all of its block's rows first, then slides a register window of the W - 1
+// previous frames down them, so each x value is read from HBM once (a
+// block's W - 1 leading frames are the previous block's last rows, which L2
+// already holds) instead of once per tap. A workgroup is one wavefront:
+// 64 CPL channels of one token block; blockIdx.y is the token block.
+//
+// The taps add oldest first from zero (acc = fma(w_j, E_j, acc)), the order
+// the reference's per-channel loop uses (kernels.cu:1659-1668), so y and the
+// frames match its values bit for bit. E = [the stored W - 1 frames (zero at
+// pos0 == 0) | x]: the window of block t0 starts as E[t0 .. t0 + W - 2] and
+// after the call's last token is E[T .. T + W - 2], the new stored state.
+// ROWS (a verify, T <= 3): the window after token t goes to the t-th state
+// buffer, and a frame entering the window is rounded by f16_sat first, as the
+// reference's row form does (kernels.cu:1704-1711).
 // ---------------------------------------------------------------------------
-__global__ void conv1d_causal_kernel(const f16* __restrict__ x, const f16* __restrict__ w,
-                                     const f16* __restrict__ st_in, f16* __restrict__ y,
-                                     f16* __restrict__ st_out, int dim, int T, int pos0,
-                                     int row_stride, int width) {
-    const int t = blockIdx.y;
-    const int d = blockIdx.x * blockDim.x + threadIdx.x;
-    if (d >= dim) return;
-    const int sl = width - 1;
-    const f16* st = st_in + (size_t)d * sl;
-    float acc = 0.f;
-    for (int j = 0; j < width; ++j) {
-        const int i = t + j;
-        float e = 0.f;
-        if (i < sl) {
-            if (pos0 > 0) e = (float)st[i];
-        } else {
-            e = (float)x[(size_t)(i - sl) * row_stride + d];
+constexpr int CONV_TB = 16;       // tokens a lane
+constexpr int CONV_WMAX = 8;      // widths 1 .. 8
+
+template <int CPL> struct ConvVec;
+template <> struct ConvVec<8> { typedef f16x8 type; };
+template <> struct ConvVec<1> { typedef f16 type; };
+
+template <int CPL>
+__device__ __forceinline__ float cv_get(const typename ConvVec<CPL>::type& v, int i) {
+    if constexpr (CPL == 8) return (float)v[i];
+    else return (float)v;
+}
+template <int CPL>
+__device__ __forceinline__ void cv_set(typename ConvVec<CPL>::type& v, int i, f16 h) {
+    if constexpr (CPL == 8) v[i] = h;
+    else v = h;
+}
+
+// N consecutive fp16 values at p as floats: N / 8 16-byte loads when VEC
+// (N a multiple of 8, p 16-byte aligned), else N 2-byte loads.
+template <int N, bool VEC>
+__device__ __forceinline__ void halves_in(float (&f)[N], const f16* p) {
+    if constexpr (VEC) {
+        static_assert(N % 8 == 0, "whole vectors");
+#pragma unroll
+        for (int m = 0; m < N / 8; ++m) {
+            const f16x8 v = *(const f16x8*)(p + 8 * m);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) f[8 * m + i] = (float)v[i];
         }
-        acc = fmaf((float)w[(size_t)d * width + j], e, acc);
-    }
-    y[(size_t)t * row_stride + d] = f16_sat(silu_f(acc));
-    if (t == T - 1) {
-        f16* so = st_out + (size_t)d * sl;
-        for (int k = 0; k < sl; ++k) {
-            const int i = T + k;
-            float e = 0.f;
-            if (i < sl) {
-                if (pos0 > 0) e = (float)st[i];
-            } else {
-                e = (float)x[(size_t)(i - sl) * row_stride + d];
-            }
-            so[k] = f16_sat(e);
-        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < N; ++i) f[i] = (float)p[i];
     }
 }
 
-__global__ void conv1d_causal_rows_kernel(const f16* __restrict__ x, const f16* __restrict__ w,
-                                          const f16* st_in, f16* __restrict__ y, f16* st0,
-                                          f16* st1, f16* st2, int dim, int T, int pos0,
-                                          int row_stride) {
-    const int d = blockIdx.x * blockDim.x + threadIdx.x;
+// The window [frame][channel] stored as the state layout [channel][frame].
+template <int H, int CPL>
+__device__ __forceinline__ void frames_out(f16* p, const float (&win)[H][CPL]) {
+    if constexpr (CPL == 8) {
+#pragma unroll
+        for (int m = 0; m < H; ++m) {
+            f16x8 v;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int flat = 8 * m + i;   // channel flat / H, frame flat % H
+                v[i] = f16_sat(win[flat % H][flat / H]);
+            }
+            *(f16x8*)(p + 8 * m) = v;
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < H; ++j) p[j] = f16_sat(win[j][0]);
+    }
+}
+
+struct ConvStates {
+    f16* st[3];   // the new state (st[0]), or a verify's one state a row
+};
+
+template <int W, int CPL, bool ROWS>
+__global__ void __launch_bounds__(64)
+conv_window_kernel(const f16* __restrict__ x, const f16* __restrict__ w, const f16* st_in,
+                   f16* __restrict__ y, ConvStates outs, int dim, int T, int pos0,
+                   int row_stride) {
+    typedef typename ConvVec<CPL>::type vec;
+    constexpr bool VEC = CPL == 8;
+    constexpr int H = W - 1;          // frames of history
+    constexpr int HW = H > 0 ? H : 1;
+    static_assert(CONV_TB >= H, "a block's leading frames are the previous block's rows");
+    constexpr int NTOK = ROWS ? 3 : CONV_TB;   // a verify has at most 3 rows
+    const int d = (blockIdx.x * 64 + threadIdx.x) * CPL;
     if (d >= dim) return;
-    float e[3];
+    const int t0 = blockIdx.y * CONV_TB;
+    const int nt = min(NTOK, T - t0);
+    // the block's rows, all requested before any arithmetic (a row past the
+    // call re-reads the last one and is not used)
+    vec xr[NTOK];
 #pragma unroll
-    for (int i = 0; i < 3; ++i) e[i] = pos0 > 0 ? (float)st_in[(size_t)d * 3 + i] : 0.f;
-    float wv[4];
+    for (int i = 0; i < NTOK; ++i)
+        xr[i] = *(const vec*)(x + (size_t)min(t0 + i, T - 1) * row_stride + d);
+    float taps[CPL * W];   // [channel][tap]
+    halves_in<CPL * W, VEC>(taps, w + (size_t)d * W);
+    float win[HW][CPL];
+    if constexpr (H > 0) {
+        if (t0 == 0) {
+            float hist[CPL * H];   // [channel][frame]
+            halves_in<CPL * H, VEC>(hist, st_in + (size_t)d * H);
+            const bool keep = pos0 > 0;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) wv[j] = (float)w[(size_t)d * 4 + j];
-    f16* dst[3] = {st0, st1, st2};
+            for (int j = 0; j < H; ++j)
 #pragma unroll
-    for (int t = 0; t < 3; ++t) {
-        if (t >= T) break;
-        const float xt = (float)x[(size_t)t * row_stride + d];
-        float acc = 0.f;
-        acc = fmaf(wv[0], e[0], acc);
-        acc = fmaf(wv[1], e[1], acc);
-        acc = fmaf(wv[2], e[2], acc);
-        acc = fmaf(wv[3], xt, acc);
-        y[(size_t)t * row_stride + d] = f16_sat(silu_f(acc));
-        e[0] = e[1];
-        e[1] = e[2];
-        e[2] = (float)f16_sat(xt);
-        f16* so = dst[t] + (size_t)d * 3;
-        so[0] = f16_sat(e[0]);
-        so[1] = f16_sat(e[1]);
-        so[2] = f16_sat(e[2]);
+                for (int c = 0; c < CPL; ++c) win[j][c] = keep ? hist[c * H + j] : 0.f;
+        } else {
+#pragma unroll
+            for (int j = 0; j < H; ++j) {
+                const vec r = *(const vec*)(x + (size_t)(t0 - H + j) * row_stride + d);
+#pragma unroll
+                for (int c = 0; c < CPL; ++c) win[j][c] = cv_get<CPL>(r, c);
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < NTOK; ++i) {
+        if (i >= nt) continue;   // uniform; keeps the trip count constant (full unroll)
+        vec out;
+        float xf[CPL];
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) {
+            xf[c] = cv_get<CPL>(xr[i], c);
+            float acc = 0.f;
+#pragma unroll
+            for (int j = 0; j < H; ++j) acc = fmaf(taps[c * W + j], win[j][c], acc);
+            acc = fmaf(taps[c * W + H], xf[c], acc);
+            cv_set<CPL>(out, c, f16_sat(silu_f(acc)));
+        }
+        *(vec*)(y + (size_t)(t0 + i) * row_stride + d) = out;
+        if constexpr (H > 0) {
+#pragma unroll
+            for (int c = 0; c < CPL; ++c) {
+#pragma unroll
+                for (int j = 0; j + 1 < H; ++j) win[j][c] = win[j + 1][c];
+                win[H - 1][c] = ROWS ? (float)f16_sat(xf[c]) : xf[c];
+            }
+            if constexpr (ROWS) frames_out<H, CPL>(outs.st[i] + (size_t)d * H, win);
+        }
+    }
+    if constexpr (!ROWS && H > 0)
+        if (t0 + nt == T) frames_out<H, CPL>(outs.st[0] + (size_t)d * H, win);
+}
+
+template <int W>
+void conv_launch(bool vec, bool rows, dim3 grid_tok, const f16* x, const f16* w,
+                 const f16* st_in, f16* y, ConvStates outs, int dim, int T, int pos0,
+                 int row_stride, hipStream_t stream) {
+    const int cpl = vec ? 8 : 1;
+    const dim3 grid((dim + 64 * cpl - 1) / (64 * cpl), grid_tok.y);
+    if (rows) {   // the verify form is width 4 only
+        if constexpr (W == 4) {
+            if (vec)
+                hipLaunchKernelGGL((conv_window_kernel<W, 8, true>), grid, dim3(64), 0, stream, x,
+                                   w, st_in, y, outs, dim, T, pos0, row_stride);
+            else
+                hipLaunchKernelGGL((conv_window_kernel<W, 1, true>), grid, dim3(64), 0, stream, x,
+                                   w, st_in, y, outs, dim, T, pos0, row_stride);
+        }
+    } else if (vec) {
+        hipLaunchKernelGGL((conv_window_kernel<W, 8, false>), grid, dim3(64), 0, stream, x, w,
+                           st_in, y, outs, dim, T, pos0, row_stride);
+    } else {
+        hipLaunchKernelGGL((conv_window_kernel<W, 1, false>), grid, dim3(64), 0, stream, x, w,
+                           st_in, y, outs, dim, T, pos0, row_stride);
     }
 }
 
@@ -253,54 +355,97 @@ __global__ void gdn_scalars_kernel(const float* __restrict__ a, const float* __r
 }
 
 // ---------------------------------------------------------------------------
-// the delta rule over T tokens, 16 tokens of k / q / v / gates staged in
-// LDS at a time. grid (V / 32, n_vheads), block 256.
+// The delta rule over T tokens (a12): one wavefront per 8 state rows of a v
+// head, no LDS and no barrier. Each lane reads the operands of its own
+// columns straight from global memory -- k and q at columns c0 + 32 j + 0..3
+// (four 8-byte loads each; the 16 wavefronts of a head share them in L2), its
+// row's v, the head's beta and decay -- SCAN_AHEAD tokens before it computes
+// with them, from a ring of registers, so the loads of later tokens are in
+// flight under the dependent chain of the current one. The rows' state stays
+// in registers from the first token to the last. Workgroups are mapped so
+// that the row blocks of neighbouring v heads (which read the same k / q
+// rows) run on one XCD, i.e. share one L2.
+// grid n_vheads * V / 8 workgroups of 64.
 // ---------------------------------------------------------------------------
-__global__ void __launch_bounds__(GR_THREADS)
+constexpr int SCAN_AHEAD = 4;
+
+struct ScanOps {
+    f16x4 k[4], q[4];
+    float v, beta, decay;
+};
+
+// 0, in a VGPR the compiler cannot see through: an index plus this makes a
+// uniform load a vector load (scalar loads complete out of order, so waiting
+// for one would also wait for every later-issued scalar load)
+__device__ __forceinline__ int opaque_zero() {
+    int z;
+    asm volatile("v_mov_b32 %0, 0" : "=v"(z));
+    return z;
+}
+
+__device__ __forceinline__ ScanOps scan_fetch(const f16* __restrict__ q, const f16* __restrict__ k,
+                                              const f16* __restrict__ v,
+                                              const float* __restrict__ beta,
+                                              const float* __restrict__ decay, int t,
+                                              size_t qk_off, size_t v_off, int hv_vz,
+                                              int qk_stride, int v_stride, int n_vheads) {
+    ScanOps o;
+    const size_t qk = (size_t)t * qk_stride + qk_off;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        o.k[j] = *(const f16x4*)(k + qk + 32 * j);
+        o.q[j] = *(const f16x4*)(q + qk + 32 * j);
+    }
+    o.v = (float)v[(size_t)t * v_stride + v_off];
+    o.beta = beta[(size_t)t * n_vheads + hv_vz];
+    o.decay = decay[(size_t)t * n_vheads + hv_vz];
+    return o;
+}
+
+__global__ void __launch_bounds__(64)
 gdn_scan_kernel(const f16* __restrict__ q, const f16* __restrict__ k, const f16* __restrict__ v,
                 const float* __restrict__ beta, const float* __restrict__ decay,
                 float* __restrict__ S, f16* __restrict__ y, int T, int n_vheads, int V,
                 int qk_stride, int v_stride, int y_stride, float out_scale, int group,
                 float* __restrict__ Ck, long long ck_step) {
-    __shared__ __attribute__((aligned(16))) float sk[GR_TC][GR_K];
-    __shared__ __attribute__((aligned(16))) float sq[GR_TC][GR_K];
-    __shared__ float sv[GR_TC][GR_ROWS];
-    __shared__ float sb[GR_TC], sd[GR_TC];
-    const int hv = blockIdx.y, hk = hv / group;
-    const int tid = threadIdx.x, ri = tid >> 3, c0 = 4 * (tid & 7);
-    const int vi = blockIdx.x * GR_ROWS + ri;
-    float* Srow = S + ((size_t)hv * V + vi) * GR_K + c0;
+    const int rbs = V / 8;   // row blocks a head
+    const int nb = n_vheads * rbs;
+    int blk = blockIdx.x;
+    if (nb % 8 == 0) blk = (blk % 8) * (nb / 8) + blk / 8;   // XCD blk % 8 takes a run of heads
+    const int hv = blk / rbs, rb = blk - hv * rbs;
+    const int lane = threadIdx.x, c0 = 4 * (lane & 7);
+    const int vi = rb * 8 + (lane >> 3);
+    const size_t row = (size_t)hv * V + vi;
+    float* Srow = S + row * GR_K + c0;
+    const size_t qk_off = (size_t)(hv / group) * GR_K + c0;
+    const int hv_vz = hv + opaque_zero();
     float reg[16];
     load_row16(reg, Srow);
-    for (int t0 = 0; t0 < T; t0 += GR_TC) {
-        const int n = min(GR_TC, T - t0);
-        __syncthreads();
-        for (int i = tid; i < n * 64; i += GR_THREADS) {
-            const int tt = i >> 6, c = (i & 63) * 2;
-            const size_t a = (size_t)(t0 + tt) * qk_stride + (size_t)hk * GR_K + c;
-            sk[tt][c] = (float)k[a];
-            sk[tt][c + 1] = (float)k[a + 1];
-            sq[tt][c] = (float)q[a];
-            sq[tt][c + 1] = (float)q[a + 1];
-        }
-        for (int i = tid; i < n * GR_ROWS; i += GR_THREADS) {
-            const int tt = i / GR_ROWS, r = i - tt * GR_ROWS;
-            sv[tt][r] = (float)v[(size_t)(t0 + tt) * v_stride + (size_t)hv * V + blockIdx.x * GR_ROWS + r];
-        }
-        if (tid < n) {
-            sb[tid] = beta[(size_t)(t0 + tid) * n_vheads + hv];
-            sd[tid] = decay[(size_t)(t0 + tid) * n_vheads + hv];
-        }
-        __syncthreads();
-        for (int tt = 0; tt < n; ++tt) {
+    ScanOps ring[SCAN_AHEAD];
+#pragma unroll
+    for (int i = 0; i < SCAN_AHEAD; ++i)
+        ring[i] = scan_fetch(q, k, v, beta, decay, min(i, T - 1), qk_off, row, hv_vz, qk_stride,
+                             v_stride, n_vheads);
+    for (int t0 = 0; t0 < T; t0 += SCAN_AHEAD) {
+#pragma unroll
+        for (int i = 0; i < SCAN_AHEAD; ++i) {
+            const int t = t0 + i;
+            if (t >= T) break;
+            const ScanOps cur = ring[i];
+            ring[i] = scan_fetch(q, k, v, beta, decay, min(t + SCAN_AHEAD, T - 1), qk_off, row,
+                                 hv_vz, qk_stride, v_stride, n_vheads);
             float kk[16], qq[16];
-            gather16(kk, sk[tt], c0);
-            gather16(qq, sq[tt], c0);
-            const float o = delta_rule_token(reg, kk, qq, sv[tt][ri], sb[tt], sd[tt]);
-            if (c0 == 0) y[(size_t)(t0 + tt) * y_stride + (size_t)hv * V + vi] = f16_sat(o * out_scale);
-            const int t = t0 + tt;
-            if (Ck != nullptr && t < T - 1)
-                store_row16(Ck + (size_t)t * ck_step + ((size_t)hv * V + vi) * GR_K + c0, reg);
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    kk[4 * j + e] = (float)cur.k[j][e];
+                    qq[4 * j + e] = (float)cur.q[j][e];
+                }
+            delta_update(reg, kk, cur.v, cur.beta, cur.decay);
+            if (Ck != nullptr && t < T - 1) store_row16(Ck + (size_t)t * ck_step + row * GR_K + c0, reg);
+            const float o = delta_out(reg, qq);
+            if (c0 == 0) y[(size_t)t * y_stride + row] = f16_sat(o * out_scale);
         }
     }
     store_row16(Srow, reg);
@@ -356,14 +501,6 @@ __device__ __forceinline__ float warp32_tree_lane0(float v) {
     v += dpp_shl<2>(v);
     v += dpp_shl<1>(v);
     return v;
-}
-
-// 0, in a VGPR the compiler cannot see through: an index plus this makes a
-// uniform load a vector load
-__device__ __forceinline__ int opaque_zero() {
-    int z;
-    asm volatile("v_mov_b32 %0, 0" : "=v"(z));
-    return z;
 }
 
 // conv1_ch split in two so the loads can be issued ahead of the state's: the
@@ -687,16 +824,45 @@ bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 extern "C" {
 
+// The 8-channel (16-byte) form needs every row, tap set and state of a lane's
+// channels on 16-byte boundaries: dim and row_stride multiples of 8 and the
+// five buffers 16-byte aligned; anything else takes the channel-a-lane form.
+static bool conv_vec_ok(const void* x, const void* w, const void* st_in, const void* y,
+                        const f16* const* st, int n_st, int dim, int row_stride) {
+    bool ok = dim % 8 == 0 && row_stride % 8 == 0 && aligned16(x) && aligned16(w) &&
+              aligned16(st_in) && aligned16(y);
+    for (int i = 0; i < n_st; ++i) ok = ok && aligned16(st[i]);
+    return ok;
+}
+
+static int conv_dispatch(const void* x, const void* w, const void* st_in, void* y,
+                         ConvStates outs, int n_st, bool rows, int dim, int T, int pos0,
+                         int row_stride, int width, hipStream_t stream) {
+    const f16* sts[3] = {outs.st[0], outs.st[1], outs.st[2]};
+    const bool vec = conv_vec_ok(x, w, st_in, y, sts, n_st, dim, row_stride);
+    const dim3 tok(1, (T + CONV_TB - 1) / CONV_TB);
+    const f16 *xp = (const f16*)x, *wp = (const f16*)w, *sp = (const f16*)st_in;
+    f16* yp = (f16*)y;
+    switch (width) {
+#define FL_CONV_W(Wd) \
+    case Wd: conv_launch<Wd>(vec, rows, tok, xp, wp, sp, yp, outs, dim, T, pos0, row_stride, stream); break;
+        FL_CONV_W(1) FL_CONV_W(2) FL_CONV_W(3) FL_CONV_W(4)
+        FL_CONV_W(5) FL_CONV_W(6) FL_CONV_W(7) FL_CONV_W(8)
+#undef FL_CONV_W
+        default: return fl::einval("1 <= width <= 8");
+    }
+    return fl::check_launch(rows ? "conv1d_causal_rows" : "conv1d_causal");
+}
+
 int fl_conv1d_causal(const void* x, const void* w, const void* st_in, void* y, void* st_out,
                      int dim, int T, int pos0, int row_stride, int width, fl_stream_t stream) {
     FL_REQUIRE(x && w && st_in && y && st_out, "null pointer");
     FL_REQUIRE(st_in != st_out, "st_in and st_out must be distinct buffers");
     FL_REQUIRE(dim >= 1 && T >= 1 && pos0 >= 0 && row_stride >= dim, "dim, T, pos0, row_stride");
-    FL_REQUIRE(width >= 2 && width <= 16, "2 <= width <= 16");
-    hipLaunchKernelGGL(conv1d_causal_kernel, dim3((dim + 255) / 256, T), dim3(256), 0,
-                       (hipStream_t)stream, (const f16*)x, (const f16*)w, (const f16*)st_in,
-                       (f16*)y, (f16*)st_out, dim, T, pos0, row_stride, width);
-    return fl::check_launch("conv1d_causal");
+    FL_REQUIRE(width >= 1 && width <= CONV_WMAX, "1 <= width <= 8");
+    ConvStates outs = {{(f16*)st_out, nullptr, nullptr}};
+    return conv_dispatch(x, w, st_in, y, outs, 1, false, dim, T, pos0, row_stride, width,
+                         (hipStream_t)stream);
 }
 
 int fl_conv1d_causal_rows(const void* x, const void* w, const void* st_in, void* y, void* st0,
@@ -706,10 +872,9 @@ int fl_conv1d_causal_rows(const void* x, const void* w, const void* st_in, void*
     FL_REQUIRE(T >= 1 && T <= 3, "1 <= T <= 3");
     FL_REQUIRE(st0 && (T < 2 || st1) && (T < 3 || st2), "a state buffer per row");
     FL_REQUIRE(dim >= 1 && pos0 >= 0 && row_stride >= dim, "dim, pos0, row_stride");
-    hipLaunchKernelGGL(conv1d_causal_rows_kernel, dim3((dim + 255) / 256), dim3(256), 0,
-                       (hipStream_t)stream, (const f16*)x, (const f16*)w, (const f16*)st_in,
-                       (f16*)y, (f16*)st0, (f16*)st1, (f16*)st2, dim, T, pos0, row_stride);
-    return fl::check_launch("conv1d_causal_rows");
+    ConvStates outs = {{(f16*)st0, (f16*)st1, (f16*)st2}};
+    return conv_dispatch(x, w, st_in, y, outs, T, true, dim, T, pos0, row_stride, 4,
+                         (hipStream_t)stream);
 }
 
 int fl_l2norm_scaled(const void* x, void* y, int n, int rows, int pitch, float eps, float scale,
@@ -739,13 +904,15 @@ int fl_gdn_scan(const void* q, const void* k, const void* v, const float* beta,
                 float* Ck, long long ck_step, fl_stream_t stream) {
     FL_REQUIRE(q && k && v && beta && decay && S && y, "null pointer");
     FL_REQUIRE(K == GR_K, "K must be 128");
-    FL_REQUIRE(V >= GR_ROWS && V % GR_ROWS == 0, "V % 32 == 0");
+    FL_REQUIRE(V >= 8 && V % 8 == 0, "V % 8 == 0");
     FL_REQUIRE(group >= 1 && n_vheads >= 1 && (n_vheads - 1) / group < n_kheads,
                "n_vheads / group <= n_kheads");
     FL_REQUIRE(T >= 1, "T >= 1");
     FL_REQUIRE(aligned16(S) && (Ck == nullptr || (aligned16(Ck) && ck_step % 4 == 0)),
                "16-byte aligned S / Ck");
-    hipLaunchKernelGGL(gdn_scan_kernel, dim3(V / GR_ROWS, n_vheads), dim3(GR_THREADS), 0,
+    FL_REQUIRE(((uintptr_t)q & 7u) == 0 && ((uintptr_t)k & 7u) == 0 && qk_stride % 4 == 0,
+               "8-byte aligned q / k rows (qk_stride % 4 == 0)");
+    hipLaunchKernelGGL(gdn_scan_kernel, dim3(n_vheads * (V / 8)), dim3(64), 0,
                        (hipStream_t)stream, (const f16*)q, (const f16*)k, (const f16*)v, beta,
                        decay, S, (f16*)y, T, n_vheads, V, qk_stride, v_stride, y_stride,
                        out_scale, group, Ck, ck_step);

@@ -229,7 +229,9 @@ int fl_attention_prefill_q8(const void* q, int q_pitch, const void* k_new, const
  * conv1d_causal over `dim` channels of rows x [T][row_stride] f16: E =
  * [st_in (width-1 frames, ZERO if pos0 == 0) | x], y[t][d] =
  * f16_sat(silu(sum_j w[d][j] E[t+j])), st_out = last width-1 frames of E.
- * w [dim][width] f16, states [dim][width-1] f16; st_in != st_out.
+ * w [dim][width] f16, states [dim][width-1] f16; st_in != st_out; y must not
+ * overlap x; 1 <= width <= 8. 16-byte loads and stores when dim and
+ * row_stride are multiples of 8 and every buffer is 16-byte aligned.
  * Replaces kernels.cu:1634-1679, runtime.py:3035-3038. */
 int fl_conv1d_causal(const void* x, const void* w, const void* st_in, void* y, void* st_out,
                      int dim, int T, int pos0, int row_stride, int width, fl_stream_t stream);
@@ -264,7 +266,8 @@ int fl_gdn_scalars(const float* a, const float* b, const float* A_log, const flo
  * v-head hv reads q/k head hv / group. Ck (nullable): the state after every
  * token but the last at Ck + t*ck_step floats.
  * Replaces kernels.cu:2831-2914 gdn_scan_rows (runtime.py:3094-3100) and
- * kernels.cu:1794-1901 gdn_scan (runtime.py:3102-3108). K == 128, V % 32 == 0. */
+ * kernels.cu:1794-1901 gdn_scan (runtime.py:3102-3108). K == 128, V % 8 == 0,
+ * q and k 8-byte aligned with qk_stride % 4 == 0. */
 int fl_gdn_scan(const void* q, const void* k, const void* v, const float* beta,
                 const float* decay, float* S, void* y, int T, int n_kheads, int n_vheads,
                 int K, int V, int qk_stride, int v_stride, int y_stride, float out_scale,

@@ -35,34 +35,113 @@ def ulp16_diff(a, b):
     return int(np.abs(ai - bi).max())
 
 
-@pytest.mark.parametrize("T,pos0", [(1, 0), (1, 9), (5, 0), (8, 3), (64, 100)])
+def _conv_case(fl, dev, orc, rng, *, T, pos0, dim=ROW, stride=None, width=4):
+    """One conv call on the GPU and in the oracle: (y, st_out) of each."""
+    stride = dim if stride is None else stride
+    x = rng.standard_normal((T, stride)).astype(np.float16)
+    w = (rng.standard_normal((dim, width)) * 0.5).astype(np.float16)
+    # width 1 keeps no history: one-element placeholders stand in for the state
+    st = rng.standard_normal((dim, width - 1) if width > 1 else (8,)).astype(np.float16)
+    y = torch.zeros((T, stride), dtype=torch.float16, device=dev)
+    so = torch.empty(st.shape, dtype=torch.float16, device=dev)
+    fl.ops.conv1d_causal(to_dev(x, dev), to_dev(w, dev), to_dev(st, dev), y, so, dim=dim, T=T,
+                         pos0=pos0, row_stride=stride, width=width)
+    torch.cuda.synchronize()
+    y_r, so_r = orc.conv1d_causal(x, w, st, dim=dim, T=T, pos0=pos0, row_stride=stride,
+                                  width=width)
+    if width == 1:
+        so, so_r = np.zeros(0, np.float16), np.zeros(0, np.float16)
+    else:
+        so = so.cpu().numpy()
+    return y.cpu().numpy()[:, :dim], so, y_r[:, :dim], so_r
+
+
+# token counts around the 16-token block a lane walks: 1, 2 (shorter than the
+# 3 frames of history: the new state mixes old frames and new ones), a block
+# and one past it, many blocks with a ragged last one
+@pytest.mark.parametrize("T,pos0", [(1, 0), (1, 9), (2, 5), (5, 0), (8, 3), (16, 1), (17, 2),
+                                    (64, 100), (333, 7)])
 def test_conv1d_vs_oracle(fl, dev, orc, rng, T, pos0):
+    y, so, y_r, so_r = _conv_case(fl, dev, orc, rng, T=T, pos0=pos0)
+    assert np.array_equal(so, so_r)
+    assert ulp16_diff(y, y_r) <= 1
+
+
+# both lane layouts (8 channels a lane with 16-byte rows; a channel a lane for
+# an odd row stride / channel count) and every supported width
+@pytest.mark.parametrize("width", [1, 2, 3, 5, 8])
+@pytest.mark.parametrize("layout", ["vec", "lane"])
+@pytest.mark.parametrize("T,pos0", [(2, 3), (21, 0)])
+def test_conv1d_widths_and_layouts(fl, dev, orc, rng, width, layout, T, pos0):
+    dim, stride = (1024, 1032) if layout == "vec" else (1001, 1003)
+    y, so, y_r, so_r = _conv_case(fl, dev, orc, rng, T=T, pos0=pos0, dim=dim, stride=stride,
+                                  width=width)
+    assert np.array_equal(so, so_r)
+    assert ulp16_diff(y, y_r) <= 1
+
+
+def test_conv1d_segment_view_and_chunk_invariance(fl, dev, orc, rng):
+    """The v segment of a q|k|v row (a view 4096 channels in, row stride
+    10240), and the reference's chunk invariance (kernels.cu:135-138): 7
+    tokens then 13 from the state the first call left equal the 20-token call,
+    y and the state bit for bit."""
+    T = 20
     x = rng.standard_normal((T, ROW)).astype(np.float16)
-    w = (rng.standard_normal((ROW, 4)) * 0.5).astype(np.float16)
-    st = rng.standard_normal((ROW, 3)).astype(np.float16)
-    y = torch.empty((T, ROW), dtype=torch.float16, device=dev)
-    so = torch.empty((ROW, 3), dtype=torch.float16, device=dev)
-    fl.ops.conv1d_causal(to_dev(x, dev), to_dev(w, dev), to_dev(st, dev), y, so, T=T, pos0=pos0)
+    w = (rng.standard_normal((6144, 4)) * 0.5).astype(np.float16)
+    st = rng.standard_normal((6144, 3)).astype(np.float16)
+    xd, wd, sd = to_dev(x, dev), to_dev(w, dev), to_dev(st, dev)
+    y = torch.zeros((T, ROW), dtype=torch.float16, device=dev)
+    so = torch.empty((6144, 3), dtype=torch.float16, device=dev)
+    fl.ops.conv1d_causal(xd[:, 4096:], wd, sd, y[:, 4096:], so, dim=6144, T=T, pos0=5)
+    y2 = torch.zeros_like(y)
+    mid = torch.empty_like(so)
+    so2 = torch.empty_like(so)
+    fl.ops.conv1d_causal(xd[:7, 4096:], wd, sd, y2[:7, 4096:], mid, dim=6144, T=7, pos0=5)
+    fl.ops.conv1d_causal(xd[7:, 4096:], wd, mid, y2[7:, 4096:], so2, dim=6144, T=13, pos0=12)
     torch.cuda.synchronize()
-    y_r, so_r = orc.conv1d_causal(x, w, st, dim=ROW, T=T, pos0=pos0, row_stride=ROW)
+    assert torch.equal(y, y2) and torch.equal(so, so2)
+    assert (y[:, :4096] == 0).all(), "wrote outside the segment"
+    y_r, so_r = orc.conv1d_causal(x[:, 4096:].copy(), w, st, dim=6144, T=T, pos0=5,
+                                  row_stride=6144)
     assert np.array_equal(so.cpu().numpy(), so_r)
-    assert ulp16_diff(y.cpu().numpy(), y_r) <= 1
+    assert ulp16_diff(y.cpu().numpy()[:, 4096:], y_r) <= 1
 
 
-@pytest.mark.parametrize("T", [1, 2, 3])
-def test_conv_rows_vs_oracle(fl, dev, orc, rng, T):
-    x = rng.standard_normal((T, ROW)).astype(np.float16)
-    w = (rng.standard_normal((ROW, 4)) * 0.5).astype(np.float16)
-    st = rng.standard_normal((ROW, 3)).astype(np.float16)
-    y = torch.empty((T, ROW), dtype=torch.float16, device=dev)
-    sts = [torch.empty((ROW, 3), dtype=torch.float16, device=dev) for _ in range(3)]
+@pytest.mark.parametrize("T,pos0,layout", [(1, 4, "vec"), (2, 4, "vec"), (3, 4, "vec"),
+                                           (3, 0, "vec"), (3, 4, "lane")])
+def test_conv_rows_vs_oracle(fl, dev, orc, rng, T, pos0, layout):
+    dim, stride = (ROW, ROW) if layout == "vec" else (1001, 1003)
+    x = rng.standard_normal((T, stride)).astype(np.float16)
+    w = (rng.standard_normal((dim, 4)) * 0.5).astype(np.float16)
+    st = rng.standard_normal((dim, 3)).astype(np.float16)
+    y = torch.zeros((T, stride), dtype=torch.float16, device=dev)
+    sts = [torch.empty((dim, 3), dtype=torch.float16, device=dev) for _ in range(3)]
     fl.ops.conv1d_causal_rows(to_dev(x, dev), to_dev(w, dev), to_dev(st, dev), y, *sts[:T], T=T,
-                              pos0=4)
+                              pos0=pos0, dim=dim, row_stride=stride)
     torch.cuda.synchronize()
-    y_r, sts_r = orc.conv1d_causal_rows(x, w, st, dim=ROW, T=T, pos0=4, row_stride=ROW)
-    assert ulp16_diff(y.cpu().numpy(), y_r) <= 1
+    y_r, sts_r = orc.conv1d_causal_rows(x, w, st, dim=dim, T=T, pos0=pos0, row_stride=stride)
+    assert ulp16_diff(y.cpu().numpy()[:, :dim], y_r[:, :dim]) <= 1
     for t in range(T):
         assert np.array_equal(sts[t].cpu().numpy(), sts_r[t])
+
+
+def test_conv_rows_state_in_place(fl, dev, orc, rng):
+    """Row 0's state may be written over st_in (kernels.cu:1681-1685): every
+    lane reads its channels' frames before it writes them."""
+    T = 3
+    x = rng.standard_normal((T, ROW)).astype(np.float16)
+    w = (rng.standard_normal((ROW, 4)) * 0.5).astype(np.float16)
+    st = rng.standard_normal((ROW, 3)).astype(np.float16)
+    y = torch.empty((T, ROW), dtype=torch.float16, device=dev)
+    s0 = to_dev(st, dev)
+    s1 = torch.empty_like(s0)
+    s2 = torch.empty_like(s0)
+    fl.ops.conv1d_causal_rows(to_dev(x, dev), to_dev(w, dev), s0, y, s0, s1, s2, T=T, pos0=9)
+    torch.cuda.synchronize()
+    y_r, sts_r = orc.conv1d_causal_rows(x, w, st, dim=ROW, T=T, pos0=9, row_stride=ROW)
+    assert ulp16_diff(y.cpu().numpy(), y_r) <= 1
+    for got, want in zip((s0, s1, s2), sts_r):
+        assert np.array_equal(got.cpu().numpy(), want)
 
 
 def test_l2norm_and_gates_vs_oracle(fl, dev, orc, rng):
@@ -102,7 +181,7 @@ def _scan_inputs(rng, T):
     return ln, beta, decay, S0
 
 
-@pytest.mark.parametrize("T", [1, 3, 40])
+@pytest.mark.parametrize("T", [1, 3, 40, 101])
 def test_gdn_scan_vs_oracle(fl, dev, orc, rng, T):
     ln, beta, decay, S0 = _scan_inputs(rng, T)
     lnd = to_dev(ln, dev)
