@@ -64,6 +64,8 @@ def graph_of(torch, fn, n):
 
 
 def time_graph(torch, g, reps=1):
+    """Mean ms of one replay of g over `reps` back-to-back replays, timed with
+    HIP events on torch's current stream (the stream the replays run on)."""
     st, en = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     st.record()
@@ -72,6 +74,27 @@ def time_graph(torch, g, reps=1):
     en.record()
     torch.cuda.synchronize()
     return st.elapsed_time(en) / reps          # ms
+
+
+def measure(torch, g, calls, samples, min_ms=2.0):
+    """Per-call time of a graph holding `calls` launches: `samples` timed
+    regions, each R back-to-back replays with R chosen so a region lasts at
+    least min_ms (graph-launch latency amortised over many launches). Returns
+    the median per-call µs and the spread over the regions."""
+    time_graph(torch, g)                       # warm (code objects, caches)
+    est = time_graph(torch, g)
+    reps = max(1, int(-(-min_ms // max(est, 1e-3))))
+    vals = sorted(time_graph(torch, g, reps) * 1e3 / calls for _ in range(samples))
+    mid = len(vals) // 2
+    med = vals[mid] if len(vals) % 2 else 0.5 * (vals[mid - 1] + vals[mid])
+    return {"us": med, "us_min": vals[0], "us_max": vals[-1], "regions": samples,
+            "replays_per_region": reps, "calls_per_replay": calls}
+
+
+# BASELINE.md's measurement rule: the median of >= 50 timed iterations for
+# decode-shaped work and >= 10 for prefill-shaped work
+DECODE_SAMPLES = 50
+PREFILL_SAMPLES = 10
 
 
 # ---------------------------------------------------------------------------
@@ -129,15 +152,20 @@ def bench_gdn_decode(torch, fl, steps, warmup):
         "graph replay differs from eager launches"
     del S0, r0, g2
 
+    # the timed graph holds whole rotations over the 48 layer states (so every
+    # replay streams all 604 MB, past the MALL), at least `steps` launches
+    n_graph = L * max(1, -(-steps // L))
     gw = graph_of(torch, step, warmup) if warmup else None
-    gt = graph_of(torch, lambda i: step(warmup + i), steps)
+    gt = graph_of(torch, lambda i: step(warmup + i), n_graph)
     if gw is not None:
-        time_graph(torch, gw)
-    ms = time_graph(torch, gt)
-    us = ms * 1e3 / steps
+        gw.replay()
+        torch.cuda.synchronize()
+    m = measure(torch, gt, n_graph, DECODE_SAMPLES)
+    us = m["us"]
     nbytes = gdn_decode_bytes()
     return {"us_per_step": us, "bytes": nbytes, "gbs": nbytes / (us * 1e-6) / 1e9,
-            "steps": steps, "ms": ms}
+            "steps": steps, "timing": {k: (round(v, 3) if isinstance(v, float) else v)
+                                       for k, v in m.items()}}
 
 
 # ---------------------------------------------------------------------------
@@ -152,7 +180,10 @@ def bench_attn_decode(torch, fl, Lmax, Bq=4, T=3, iters=20, seed=0, kv8=False, p
     import numpy as np
 
     rng = np.random.default_rng(seed + Lmax)
-    lens = [int(v) for v in rng.integers(int(np.ceil(0.9 * Lmax)), Lmax + 1, size=Bq)]
+    if Bq == 1:     # config 0: one sequence at exactly the stated context
+        lens = [Lmax]
+    else:           # config 2: lengths seeded-uniform in [0.9 L, L], so sequences differ
+        lens = [int(v) for v in rng.integers(int(np.ceil(0.9 * Lmax)), Lmax + 1, size=Bq)]
     g = torch.Generator(device=dev).manual_seed(seed)
     row = 4 * (256 + 16) if kv8 else 4 * 256 * 2          # bytes a position, K or V
     kv_bytes = sum(lens) * row * 2
@@ -192,13 +223,13 @@ def bench_attn_decode(torch, fl, Lmax, Bq=4, T=3, iters=20, seed=0, kv8=False, p
             fl.ops.attn_decode(qg, ks, vs, pos0, z=z, work=work)
 
     gr = graph_of(torch, call, iters)
-    time_graph(torch, gr)
-    ms = time_graph(torch, gr, reps=3)
-    us = ms * 1e3 / iters
+    m = measure(torch, gr, iters, DECODE_SAMPLES)
+    us = m["us"]
     nbytes = kv_bytes + Bq * T * 24 * 512 * 2 + Bq * T * 24 * 256 * 2
     flops = sum(4 * T * 24 * 256 * L for L in lens)
     name = ("decode8_perseq" if per_seq else "decode8_verify" if kv8 else "decode_verify")
     return {"config": f"{name}_B{Bq}_T{T}_L{Lmax}", "us_per_step": round(us, 2),
+            "us_min": round(m["us_min"], 2), "us_max": round(m["us_max"], 2),
             "GBs": round(nbytes / (us * 1e-6) / 1e9, 1),
             "hbm_frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 3),
             "TFLOPs": round(flops / (us * 1e-6) / 1e12, 1), "lens": lens}
@@ -208,7 +239,7 @@ def bench_attn_decode(torch, fl, Lmax, Bq=4, T=3, iters=20, seed=0, kv8=False, p
 # config 3: causal prefill attention
 # ---------------------------------------------------------------------------
 
-def bench_prefill(torch, fl, L, iters=3, kv8=False):
+def bench_prefill(torch, fl, L, iters=1, kv8=False):
     """kv8: over an int8 cache (kv_store_q8 fused in front, as for fp16)."""
     dev = torch.device("cuda:0")
     g = torch.Generator(device=dev).manual_seed(L)
@@ -230,12 +261,12 @@ def bench_prefill(torch, fl, L, iters=3, kv8=False):
             fl.ops.attention_prefill(q, kc, vc, pos0=0, scale=1.0, z=z, k_new=k, v_new=v)
 
     gr = graph_of(torch, call, iters)
-    time_graph(torch, gr)
-    ms = time_graph(torch, gr)
-    us = ms * 1e3 / iters
+    m = measure(torch, gr, iters, PREFILL_SAMPLES)
+    us = m["us"]
     flops = 4 * 24 * 256 * L * (L + 1) / 2
     tf = flops / (us * 1e-6) / 1e12
     return {"config": f"prefill{'8' if kv8 else ''}_L{L}", "us": round(us, 1),
+            "us_min": round(m["us_min"], 1), "us_max": round(m["us_max"], 1),
             "tok_s": round(L / (us * 1e-6)),
             "TFLOPs": round(tf, 1), "mfma_frac": round(tf / MFMA_F16_PEAK_TFLOPS, 3)}
 
@@ -274,9 +305,7 @@ def bench_attn_prep(torch, fl, T, iters=50):
         fl.ops.attn_prep(qg, k, v, wq, wk, kc, vc, pos0=4096 - (i % 7))
 
     gr = graph_of(torch, call, iters)
-    time_graph(torch, gr)
-    ms = time_graph(torch, gr, reps=3)
-    us = ms * 1e3 / iters
+    us = measure(torch, gr, iters, DECODE_SAMPLES)["us"]
     nbytes = attn_prep_bytes(T)
     return {"config": f"attn_prep_T{T}", "us": round(us, 2),
             "GBs": round(nbytes / (us * 1e-6) / 1e9, 1),
@@ -300,15 +329,13 @@ def bench_gdn_out_norm(torch, fl, T, iters=50):
         fl.ops.rmsnorm_gated(o, z, w, y)
 
     gr = graph_of(torch, call, iters)
-    time_graph(torch, gr)
-    ms = time_graph(torch, gr, reps=3)
-    us = ms * 1e3 / iters
+    us = measure(torch, gr, iters, DECODE_SAMPLES)["us"]
     return {"config": f"gdn_out_norm_T{T}", "us": round(us, 2),
             "GBs": round(nbytes / (us * 1e-6) / 1e9, 1),
             "hbm_frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 3)}
 
 
-def bench_gdn_verify(torch, fl, T=3, steps=256, warmup=16):
+def bench_gdn_verify(torch, fl, T=3, steps=96, warmup=16):
     """The GDN step of an MTP verify (runtime.py:3040-3053, gdn_scan_rows_f):
     B = 4 sequences, T = 3 conv'd rows each, the state updated over the three
     tokens with the checkpoints after the first two; 48 layer states rotated
@@ -335,9 +362,8 @@ def bench_gdn_verify(torch, fl, T=3, steps=256, warmup=16):
 
     gw = graph_of(torch, step, warmup)
     gt = graph_of(torch, lambda i: step(warmup + i), steps)
-    time_graph(torch, gw)
-    ms = time_graph(torch, gt)
-    us = ms * 1e3 / steps
+    gw.replay()
+    us = measure(torch, gt, steps, DECODE_SAMPLES)["us"]
     nbytes = B * (2 * state + (T - 1) * state + T * row * 2 + 2 * T * nv * 4 + T * nv * 128 * 2) \
         + 2 * nv * 4
     return {"config": f"gdn_verify_B{B}_T{T}", "us_per_step": round(us, 2),
@@ -349,7 +375,7 @@ def bench_gdn_verify(torch, fl, T=3, steps=256, warmup=16):
 # config 4: chunked GDN prefill
 # ---------------------------------------------------------------------------
 
-def bench_chunked(torch, fl, L=8192, iters=3):
+def bench_chunked(torch, fl, L=8192, iters=1):
     dev = torch.device("cuda:0")
     g = torch.Generator(device=dev).manual_seed(4)
     c = torch.randn((L, 10240), generator=g, device=dev)
@@ -368,9 +394,8 @@ def bench_chunked(torch, fl, L=8192, iters=3):
                                    T=L, work=work)
 
     gr = graph_of(torch, call, iters)
-    time_graph(torch, gr)
-    ms = time_graph(torch, gr)
-    us = ms * 1e3 / iters
+    m = measure(torch, gr, iters, PREFILL_SAMPLES)
+    us = m["us"]
     nbytes = L * 16 * 128 * 2 * 2 + L * 48 * 128 * 2 * 2 + L * 48 * 4 * 2 + 2 * 48 * 128 * 128 * 4
     n_chunks = -(-L // 64)
     flops = n_chunks * 48 * (10 * 64 * 64 * 128 + 6 * 64 * 128 * 128)
@@ -385,12 +410,46 @@ def bench_chunked(torch, fl, L=8192, iters=3):
 # CPU baseline: PyTorch fp32 on the host's cores
 # ---------------------------------------------------------------------------
 
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_threads() -> int:
+    """All of the host's cores, capped by OMP_NUM_THREADS where the job
+    environment sets one (the GPU box's CPU share)."""
+    n = os.cpu_count() or 1
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    return min(n, int(env)) if env.isdigit() and int(env) > 0 else n
+
+
+def _cpu_runs(fn, runs=3, budget_s=6.0):
+    """Median seconds of `runs` calls after one warm-up (fewer if the budget
+    is spent; at least one)."""
+    fn()
+    ts, t_end = [], time.perf_counter() + budget_s
+    while len(ts) < runs and (not ts or time.perf_counter() < t_end):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    ts.sort()
+    return ts[len(ts) // 2], len(ts)
+
+
 def cpu_baseline(budget_s=12.0):
+    """configs[1] (the primary): the fused GDN decode step of B = 4 sequences
+    in PyTorch fp32 on the host's cores, over a bounded number of steps."""
     import torch
 
     from oracle import torch_ref as tr
 
-    threads = tr.set_threads()
+    threads = tr.set_threads(cpu_threads())
     gen = torch.Generator().manual_seed(7)
     row, nv = 10240, 48
     x = torch.randn((B, row), generator=gen).half()
@@ -408,9 +467,72 @@ def cpu_baseline(budget_s=12.0):
         n += 1
     dt_s = (time.perf_counter() - t0) / n
     return {"value": round(dt_s * 1e6, 1), "unit": "us/step", "cores": threads, "kind": "port",
+            "cpu_model": cpu_model(), "os_cpu_count": os.cpu_count(),
             "gbs": round(gdn_decode_bytes() / dt_s / 1e9, 2),
             "sample": f"{n} fused GDN decode steps (B=4, one layer's state), oracle/torch_ref.py "
-                      f"fp32 on {os.cpu_count()} host cpus"}
+                      f"fp32, torch threads {threads}"}
+
+
+def cpu_extra():
+    """The other configs' PyTorch fp32 CPU timings (oracle/torch_ref.py), each
+    the median of 3 runs after a warm-up on the same shapes the GPU lines use:
+    config 0 exactly (B=1, T=1, L=4096), config 2 at 8k (B=4, T=3), config 3
+    at 2k and config 4 (8192 tokens)."""
+    import numpy as np
+    import torch
+
+    from oracle import torch_ref as tr
+
+    threads = tr.set_threads(cpu_threads())
+    gen = torch.Generator().manual_seed(11)
+    out = []
+
+    def line(config, sec, runs, **kw):
+        r = {"config": config, "cores": threads, "runs": runs, **kw}
+        log(f"bench: cpu {r}")
+        out.append(r)
+
+    # config 0 / config 2: decode + verify attention with the sigmoid gate
+    for Lmax, Bq, T in ((4096, 1, 1), (8192, 4, 3)):
+        if Bq == 1:
+            lens = [Lmax]
+        else:
+            rng = np.random.default_rng(Lmax)
+            lens = [int(v) for v in rng.integers(int(np.ceil(0.9 * Lmax)), Lmax + 1, size=Bq)]
+        caches = [(torch.randn((L, 4, 256), generator=gen).half(),
+                   torch.randn((L, 4, 256), generator=gen).half()) for L in lens]
+        qg = torch.randn((Bq, T, 24, 512), generator=gen).half()
+        qg[..., :256] *= 1 / 16
+
+        def dec():
+            for b, (kc, vc) in enumerate(caches):
+                tr.attention_decode(qg[b], kc, vc, lens[b] - T, scale=1 / 16)
+
+        sec, runs = _cpu_runs(dec)
+        nbytes = sum(lens) * 4 * 256 * 2 * 2 + Bq * T * 24 * 768 * 2
+        line(f"decode_verify_B{Bq}_T{T}_L{Lmax}", sec, runs, us_per_step=round(sec * 1e6, 1),
+             GBs=round(nbytes / sec / 1e9, 2), lens=lens)
+
+    # config 3 at 2k: causal prefill, q pre-scaled, scale 1
+    L = 2048
+    q = (torch.randn((L, 24, 256), generator=gen) / 16).half()
+    kc = torch.randn((L, 4, 256), generator=gen).half()
+    vc = torch.randn((L, 4, 256), generator=gen).half()
+    sec, runs = _cpu_runs(lambda: tr.attention_prefill(q, kc, vc, 0, scale=1.0))
+    line(f"prefill_L{L}", sec, runs, us=round(sec * 1e6, 1), tok_s=round(L / sec),
+         GFLOPs=round(12288 * L * (L + 1) / sec / 1e9, 1))
+
+    # config 4: the chunked WY scan over 8192 tokens
+    L = 8192
+    qk = torch.nn.functional.normalize(torch.randn((L, 2, 16, 128), generator=gen), dim=-1).half()
+    v = torch.randn((L, 48, 128), generator=gen).half()
+    beta = torch.sigmoid(torch.randn((L, 48), generator=gen))
+    decay = torch.exp(-torch.nn.functional.softplus(torch.randn((L, 48), generator=gen)))
+    S0 = torch.randn((48, 128, 128), generator=gen) * 0.02
+    sec, runs = _cpu_runs(lambda: tr.gdn_chunked(qk[:, 0], qk[:, 1], v, beta, decay, S0.clone()),
+                          budget_s=20.0)
+    line(f"gdn_chunked_L{L}", sec, runs, us=round(sec * 1e6, 1), tok_s=round(L / sec))
+    return out
 
 
 # ---------------------------------------------------------------------------
@@ -550,6 +672,7 @@ def main():
     cpu = None if args.no_cpu else cpu_baseline()
     if cpu:
         log(f"bench: cpu baseline {cpu}")
+    cpu_more = [] if (args.no_cpu or args.quick) else cpu_extra()
 
     gbs = prim["gbs"]
     line = {
@@ -574,6 +697,8 @@ def main():
                      "traffic": GDN_DECODE_TRAFFIC_BYTES,
                      "bytes_per_launch": prim["bytes"]},
         "cpu_baseline": cpu,
+        "cpu_extra": cpu_more,
+        "timing": prim["timing"],
         "extra": extra,
     }
     print(json.dumps(line), flush=True)
