@@ -46,6 +46,8 @@
 //     position (the reference asserts this, runtime.py:2062-2069).
 #include "fl_common.hpp"
 
+#include <mutex>
+
 #include <limits.h>
 #include <type_traits>
 
@@ -669,6 +671,48 @@ int attn_decode_batched(const void* qg, int q_pitch, const void* const* kcache,
 
 }  // namespace
 
+// ---------------------------------------------------------------------------
+// Partials of fl_attn_decode_noalloc: one array a GPU (every device that
+// loads the library holds its own copy until the process ends), shared by
+// every call of that entry point on the device. The split kernel writes every
+// partial slot the merge reads (empty splits included), so nothing here has
+// to start at zero; two calls that overlap on one GPU race on it.
+// ---------------------------------------------------------------------------
+constexpr size_t DEC_SCRATCH_BYTES = (size_t)32 << 20;
+static __device__ __align__(256) unsigned char scratch[DEC_SCRATCH_BYTES];
+
+namespace {
+constexpr int DEC_SCRATCH_DEVICES = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[DEC_SCRATCH_DEVICES];   // `scratch`'s address on each device
+
+// The device address of `scratch` on the current device, looked up once per
+// device (with that device current) and kept: the array's name is a host-side
+// stand-in, never a device address.
+int scratch_on_current_device(void** out) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) {
+        fl::set_error("hipGetDevice: %s", hipGetErrorString(e));
+        return FL_ELAUNCH;
+    }
+    FL_REQUIRE(dev >= 0 && dev < DEC_SCRATCH_DEVICES, "device index < 64");
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch_ptr[dev] == nullptr) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || p == nullptr) {
+            fl::set_error("hipGetSymbolAddress(scratch) on device %d: %s", dev,
+                          hipGetErrorString(e));
+            return FL_ELAUNCH;
+        }
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return FL_OK;
+}
+}  // namespace
+
 extern "C" {
 
 int fl_kv_store(const void* k, const void* v, void* kcache, void* vcache, int layer, int pos0,
@@ -824,6 +868,28 @@ int fl_attn_decode(const void* qg, int q_pitch, const void* const* kcache,
                                       n_kv_heads, head_dim, scale, split_rows, split, gate,
                                       g_pitch, g_off, z, z_pitch, work, work_bytes, stream);
 }
+
+int fl_attn_decode_noalloc(const void* qg, int q_pitch, const void* const* kcache,
+                           const void* const* vcache, const int* pos0, const int* cap, int B,
+                           int T, int n_q_heads, int n_kv_heads, int head_dim, float scale,
+                           int split_rows, int split, const void* gate, int g_pitch, int g_off,
+                           void* z, int z_pitch, fl_stream_t stream) {
+    const size_t need = fl_attn_decode_work_bytes(B, T, n_q_heads, head_dim, split);
+    if (need > DEC_SCRATCH_BYTES) {
+        fl::set_error("fl_attn_decode_noalloc: B %d x T %d x %d heads x %d splits need %zu bytes of "
+                      "partials; the static scratch holds %zu (use fl_attn_decode with a work "
+                      "buffer)", B, T, n_q_heads, split, need, DEC_SCRATCH_BYTES);
+        return FL_ESCRATCH;
+    }
+    void* ptr = nullptr;
+    const int rc = scratch_on_current_device(&ptr);
+    if (rc) return rc;
+    return attn_decode_batched<false>(qg, q_pitch, kcache, vcache, pos0, cap, B, T, n_q_heads,
+                                      n_kv_heads, head_dim, scale, split_rows, split, gate,
+                                      g_pitch, g_off, z, z_pitch, ptr, DEC_SCRATCH_BYTES, stream);
+}
+
+size_t fl_attn_decode_noalloc_max_bytes(void) { return DEC_SCRATCH_BYTES; }
 
 int fl_attn_decode_q8(const void* qg, int q_pitch, const void* const* kcache,
                       const void* const* vcache, const int* pos0, const int* cap, int B, int T,

@@ -199,6 +199,32 @@ def attn_decode(qg, kcaches, vcaches, pos0s, *, z=None, gate: bool = True,
     return z
 
 
+def attn_decode_noalloc(qg, kcaches, vcaches, pos0s, z, *, gate: bool = True,
+                        n_kv_heads: int = N_KV, scale: float = ATTN_SCALE,
+                        split_rows: int = SPLIT_ROWS, split: int = SPLIT_MAX):
+    """attn_decode without a work buffer (fl_attn_decode_noalloc): the partials
+    live in the library's static per-GPU array, so nothing is allocated; z
+    [B, T, n_q_heads, head_dim] fp16 must be given. Calls that overlap on one
+    GPU race on that array."""
+    B, T, n_q_heads, q_pitch = qg.shape
+    head_dim = kcaches[0].shape[-1]
+    _contig(qg, "qg")
+    if len(kcaches) != B or len(vcaches) != B or len(pos0s) != B:
+        raise ValueError("one cache pair and one pos0 per sequence")
+    for b in range(B):
+        for name, c in (("kcache", kcaches[b]), ("vcache", vcaches[b])):
+            _contig(c, name)
+            _ptr(c, F16, name, c.shape[-3] * n_kv_heads * head_dim)
+    _lib.call("fl_attn_decode_noalloc", _ptr(qg, F16, "qg", B * T * n_q_heads * q_pitch), q_pitch,
+              _lib.ptr_array([c.data_ptr() for c in kcaches]),
+              _lib.ptr_array([c.data_ptr() for c in vcaches]), _lib.int_array(pos0s),
+              _lib.int_array([c.shape[-3] for c in kcaches]), B, T, n_q_heads, n_kv_heads,
+              head_dim, float(scale), split_rows, split, qg.data_ptr() if gate else None, q_pitch,
+              GATE_OFF if gate else 0, _ptr(z, F16, "z", B * T * n_q_heads * head_dim),
+              z.shape[-1], _stream())
+    return z
+
+
 def attention_prefill(q, kcache, vcache, *, pos0: int, T: int | None = None, z=None,
                       k_new=None, v_new=None, layer: int = 0, n_q_heads: int = N_HEADS,
                       n_kv_heads: int = N_KV, q_pitch: int | None = None,

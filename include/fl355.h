@@ -217,6 +217,22 @@ int fl_attn_decode_q8(const void* qg, int q_pitch, const void* const* kcache,
                       int split, const void* gate, int g_pitch, int g_off, void* z, int z_pitch,
                       void* work, size_t work_bytes, fl_stream_t stream);
 
+/* fl_attn_decode without a work buffer: the partials live in a static device
+ * array of fl_attn_decode_noalloc_max_bytes() (32 MiB) bytes per GPU, so the
+ * call allocates nothing (no hipMalloc / hipFree, no allocating library
+ * routine). No counterpart in the reference: it is for callers that cannot
+ * allocate -- code under HIP graph capture, tight serving loops, harnesses that
+ * forbid allocation. Refuses (FL_ESCRATCH) a call whose
+ * fl_attn_decode_work_bytes(B, T, n_q_heads, head_dim, split) exceeds the
+ * array; B = 4, T = 3, 24 heads, 64 splits take 19 MB. Every call on one GPU
+ * shares that GPU's array: calls that overlap on one GPU race. */
+int fl_attn_decode_noalloc(const void* qg, int q_pitch, const void* const* kcache,
+                           const void* const* vcache, const int* pos0, const int* cap, int B,
+                           int T, int n_q_heads, int n_kv_heads, int head_dim, float scale,
+                           int split_rows, int split, const void* gate, int g_pitch, int g_off,
+                           void* z, int z_pitch, fl_stream_t stream);
+size_t fl_attn_decode_noalloc_max_bytes(void);
+
 /* fl_attention_prefill over an int8 cache (k_new / v_new, when given, are
  * stored first with kv_store_q8). Replaces kernels.cu:2778-2786
  * attention_prefill_fh_q8 (+ merge_fh), launched by runtime.py:2943-2959. */

@@ -91,3 +91,20 @@ def test_op_layer_refuses_cpu_tensors(fl):
     with pytest.raises(ValueError):
         fl.ops.kv_store(k, k, torch.zeros((8, 4, 256), dtype=torch.float16),
                         torch.zeros((8, 4, 256), dtype=torch.float16), pos0=0)
+
+
+def test_noalloc_decode_refuses_beyond_its_static_scratch(fl):
+    """fl_attn_decode_noalloc checks the partials' size against its static
+    array before anything touches the device."""
+    lib = fl._lib.lib()
+    assert lib.fl_attn_decode_noalloc_max_bytes() == 32 << 20
+    need = lib.fl_attn_decode_work_bytes(16, 5, 24, 256, 64)
+    assert need > lib.fl_attn_decode_noalloc_max_bytes()
+    fake = ctypes.c_void_p(0x1000)
+    arr = fl._lib.ptr_array([0x1000] * 16)
+    ints = fl._lib.int_array([100] * 16)
+    rc = _call(fl, "fl_attn_decode_noalloc", fake, 512, arr, arr, ints, ints, 16, 5, 24, 4, 256,
+               0.0625, 256, 64, None, 512, 256, fake, 256, None)
+    assert rc == 3                                  # FL_ESCRATCH
+    assert b"static scratch" in lib.fl_last_error()
+
