@@ -271,6 +271,40 @@ def bench_prefill(torch, fl, L, iters=1, kv8=False):
             "TFLOPs": round(tf, 1), "mfma_frac": round(tf / MFMA_F16_PEAK_TFLOPS, 3)}
 
 
+def bench_prefill_chunk(torch, fl, T=1024, pos0=98000, split=None, iters=4):
+    """The reference's own prefill shape (runtime.py:196, 1939-1966): a
+    1024-token chunk of a long prompt at pos0, its k / v stored by the fused
+    kv_store, the KV range split per fl_attention_prefill_split_count (split=1:
+    one pass)."""
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(T + pos0)
+    L = pos0 + T
+    q = (torch.randn((T, 24, 256), generator=g, device=dev) / 16).half()
+    kc = torch.randn((L, 4, 256), generator=g, device=dev).half()
+    vc = torch.randn((L, 4, 256), generator=g, device=dev).half()
+    k = kc[pos0:].clone()
+    v = vc[pos0:].clone()
+    z = torch.empty((T, 24, 256), dtype=torch.float16, device=dev)
+    S = fl.ops.prefill_split_count(T, pos0) if split is None else split
+    work = None
+    if S > 1:
+        work = torch.empty(fl._lib.lib().fl_attention_prefill_work_bytes(T, 24, 256, S),
+                           dtype=torch.uint8, device=dev)
+
+    def call(i):
+        fl.ops.attention_prefill(q, kc, vc, pos0=pos0, scale=1.0, z=z, k_new=k, v_new=v, split=S,
+                                 work=work)
+
+    gr = graph_of(torch, call, iters)
+    m = measure(torch, gr, iters, PREFILL_SAMPLES)
+    us = m["us"]
+    flops = 4 * 24 * 256 * (T * pos0 + T * (T + 1) / 2)
+    tf = flops / (us * 1e-6) / 1e12
+    return {"config": f"prefill_T{T}_pos{pos0 // 1000}k" + ("" if split is None else f"_split{S}"),
+            "split": S, "us": round(us, 1), "tok_s": round(T / (us * 1e-6)),
+            "TFLOPs": round(tf, 1), "mfma_frac": round(tf / MFMA_F16_PEAK_TFLOPS, 3)}
+
+
 # ---------------------------------------------------------------------------
 # attention prep: q / k RMSNorm + partial RoPE + KV store (fused, one launch)
 # ---------------------------------------------------------------------------
@@ -599,6 +633,8 @@ EXTRA_CONFIGS = {
     "prefill_L2048": (bench_prefill, {"L": 2048}),
     "prefill_L8192": (bench_prefill, {"L": 8192}),
     "prefill_L32768": (bench_prefill, {"L": 32768}),
+    "prefill_T1024_pos98k": (bench_prefill_chunk, {}),
+    "prefill_T1024_pos98k_split1": (bench_prefill_chunk, {"split": 1}),
     "decode8_verify_B4_T3_L8192": (bench_attn_decode, {"Lmax": 8192, "kv8": True}),
     "decode8_verify_B4_T3_L32768": (bench_attn_decode, {"Lmax": 32768, "kv8": True}),
     "decode8_verify_B4_T3_L102400": (bench_attn_decode, {"Lmax": 102400, "kv8": True}),

@@ -44,6 +44,12 @@ SIGNATURES = {
     "fl_attn_decode_noalloc": (_I, [_P, _I, _PP, _PP, _IP, _IP, _I, _I, _I, _I, _I, _F, _I, _I,
                                     _P, _I, _I, _P, _I, _P]),
     "fl_attn_decode_noalloc_max_bytes": (_SZ, []),
+    "fl_attention_prefill_split_count": (_I, [_I, _I, _I, _I]),
+    "fl_attention_prefill_work_bytes": (_SZ, [_I, _I, _I, _I]),
+    "fl_attention_prefill_kv": (_I, [_P, _I, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _I, _I,
+                                     _P, _I, _P, _SZ, _P]),
+    "fl_attention_prefill_kv_q8": (_I, [_P, _I, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _I,
+                                        _I, _P, _I, _P, _SZ, _P]),
     "fl_kv_store_q8": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P]),
     "fl_attn_prep_q8": (_I, [_P, _I, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _F,
                              _F, _P]),

@@ -37,6 +37,8 @@
 // (byte * scale exact), here it is rounded to fp16 once.
 #include "fl_common.hpp"
 
+#include <mutex>
+
 namespace {
 
 constexpr int PF_WAVES = 4;
@@ -241,13 +243,28 @@ __device__ __forceinline__ f16x8 deq8(uint32_t a, uint32_t b, f16 s) {
     return (f16x8){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 }
 
+// The KV-split form's partials (attention_prefill_fh with gridDim.z > 1,
+// kernels.cu:2461-2486 / 2763): split s of a workgroup walks tiles
+// [n_tiles s / n, n_tiles (s + 1) / n) of its causal range and leaves, per
+// (token, q head), the unnormalised O in pacc [T][heads][n][256], the running
+// max in natural-log units in pm and the sum in pd ([T][heads][n]) -- the
+// decode partials' layout, so attn_merge_kernel combines them. A split with no
+// tile writes the empty partial (m = -1e30, d = 0, O = 0).
+struct PfSplit {
+    float* pacc;
+    float* pm;
+    float* pd;
+    int n;
+};
+
 // Q8: kc / vc are int8 values, ksc / vsc their scales (unused for fp16).
-template <bool Q8>
+// SPLIT: blockIdx.z is the KV split and the result goes to `sp`, not z.
+template <bool Q8, bool SPLIT>
 __global__ void __launch_bounds__(PF_THREADS)
 attn_prefill_kernel(const f16* __restrict__ q, int q_pitch, const void* __restrict__ kc,
                     const void* __restrict__ vc, const f16* __restrict__ ksc,
                     const f16* __restrict__ vsc, f16* __restrict__ z, int z_pitch, int n_q_heads,
-                    int n_kv, int pos0, int T, float sl2, int n_row_tiles) {
+                    int n_kv, int pos0, int T, float sl2, int n_row_tiles, PfSplit sp) {
     extern __shared__ __attribute__((aligned(16))) char smem[];
 
     int tile, h;
@@ -273,6 +290,26 @@ attn_prefill_kernel(const f16* __restrict__ q, int q_pitch, const void* __restri
     const int blast = min(R0 + PF_BQ - 1, RT - 1);
     const int kv_end = __builtin_amdgcn_readfirstlane(pos0 + blast / G + 1);   // rows seen here
     const int n_tiles = (kv_end + PF_BK - 1) / PF_BK;
+    // this workgroup's tiles [j_lo, j_hi): all of them, or split s's share
+    const int s_idx = SPLIT ? (int)blockIdx.z : 0;
+    // (uniform: the divisions are VALU code, and the copies need scalar bases)
+    const int j_lo = SPLIT ? __builtin_amdgcn_readfirstlane(n_tiles * s_idx / sp.n) : 0;
+    const int j_hi = SPLIT ? __builtin_amdgcn_readfirstlane(n_tiles * (s_idx + 1) / sp.n) : n_tiles;
+    if constexpr (SPLIT) {
+        if (j_lo == j_hi) {   // an empty split (uniform: the whole workgroup leaves here)
+            if (rvalid) {
+                const size_t part = ((size_t)t * n_q_heads + h * G + g) * sp.n + s_idx;
+                float* acc = sp.pacc + part * PF_HD + 4 * hh;
+#pragma unroll
+                for (int i = 0; i < 32; ++i) *(f32x4*)(acc + 8 * i) = (f32x4)(0.f);
+                if (hh == 0) {
+                    sp.pm[part] = -1e30f;
+                    sp.pd[part] = 0.f;
+                }
+            }
+            return;
+        }
+    }
 
     const uint32_t rsb = (uint32_t)n_kv * ROW_B;   // bytes between cache rows
     const char* kb = uniform_ptr((const char*)((const f16*)kc + (size_t)h * PF_HD));
@@ -318,9 +355,9 @@ attn_prefill_kernel(const f16* __restrict__ q, int q_pitch, const void* __restri
     };
 
     if constexpr (Q8)
-        q8_load(0);
+        q8_load(j_lo * PF_BK);
     else
-        issue_tile(lds_base, 0, kb, vb, rsb, 0, kv_end, w, lane, loff);
+        issue_tile(lds_base, 0, kb, vb, rsb, j_lo * PF_BK, kv_end, w, lane, loff);
 
     f16x8 qreg[16];   // Q[row][128 hh + 8 ks + 0..7]
     {
@@ -361,12 +398,12 @@ attn_prefill_kernel(const f16* __restrict__ q, int q_pitch, const void* __restri
 
     typedef __attribute__((address_space(3))) const f16x8 lds_f16x8;
     typedef __attribute__((address_space(3))) const char lds_char;
-    for (int j = 0; j < n_tiles; ++j) {
-        const int st = j & 1;
+    for (int j = j_lo; j < j_hi; ++j) {
+        const int st = (j - j_lo) & 1;
         if constexpr (Q8) {
-            if (j + 1 < n_tiles) q8_load((j + 1) * PF_BK);   // in registers during the math
+            if (j + 1 < j_hi) q8_load((j + 1) * PF_BK);   // in registers during the math
         } else {
-            if (j + 1 < n_tiles) {
+            if (j + 1 < j_hi) {
                 issue_tile(lds_base, st ^ 1, kb, vb, rsb, (j + 1) * PF_BK, kv_end, w, lane, loff);
                 WAIT_VMCNT(16);   // this tile's 16 copies done, the next tile's in flight
             } else {
@@ -450,12 +487,31 @@ attn_prefill_kernel(const f16* __restrict__ q, int q_pitch, const void* __restri
         }
         if constexpr (Q8) {
             // the other stage's last readers passed the previous barrier
-            if (j + 1 < n_tiles) q8_store(st ^ 1);
+            if (j + 1 < j_hi) q8_store(st ^ 1);
         }
         tile_done();   // this stage is refilled two tiles on
     }
 
     acc_settle(o);
+    if constexpr (SPLIT) {
+        if (rvalid) {
+            // dims 32 mb + 8 r4 + 4 hh + 0..3 of O, unnormalised; m in natural-log units
+            const size_t part = ((size_t)t * n_q_heads + h * G + g) * sp.n + s_idx;
+            float* acc = sp.pacc + part * PF_HD + 4 * hh;
+#pragma unroll
+            for (int mb = 0; mb < 8; ++mb)
+#pragma unroll
+                for (int r4 = 0; r4 < 4; ++r4)
+                    *(f32x4*)(acc + 32 * mb + 8 * r4) =
+                        (f32x4){o[mb][4 * r4], o[mb][4 * r4 + 1], o[mb][4 * r4 + 2],
+                                o[mb][4 * r4 + 3]};
+            if (hh == 0) {
+                sp.pm[part] = l_run > 0.f ? m_run * FL_LN2 : -1e30f;
+                sp.pd[part] = l_run;
+            }
+        }
+        return;
+    }
     if (rvalid) {
         const float inv = 1.f / l_run;
         f16* zrow = z + ((size_t)t * n_q_heads + h * G + g) * z_pitch + 4 * hh;
@@ -759,10 +815,83 @@ attn_prefill_r64_kernel(const f16* __restrict__ q, int q_pitch, const f16* __res
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
+// Dynamic LDS above the default limit, raised once per device for each
+// prefill kernel (a mutex: callers may come from several threads).
+std::mutex g_lds_mu;
+constexpr int PF_MAX_DEVICES = 64;
+bool g_lds_done[PF_MAX_DEVICES];
+
+int raise_lds_limits() {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= PF_MAX_DEVICES) {
+        fl::set_error("attn_prefill: no current device below index %d", PF_MAX_DEVICES);
+        return FL_ELAUNCH;
+    }
+    std::lock_guard<std::mutex> lock(g_lds_mu);
+    if (g_lds_done[dev]) return FL_OK;
+    const void* fns[] = {(const void*)attn_prefill_kernel<false, false>,
+                         (const void*)attn_prefill_kernel<false, true>,
+                         (const void*)attn_prefill_kernel<true, false>,
+                         (const void*)attn_prefill_kernel<true, true>};
+    for (const void* f : fns)
+        if (hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, LDS_B) !=
+            hipSuccess) {
+            fl::set_error("attn_prefill: cannot raise the dynamic LDS limit to %d bytes", LDS_B);
+            return FL_ELAUNCH;
+        }
+    if (hipFuncSetAttribute((const void*)attn_prefill_r64_kernel,
+                            hipFuncAttributeMaxDynamicSharedMemorySize, R64_LDS) != hipSuccess) {
+        fl::set_error("attn_prefill: cannot raise the dynamic LDS limit to %d bytes", R64_LDS);
+        return FL_ELAUNCH;
+    }
+    g_lds_done[dev] = true;
+    return FL_OK;
+}
+
+// The 64-rows-a-wave kernel takes a call once there are enough 256-row
+// workgroups to fill the chip twice over.
+bool use_r64(int T, int n_q_heads, int n_kv_heads) {
+    const int rows = T * (n_q_heads / n_kv_heads);
+    return (rows + R64_BQ - 1) / R64_BQ * n_kv_heads >= R64_MIN_WGS;
+}
+
+constexpr int PF_SPLIT_MAX = 16;
+constexpr int PF_CUS = 256;         // MI355X: 256 CUs, one 128 KiB-LDS workgroup each
+constexpr int PF_SPLIT_OVH = 2;     // a split's fixed cost in tile units: prologue, partials, merge
+
+// The KV split of a prefill call whose 128-row workgroups are too few to fill
+// the CUs (a short chunk deep into a long prompt, runtime.py:196 / 2932-2941):
+// the count that minimises (rounds of one workgroup a CU) x (tiles the
+// heaviest workgroup walks + a split's fixed cost). 1 where the 64-rows-a-wave
+// kernel runs or the grid already fills the chip.
+int split_policy(int T, int pos0, int n_q_heads, int n_kv_heads) {
+    if (T < 1 || pos0 < 0 || n_kv_heads < 1 || n_q_heads % n_kv_heads != 0) return 1;
+    if (use_r64(T, n_q_heads, n_kv_heads)) return 1;
+    const int wgs = n_kv_heads * ((T * (n_q_heads / n_kv_heads) + PF_BQ - 1) / PF_BQ);
+    if (wgs >= PF_CUS) return 1;
+    const int nkt = (pos0 + T + PF_BK - 1) / PF_BK;
+    int best = 1;
+    long long best_cost = -1;
+    for (int S = 1; S <= PF_SPLIT_MAX && S <= nkt; ++S) {
+        const long long rounds = ((long long)wgs * S + PF_CUS - 1) / PF_CUS;
+        const long long cost = rounds * ((nkt + S - 1) / S + PF_SPLIT_OVH);
+        if (best_cost < 0 || cost < best_cost) {
+            best_cost = cost;
+            best = S;
+        }
+    }
+    return best;
+}
+
+size_t split_work_bytes(int T, int n_q_heads, int head_dim, int split) {
+    return (size_t)T * n_q_heads * split * ((size_t)head_dim * 4 + 8);
+}
+
 template <bool Q8>
 int prefill(const void* q, int q_pitch, const void* k_new, const void* v_new, void* kcache,
             void* vcache, int layer, int n_q_heads, int n_kv_heads, int head_dim, int pos0,
-            int max_pos, float scale, int T, void* z, int z_pitch, fl_stream_t stream) {
+            int max_pos, float scale, int T, void* z, int z_pitch, int split, void* work,
+            size_t work_bytes, fl_stream_t stream) {
     FL_REQUIRE(q && kcache && vcache && z, "null pointer");
     FL_REQUIRE(head_dim == PF_HD, "head_dim must be 256");
     FL_REQUIRE(n_kv_heads > 0 && n_q_heads > 0 && n_q_heads % n_kv_heads == 0,
@@ -774,6 +903,15 @@ int prefill(const void* q, int q_pitch, const void* k_new, const void* v_new, vo
     FL_REQUIRE((k_new == nullptr) == (v_new == nullptr), "k_new and v_new together");
     FL_REQUIRE(aligned16(q) && aligned16(kcache) && aligned16(vcache) && ((uintptr_t)z & 7u) == 0,
                "aligned buffers");
+    FL_REQUIRE(split >= 1 && split <= 1024, "1 <= split <= 1024");
+    if (split > 1) {
+        FL_REQUIRE(work != nullptr && aligned16(work), "16-byte aligned work for a split");
+        if (work_bytes < split_work_bytes(T, n_q_heads, head_dim, split)) {
+            fl::set_error("work: %zu bytes, fl_attention_prefill_work_bytes asks %zu", work_bytes,
+                          split_work_bytes(T, n_q_heads, head_dim, split));
+            return FL_ESCRATCH;
+        }
+    }
     if (k_new != nullptr) {
         const int rc = Q8 ? fl_kv_store_q8(k_new, v_new, kcache, vcache, layer, pos0, T,
                                            n_kv_heads, head_dim, max_pos, stream)
@@ -781,20 +919,8 @@ int prefill(const void* q, int q_pitch, const void* k_new, const void* v_new, vo
                                         head_dim, max_pos, stream);
         if (rc) return rc;
     }
-    static bool lds_attr_set = false;   // 128 KiB of dynamic LDS is above the default limit
-    if (!lds_attr_set) {
-        if (hipFuncSetAttribute((const void*)attn_prefill_kernel<Q8>,
-                                hipFuncAttributeMaxDynamicSharedMemorySize, LDS_B) !=
-                hipSuccess ||
-            (!Q8 && hipFuncSetAttribute((const void*)attn_prefill_r64_kernel,
-                                        hipFuncAttributeMaxDynamicSharedMemorySize,
-                                        R64_LDS) != hipSuccess)) {
-            fl::set_error("attn_prefill: cannot raise the dynamic LDS limit to %d bytes",
-                          LDS_B);
-            return FL_ELAUNCH;
-        }
-        lds_attr_set = true;
-    }
+    int rc = raise_lds_limits();
+    if (rc) return rc;
     const void* kc;
     const void* vc;
     const f16* ksc = nullptr;
@@ -811,10 +937,8 @@ int prefill(const void* q, int q_pitch, const void* k_new, const void* v_new, vo
         vc = (const f16*)vcache + off;
     }
     const int rows = T * (n_q_heads / n_kv_heads);
-    // 64 rows a wave once there are enough 256-row workgroups to fill the
-    // chip twice over; below that the 128-row workgroups keep more CUs busy
     const int r64_tiles = (rows + R64_BQ - 1) / R64_BQ;
-    if (!Q8 && r64_tiles * n_kv_heads >= R64_MIN_WGS) {
+    if (!Q8 && split == 1 && use_r64(T, n_q_heads, n_kv_heads)) {
         hipLaunchKernelGGL(attn_prefill_r64_kernel, dim3(r64_tiles, n_kv_heads), dim3(PF_THREADS),
                            R64_LDS, (hipStream_t)stream, (const f16*)q, q_pitch,
                            (const f16*)kc, (const f16*)vc, (f16*)z, z_pitch, n_q_heads,
@@ -822,11 +946,25 @@ int prefill(const void* q, int q_pitch, const void* k_new, const void* v_new, vo
         return fl::check_launch("attn_prefill_r64");
     }
     const int n_row_tiles = (rows + PF_BQ - 1) / PF_BQ;
-    hipLaunchKernelGGL(attn_prefill_kernel<Q8>, dim3(n_row_tiles, n_kv_heads), dim3(PF_THREADS),
-                       LDS_B, (hipStream_t)stream, (const f16*)q, q_pitch, kc, vc, ksc, vsc,
-                       (f16*)z, z_pitch, n_q_heads, n_kv_heads, pos0, T, scale * FL_LOG2E,
-                       n_row_tiles);
-    return fl::check_launch("attn_prefill");
+    if (split == 1) {
+        hipLaunchKernelGGL((attn_prefill_kernel<Q8, false>), dim3(n_row_tiles, n_kv_heads),
+                           dim3(PF_THREADS), LDS_B, (hipStream_t)stream, (const f16*)q, q_pitch,
+                           kc, vc, ksc, vsc, (f16*)z, z_pitch, n_q_heads, n_kv_heads, pos0, T,
+                           scale * FL_LOG2E, n_row_tiles, PfSplit{nullptr, nullptr, nullptr, 1});
+        return fl::check_launch("attn_prefill");
+    }
+    const size_t parts = (size_t)T * n_q_heads * split;
+    PfSplit sp = {(float*)work, nullptr, nullptr, split};
+    sp.pm = sp.pacc + parts * PF_HD;
+    sp.pd = sp.pm + parts;
+    hipLaunchKernelGGL((attn_prefill_kernel<Q8, true>), dim3(n_row_tiles, n_kv_heads, split),
+                       dim3(PF_THREADS), LDS_B, (hipStream_t)stream, (const f16*)q, q_pitch, kc,
+                       vc, ksc, vsc, (f16*)z, z_pitch, n_q_heads, n_kv_heads, pos0, T,
+                       scale * FL_LOG2E, n_row_tiles, sp);
+    rc = fl::check_launch("attn_prefill (kv split)");
+    if (rc) return rc;
+    return fl_attention_merge(sp.pacc, sp.pm, sp.pd, z, n_q_heads, head_dim, z_pitch, T, split,
+                              nullptr, 0, 0, stream);
 }
 
 }  // namespace
@@ -837,7 +975,7 @@ extern "C" int fl_attention_prefill(const void* q, int q_pitch, const void* k_ne
                                     int max_pos, float scale, int T, void* z, int z_pitch,
                                     fl_stream_t stream) {
     return prefill<false>(q, q_pitch, k_new, v_new, kcache, vcache, layer, n_q_heads, n_kv_heads,
-                          head_dim, pos0, max_pos, scale, T, z, z_pitch, stream);
+                          head_dim, pos0, max_pos, scale, T, z, z_pitch, 1, nullptr, 0, stream);
 }
 
 extern "C" int fl_attention_prefill_q8(const void* q, int q_pitch, const void* k_new,
@@ -846,5 +984,38 @@ extern "C" int fl_attention_prefill_q8(const void* q, int q_pitch, const void* k
                                        int max_pos, float scale, int T, void* z, int z_pitch,
                                        fl_stream_t stream) {
     return prefill<true>(q, q_pitch, k_new, v_new, kcache, vcache, layer, n_q_heads, n_kv_heads,
-                         head_dim, pos0, max_pos, scale, T, z, z_pitch, stream);
+                         head_dim, pos0, max_pos, scale, T, z, z_pitch, 1, nullptr, 0, stream);
+}
+
+extern "C" int fl_attention_prefill_split_count(int T, int pos0, int n_q_heads, int n_kv_heads) {
+    return split_policy(T, pos0, n_q_heads, n_kv_heads);
+}
+
+extern "C" size_t fl_attention_prefill_work_bytes(int T, int n_q_heads, int head_dim, int split) {
+    if (T < 1 || n_q_heads < 1 || head_dim < 1 || split < 1) return 0;
+    return split > 1 ? split_work_bytes(T, n_q_heads, head_dim, split) : 0;
+}
+
+extern "C" int fl_attention_prefill_kv(const void* q, int q_pitch, const void* k_new,
+                                       const void* v_new, void* kcache, void* vcache, int layer,
+                                       int n_q_heads, int n_kv_heads, int head_dim, int pos0,
+                                       int max_pos, float scale, int T, int split, void* z,
+                                       int z_pitch, void* work, size_t work_bytes,
+                                       fl_stream_t stream) {
+    if (split == 0) split = split_policy(T, pos0, n_q_heads, n_kv_heads);
+    return prefill<false>(q, q_pitch, k_new, v_new, kcache, vcache, layer, n_q_heads, n_kv_heads,
+                          head_dim, pos0, max_pos, scale, T, z, z_pitch, split, work, work_bytes,
+                          stream);
+}
+
+extern "C" int fl_attention_prefill_kv_q8(const void* q, int q_pitch, const void* k_new,
+                                          const void* v_new, void* kcache, void* vcache,
+                                          int layer, int n_q_heads, int n_kv_heads, int head_dim,
+                                          int pos0, int max_pos, float scale, int T, int split,
+                                          void* z, int z_pitch, void* work, size_t work_bytes,
+                                          fl_stream_t stream) {
+    if (split == 0) split = split_policy(T, pos0, n_q_heads, n_kv_heads);
+    return prefill<true>(q, q_pitch, k_new, v_new, kcache, vcache, layer, n_q_heads, n_kv_heads,
+                         head_dim, pos0, max_pos, scale, T, z, z_pitch, split, work, work_bytes,
+                         stream);
 }

@@ -228,12 +228,15 @@ def attn_decode_noalloc(qg, kcaches, vcaches, pos0s, z, *, gate: bool = True,
 def attention_prefill(q, kcache, vcache, *, pos0: int, T: int | None = None, z=None,
                       k_new=None, v_new=None, layer: int = 0, n_q_heads: int = N_HEADS,
                       n_kv_heads: int = N_KV, q_pitch: int | None = None,
-                      scale: float = ATTN_SCALE, max_pos: int | None = None):
+                      scale: float = ATTN_SCALE, max_pos: int | None = None,
+                      split: int | None = None, work=None):
     """attention_prefill_fh + attention_merge_fh (kernels.cu:2461-2807, host
     _attn_fh runtime.py:2943-2959), with kv_store (kernels.cu:465-484) of
     k_new / v_new [T, n_kv, head_dim] fused in front when given. q [T,
-    n_q_heads, q_pitch] fp16 (q first in a head's row). Returns z [T,
-    n_q_heads, head_dim] fp16."""
+    n_q_heads, q_pitch] fp16 (q first in a head's row). split: the KV split
+    (None: prefill_split_count's choice; a split > 1 leaves partials in `work`,
+    a uint8 tensor, allocated here unless given). Returns z [T, n_q_heads,
+    head_dim] fp16."""
     T = q.shape[0] if T is None else T
     q_pitch = q.shape[-1] if q_pitch is None else q_pitch
     head_dim = kcache.shape[-1]
@@ -241,13 +244,35 @@ def attention_prefill(q, kcache, vcache, *, pos0: int, T: int | None = None, z=N
     row = n_kv_heads * head_dim
     if z is None:
         z = torch.empty((T, n_q_heads, head_dim), dtype=F16, device=q.device)
-    _lib.call("fl_attention_prefill", _ptr(q, F16, "q", T * n_q_heads * q_pitch), q_pitch,
-              _ptr(k_new, F16, "k_new", T * row), _ptr(v_new, F16, "v_new", T * row),
-              _ptr(kcache, F16, "kcache", (layer + 1) * max_pos * row),
-              _ptr(vcache, F16, "vcache", (layer + 1) * max_pos * row), layer, n_q_heads,
-              n_kv_heads, head_dim, pos0, max_pos, float(scale), T,
-              _ptr(z, F16, "z", T * n_q_heads * z.shape[-1]), z.shape[-1], _stream())
+    split, work = _prefill_split(T, pos0, n_q_heads, n_kv_heads, head_dim, split, work, q.device)
+    args = (_ptr(q, F16, "q", T * n_q_heads * q_pitch), q_pitch,
+            _ptr(k_new, F16, "k_new", T * row), _ptr(v_new, F16, "v_new", T * row),
+            _ptr(kcache, F16, "kcache", (layer + 1) * max_pos * row),
+            _ptr(vcache, F16, "vcache", (layer + 1) * max_pos * row), layer, n_q_heads,
+            n_kv_heads, head_dim, pos0, max_pos, float(scale), T)
+    zargs = (_ptr(z, F16, "z", T * n_q_heads * z.shape[-1]), z.shape[-1])
+    if split == 1:
+        _lib.call("fl_attention_prefill", *args, *zargs, _stream())
+    else:
+        _lib.call("fl_attention_prefill_kv", *args, split, *zargs,
+                  _ptr(work, torch.uint8, "work", work.numel()), work.numel(), _stream())
     return z
+
+
+def prefill_split_count(T: int, pos0: int, n_q_heads: int = N_HEADS,
+                        n_kv_heads: int = N_KV) -> int:
+    """The KV split the prefill takes for T queries at pos0 (runtime.py:
+    2932-2941's role): 1 unless the 128-row workgroups are too few for the CUs."""
+    return int(_lib.lib().fl_attention_prefill_split_count(T, pos0, n_q_heads, n_kv_heads))
+
+
+def _prefill_split(T, pos0, n_q_heads, n_kv_heads, head_dim, split, work, device):
+    if split is None:
+        split = prefill_split_count(T, pos0, n_q_heads, n_kv_heads)
+    if split > 1 and work is None:
+        need = int(_lib.lib().fl_attention_prefill_work_bytes(T, n_q_heads, head_dim, split))
+        work = torch.empty(need, dtype=torch.uint8, device=device)
+    return split, work
 
 
 # ---------------------------------------------------------------------------
@@ -369,7 +394,7 @@ def attn_decode_q8(qg, kcaches, vcaches, pos0s, caps, *, z=None, gate: bool = Tr
 def attention_prefill_q8(q, kcache, vcache, *, pos0: int, max_pos: int, T: int | None = None,
                          z=None, k_new=None, v_new=None, n_q_heads: int = N_HEADS,
                          n_kv_heads: int = N_KV, q_pitch: int | None = None,
-                         scale: float = ATTN_SCALE):
+                         scale: float = ATTN_SCALE, split: int | None = None, work=None):
     """attention_prefill_fh_q8 (kernels.cu:2778-2786) over an int8 cache, with
     kv_store_q8 of k_new / v_new fused in front when given."""
     T = q.shape[0] if T is None else T
@@ -377,12 +402,18 @@ def attention_prefill_q8(q, kcache, vcache, *, pos0: int, max_pos: int, T: int |
     row = n_kv_heads * HEAD_DIM
     if z is None:
         z = torch.empty((T, n_q_heads, HEAD_DIM), dtype=F16, device=q.device)
-    _lib.call("fl_attention_prefill_q8", _ptr(q, F16, "q", T * n_q_heads * q_pitch), q_pitch,
-              _ptr(k_new, F16, "k_new", T * row), _ptr(v_new, F16, "v_new", T * row),
-              _kv8(kcache, "kcache", max_pos, n_kv_heads, HEAD_DIM),
-              _kv8(vcache, "vcache", max_pos, n_kv_heads, HEAD_DIM), 0, n_q_heads, n_kv_heads,
-              HEAD_DIM, pos0, max_pos, float(scale), T,
-              _ptr(z, F16, "z", T * n_q_heads * z.shape[-1]), z.shape[-1], _stream())
+    split, work = _prefill_split(T, pos0, n_q_heads, n_kv_heads, HEAD_DIM, split, work, q.device)
+    args = (_ptr(q, F16, "q", T * n_q_heads * q_pitch), q_pitch,
+            _ptr(k_new, F16, "k_new", T * row), _ptr(v_new, F16, "v_new", T * row),
+            _kv8(kcache, "kcache", max_pos, n_kv_heads, HEAD_DIM),
+            _kv8(vcache, "vcache", max_pos, n_kv_heads, HEAD_DIM), 0, n_q_heads, n_kv_heads,
+            HEAD_DIM, pos0, max_pos, float(scale), T)
+    zargs = (_ptr(z, F16, "z", T * n_q_heads * z.shape[-1]), z.shape[-1])
+    if split == 1:
+        _lib.call("fl_attention_prefill_q8", *args, *zargs, _stream())
+    else:
+        _lib.call("fl_attention_prefill_kv_q8", *args, split, *zargs,
+                  _ptr(work, torch.uint8, "work", work.numel()), work.numel(), _stream())
     return z
 
 

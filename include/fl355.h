@@ -233,6 +233,29 @@ int fl_attn_decode_noalloc(const void* qg, int q_pitch, const void* const* kcach
                            void* z, int z_pitch, fl_stream_t stream);
 size_t fl_attn_decode_noalloc_max_bytes(void);
 
+/* The prefill with a KV split (attention_prefill_fh with gridDim.z = S and
+ * attention_merge_fh, kernels.cu:2461-2486 / 2763 / 2788-2807; split chosen by
+ * _fh_split, runtime.py:2932-2959): split s of every workgroup walks a share
+ * of its causal KV tiles and leaves partials in `work` (the reference's `pt`
+ * arena: pacc [T][n_q_heads][S][head_dim], pm (natural log) and pd
+ * [T][n_q_heads][S], f32); one merge writes z. For calls whose 128-row
+ * workgroups are too few to fill the CUs -- a 1024-token chunk deep into a
+ * long prompt (runtime.py:196). split 0: fl_attention_prefill_split_count's
+ * choice; split 1: fl_attention_prefill (no work needed). */
+int fl_attention_prefill_split_count(int T, int pos0, int n_q_heads, int n_kv_heads);
+size_t fl_attention_prefill_work_bytes(int T, int n_q_heads, int head_dim, int split);
+int fl_attention_prefill_kv(const void* q, int q_pitch, const void* k_new, const void* v_new,
+                            void* kcache, void* vcache, int layer, int n_q_heads, int n_kv_heads,
+                            int head_dim, int pos0, int max_pos, float scale, int T, int split,
+                            void* z, int z_pitch, void* work, size_t work_bytes,
+                            fl_stream_t stream);
+/* ... over an int8 cache (attention_prefill_fh_q8, kernels.cu:2778-2786). */
+int fl_attention_prefill_kv_q8(const void* q, int q_pitch, const void* k_new, const void* v_new,
+                               void* kcache, void* vcache, int layer, int n_q_heads,
+                               int n_kv_heads, int head_dim, int pos0, int max_pos, float scale,
+                               int T, int split, void* z, int z_pitch, void* work,
+                               size_t work_bytes, fl_stream_t stream);
+
 /* fl_attention_prefill over an int8 cache (k_new / v_new, when given, are
  * stored first with kv_store_q8). Replaces kernels.cu:2778-2786
  * attention_prefill_fh_q8 (+ merge_fh), launched by runtime.py:2943-2959. */

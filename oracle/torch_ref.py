@@ -53,27 +53,34 @@ def attention_prefill(q: torch.Tensor, kc: torch.Tensor, vc: torch.Tensor, pos0:
                       scale: float, rows: slice | None = None, block: int = 512) -> torch.Tensor:
     """Causal GQA prefill (kernels.cu:2461-2807): q [T, 24, d] fp16, query t
     at position pos0 + t. `rows` limits the computed query rows (a bounded
-    CPU sample). P is rounded to fp16 before P V, as the reference does."""
+    CPU sample). P is rounded to fp16 before P V, as the reference does.
+    Runs on whatever device the tensors are on (fp32 matmuls over contiguous
+    operands, blocks of `block` query rows)."""
     T, H, d = q.shape
     n_kv = kc.shape[1]
     G = H // n_kv
+    dev = q.device
     rows = rows or slice(0, T)
-    t_idx = torch.arange(T)[rows]
-    out = torch.empty((len(t_idx), H, d), dtype=F16)
+    t_idx = torch.arange(T, device=dev)[rows]
+    out = torch.empty((len(t_idx), H, d), dtype=F16, device=dev)
     for b0 in range(0, len(t_idx), block):
         tb = t_idx[b0:b0 + block]
+        nb = len(tb)
         n = pos0 + int(tb[-1]) + 1
-        qb = q[tb].to(F32).view(len(tb), n_kv, G, d)
-        k = kc[:n].to(F32).permute(1, 0, 2)
-        v = vc[:n].to(F32).permute(1, 0, 2)
-        s = torch.einsum("tkgd,knd->tkgn", qb, k) * scale
-        mask = torch.arange(n)[None, :] > (pos0 + tb)[:, None]
-        s = s.masked_fill(mask[:, None, None, :], float("-inf"))
+        # [kv, nb * G, d] query rows of each kv head; [kv, d, n] keys; [kv, n, d] values
+        qb = q[tb].to(F32).view(nb, n_kv, G, d).permute(1, 0, 2, 3).reshape(n_kv, nb * G, d)
+        kt = kc[:n].to(F32).permute(1, 2, 0).contiguous()
+        v = vc[:n].to(F32).permute(1, 0, 2).contiguous()
+        s = torch.matmul(qb.contiguous(), kt) * scale                    # [kv, nb * G, n]
+        qpos = (pos0 + tb).repeat_interleave(G)                           # row (t, g) -> t
+        mask = torch.arange(n, device=dev)[None, :] > qpos[:, None]
+        s = s.masked_fill(mask[None], float("-inf"))
         m = s.amax(dim=-1, keepdim=True)
         p = torch.exp(s - m)
         l = p.sum(dim=-1, keepdim=True)
-        o = torch.einsum("tkgn,knd->tkgd", r16(p), v) / l
-        out[b0:b0 + len(tb)] = r16(o).reshape(len(tb), H, d).to(F16)
+        o = torch.matmul(r16(p), v) / l                                    # [kv, nb * G, d]
+        out[b0:b0 + nb] = r16(o).view(n_kv, nb, G, d).permute(1, 0, 2, 3).reshape(nb, H, d) \
+            .to(F16)
     return out
 
 

@@ -181,6 +181,52 @@ def test_prefill_growing_scores(fl, dev, orc, rng, T, pos0):
     assert ok, f"T={T} pos0={pos0}: max|err| {err}"
 
 
+def test_prefill_config3_scaling_full_rows_2k(fl, dev, orc):
+    """Config 3's own scaling at 2k: q ~ N(0,1)/16 pre-scaled and scale 1 in
+    the kernel (scores of std 1, a peaked softmax), every row of every head
+    against the C oracle."""
+    L = 2048
+    rng = np.random.default_rng(2048)
+    kc, vc = rand_cache(rng, L)
+    q = (rng.standard_normal((L, 24, 256)) / 16).astype(np.float16)
+    kd = torch.zeros((L, 4, 256), dtype=torch.float16, device=dev)
+    vd = torch.zeros_like(kd)
+    z = fl.ops.attention_prefill(to_dev(q, dev), kd, vd, pos0=0, scale=1.0,
+                                 k_new=to_dev(kc, dev), v_new=to_dev(vc, dev))
+    torch.cuda.synchronize()
+    want = orc.attention_prefill(q, kc, vc, q_pitch=256, pos0=0, max_pos=L, scale=1.0, T=L)
+    err, ok = close(z.cpu().numpy(), want, ATOL, RTOL)
+    assert ok, f"max|err| {err}"
+
+
+@pytest.mark.parametrize("L", [8192, 32768])
+def test_prefill_config3_full_rows(fl, dev, L):
+    """Config 3 at full size, every row of every head: the kernel against
+    oracle/torch_ref.attention_prefill (fp32 matmuls, P rounded to fp16 as
+    the reference does; pinned to the C oracle by tests/test_oracle_torch.py)
+    run on the GPU, so each of the XCD-mapped row tiles is checked."""
+    from oracle import torch_ref as tr
+
+    g = torch.Generator(device=dev).manual_seed(L)
+    q = (torch.randn((L, 24, 256), generator=g, device=dev) / 16).half()
+    k = torch.randn((L, 4, 256), generator=g, device=dev).half()
+    v = torch.randn((L, 4, 256), generator=g, device=dev).half()
+    kd = torch.zeros_like(k)
+    vd = torch.zeros_like(v)
+    z = fl.ops.attention_prefill(q, kd, vd, pos0=0, scale=1.0, k_new=k, v_new=v)
+    torch.cuda.synchronize()
+    assert torch.equal(kd, k) and torch.equal(vd, v)
+    want = tr.attention_prefill(q, k, v, 0, 1.0, block=256)
+    err = (z.float() - want.float()).abs()
+    bound = ATOL + RTOL * want.float().abs()
+    bad = int((err > bound).sum())
+    print(f"config 3 L={L}: all {L * 24} rows, max|err| {float(err.max()):.2e}, "
+          f"{bad} elements over the bar")
+    assert torch.isfinite(z.float()).all()
+    assert bad == 0, f"L={L}: max|err| {float(err.max())}"
+    assert float(err.max()) <= 1e-2 * float(want.float().abs().max())
+
+
 @pytest.mark.parametrize("L", [8192, 32768])
 def test_prefill_config3_sampled_rows(fl, dev, orc, L):
     """Config 3 at full size: q pre-scaled by 1/16 (scale 1 in the kernel); sampled
@@ -263,3 +309,79 @@ def test_prefill_long_sampled_rows(fl, dev, orc, T, pos0, ramp):
                                    scale=SCALE, T=1)
         err, ok = close(zh[t:t + 1], want, ATOL, RTOL)
         assert ok, f"T={T} pos0={pos0} row {t}: max|err| {err}"
+
+# --------------------------------------------------------------------------
+# prefill with a KV split (attention_prefill_fh's gridDim.z + attention_merge_fh)
+# --------------------------------------------------------------------------
+
+@pytest.mark.parametrize("T,pos0,split", [(300, 500, 2), (300, 500, 3), (129, 1000, 7),
+                                          (40, 3, 4), (1, 70, 5), (700, 0, 16)])
+def test_prefill_kv_split_vs_oracle(fl, dev, orc, rng, T, pos0, split):
+    """Forced KV splits against the C oracle, every row: splits that leave some
+    workgroups' shares empty (40 tokens from pos0 3 are one or two 64-row
+    tiles for 4 splits; 16 splits of a fresh 700-token prompt), one query
+    token, and the fused kv_store in front."""
+    L = pos0 + T
+    kc, vc = rand_cache(rng, L)
+    qg = rand_qg(rng, T)
+    kd = torch.zeros((L, 4, 256), dtype=torch.float16, device=dev)
+    vd = torch.zeros_like(kd)
+    kd[:pos0] = to_dev(kc[:pos0], dev)
+    vd[:pos0] = to_dev(vc[:pos0], dev)
+    z = fl.ops.attention_prefill(to_dev(qg, dev), kd, vd, pos0=pos0, split=split,
+                                 k_new=to_dev(kc[pos0:], dev), v_new=to_dev(vc[pos0:], dev))
+    torch.cuda.synchronize()
+    assert np.array_equal(kd.cpu().numpy(), kc) and np.array_equal(vd.cpu().numpy(), vc)
+    want = orc.attention_prefill(qg, kc, vc, q_pitch=512, pos0=pos0, max_pos=L, scale=SCALE, T=T)
+    err, ok = close(z.cpu().numpy(), want, ATOL, RTOL)
+    assert ok, f"T={T} pos0={pos0} split={split}: max|err| {err}"
+
+
+def test_prefill_kv_split_chunk_deep_in_prompt(fl, dev):
+    """The reference's own prefill shape: a 1024-token chunk (MAX_CHUNK,
+    runtime.py:196) at pos0 = 98000, where the 128-row workgroups (192) are
+    fewer than the CUs and the policy splits the KV range 4 ways. Every row
+    against oracle/torch_ref.attention_prefill (fp32 on the GPU), and the
+    unsplit call within the same bar."""
+    from oracle import torch_ref as tr
+
+    T, pos0 = 1024, 98000
+    assert fl.ops.prefill_split_count(T, pos0) == 4
+    L = pos0 + T
+    g = torch.Generator(device=dev).manual_seed(98)
+    q = (torch.randn((T, 24, 256), generator=g, device=dev) / 16).half()
+    kd = torch.randn((L, 4, 256), generator=g, device=dev).half()
+    vd = torch.randn((L, 4, 256), generator=g, device=dev).half()
+    z = fl.ops.attention_prefill(q, kd, vd, pos0=pos0, scale=1.0)
+    z1 = fl.ops.attention_prefill(q, kd, vd, pos0=pos0, scale=1.0, split=1)
+    want = tr.attention_prefill(q, kd, vd, pos0, 1.0, block=256)
+    torch.cuda.synchronize()
+    scale_out = float(want.float().abs().max())
+    for name, got in (("split 4", z), ("split 1", z1)):
+        err = (got.float() - want.float()).abs()
+        bad = int((err > ATOL + RTOL * want.float().abs()).sum())
+        print(f"T={T} pos0={pos0} {name}: max|err| {float(err.max()):.2e} "
+              f"(max|z| {scale_out:.2e}), {bad} over the bar")
+        assert torch.isfinite(got.float()).all() and bad == 0, name
+        # outputs average ~99k values (|z| ~ 1e-2), so the absolute bar alone
+        # is loose: a tile range lost or counted twice moves z by ~1/4 of itself
+        assert float(err.max()) <= 1e-2 * scale_out, name
+
+
+@pytest.mark.parametrize("T,pos0,split", [(200, 700, 3), (64, 100, 6)])
+def test_prefill_q8_kv_split_vs_oracle(fl, dev, orc, rng, T, pos0, split):
+    """The KV split over the int8 cache (attention_prefill_fh_q8 with
+    gridDim.z > 1) against the C oracle's int8 prefill, every row."""
+    from test_gpu_q8 import oracle_cache
+
+    L = pos0 + T
+    k, v, kc8, vc8 = oracle_cache(orc, rng, L, L)
+    qg = rand_qg(rng, T)
+    kd, vd = fl.ops.kv8_cache(L), fl.ops.kv8_cache(L)
+    fl.ops.kv_store_q8(to_dev(k, dev), to_dev(v, dev), kd, vd, pos0=0, max_pos=L)
+    z = fl.ops.attention_prefill_q8(to_dev(qg, dev), kd, vd, pos0=pos0, max_pos=L, split=split)
+    torch.cuda.synchronize()
+    want = orc.attention_prefill_q8(qg, kc8, vc8, q_pitch=512, pos0=pos0, max_pos=L, scale=SCALE,
+                                    T=T)
+    err, ok = close(z.cpu().numpy(), want, ATOL, RTOL)
+    assert ok, f"T={T} pos0={pos0} split={split}: max|err| {err}"

@@ -346,11 +346,17 @@ def test_chunked_vs_recurrence(fl, dev, orc, T):
     assert ok, f"T={T}: max|dy| {err}"
 
 
-@pytest.mark.parametrize("T,rows", [(1, 48), (3, 5), (7, 48)])
+# the 16-lanes-a-row kernel takes calls of >= 8192 rows with 16-byte aligned
+# rows: 171 x 48 = 8208 and 8193 x 1 rows reach it with a ragged last wave
+# (8208 % 16 == 0 but 8193 % 16 == 1; 8211 = 1173 x 7 leaves 3 rows in the last
+# wave); the small cases keep the wave-a-row kernel on both pitches
+@pytest.mark.parametrize("T,rows", [(1, 48), (3, 5), (7, 48), (171, 48), (8193, 1),
+                                    (1173, 7)])
 def test_rmsnorm_gated_row_layouts(fl, dev, orc, rng, T, rows):
-    """Rows 16-byte aligned (pitch 136: 16 lanes a row, 8 rows a wave) and
-    not (pitch 130: a wave a row) give the same bits, and the oracle's; row
-    counts that leave a wave's last rows empty."""
+    """Rows 16-byte aligned (pitch 136: from 8192 rows up, 16 lanes a row and
+    4 rows a wave) and not (pitch 130: a wave a row) give the same bits, the
+    oracle's, and leave the padding after each row untouched; row counts that
+    leave a wave's last rows empty."""
     o = (rng.standard_normal((T, rows, 128)) * 0.7).astype(np.float16)
     z = (rng.standard_normal((T, rows, 128)) * 2).astype(np.float16)
     w = (1 + rng.standard_normal(128) * 0.2).astype(np.float32)
