@@ -76,14 +76,19 @@ def time_graph(torch, g, reps=1):
     return st.elapsed_time(en) / reps          # ms
 
 
-def measure(torch, g, calls, samples, min_ms=2.0):
+def measure(torch, g, calls, samples, min_ms=2.0, warm_ms=200.0):
     """Per-call time of a graph holding `calls` launches: `samples` timed
     regions, each R back-to-back replays with R chosen so a region lasts at
-    least min_ms (graph-launch latency amortised over many launches). Returns
-    the median per-call µs and the spread over the regions."""
+    least min_ms (graph-launch latency amortised over many launches), after
+    warm_ms of untimed replays (the GPU's clocks ramp up over the first tens
+    of ms of load after idle: a 1-replay warm-up left the first regions of an
+    8k prefill 20 % slow). Returns the median per-call µs and the spread over
+    the regions."""
     time_graph(torch, g)                       # warm (code objects, caches)
     est = time_graph(torch, g)
     reps = max(1, int(-(-min_ms // max(est, 1e-3))))
+    for _ in range(max(1, int(warm_ms / max(est * reps, 1e-3)))):
+        time_graph(torch, g, reps)
     vals = sorted(time_graph(torch, g, reps) * 1e3 / calls for _ in range(samples))
     mid = len(vals) // 2
     med = vals[mid] if len(vals) % 2 else 0.5 * (vals[mid - 1] + vals[mid])

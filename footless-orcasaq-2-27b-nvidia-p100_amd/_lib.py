@@ -44,6 +44,7 @@ SIGNATURES = {
     "fl_attn_decode_noalloc": (_I, [_P, _I, _PP, _PP, _IP, _IP, _I, _I, _I, _I, _I, _F, _I, _I,
                                     _P, _I, _I, _P, _I, _P]),
     "fl_attn_decode_noalloc_max_bytes": (_SZ, []),
+    "fl_attention_prefill_plan": (_I, [_I, _I, _I, _I, _I, _P, _I]),
     "fl_attention_prefill_split_count": (_I, [_I, _I, _I, _I]),
     "fl_attention_prefill_work_bytes": (_SZ, [_I, _I, _I, _I]),
     "fl_attention_prefill_kv": (_I, [_P, _I, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _I, _I,

@@ -37,7 +37,10 @@
 // (byte * scale exact), here it is rounded to fp16 once.
 #include "fl_common.hpp"
 
+#include <algorithm>
+#include <cstdlib>
 #include <mutex>
+#include <vector>
 
 namespace {
 
@@ -576,6 +579,21 @@ constexpr int R64_COPIES = 8;               // copy instructions a wave a tile (
 // 5120) 378 against 410-422 us.
 constexpr int R64_MIN_WGS = 384;
 
+// Persistent launch: one workgroup a CU, each walking the row tiles of its
+// bin, heaviest first. A CU runs one 128 KiB-LDS workgroup at a time, and
+// the hardware hands an XCD's workgroups round-robin to its 4 shader engines
+// in launch order, a workgroup waiting for a CU of its own engine and the
+// ones behind it waiting for it; with 3 row tiles a CU (T = 8192) that left
+// 12 % of the CU time idle, the heavier tiles stranded behind the lighter.
+// The host balances the bins (kv tiles walked + a fixed cost a row tile).
+// Plan layout: v[0 .. bins] = offsets of each bin's list in the row-tile
+// indices at v[bins + 1 ..].
+constexpr int R64_PLAN_MAX = 1024;     // bins + 1 + row tiles a kv head: 2 KiB of arguments
+constexpr int R64_ITEM_COST = 5;       // a row tile's fixed cost in kv tiles (Q, pipeline fill, z)
+struct R64Plan {
+    uint16_t v[R64_PLAN_MAX];
+};
+
 // Copy tile kv0 (K and V, 32 rows each) into the stage at dst: wave w copies
 // rows 8 w .. 8 w + 7, two a copy instruction (as issue_rows: loff[n] = this
 // lane's source offset from row 8 w, row 2 n + lane / 32, swizzled chunk).
@@ -662,36 +680,27 @@ __device__ __forceinline__ void r64_vfrags(s16x4 (&vb)[8], const char* vt,
 __global__ void __launch_bounds__(PF_THREADS)
 attn_prefill_r64_kernel(const f16* __restrict__ q, int q_pitch, const f16* __restrict__ kc,
                         const f16* __restrict__ vc, f16* __restrict__ z, int z_pitch,
-                        int n_q_heads, int n_kv, int pos0, int T, float sl2, int n_row_tiles) {
+                        int n_q_heads, int n_kv, int pos0, int T, float sl2, int n_row_tiles,
+                        int bins, const R64Plan plan) {
     extern __shared__ __attribute__((aligned(16))) char smem[];
 
-    int tile, h;
-    xcd_tile(n_row_tiles, n_kv, tile, h);
+    // This workgroup's row tiles: one, of a grid of row tiles x kv heads
+    // (bins == 0), or the list of its bin, of a grid of one workgroup a CU.
+    int h, tile = 0, item0 = 0, n_items = 1;
+    if (bins == 0) {
+        xcd_tile(n_row_tiles, n_kv, tile, h);
+    } else {
+        const int id = blockIdx.x, xcd = id & 7, per = 8 / n_kv;
+        h = xcd / per;
+        const int bin = (id >> 3) * per + xcd % per;
+        item0 = plan.v[bin];
+        n_items = plan.v[bin + 1] - item0;
+    }
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int ql = lane & 31, hh = lane >> 5;
     const int G = n_q_heads / n_kv;
     const int RT = T * G;
-    const int R0 = tile * R64_BQ;
-    // this lane's two query rows (columns of the two MFMA blocks)
-    int row[2], t[2], g[2], qpos[2];
-    bool rvalid[2];
-#pragma unroll
-    for (int nb = 0; nb < 2; ++nb) {
-        row[nb] = R0 + 64 * w + 32 * nb + ql;
-        rvalid[nb] = row[nb] < RT;
-        t[nb] = rvalid[nb] ? row[nb] / G : 0;
-        g[nb] = rvalid[nb] ? row[nb] - t[nb] * G : 0;
-        qpos[nb] = rvalid[nb] ? pos0 + t[nb] : -1;
-    }
-    const int wfirst = R0 + 64 * w;
-    const int wlast = min(wfirst + 63, RT - 1);
-    const int wqmax = __builtin_amdgcn_readfirstlane(wlast >= wfirst ? pos0 + wlast / G : -1);
-    const int wqmin = __builtin_amdgcn_readfirstlane(pos0 + wfirst / G);
-    const int blast = min(R0 + R64_BQ - 1, RT - 1);
-    const int kv_end = __builtin_amdgcn_readfirstlane(pos0 + blast / G + 1);
-    const int n_tiles = (kv_end + R64_BK - 1) / R64_BK;
-
     const uint32_t rsb = (uint32_t)n_kv * ROW_B;
     const char* kb = uniform_ptr((const char*)(kc + (size_t)h * PF_HD));
     const char* vb = uniform_ptr((const char*)(vc + (size_t)h * PF_HD));
@@ -702,28 +711,6 @@ attn_prefill_r64_kernel(const f16* __restrict__ q, int q_pitch, const f16* __res
         loff[n] = r * rsb + 16 * ((lane & 31) ^ sw(8 * w + r));
     }
     const uint32_t lds_base = (uint32_t)(uintptr_t)((__attribute__((address_space(3))) char*)smem);
-
-#pragma unroll
-    for (int d = 0; d < R64_DIST; ++d)
-        if (d < n_tiles) r64_issue(lds_base + d * R64_STAGE, kb, vb, rsb, d * R64_BK, kv_end, w, lane, loff);
-
-    f16x8 qreg[2][16];   // Q[row nb][128 hh + 8 ks + 0..7]
-#pragma unroll
-    for (int nb = 0; nb < 2; ++nb) {
-        const f16* qrow = q + ((size_t)t[nb] * n_q_heads + h * G + g[nb]) * q_pitch + 128 * hh;
-#pragma unroll
-        for (int ks = 0; ks < 16; ++ks)
-            qreg[nb][ks] = rvalid[nb] ? *(const f16x8*)(qrow + 8 * ks) : (f16x8)(0);
-    }
-    WAIT_VMCNT(0);   // Q and the first tiles: the wait left to the compiler lands in the loop
-
-    f32x16 o[2][8];
-#pragma unroll
-    for (int nb = 0; nb < 2; ++nb)
-#pragma unroll
-        for (int mb = 0; mb < 8; ++mb) acc_zero(o[nb][mb], (f16x8)(0));
-    float m_run[2] = {-1e30f, -1e30f}, l_run[2] = {0.f, 0.f};
-
     // K operand of k-step ks: tile row ql, chunk 16 hh + ks, at 16 hh + (ks ^ sw(ql))
     const uint32_t koff = ql * ROW_B + 256 * hh + 16 * sw(ql);
     const int tr_r = (lane & 15) >> 2;
@@ -736,99 +723,150 @@ attn_prefill_r64_kernel(const f16* __restrict__ q, int q_pitch, const f16* __res
             troff[2 * u + s2] = (4 * hh + tr_r + 8 * s2) * ROW_B + 64 * (u ^ tr_r) +
                                 16 * ((tr_d >> 3) ^ (hh + 2 * s2)) + 2 * (tr_d & 7);
 
-    typedef __attribute__((address_space(3))) const f16x8 lds_f16x8;
-    typedef __attribute__((address_space(3))) const char lds_char;
-    int st = 0;   // stage of tile j
-    for (int j = 0; j < n_tiles; ++j) {
-        // tile j landed: the copies of the min(DIST - 1, n_tiles - 1 - j)
-        // tiles issued after it may still be in flight
-        const int ahead = min(R64_DIST - 1, n_tiles - 1 - j);
-        if (ahead >= 3) WAIT_VMCNT(3 * R64_COPIES);
-        else if (ahead == 2) WAIT_VMCNT(2 * R64_COPIES);
-        else if (ahead == 1) WAIT_VMCNT(R64_COPIES);
-        else WAIT_VMCNT(0);
-        tile_done();   // every wave is past tile j - 1: its stage can be refilled
-        if (j + R64_DIST < n_tiles) {
-            const int sn = st == 0 ? R64_NST - 1 : st - 1;   // (j + DIST) % NST == (j - 1) % NST
-            r64_issue(lds_base + sn * R64_STAGE, kb, vb, rsb, (j + R64_DIST) * R64_BK, kv_end, w,
-                      lane, loff);
+    for (int it = 0; it < n_items; ++it) {
+        if (bins != 0) tile = __builtin_amdgcn_readfirstlane(plan.v[bins + 1 + item0 + it]);
+        if (it > 0) tile_done();   // every wave is done with the previous row tile's stages
+        const int R0 = tile * R64_BQ;
+        // this lane's two query rows (columns of the two MFMA blocks)
+        int row[2], t[2], g[2], qpos[2];
+        bool rvalid[2];
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb) {
+            row[nb] = R0 + 64 * w + 32 * nb + ql;
+            rvalid[nb] = row[nb] < RT;
+            t[nb] = rvalid[nb] ? row[nb] / G : 0;
+            g[nb] = rvalid[nb] ? row[nb] - t[nb] * G : 0;
+            qpos[nb] = rvalid[nb] ? pos0 + t[nb] : -1;
         }
-        const int kv0 = j * R64_BK;
-        if (kv0 <= wqmax) {
-            const uint32_t kst = koff + st * R64_STAGE;
-            f32x16 s[2] = {(f32x16)(0.f), (f32x16)(0.f)};
-            constexpr int KPF = R64_KPF;
-            f16x8 ka[KPF];
-#pragma unroll
-            for (int ks = 0; ks < KPF; ++ks) ka[ks] = *(lds_f16x8*)((lds_char*)smem + (kst ^ (16 * ks)));
-#pragma unroll
-            for (int ks = 0; ks < 16; ++ks) {
-                const f16x8 a = ka[ks % KPF];
-                if (ks + KPF < 16)
-                    ka[ks % KPF] = *(lds_f16x8*)((lds_char*)smem + (kst ^ (16 * (ks + KPF))));
-                s[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qreg[0][ks], s[0], 0, 0, 0);
-                s[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qreg[1][ks], s[1], 0, 0, 0);
-                __builtin_amdgcn_sched_barrier(0);   // keep the reads ahead
-            }
-            const bool diag = kv0 + R64_BK - 1 > wqmin;   // wave-uniform
-            f16x8 pk[2][2];
-            r64_softmax(s[0], diag, qpos[0] - kv0 - 4 * hh, sl2, m_run[0], l_run[0], o[0], pk[0]);
-            r64_softmax(s[1], diag, qpos[1] - kv0 - 4 * hh, sl2, m_run[1], l_run[1], o[1], pk[1]);
-            // O^T += V^T P^T: 4 steps (kq, dim half) of 4 fragments x 2 blocks,
-            // the next step's fragments read under this step's MFMAs
-            const char* vt = smem + st * R64_STAGE + R64_TILE;
-            s16x4 vf[2][8];
-            r64_vfrags(vf[0], vt, troff, 0);
-#pragma unroll
-            for (int n = 0; n < 4; ++n) {
-                if (n + 1 < 4) r64_vfrags(vf[(n + 1) & 1], vt, troff, n + 1);
-#pragma unroll
-                for (int u = 0; u < 4; ++u) {
-                    const f16x4 lf = __builtin_bit_cast(f16x4, vf[n & 1][2 * u]);
-                    const f16x4 hf = __builtin_bit_cast(f16x4, vf[n & 1][2 * u + 1]);
-                    const f16x8 av = {lf[0], lf[1], lf[2], lf[3], hf[0], hf[1], hf[2], hf[3]};
-                    acc_mfma(o[0][4 * (n & 1) + u], av, pk[0][n >> 1]);
-                    acc_mfma(o[1][4 * (n & 1) + u], av, pk[1][n >> 1]);
-                }
-                __builtin_amdgcn_sched_barrier(0);
-            }
-        }
-        st = st == R64_NST - 1 ? 0 : st + 1;
-    }
+        const int wfirst = R0 + 64 * w;
+        const int wlast = min(wfirst + 63, RT - 1);
+        const int wqmax = __builtin_amdgcn_readfirstlane(wlast >= wfirst ? pos0 + wlast / G : -1);
+        const int wqmin = __builtin_amdgcn_readfirstlane(pos0 + wfirst / G);
+        const int blast = min(R0 + R64_BQ - 1, RT - 1);
+        const int kv_end = __builtin_amdgcn_readfirstlane(pos0 + blast / G + 1);
+        const int n_tiles = (kv_end + R64_BK - 1) / R64_BK;
 
-    acc_settle(o[0]);
-    acc_settle(o[1]);
+
 #pragma unroll
-    for (int nb = 0; nb < 2; ++nb) {
-        if (!rvalid[nb]) continue;
-        const float inv = 1.f / l_run[nb];
-        f16* zrow = z + ((size_t)t[nb] * n_q_heads + h * G + g[nb]) * z_pitch + 4 * hh;
+        for (int d = 0; d < R64_DIST; ++d)
+            if (d < n_tiles) r64_issue(lds_base + d * R64_STAGE, kb, vb, rsb, d * R64_BK, kv_end, w, lane, loff);
+
+        f16x8 qreg[2][16];   // Q[row nb][128 hh + 8 ks + 0..7]
 #pragma unroll
-        for (int mb = 0; mb < 8; ++mb)
+        for (int nb = 0; nb < 2; ++nb) {
+            const f16* qrow = q + ((size_t)t[nb] * n_q_heads + h * G + g[nb]) * q_pitch + 128 * hh;
 #pragma unroll
-            for (int r4 = 0; r4 < 4; ++r4)
-                *(f16x4*)(zrow + 32 * mb + 8 * r4) = (f16x4){
-                    f16_sat(o[nb][mb][4 * r4] * inv), f16_sat(o[nb][mb][4 * r4 + 1] * inv),
-                    f16_sat(o[nb][mb][4 * r4 + 2] * inv), f16_sat(o[nb][mb][4 * r4 + 3] * inv)};
+            for (int ks = 0; ks < 16; ++ks)
+                qreg[nb][ks] = rvalid[nb] ? *(const f16x8*)(qrow + 8 * ks) : (f16x8)(0);
+        }
+        WAIT_VMCNT(0);   // Q and the first tiles: the wait left to the compiler lands in the loop
+
+        f32x16 o[2][8];
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+            for (int mb = 0; mb < 8; ++mb) acc_zero(o[nb][mb], (f16x8)(0));
+        float m_run[2] = {-1e30f, -1e30f}, l_run[2] = {0.f, 0.f};
+
+        typedef __attribute__((address_space(3))) const f16x8 lds_f16x8;
+        typedef __attribute__((address_space(3))) const char lds_char;
+        int st = 0;   // stage of tile j
+        for (int j = 0; j < n_tiles; ++j) {
+            // tile j landed: the copies of the min(DIST - 1, n_tiles - 1 - j)
+            // tiles issued after it may still be in flight
+            const int ahead = min(R64_DIST - 1, n_tiles - 1 - j);
+            if (ahead >= 3) WAIT_VMCNT(3 * R64_COPIES);
+            else if (ahead == 2) WAIT_VMCNT(2 * R64_COPIES);
+            else if (ahead == 1) WAIT_VMCNT(R64_COPIES);
+            else WAIT_VMCNT(0);
+            tile_done();   // every wave is past tile j - 1: its stage can be refilled
+            if (j + R64_DIST < n_tiles) {
+                const int sn = st == 0 ? R64_NST - 1 : st - 1;   // (j + DIST) % NST == (j - 1) % NST
+                r64_issue(lds_base + sn * R64_STAGE, kb, vb, rsb, (j + R64_DIST) * R64_BK, kv_end, w,
+                          lane, loff);
+            }
+            const int kv0 = j * R64_BK;
+            if (kv0 <= wqmax) {
+                const uint32_t kst = koff + st * R64_STAGE;
+                f32x16 s[2] = {(f32x16)(0.f), (f32x16)(0.f)};
+                constexpr int KPF = R64_KPF;
+                f16x8 ka[KPF];
+#pragma unroll
+                for (int ks = 0; ks < KPF; ++ks) ka[ks] = *(lds_f16x8*)((lds_char*)smem + (kst ^ (16 * ks)));
+#pragma unroll
+                for (int ks = 0; ks < 16; ++ks) {
+                    const f16x8 a = ka[ks % KPF];
+                    if (ks + KPF < 16)
+                        ka[ks % KPF] = *(lds_f16x8*)((lds_char*)smem + (kst ^ (16 * (ks + KPF))));
+                    s[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qreg[0][ks], s[0], 0, 0, 0);
+                    s[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qreg[1][ks], s[1], 0, 0, 0);
+                    __builtin_amdgcn_sched_barrier(0);   // keep the reads ahead
+                }
+                const bool diag = kv0 + R64_BK - 1 > wqmin;   // wave-uniform
+                f16x8 pk[2][2];
+                r64_softmax(s[0], diag, qpos[0] - kv0 - 4 * hh, sl2, m_run[0], l_run[0], o[0], pk[0]);
+                r64_softmax(s[1], diag, qpos[1] - kv0 - 4 * hh, sl2, m_run[1], l_run[1], o[1], pk[1]);
+                // O^T += V^T P^T: 4 steps (kq, dim half) of 4 fragments x 2 blocks,
+                // the next step's fragments read under this step's MFMAs
+                const char* vt = smem + st * R64_STAGE + R64_TILE;
+                s16x4 vf[2][8];
+                r64_vfrags(vf[0], vt, troff, 0);
+#pragma unroll
+                for (int n = 0; n < 4; ++n) {
+                    if (n + 1 < 4) r64_vfrags(vf[(n + 1) & 1], vt, troff, n + 1);
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) {
+                        const f16x4 lf = __builtin_bit_cast(f16x4, vf[n & 1][2 * u]);
+                        const f16x4 hf = __builtin_bit_cast(f16x4, vf[n & 1][2 * u + 1]);
+                        const f16x8 av = {lf[0], lf[1], lf[2], lf[3], hf[0], hf[1], hf[2], hf[3]};
+                        acc_mfma(o[0][4 * (n & 1) + u], av, pk[0][n >> 1]);
+                        acc_mfma(o[1][4 * (n & 1) + u], av, pk[1][n >> 1]);
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            }
+            st = st == R64_NST - 1 ? 0 : st + 1;
+        }
+
+        acc_settle(o[0]);
+        acc_settle(o[1]);
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb) {
+            if (!rvalid[nb]) continue;
+            const float inv = 1.f / l_run[nb];
+            f16* zrow = z + ((size_t)t[nb] * n_q_heads + h * G + g[nb]) * z_pitch + 4 * hh;
+#pragma unroll
+            for (int mb = 0; mb < 8; ++mb)
+#pragma unroll
+                for (int r4 = 0; r4 < 4; ++r4)
+                    *(f16x4*)(zrow + 32 * mb + 8 * r4) = (f16x4){
+                        f16_sat(o[nb][mb][4 * r4] * inv), f16_sat(o[nb][mb][4 * r4 + 1] * inv),
+                        f16_sat(o[nb][mb][4 * r4 + 2] * inv), f16_sat(o[nb][mb][4 * r4 + 3] * inv)};
+        }
     }
 }
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 // Dynamic LDS above the default limit, raised once per device for each
-// prefill kernel (a mutex: callers may come from several threads).
+// prefill kernel, and the device's CU count (a mutex: callers may come from
+// several threads).
 std::mutex g_lds_mu;
 constexpr int PF_MAX_DEVICES = 64;
 bool g_lds_done[PF_MAX_DEVICES];
+int g_cus[PF_MAX_DEVICES];
 
-int raise_lds_limits() {
+int prefill_device_setup(int& n_cu) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= PF_MAX_DEVICES) {
         fl::set_error("attn_prefill: no current device below index %d", PF_MAX_DEVICES);
         return FL_ELAUNCH;
     }
     std::lock_guard<std::mutex> lock(g_lds_mu);
-    if (g_lds_done[dev]) return FL_OK;
+    if (g_lds_done[dev]) {
+        n_cu = g_cus[dev];
+        return FL_OK;
+    }
     const void* fns[] = {(const void*)attn_prefill_kernel<false, false>,
                          (const void*)attn_prefill_kernel<false, true>,
                          (const void*)attn_prefill_kernel<true, false>,
@@ -844,8 +882,156 @@ int raise_lds_limits() {
         fl::set_error("attn_prefill: cannot raise the dynamic LDS limit to %d bytes", R64_LDS);
         return FL_ELAUNCH;
     }
+    if (hipDeviceGetAttribute(&g_cus[dev], hipDeviceAttributeMultiprocessorCount, dev) !=
+        hipSuccess) {
+        fl::set_error("attn_prefill: cannot read the CU count of device %d", dev);
+        return FL_ELAUNCH;
+    }
     g_lds_done[dev] = true;
+    n_cu = g_cus[dev];
     return FL_OK;
+}
+
+// The persistent plan of the r64 kernel for T rows from pos0 (G query heads a
+// kv head) on n_cu CUs: bins = n_cu / n_kv bins a kv head (a kv head's row
+// tiles on 8 / n_kv XCDs). A row tile's weight is the kv tiles it walks +
+// R64_ITEM_COST; the heaviest go first, each to the lightest bin; then, for
+// each pair of bins, the single move or swap that best closes their gap, and
+// last single moves and swaps off the heaviest bin while they lower its
+// load. Returns the
+// entries used (bins + 1 + row tiles), 0 where the grid of row tiles x kv
+// heads is launched instead: a kv-head count that does not divide the 8 XCDs,
+// no more row tiles than bins, or a plan over R64_PLAN_MAX entries.
+int r64_build_plan(int T, int pos0, int G, int n_kv, int n_cu, R64Plan& plan) {
+    if (T < 1 || pos0 < 0 || G < 1 || n_kv < 1 || 8 % n_kv != 0 || n_cu < 8 || n_cu % 8 != 0)
+        return 0;
+    const int RT = T * G;
+    const int N = (RT + R64_BQ - 1) / R64_BQ;
+    const int bins = n_cu / n_kv;
+    if (N <= bins || bins + 1 + N > R64_PLAN_MAX) return 0;
+    std::vector<int> wt(N);
+    for (int t = 0; t < N; ++t) {
+        const int kv_end = pos0 + std::min(t * R64_BQ + R64_BQ - 1, RT - 1) / G + 1;
+        wt[t] = (kv_end + R64_BK - 1) / R64_BK + R64_ITEM_COST;
+    }
+    std::vector<int> order(N);
+    for (int t = 0; t < N; ++t) order[t] = N - 1 - t;   // weights grow with t
+    std::stable_sort(order.begin(), order.end(), [&](int a, int b) { return wt[a] > wt[b]; });
+    std::vector<std::vector<int>> bin(bins);
+    std::vector<long long> load(bins, 0);
+    for (int t : order) {
+        int lo = 0;
+        for (int b = 1; b < bins; ++b)
+            if (load[b] < load[lo]) lo = b;
+        bin[lo].push_back(t);
+        load[lo] += wt[t];
+    }
+    auto move = [&](int a, int xa, int b, int yb) {   // bin[a][xa] to b, bin[b][yb] (if >= 0) to a
+        const int tx = bin[a][xa];
+        bin[a].erase(bin[a].begin() + xa);
+        load[a] -= wt[tx];
+        if (yb >= 0) {
+            const int ty = bin[b][yb];
+            bin[b].erase(bin[b].begin() + yb);
+            load[b] -= wt[ty];
+            bin[a].push_back(ty);
+            load[a] += wt[ty];
+        }
+        bin[b].push_back(tx);
+        load[b] += wt[tx];
+    };
+    long long total = 0;
+    int wmax = 0;
+    for (int t = 0; t < N; ++t) total += wt[t], wmax = std::max(wmax, wt[t]);
+    const long long bound = std::max<long long>((total + bins - 1) / bins, wmax);
+    // pairs of a bin above and one below the mean (unless within 0.2 % of the
+    // bound already): the move or swap that best closes their gap
+    for (int round = 0; round < 16 && *std::max_element(load.begin(), load.end()) > bound + bound / 500;
+         ++round) {
+        bool changed = false;
+        for (int a = 0; a < bins; ++a)
+            for (int b = 0; b < bins; ++b) {
+                const long long gap = load[a] - load[b];
+                if (gap <= 0 || load[a] * bins < total || load[b] * bins > total) continue;
+                long long best = gap;
+                int bx = -1, by = -1;
+                for (int x = 0; x < (int)bin[a].size(); ++x) {
+                    const int wx = wt[bin[a][x]];
+                    if (std::llabs(gap - 2 * wx) < best) best = std::llabs(gap - 2 * wx), bx = x, by = -1;
+                    for (int y = 0; y < (int)bin[b].size(); ++y) {
+                        const int d = wx - wt[bin[b][y]];
+                        if (d > 0 && std::llabs(gap - 2 * d) < best)
+                            best = std::llabs(gap - 2 * d), bx = x, by = y;
+                    }
+                }
+                if (bx >= 0) move(a, bx, b, by), changed = true;
+            }
+        if (!changed) break;
+    }
+    // then single moves and swaps off the heaviest bin, to the same 0.2 %
+    for (int iter = 0; iter < 4 * N; ++iter) {
+        int hi = 0;
+        for (int b = 1; b < bins; ++b)
+            if (load[b] > load[hi]) hi = b;
+        if (load[hi] <= bound + bound / 500) break;
+        long long best = load[hi];
+        int bx = -1, by = -1, blo = -1;   // move bin[hi][bx] to blo (by < 0) or swap it with bin[blo][by]
+        for (int lo = 0; lo < bins; ++lo) {
+            if (lo == hi) continue;
+            for (int x = 0; x < (int)bin[hi].size(); ++x) {
+                const int wx = wt[bin[hi][x]];
+                const long long mv = std::max(load[hi] - wx, load[lo] + wx);
+                if (mv < best) best = mv, bx = x, by = -1, blo = lo;
+                for (int y = 0; y < (int)bin[lo].size(); ++y) {
+                    const int d = wx - wt[bin[lo][y]];
+                    if (d <= 0) continue;
+                    const long long sv = std::max(load[hi] - d, load[lo] + d);
+                    if (sv < best) best = sv, bx = x, by = y, blo = lo;
+                }
+            }
+        }
+        if (bx < 0) break;
+        move(hi, bx, blo, by);
+    }
+    int k = bins + 1;
+    for (int b = 0; b < bins; ++b) {
+        std::stable_sort(bin[b].begin(), bin[b].end(), [&](int a, int c) { return wt[a] > wt[c]; });
+        plan.v[b] = (uint16_t)(k - bins - 1);
+        for (int t : bin[b]) plan.v[k++] = (uint16_t)t;
+    }
+    plan.v[bins] = (uint16_t)(k - bins - 1);
+    return k;
+}
+
+// r64_build_plan, kept for the last few shapes (a serving loop repeats its
+// chunk shapes); copied out under the lock.
+struct R64PlanEntry {
+    int T, pos0, G, n_kv, n_cu, used;
+    R64Plan plan;
+};
+constexpr int R64_PLAN_CACHE = 8;
+std::mutex g_plan_mu;
+R64PlanEntry g_plan_cache[R64_PLAN_CACHE];
+int g_plan_fill, g_plan_next;
+
+int r64_plan(int T, int pos0, int G, int n_kv, int n_cu, R64Plan& plan) {
+    {
+        std::lock_guard<std::mutex> lock(g_plan_mu);
+        for (int i = 0; i < g_plan_fill; ++i) {
+            const R64PlanEntry& e = g_plan_cache[i];
+            if (e.T == T && e.pos0 == pos0 && e.G == G && e.n_kv == n_kv && e.n_cu == n_cu) {
+                plan = e.plan;
+                return e.used;
+            }
+        }
+    }
+    const int used = r64_build_plan(T, pos0, G, n_kv, n_cu, plan);
+    std::lock_guard<std::mutex> lock(g_plan_mu);
+    R64PlanEntry& e = g_plan_cache[g_plan_next];
+    e = {T, pos0, G, n_kv, n_cu, used, plan};
+    g_plan_next = (g_plan_next + 1) % R64_PLAN_CACHE;
+    g_plan_fill = std::min(g_plan_fill + 1, R64_PLAN_CACHE);
+    return used;
 }
 
 // The 64-rows-a-wave kernel takes a call once there are enough 256-row
@@ -919,7 +1105,8 @@ int prefill(const void* q, int q_pitch, const void* k_new, const void* v_new, vo
                                         head_dim, max_pos, stream);
         if (rc) return rc;
     }
-    int rc = raise_lds_limits();
+    int n_cu = 0;
+    int rc = prefill_device_setup(n_cu);
     if (rc) return rc;
     const void* kc;
     const void* vc;
@@ -939,10 +1126,14 @@ int prefill(const void* q, int q_pitch, const void* k_new, const void* v_new, vo
     const int rows = T * (n_q_heads / n_kv_heads);
     const int r64_tiles = (rows + R64_BQ - 1) / R64_BQ;
     if (!Q8 && split == 1 && use_r64(T, n_q_heads, n_kv_heads)) {
-        hipLaunchKernelGGL(attn_prefill_r64_kernel, dim3(r64_tiles, n_kv_heads), dim3(PF_THREADS),
-                           R64_LDS, (hipStream_t)stream, (const f16*)q, q_pitch,
-                           (const f16*)kc, (const f16*)vc, (f16*)z, z_pitch, n_q_heads,
-                           n_kv_heads, pos0, T, scale * FL_LOG2E, r64_tiles);
+        R64Plan plan;
+        const int G = n_q_heads / n_kv_heads;
+        const int bins = r64_plan(T, pos0, G, n_kv_heads, n_cu, plan) > 0 ? n_cu / n_kv_heads : 0;
+        const dim3 grid = bins > 0 ? dim3(n_cu) : dim3(r64_tiles, n_kv_heads);
+        hipLaunchKernelGGL(attn_prefill_r64_kernel, grid, dim3(PF_THREADS), R64_LDS,
+                           (hipStream_t)stream, (const f16*)q, q_pitch, (const f16*)kc,
+                           (const f16*)vc, (f16*)z, z_pitch, n_q_heads, n_kv_heads, pos0, T,
+                           scale * FL_LOG2E, r64_tiles, bins, plan);
         return fl::check_launch("attn_prefill_r64");
     }
     const int n_row_tiles = (rows + PF_BQ - 1) / PF_BQ;
@@ -985,6 +1176,19 @@ extern "C" int fl_attention_prefill_q8(const void* q, int q_pitch, const void* k
                                        fl_stream_t stream) {
     return prefill<true>(q, q_pitch, k_new, v_new, kcache, vcache, layer, n_q_heads, n_kv_heads,
                          head_dim, pos0, max_pos, scale, T, z, z_pitch, 1, nullptr, 0, stream);
+}
+
+extern "C" int fl_attention_prefill_plan(int T, int pos0, int n_q_heads, int n_kv_heads,
+                                         int n_cu, unsigned short* out, int cap) {
+    if (n_kv_heads < 1 || n_q_heads < 1 || n_q_heads % n_kv_heads != 0) return 0;
+    if (split_policy(T, pos0, n_q_heads, n_kv_heads) != 1 ||
+        !use_r64(T, n_q_heads, n_kv_heads))
+        return 0;
+    R64Plan plan;
+    const int used = r64_build_plan(T, pos0, n_q_heads / n_kv_heads, n_kv_heads, n_cu, plan);
+    if (out != nullptr)
+        for (int i = 0; i < used && i < cap; ++i) out[i] = plan.v[i];
+    return used;
 }
 
 extern "C" int fl_attention_prefill_split_count(int T, int pos0, int n_q_heads, int n_kv_heads) {

@@ -150,6 +150,17 @@ int fl_attention_prefill(const void* q, int q_pitch, const void* k_new, const vo
                          int head_dim, int pos0, int max_pos, float scale, int T, void* z,
                          int z_pitch, fl_stream_t stream);
 
+/* Long fp16 prefills (the 256-row-workgroup kernel) launch one workgroup a CU,
+ * each walking a host-balanced list of 256-row tiles of one kv head. The plan
+ * for n_cu CUs: out[0 .. bins] = offsets of each bin's list in the row-tile
+ * indices at out[bins + 1 ..] (bins = n_cu / n_kv_heads; bin b runs on the
+ * workgroups whose XCD serves kv head b / (n_cu / n_kv_heads)). Returns the
+ * entries (bins + 1 + row tiles; at most `cap` written), 0 where the call
+ * launches a grid of row tiles x kv heads instead. No reference counterpart:
+ * a query of this library's launch, for tests and tuning. */
+int fl_attention_prefill_plan(int T, int pos0, int n_q_heads, int n_kv_heads, int n_cu,
+                              unsigned short* out, int cap);
+
 /* ---- int8 KV cache --------------------------------------------------------
  * The reference's int8 cache format (kernels.cu:486-520, runtime.py:119-132),
  * one buffer a layer and K / V: for capacity max_pos, the values

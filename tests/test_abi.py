@@ -123,3 +123,48 @@ def test_prefill_split_policy(fl):
     assert lib.fl_attention_prefill_work_bytes(1024, 24, 256, 4) == 1024 * 24 * 4 * (256 * 4 + 8)
     assert lib.fl_attention_prefill_work_bytes(1024, 24, 256, 1) == 0
 
+
+
+def _plan_weights(T, pos0, G):
+    RT = T * G
+    N = (RT + 255) // 256
+    return [(pos0 + min(t * 256 + 255, RT - 1) // G + 1 + 31) // 32 + 5 for t in range(N)]
+
+
+@pytest.mark.parametrize("T,pos0", [(6144, 0), (8192, 0), (12288, 0), (32768, 0), (8192, 20000)])
+def test_prefill_persistent_plan(fl, T, pos0):
+    """The persistent plan of the long-prefill kernel on 256 CUs: every 256-row
+    tile of a kv head in exactly one of the 64 bins, each bin heaviest first,
+    and the heaviest bin within 4 % of the bound max(mean load, heaviest
+    tile) -- greedy longest-first alone is 10 % over it at T = 8192."""
+    lib = fl._lib.lib()
+    buf = (ctypes.c_ushort * 1024)()
+    n = lib.fl_attention_prefill_plan(T, pos0, 24, 4, 256, buf, 1024)
+    bins = 64
+    w = _plan_weights(T, pos0, 6)
+    assert n == bins + 1 + len(w)
+    v = list(buf[:n])
+    items = v[bins + 1:]
+    assert sorted(items) == list(range(len(w)))
+    assert v[0] == 0 and v[bins] == len(w) and all(v[b] <= v[b + 1] for b in range(bins))
+    loads = []
+    for b in range(bins):
+        mine = [w[t] for t in items[v[b]:v[b + 1]]]
+        assert mine == sorted(mine, reverse=True)
+        loads.append(sum(mine))
+    bound = max(sum(w) / bins, max(w))
+    assert max(loads) <= 1.04 * bound, (max(loads), bound)
+
+
+def test_prefill_plan_falls_back_to_the_tile_grid(fl):
+    """No plan (a grid of row tiles x kv heads) where the kernel does not run
+    (short prompts, the KV-split chunk), where the row tiles do not outnumber
+    the bins, where the kv heads do not divide the 8 XCDs, or where the plan
+    would pass 2 KiB of kernel arguments."""
+    lib = fl._lib.lib()
+    assert lib.fl_attention_prefill_plan(2048, 0, 24, 4, 256, None, 0) == 0
+    assert lib.fl_attention_prefill_plan(1024, 98000, 24, 4, 256, None, 0) == 0
+    assert lib.fl_attention_prefill_plan(65536, 0, 24, 4, 256, None, 0) == 0
+    assert lib.fl_attention_prefill_plan(8192, 0, 24, 3, 256, None, 0) == 0
+    assert lib.fl_attention_prefill_plan(8192, 0, 24, 4, 250, None, 0) == 0
+    assert lib.fl_attention_prefill_plan(8192, 0, 24, 4, 256, None, 0) == 64 + 1 + 192
