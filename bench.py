@@ -177,10 +177,12 @@ def bench_gdn_decode(torch, fl, steps, warmup):
 # config 2: GQA decode + MTP verify; config 0
 # ---------------------------------------------------------------------------
 
-def bench_attn_decode(torch, fl, Lmax, Bq=4, T=3, iters=20, seed=0, kv8=False, per_seq=False):
+def bench_attn_decode(torch, fl, Lmax, Bq=4, T=3, iters=20, seed=0, kv8=False, per_seq=False,
+                      eager=0):
     """kv8: int8 caches (fl_attn_decode_q8); per_seq: the reference's int8
     launch shape instead -- attention_dec_q8 + the gated dec merge per sequence
-    (runtime.py:2907-2920, tmin 1 / smax 28)."""
+    (runtime.py:2907-2920, tmin 1 / smax 28). eager > 0: that many untimed
+    eager calls instead (counter collection)."""
     dev = torch.device("cuda:0")
     import numpy as np
 
@@ -227,6 +229,10 @@ def bench_attn_decode(torch, fl, Lmax, Bq=4, T=3, iters=20, seed=0, kv8=False, p
         else:
             fl.ops.attn_decode(qg, ks, vs, pos0, z=z, work=work)
 
+    if eager:
+        for i in range(eager):
+            call(i)
+        return None
     gr = graph_of(torch, call, iters)
     m = measure(torch, gr, iters, DECODE_SAMPLES)
     us = m["us"]
@@ -414,7 +420,7 @@ def bench_gdn_verify(torch, fl, T=3, steps=96, warmup=16):
 # config 4: chunked GDN prefill
 # ---------------------------------------------------------------------------
 
-def bench_chunked(torch, fl, L=8192, iters=1):
+def bench_chunked(torch, fl, L=8192, iters=1, eager=0):
     dev = torch.device("cuda:0")
     g = torch.Generator(device=dev).manual_seed(4)
     c = torch.randn((L, 10240), generator=g, device=dev)
@@ -432,6 +438,10 @@ def bench_chunked(torch, fl, L=8192, iters=1):
         fl.ops.gdn_prefill_chunked(c[:, :2048], c[:, 2048:4096], c[:, 4096:], beta, decay, S, y,
                                    T=L, work=work)
 
+    if eager:
+        for i in range(eager):
+            call(i)
+        return None
     gr = graph_of(torch, call, iters)
     m = measure(torch, gr, iters, PREFILL_SAMPLES)
     us = m["us"]
@@ -583,7 +593,9 @@ def run_counter_workloads(torch, fl, names):
     copy (a 256 MiB device copy, the scale reference for FETCH_SIZE /
     WRITE_SIZE), gdn (config 1: 96 fused decode steps, 48 layer states
     rotated), prefill8k (config 3 at 8k, 3 launches), decode100k (config 2
-    at 100k, B=4 T=3, 10 launches)."""
+    at 100k, B=4 T=3, 10 launches), decode4k_B1 / decode8k / decode32k
+    (configs 0 and 2, 10 eager launches), chunked (config 4 at 8k, 3
+    launches)."""
     dev = torch.device("cuda:0")
     for name in names:
         log(f"counters: {name}")
@@ -623,6 +635,12 @@ def run_counter_workloads(torch, fl, names):
                 fl.ops.attention_prefill(q, kc, vc, pos0=0, scale=1.0)
         elif name == "decode100k":
             bench_attn_decode(torch, fl, 102400, iters=10)
+        elif name in ("decode4k_B1", "decode8k", "decode32k"):
+            L, Bq, T = {"decode4k_B1": (4096, 1, 1), "decode8k": (8192, 4, 3),
+                        "decode32k": (32768, 4, 3)}[name]
+            bench_attn_decode(torch, fl, L, Bq=Bq, T=T, eager=10)
+        elif name == "chunked":
+            bench_chunked(torch, fl, 8192, eager=3)
         else:
             raise SystemExit(f"unknown counter workload {name!r}")
         torch.cuda.synchronize()

@@ -22,6 +22,8 @@
 // chunk).
 #include "fl_common.hpp"
 
+#include <mutex>
+
 #pragma clang fp contract(off)
 
 namespace {
@@ -237,10 +239,10 @@ chunk_state_kernel(const f16* __restrict__ q, const f16* __restrict__ k, float* 
 #pragma unroll
             for (int kq = 0; kq < 2; ++kq) {
                 wf[mb][kq] = *(const f32x4*)(Wg + (size_t)(16 * mb + m) * CK_K + k0 + 16 * kq + 4 * kk);
-                const int i = 16 * mb + m;
-                qf[mb][kq] = i < n ? *(const f16x4*)(q + (size_t)(t0 + i) * qk_stride +
-                                                     (size_t)hk * CK_K + k0 + 16 * kq + 4 * kk)
-                                   : (f16x4)(0);
+                const int i = 16 * mb + m;   // row clamped, zeroed by select (no branch)
+                const f16x4 qv = *(const f16x4*)(q + (size_t)(t0 + min(i, n - 1)) * qk_stride +
+                                                 (size_t)hk * CK_K + k0 + 16 * kq + 4 * kk);
+                qf[mb][kq] = i < n ? qv : (f16x4)(0);
             }
     };
     auto load_rest = [&](int c) {
@@ -261,9 +263,9 @@ chunk_state_kernel(const f16* __restrict__ q, const f16* __restrict__ k, float* 
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int idx = l + 64 * j, row = idx >> 2, c16 = idx & 3;
-            kv[j] = row < n ? *(const f16x8*)(k + (size_t)(t0 + row) * qk_stride +
-                                              (size_t)hk * CK_K + k0 + 8 * c16)
-                            : (f16x8)(0);
+            const f16x8 kr = *(const f16x8*)(k + (size_t)(t0 + min(row, n - 1)) * qk_stride +
+                                             (size_t)hk * CK_K + k0 + 8 * c16);
+            kv[j] = row < n ? kr : (f16x8)(0);
         }
     };
     // the K slice into LDS: row r's 32-byte half kb at kb ^ ((r / 4) % 2), so
@@ -298,7 +300,7 @@ chunk_state_kernel(const f16* __restrict__ q, const f16* __restrict__ k, float* 
                     p[mb] = mfma4(wf[mb][kq][r], st[kq][r], p[mb]);
                     qs[mb] = mfma4((float)qf[mb][kq][r], st[kq][r], qs[mb]);
                 }
-        if (c + 1 < n_chunks) load_wq(c + 1);
+        load_wq(min(c + 1, n_chunks - 1));   // unconditional: see load_rest below
         f32x4* mine = part + par * (CS_PART) + w * (2 * 4 * 64);
 #pragma unroll
         for (int mb = 0; mb < 4; ++mb) {
@@ -306,7 +308,10 @@ chunk_state_kernel(const f16* __restrict__ q, const f16* __restrict__ k, float* 
             mine[4 * 64 + mb * 64 + l] = qs[mb];
         }
         stage_k();   // this wave's own region: its reads of the previous slice came before
-        __syncthreads();
+        // The partials are LDS writes: wait for those alone, then the barrier
+        // (__syncthreads would first drain vmcnt, i.e. wait for the next
+        // chunk's W / Q loads just issued and the y stores, every chunk).
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
         const f32x4* all = part + par * (CS_PART);
         f32x4 d[4];   // Delta rows tok = 16 mb + 4 kk + r, column v0 + m
 #pragma unroll
@@ -359,10 +364,36 @@ chunk_state_kernel(const f16* __restrict__ q, const f16* __restrict__ k, float* 
 #pragma unroll
                 for (int kb = 0; kb < 2; ++kb) st[kb] = mfma4(ka[kb][r], d[kq][r], st[kb]);
         }
-        if (c + 1 < n_chunks) load_rest(c + 1);
+        // Unconditional (the last chunk re-reads its own operands): under a
+        // branch the compiler's wait for the K slice before the barrier could
+        // not count the loads issued after it and drained them all.
+        load_rest(min(c + 1, n_chunks - 1));
     }
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) *(f32x4*)(Sv + 16 * kb) = st[kb];
+}
+
+// The state pass's dynamic LDS is above the 64 KiB default: raised once per
+// device (a mutex: callers may come from several threads).
+std::mutex g_cs_mu;
+constexpr int CS_MAX_DEVICES = 64;
+bool g_cs_done[CS_MAX_DEVICES];
+
+int raise_state_lds_limit() {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= CS_MAX_DEVICES) {
+        fl::set_error("gdn_chunk_state: no current device below index %d", CS_MAX_DEVICES);
+        return FL_ELAUNCH;
+    }
+    std::lock_guard<std::mutex> lock(g_cs_mu);
+    if (g_cs_done[dev]) return FL_OK;
+    if (hipFuncSetAttribute((const void*)chunk_state_kernel,
+                            hipFuncAttributeMaxDynamicSharedMemorySize, CS_LDS) != hipSuccess) {
+        fl::set_error("gdn_chunk_state: cannot raise the dynamic LDS limit to %d bytes", CS_LDS);
+        return FL_ELAUNCH;
+    }
+    g_cs_done[dev] = true;
+    return FL_OK;
 }
 
 }  // namespace
@@ -399,15 +430,8 @@ int fl_gdn_prefill_chunked(const void* q, const void* k, const void* v, const fl
                        decay, T, n_vheads, qk_stride, v_stride, group, (float*)work);
     int rc = fl::check_launch("gdn_chunk_prep");
     if (rc) return rc;
-    static bool lds_attr_set = false;   // above the 64 KiB default of dynamic LDS
-    if (!lds_attr_set) {
-        if (hipFuncSetAttribute((const void*)chunk_state_kernel,
-                                hipFuncAttributeMaxDynamicSharedMemorySize, CS_LDS) != hipSuccess) {
-            fl::set_error("gdn_chunk_state: cannot raise the dynamic LDS limit to %d bytes", CS_LDS);
-            return FL_ELAUNCH;
-        }
-        lds_attr_set = true;
-    }
+    rc = raise_state_lds_limit();
+    if (rc) return rc;
     hipLaunchKernelGGL(chunk_state_kernel, dim3(n_vheads, CK_V / CS_ROWS), dim3(256), CS_LDS,
                        (hipStream_t)stream, (const f16*)q, (const f16*)k, S, (f16*)y, T, n_vheads,
                        qk_stride, y_stride, out_scale, group, (const float*)work);
