@@ -58,39 +58,8 @@ constexpr int V_OFF = 2 * TILE_B;
 // and the O / l rescale is skipped on almost every tile.
 constexpr float RESCALE_LOG2 = 8.f;
 
-typedef short s16x4 __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) void lds_void;
-typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
-
 // the chunk swizzle of tile row r: chunk c is stored at c ^ sw(r)
 __device__ __forceinline__ int sw(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
-
-// s_waitcnt vmcnt(n) (n < 64), every other counter left alone
-#define WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt((((n) & 15) | (((n) >> 4) << 14)) | 0x0F70)
-
-// Workgroup barriers that are compiler memory barriers but add no vmcnt
-// wait: __syncthreads() would drain vmcnt, i.e. wait for the next tile's
-// copies too. tile_ready follows the explicit WAIT_VMCNT for this tile's
-// copies; tile_done also waits for this wave's outstanding LDS reads, so no
-// read of a stage can still be in flight when the copy that refills it is
-// issued after the barrier.
-__device__ __forceinline__ void tile_ready() { asm volatile("s_barrier" ::: "memory"); }
-__device__ __forceinline__ void tile_done() {
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-}
-
-// One 16-byte-a-lane HBM -> LDS copy (global_load_lds_dwordx4): lane l's 16
-// bytes land at LDS m0 + 16 l. Issued as asm so that the compiler does not
-// track it as an LDS write in flight: it would otherwise drain vmcnt (wait for
-// the next tile's copy) before every LDS read it cannot prove disjoint. The
-// copies are waited for explicitly (WAIT_VMCNT + tile_ready). The s_nop is the
-// wait state between the m0 write and its use by the copy.
-__device__ __forceinline__ void copy16(const char* sbase, uint32_t voff, uint32_t lds) {
-    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(lds));
-}
-__device__ __forceinline__ void copy16_v(const char* vptr, uint32_t lds) {
-    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(vptr), "{m0}"(lds));
-}
 
 // The O^T accumulators live in AGPRs and are touched only through the asm
 // below. With compiler-generated MFMAs O would be either in VGPRs (leaving no
@@ -205,13 +174,6 @@ __device__ __forceinline__ void issue_tile(uint32_t lds_base, int st, const char
     }
 }
 
-// p as a wave-uniform (scalar) value: the copies take their row base in SGPRs
-__device__ __forceinline__ const char* uniform_ptr(const char* p) {
-    const uint64_t v = (uint64_t)(uintptr_t)p;
-    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
-    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
-    return (const char*)(uintptr_t)(((uint64_t)hi << 32) | lo);
-}
 
 // The workgroup's (row tile, kv head), heaviest row tiles first. Workgroups
 // go to the 8 XCDs round-robin by flat id, and each XCD has its own L2: when

@@ -4,22 +4,52 @@
 // (gdn_scan_rows, kernels.cu:2809-2914) and names the chunked scan as the
 // undone optimisation (kernels.cu:1788-1791). This computes the same
 // recurrence (S *= decay; delta = beta (v - S k); S += delta k^T; o = S q)
-// chunk by chunk. For a chunk of C tokens with start state S0 [V][K], g_i the
-// in-chunk prefix sum of log(decay):
-//   A[i][j] = beta_i e^{g_i - g_j} (k_i . k_j), j < i      (strictly lower)
-//   (I + A) W = diag(beta e^{g}) K,  (I + A) U = diag(beta) V   (forward subst.)
-//   Delta = U - W S0^T                                       (C x V)
-//   O     = diag(e^{g}) Q S0^T + (M o Q K^T) Delta,  M[i][j] = e^{g_i - g_j}, j <= i
-//   S_C   = e^{g_C} S0 + Delta^T diag(e^{g_C - g_j}) K
-// The decay ratios are formed as e^{g_i - g_j} with j <= i (never 1 / gamma_j,
-// which overflows over a chunk of strong decay).
+// chunk by chunk. For a chunk of C = 64 tokens with start state S0 [V][K] and
+// g_i the in-chunk prefix sum of log(decay):
+//   A[i][j] = beta_i e^{g_i - g_j} (k_i . k_j), j < i          (strictly lower)
+//   T = (I + A)^-1                                              (unit lower)
+//   X = K S0^T,  Y = diag(beta) (V - diag(e^g) X)               (C x V)
+//   Delta = T Y
+//   O   = diag(e^g) Q S0^T + (M o Q K^T) Delta,  M[i][j] = e^{g_i - g_j}, j <= i
+//   S_C = e^{g_C} S0 + Delta^T diag(e^{g_C - g}) K
+// (Delta = U - W S0^T with W = T diag(beta e^g) K and U = T diag(beta) V is
+// the same product grouped otherwise; this grouping keeps only T and M o QK^T
+// in the workspace and feeds K, Q and V, exact in fp16, straight to the
+// matrix cores.) The decay ratios are formed as e^{g_i - g_j} with j <= i
+// (never 1 / gamma_j, which overflows over a chunk of strong decay).
 //
-// Two launches: chunk_prep (every (chunk, v head) in parallel: Q K^T and K K^T
-// on MFMA, W and U by forward substitution in fp32, into the caller's
-// workspace), then chunk_state (one workgroup per (v head, 16 state rows),
-// sequential over the chunks with the state in MFMA accumulators spread over
-// four waves; fp32 MFMA (v_mfma_f32_16x16x4_f32) for the three products of a
-// chunk).
+// Two launches. chunk_prep_kernel, every (chunk, v head) in parallel: K K^T
+// and Q K^T on MFMA, the prefix sums, A, T by forward substitution in fp32,
+// the gates, and T and M o QK^T written as fp16 MFMA operands.
+// chunk_state_kernel: one wavefront per 16 state rows (v) of a v head, all
+// 128 k columns of them in fp32 registers, sequential over the chunks with no
+// barrier or exchange on its own chain; the two wavefronts of a workgroup
+// share each chunk's operands, copied HBM -> LDS one chunk ahead.
+//
+// Precision. Every product runs on v_mfma_f32_16x16x32_f16 (fp16 inputs,
+// fp32 accumulate: the product of two fp16 values is exact in fp32). K, Q and
+// V are fp16 data. An fp32 operand x of the recurrence's products (the state,
+// Y, T, the decayed Delta) is scaled by a power of two 2^s chosen from its
+// block's maximum (max |x| 2^s in [128, 256)) and split x 2^s = hi + lo, both
+// fp16: two MFMAs (hi, lo) against an exact operand, three (hi.hi, hi.lo,
+// lo.hi) between two split operands, which leaves an error of ~2^-22 of the
+// block's maximum, fp32's order. The output's products need it too: one fp16
+// pass leaves y within its own tolerance, but its two terms cancel in places
+// and the gated norm that follows divides each head's row by its RMS (7e-3 of
+// the row's RMS against 2e-3 for fp32 products). Emulated in numpy before the
+// kernels were written, on the test's inputs: the state within 1.2e-6 of the
+// sequential recurrence after 8192 tokens and y as close as with all-fp32
+// products.
+//
+// MFMA operand layout (v_mfma_f32_16x16x32_f16, lane l = 16 g + i): the A
+// operand of rows r0 .. r0 + 15 and a 32-wide k-step at k0 holds, in lane l,
+// row r0 + i at k = k0 + kap(g, e), e = 0..7, kap(g, e) = 4 g + e (e < 4) or
+// 16 + 4 g + (e - 4); the B operand holds column c0 + i at the same k. The
+// result holds, in lane l, rows 4 g + r (r = 0..3) of column i. The matrix
+// core pairs A and B by (lane group, slot), so any k order the two share is
+// the same product; with kap, the results of two consecutive 16-row blocks
+// are, as they stand in the registers, the B operand of the next product
+// over those 32 rows: the state, X, Y and Delta never move between lanes.
 #include "fl_common.hpp"
 
 #include <mutex>
@@ -31,41 +61,88 @@ namespace {
 constexpr int CK_C = 64;       // tokens a chunk
 constexpr int CK_K = 128;      // key dim
 constexpr int CK_V = 128;      // value dim
-constexpr int CK_KP = CK_K + 8;   // f16 pitch of staged K / Q rows
-constexpr int CK_AP = 68;      // f32 pitch of the A matrix rows
 
-// workspace block of one (chunk, v head): W [C][K], U^T [V][C], QKm [C][C], then
-// G [C] (in-chunk prefix sums of log decay), e^{G} [C], e^{G_last - G} [C]
-constexpr size_t CK_BLK = (size_t)CK_C * CK_K + (size_t)CK_C * CK_V + (size_t)CK_C * CK_C + 3 * CK_C;
+// Workspace block of one (chunk, v head), bytes: T and M o QK^T, each as hi
+// and lo fp16 A operands [4 row blocks][2 k-steps][64 lanes][8] (8 KiB each),
+// then beta, e^{g} and e^{g_C - g} [64] f32 (beta 0 past the chunk's last
+// token), then e^{g_C}, 2^-tau and 2^-kappa (T's and M o QK^T's scales).
+constexpr int WS_T_HI = 0, WS_T_LO = 8192, WS_Q_HI = 16384, WS_Q_LO = 24576, WS_BETA = 32768,
+              WS_EG = 33024, WS_DK = 33280, WS_SC = 33536;
+constexpr int CK_BLK = 33792;
+
+typedef __attribute__((address_space(3))) const f16x4 lds_f16x4;
+typedef __attribute__((address_space(3))) const f16x8 lds_f16x8;
+typedef __attribute__((address_space(3))) const f32x4 lds_f32x4;
+
+__device__ __forceinline__ f32x4 mfma16(f16x8 a, f16x8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+// max over the 64 lanes, on every lane: quad exchanges and row rotations by
+// 4 and 8 (DPP), then v_permlane16_swap and v_permlane32_swap
+__device__ __forceinline__ float wave_max(float v) {
+    v = fmaxf(v, dpp_xor1(v));
+    v = fmaxf(v, dpp_xor2(v));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x124, 0xF, 0xF, true)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x128, 0xF, 0xF, true)));
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                    false);
+    return pair32_max(fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1])));
+}
+
+// The power of two s with m s in [2^P, 2^(P+1)) for a block maximum m >= 0
+// (from m's exponent field; at most 2^126, so 1 / s stays normal); inv = 1 / s.
+template <int P>
+__device__ __forceinline__ float pow2_scale(float m, float& inv) {
+    const int e = (int)((__float_as_uint(m) >> 23) & 0xff);
+    const int se = min(254 + P - e, 253);
+    inv = __uint_as_float((uint32_t)(254 - se) << 23);
+    return __uint_as_float((uint32_t)se << 23);
+}
+
+// x s = hi + lo, both fp16 (round to nearest): the B operand of a k-step from
+// the accumulators a (slots 0..3) and b (slots 4..7)
+__device__ __forceinline__ void split8(f32x4 a, f32x4 b, float s, f16x8& hi, f16x8& lo) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const float x = (e < 4 ? a[e] : b[e - 4]) * s;
+        const f16 h = (f16)x;
+        hi[e] = h;
+        lo[e] = (f16)(x - (float)h);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// chunk_prep_kernel: one workgroup of 4 waves a (chunk, v head)
+// ---------------------------------------------------------------------------
+constexpr int PK_P = CK_K + 8;   // f16 pitch of staged K / Q rows
+constexpr int PA_P = CK_C + 4;   // f32 pitch of the A / T and M o QK^T rows
+static_assert(CK_C * PA_P * 4 == CK_C * PK_P * 2, "A / QKm reuse the K / Q storage");
 
 __device__ __forceinline__ float safe_log(float d) { return logf(fmaxf(d, 1.17549435e-38f)); }
 
+
 __global__ void __launch_bounds__(256)
-chunk_prep_kernel(const f16* __restrict__ q, const f16* __restrict__ k, const f16* __restrict__ v,
+chunk_prep_kernel(const f16* __restrict__ q, const f16* __restrict__ k,
                   const float* __restrict__ beta, const float* __restrict__ decay, int T,
-                  int n_vheads, int qk_stride, int v_stride, int group, float* __restrict__ work) {
-    __shared__ __attribute__((aligned(16))) f16 sK[CK_C][CK_KP];
-    __shared__ __attribute__((aligned(16))) f16 sQ[CK_C][CK_KP];
-    __shared__ __attribute__((aligned(16))) float sA[CK_C][CK_AP];
-    __shared__ float sG[CK_C], sB[CK_C], sEG[CK_C];
+                  int n_vheads, int qk_stride, int group, char* __restrict__ work) {
+    __shared__ __attribute__((aligned(16))) char smem[2 * CK_C * PK_P * 2];
+    __shared__ float sG[CK_C], sB[CK_C], sRed[8];
+    f16(*sK)[PK_P] = (f16(*)[PK_P])smem;
+    f16(*sQ)[PK_P] = (f16(*)[PK_P])(smem + CK_C * PK_P * 2);
+    float(*sA)[PA_P] = (float(*)[PA_P])smem;                     // after the products
+    float(*sM)[PA_P] = (float(*)[PA_P])(smem + CK_C * PA_P * 4);
 
     const int c = blockIdx.x, hv = blockIdx.y, hk = hv / group;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int ql = lane & 31, hh = lane >> 5;
     const int t0 = c * CK_C;
     const int n = min(CK_C, T - t0);
-    float* blk = work + ((size_t)c * n_vheads + hv) * CK_BLK;
-    float* Wg = blk;
-    float* Ug = Wg + CK_C * CK_K;
-    float* QKg = Ug + CK_C * CK_V;
-    float* Gg = QKg + CK_C * CK_C;
+    char* blk = work + ((size_t)c * n_vheads + hv) * CK_BLK;
 
-    // Every global load of the chunk is issued up front and unconditionally,
-    // rows clamped to the chunk's last token, past-the-end rows then zeroed
-    // by a select: a load under a branch is waited for inside it, one HBM
-    // round trip after another.
-    // K, Q (4 rows x 16 B a thread), the gates, and this thread's v column
-    // (U threads, tid >= 128: column tid - 128, every token)
+    // Every global load issued up front and unconditionally, rows clamped to
+    // the chunk's last token, past-the-end rows zeroed by a select: K and Q
+    // (4 rows x 16 B a thread), beta and decay.
     f16x8 kv8[4], qv8[4];
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
@@ -77,300 +154,439 @@ chunk_prep_kernel(const f16* __restrict__ q, const f16* __restrict__ k, const f1
     const int tg = min(tid & (CK_C - 1), n - 1);
     const float dec = decay[(size_t)(t0 + tg) * n_vheads + hv];
     const float bet = beta[(size_t)(t0 + tg) * n_vheads + hv];
-    const bool isW = tid < CK_K;
-    const int col = isW ? tid : tid - CK_K;
-    f16 vcol[CK_C];
-#pragma unroll
-    for (int i = 0; i < CK_C; ++i)
-        vcol[i] = v[(size_t)(t0 + min(i, n - 1)) * v_stride + (size_t)hv * CK_V + col];
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
         const int idx = tid + 256 * m, i = idx >> 4, c8 = (idx & 15) * 8;
         *(f16x8*)&sK[i][c8] = i < n ? kv8[m] : (f16x8)(0);
         *(f16x8*)&sQ[i][c8] = i < n ? qv8[m] : (f16x8)(0);
     }
-    if (tid < CK_C) {
+    if (tid < CK_C) {   // decay 1 and beta 0 past the end: g stays at the last token's
         sG[tid] = tid < n ? safe_log(dec) : 0.f;
         sB[tid] = tid < n ? bet : 0.f;
     }
     __syncthreads();
     if (tid == 0) {   // the in-chunk prefix sums of log decay, in token order
-        float g[CK_C];
+        float gs[CK_C];
 #pragma unroll
-        for (int i = 0; i < CK_C; ++i) g[i] = sG[i];
+        for (int i = 0; i < CK_C; ++i) gs[i] = sG[i];
         float a = 0.f;
 #pragma unroll
         for (int i = 0; i < CK_C; ++i) {
-            a += g[i];
+            a += gs[i];
             sG[i] = a;
         }
     }
     __syncthreads();
-    if (tid < CK_C) sEG[tid] = expf(sG[tid]);   // read after the next barrier
 
-    // K K^T and Q K^T: wave w takes the 32x32 block (bi, bj)
-    {
-        const int bi = w >> 1, bj = w & 1;
-        f32x16 kk = (f32x16)(0.f), qk = (f32x16)(0.f);
+    // K K^T and Q K^T: wave w the 32 x 32 block (bi, bj)
+    const int bi = w >> 1, bj = w & 1;
+    f32x16 kk = (f32x16)(0.f), qk = (f32x16)(0.f);
 #pragma unroll
-        for (int ks = 0; ks < CK_K / 16; ++ks) {
-            const f16x8 bk = *(const f16x8*)&sK[32 * bj + ql][16 * ks + 8 * hh];
-            const f16x8 ak = *(const f16x8*)&sK[32 * bi + ql][16 * ks + 8 * hh];
-            const f16x8 aq = *(const f16x8*)&sQ[32 * bi + ql][16 * ks + 8 * hh];
-            kk = __builtin_amdgcn_mfma_f32_32x32x16_f16(ak, bk, kk, 0, 0, 0);
-            qk = __builtin_amdgcn_mfma_f32_32x32x16_f16(aq, bk, qk, 0, 0, 0);
-        }
+    for (int ks = 0; ks < CK_K / 16; ++ks) {
+        const f16x8 bk = *(const f16x8*)&sK[32 * bj + ql][16 * ks + 8 * hh];
+        const f16x8 ak = *(const f16x8*)&sK[32 * bi + ql][16 * ks + 8 * hh];
+        const f16x8 aq = *(const f16x8*)&sQ[32 * bi + ql][16 * ks + 8 * hh];
+        kk = __builtin_amdgcn_mfma_f32_32x32x16_f16(ak, bk, kk, 0, 0, 0);
+        qk = __builtin_amdgcn_mfma_f32_32x32x16_f16(aq, bk, qk, 0, 0, 0);
+    }
+    __syncthreads();   // every K / Q read done: A and M o QK^T take their storage
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int i = 32 * bi + 8 * (r >> 2) + 4 * hh + (r & 3);
-            const int j = 32 * bj + ql;
-            const float ratio = j <= i ? expf(sG[i] - sG[j]) : 0.f;
-            sA[i][j] = j < i ? sB[i] * ratio * kk[r] : 0.f;
-            QKg[(size_t)i * CK_C + j] = j <= i ? ratio * qk[r] : 0.f;
-        }
+    for (int r = 0; r < 16; ++r) {
+        const int i = 32 * bi + 8 * (r >> 2) + 4 * hh + (r & 3);
+        const int j = 32 * bj + ql;
+        const float ratio = j <= i ? fast_exp2((sG[i] - sG[j]) * FL_LOG2E) : 0.f;
+        sA[i][j] = j < i ? sB[i] * ratio * kk[r] : 0.f;
+        sM[i][j] = j <= i ? ratio * qk[r] : 0.f;
     }
     __syncthreads();
 
-    // forward substitution: thread c < 128 solves column c of W, c >= 128 of U
-    // (sB and the staged K rows are zero past the chunk end; v by select)
-    {
-        float x[CK_C];
+    // T = (I + A)^-1 by forward substitution in fp32, column j by thread j:
+    // x[i] = [i == j] - sum_{m < i} A[i][m] x[m] (x[m] = 0 above the
+    // diagonal), the sum over m in four interleaved chains (m mod 4)
+    float x[CK_C];
+    if (tid < CK_C) {
 #pragma unroll
-        for (int i = 0; i < CK_C; ++i)
-            x[i] = isW ? sB[i] * sEG[i] * (float)sK[i][col] : (i < n ? sB[i] * (float)vcol[i] : 0.f);
+        for (int i = 0; i < CK_C; ++i) {
+            float acc[4] = {i == tid ? 1.f : 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int i = 1; i < CK_C; ++i) {
-            float acc = x[i];
-#pragma unroll
-            for (int j = 0; j < i; j += 4) {
-                const f32x4 a4 = *(const f32x4*)&sA[i][j];
+            for (int m = 0; m < i; m += 4) {
+                const f32x4 a4 = *(const f32x4*)&sA[i][m];
 #pragma unroll
                 for (int e = 0; e < 4; ++e)
-                    if (j + e < i) acc = fmaf(-a4[e], x[j + e], acc);
+                    if (m + e < i) acc[e] = fmaf(-a4[e], x[m + e], acc[e]);
             }
-            x[i] = acc;
+            x[i] = (acc[0] + acc[1]) + (acc[2] + acc[3]);
         }
-        if (isW) {
+    }
+    __syncthreads();   // every read of A done: T takes its storage
+    if (tid < CK_C) {
 #pragma unroll
-            for (int i = 0; i < CK_C; ++i) Wg[(size_t)i * CK_K + col] = x[i];
-        } else {   // U transposed: a v row's 64 tokens contiguous
+        for (int i = 0; i < CK_C; ++i) sA[i][tid] = x[i];
+    }
+    __syncthreads();
+
+    // the scales: block maxima of |T| and |M o QK^T|
+    float mt = 0.f, mq = 0.f;
 #pragma unroll
-            for (int i = 0; i < CK_C; i += 4)
-                *(f32x4*)(Ug + (size_t)col * CK_C + i) = (f32x4){x[i], x[i + 1], x[i + 2], x[i + 3]};
+    for (int m = 0; m < CK_C * CK_C / 256; ++m) {
+        const int idx = tid + 256 * m, i = idx >> 6, j = idx & 63;
+        mt = fmaxf(mt, fabsf(sA[i][j]));
+        mq = fmaxf(mq, fabsf(sM[i][j]));
+    }
+    mt = wave_max(mt);
+    mq = wave_max(mq);
+    if (lane == 0) {
+        sRed[w] = mt;
+        sRed[4 + w] = mq;
+    }
+    __syncthreads();
+    mt = fmaxf(fmaxf(sRed[0], sRed[1]), fmaxf(sRed[2], sRed[3]));
+    mq = fmaxf(fmaxf(sRed[4], sRed[5]), fmaxf(sRed[6], sRed[7]));
+    float t_inv, q_inv;
+    const float t_sc = pow2_scale<7>(mt, t_inv);
+    const float q_sc = pow2_scale<7>(mq, q_inv);
+
+    // the operands: slot (which: T hi, T lo, M o QK^T hi, lo; row block mb,
+    // k-step kq, lane l = 16 g + i) holds row 16 mb + i at columns
+    // 32 kq + kap(g, e)
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+        const int s = tid + 256 * m;
+        const int which = s >> 9, mb = (s >> 7) & 3, kq = (s >> 6) & 1, l = s & 63;
+        const int g = l >> 4, row = 16 * mb + (l & 15);
+        f16x8 o;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int col = 32 * kq + (e < 4 ? 4 * g + e : 12 + 4 * g + e);
+            const float xs = which < 2 ? sA[row][col] * t_sc : sM[row][col] * q_sc;
+            const f16 h = (f16)xs;
+            o[e] = (which & 1) == 0 ? h : (f16)(xs - (float)h);
         }
+        *(f16x8*)(blk + 8192 * which + ((mb * 2 + kq) * 64 + l) * 16) = o;
     }
     if (tid < CK_C) {
-        Gg[tid] = sG[tid];
-        Gg[CK_C + tid] = sEG[tid];
-        Gg[2 * CK_C + tid] = expf(sG[CK_C - 1] - sG[tid]);
+        const float gC = sG[CK_C - 1];
+        ((float*)(blk + WS_BETA))[tid] = sB[tid];
+        ((float*)(blk + WS_EG))[tid] = expf(sG[tid]);
+        ((float*)(blk + WS_DK))[tid] = expf(gC - sG[tid]);
+        if (tid < 4)
+            ((float*)(blk + WS_SC))[tid] = tid == 0 ? expf(gC) : tid == 1 ? t_inv : tid == 2 ? q_inv : 0.f;
     }
 }
 
-typedef short s16x4 __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+// ---------------------------------------------------------------------------
+// chunk_state_kernel: CS_WAVES wavefronts a workgroup, 16 state rows each
+// ---------------------------------------------------------------------------
+constexpr int CS_WAVES = 4;
+constexpr int CS_VW = 16 * CS_WAVES;   // state rows (v) a workgroup
+// One LDS stage: K and Q rows [64][256 B] (16-byte chunk c of row r at
+// c ^ (r & 15)), the workgroup's V columns [64][CS_VW] fp16, then the
+// workspace block (T and M o QK^T operands, the gates) as it is in HBM.
+constexpr int ST_K = 0, ST_Q = 16384, ST_V = 32768, ST_W = ST_V + CK_C * CS_VW * 2;
+constexpr int ST_BYTES = ST_W + CK_BLK;
+// then each wave's y tile [64 tokens][16 rows] fp16, written in the result
+// layout and read back as rows for 16-byte stores
+constexpr int ST_Y = 2 * ST_BYTES;
+constexpr int CS_LDS = ST_Y + CS_WAVES * CK_C * 16 * 2;
+static_assert(CS_LDS <= 160 * 1024, "two stages and the y tiles in 160 KiB of LDS");
+// copy instructions (1 KiB each, 16 B a lane) of a stage
+constexpr int CP_K = 16, CP_V = CK_C * CS_VW * 2 / 1024, CP_W = CK_BLK / 1024;
+constexpr int CP_ALL = 2 * CP_K + CP_V + CP_W;
+static_assert(CK_BLK % 1024 == 0 && (CK_C * CS_VW * 2) % 1024 == 0, "whole copy instructions");
+// y stores a wavefront issues a chunk (the vmcnt wait for the next stage's
+// copies, issued before them, counts them)
+constexpr int CS_NSTORE = 2;
 
-__device__ __forceinline__ f32x4 mfma4(float a, float b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+// The copies of chunk c's stage, instructions w, w + CS_WAVES, .. by wave w.
+// Rows past the chunk's last token repeat it (beta is 0 there). The LDS
+// destination (m0) is marked uniform: the compiler cannot prove it and would
+// wrap each copy in a loop over the distinct values.
+__device__ __forceinline__ void cs_issue(uint32_t dst, const char* kb, const char* qb,
+                                         const char* vb, const char* wb, int t0, int n,
+                                         int qk_bytes, int v_bytes, int w, int lane) {
+#pragma unroll
+    for (int j = 0; j < (CP_ALL + CS_WAVES - 1) / CS_WAVES; ++j) {
+        const int m = CS_WAVES * j + w;
+        if (m >= CP_ALL) break;
+        if (m < 2 * CP_K) {   // K (m < 16) or Q rows 4 (m % 16) .. + 3
+            const int isq = m >= CP_K, nn = isq ? m - CP_K : m;
+            const int r = 4 * nn + (lane >> 4), p = lane & 15;
+            const char* src = (isq ? qb : kb) + (size_t)(t0 + min(r, n - 1)) * qk_bytes +
+                              16 * (p ^ (r & 15));
+            copy16_v(src, __builtin_amdgcn_readfirstlane(dst + (isq ? ST_Q : ST_K) + 1024 * nn));
+        } else if (m < 2 * CP_K + CP_V) {   // V rows, CS_VW * 2 bytes each
+            constexpr int PR = CS_VW * 2 / 16;   // 16-byte pieces a row
+            const int nn = m - 2 * CP_K;
+            const int r = (64 / PR) * nn + lane / PR, p = lane % PR;
+            copy16_v(vb + (size_t)(t0 + min(r, n - 1)) * v_bytes + 16 * p,
+                     __builtin_amdgcn_readfirstlane(dst + ST_V + 1024 * nn));
+        } else {   // the workspace block, as it is
+            const int nn = m - 2 * CP_K - CP_V;
+            copy16_v(wb + 1024 * nn + 16 * lane, __builtin_amdgcn_readfirstlane(dst + ST_W + 1024 * nn));
+        }
+    }
 }
 
-// The state pass, with the state's k columns split over the 4 waves of a
-// workgroup (four waves on each sequential chain, a quarter of its MFMAs
-// each). A workgroup owns 16 state rows (v) of one v head; wave w the k
-// range [32 w, 32 w + 32) of them, as two 16 x 16 blocks of S^T in the D
-// layout of v_mfma_f32_16x16x4_f32 (block kb, lane l: k = 32 w + 16 kb +
-// 4 (l / 16) + r, v = v0 + l % 16). Per chunk:
-//   A: the wave's partials P_w = W[:, k_w] S^T[k_w, :] and QS_w = Q[:, k_w]
-//      S^T[k_w, :] (64 tokens x 16 v, 64 MFMA) into LDS; one barrier;
-//      every wave adds the four partials of P in wave order: Delta = U - P
-//   B: wave w's token block of O = e^{g} o QS + QKm Delta (QS summed the
-//      same way), the causal blocks only
-//   C: its k range of S^T = e^{g_C} S^T + Kd^T Delta (32 MFMA; Kd^T read
-//      from this wave's K slice in LDS with ds_read_b64_tr_b16)
-// Every operand is read by one wave only (W, Q and K by k range, QKm by
-// token block; U and the decay factors by all four), straight from the
-// workspace into registers: W and Q of the next chunk are requested after
-// phase A, the rest after phase C, so each load has half a chunk to land.
-// The partial buffers alternate between chunks (one barrier a chunk).
-constexpr int CS_ROWS = 16;                       // state rows (v) a workgroup
-constexpr int CS_PART = 2 * 4 * 4 * 64;           // f32x4 of one parity: [wave][P | QS][mb][lane]
-constexpr int CS_KSLICE = 64 * 64;                // bytes of one wave's K slice (64 tok x 32 k f16)
-constexpr int CS_LDS = 2 * CS_PART * 16 + 4 * CS_KSLICE;   // 64 KiB + 16 KiB
+// A operand of X = K S^T (or Q S^T) for row block mb, k-step js: row
+// 16 mb + i at k = 32 js + kap(g, e): two 8-byte reads of the swizzled row
+__device__ __forceinline__ f16x8 row_frag(uint32_t base, int mb, int js, int g, int i) {
+    const int row = 16 * mb + i;
+    const uint32_t rb = base + row * 256 + 8 * (g & 1);
+    const f16x4 a = *(lds_f16x4*)(uintptr_t)(rb + 16 * ((4 * js + (g >> 1)) ^ (row & 15)));
+    const f16x4 b = *(lds_f16x4*)(uintptr_t)(rb + 16 * ((4 * js + 2 + (g >> 1)) ^ (row & 15)));
+    return (f16x8){a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+}
 
-__global__ void __launch_bounds__(256, 2)   // two workgroups a CU: <= 256 registers a lane
-chunk_state_kernel(const f16* __restrict__ q, const f16* __restrict__ k, float* __restrict__ S,
-                   f16* __restrict__ y, int T, int n_vheads, int qk_stride, int y_stride,
-                   float out_scale, int group, const float* __restrict__ work) {
+// A operand of K^T Delta' for k rows 16 kb .., token step kq: lane 16 g + i
+// gets K[32 kq + kap(g, e)][16 kb + i] by two transposed reads (each: the
+// group's 16 lanes read a 4-row x 16-column block, lane i addressing row
+// i / 4, columns 4 (i % 4) .., and receiving column i of the four rows)
+__device__ __forceinline__ f16x8 col_frag(uint32_t base, int kb, int kq, int g, int i) {
+    const int c16 = 2 * kb + ((i & 3) >> 1), half = 8 * (i & 1);
+    const int r0 = 32 * kq + 4 * g + (i >> 2), r1 = r0 + 16;
+    const s16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (lds_s16x4*)(uintptr_t)(base + r0 * 256 + 16 * (c16 ^ (r0 & 15)) + half));
+    const s16x4 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (lds_s16x4*)(uintptr_t)(base + r1 * 256 + 16 * (c16 ^ (r1 & 15)) + half));
+    const f16x4 ah = __builtin_bit_cast(f16x4, a), bh = __builtin_bit_cast(f16x4, b);
+    return (f16x8){ah[0], ah[1], ah[2], ah[3], bh[0], bh[1], bh[2], bh[3]};
+}
+
+__global__ void __launch_bounds__(64 * CS_WAVES)
+chunk_state_kernel(const f16* __restrict__ q, const f16* __restrict__ k,
+                   const f16* __restrict__ v, float* __restrict__ S, f16* __restrict__ y, int T,
+                   int n_vheads, int qk_stride, int v_stride, int y_stride, float out_scale,
+                   int group, const char* __restrict__ work) {
     extern __shared__ __attribute__((aligned(16))) char smem[];
-    f32x4* part = (f32x4*)smem;
-    // grid (v heads, row blocks): the workgroups of a v head, which read the
-    // same W / QKm / K of every chunk, are dispatched n_vheads apart and so,
-    // with n_vheads a multiple of 8 (48 here), land on one XCD (dispatch goes
+    // a v head's workgroups are n_vheads apart in the flat id, so with
+    // n_vheads a multiple of 8 (48 here) they land on one XCD (dispatch goes
     // round robin over the 8) and share its L2
-    const int hv = blockIdx.x, rb = blockIdx.y, hk = hv / group;
+    const int hv = blockIdx.x % n_vheads, part = blockIdx.x / n_vheads, hk = hv / group;
     const int tid = threadIdx.x, l = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int m = l & 15, kk = l >> 4;
-    const int v0 = rb * CS_ROWS, k0 = 32 * w;
-    char* ksl = smem + 2 * CS_PART * 16 + w * CS_KSLICE;   // this wave's K slice
-    typedef __attribute__((address_space(3))) const char lds_char;
-    const uint32_t ksl_lds = (uint32_t)(uintptr_t)((__attribute__((address_space(3))) char*)ksl);
-
-    float* Sv = S + ((size_t)hv * CK_V + v0 + m) * CK_K + k0 + 4 * kk;   // S[v0 + m][k0 + 4 kk ..]
-    f32x4 st[2];
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) st[kb] = *(const f32x4*)(Sv + 16 * kb);
-
-    // operands of a chunk
-    f32x4 wf[4][2];    // W[16 mb + m][k0 + 16 kq + 4 kk ..]
-    f16x4 qf[4][2];    // Q[t0 + 16 mb + m][k0 + 16 kq + 4 kk ..]
-    f32x4 qkm[4];      // QKm[16 w + m][16 kq + 4 kk ..]
-    f32x4 u[4];        // U^T[v0 + m][16 mb + 4 kk ..]
-    f32x4 dk[4];       // e^{g_C - g}[16 kq + 4 kk ..]
-    f32x4 eg;          // e^{g}[16 w + 4 kk ..]
-    float eC;          // e^{g_C}
-    f16x8 kv[4];       // K slice staging: 16-byte chunk l + 64 j of the wave's [64 tok][32 k]
-    auto blk_of = [&](int c) { return work + ((size_t)c * n_vheads + hv) * CK_BLK; };
-    auto load_wq = [&](int c) {
-        const int t0 = c * CK_C;
-        const int n = min(CK_C, T - t0);
-        const float* Wg = blk_of(c);
-#pragma unroll
-        for (int mb = 0; mb < 4; ++mb)
-#pragma unroll
-            for (int kq = 0; kq < 2; ++kq) {
-                wf[mb][kq] = *(const f32x4*)(Wg + (size_t)(16 * mb + m) * CK_K + k0 + 16 * kq + 4 * kk);
-                const int i = 16 * mb + m;   // row clamped, zeroed by select (no branch)
-                const f16x4 qv = *(const f16x4*)(q + (size_t)(t0 + min(i, n - 1)) * qk_stride +
-                                                 (size_t)hk * CK_K + k0 + 16 * kq + 4 * kk);
-                qf[mb][kq] = i < n ? qv : (f16x4)(0);
-            }
-    };
-    auto load_rest = [&](int c) {
-        const int t0 = c * CK_C;
-        const int n = min(CK_C, T - t0);
-        const float* Wg = blk_of(c);
-        const float* UTg = Wg + CK_C * CK_K;
-        const float* QKg = UTg + CK_C * CK_V;
-        const float* Gg = QKg + CK_C * CK_C;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            qkm[j] = *(const f32x4*)(QKg + (size_t)(16 * w + m) * CK_C + 16 * j + 4 * kk);
-            u[j] = *(const f32x4*)(UTg + (size_t)(v0 + m) * CK_C + 16 * j + 4 * kk);
-            dk[j] = *(const f32x4*)(Gg + 2 * CK_C + 16 * j + 4 * kk);
-        }
-        eg = *(const f32x4*)(Gg + CK_C + 16 * w + 4 * kk);
-        eC = Gg[2 * CK_C - 1];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int idx = l + 64 * j, row = idx >> 2, c16 = idx & 3;
-            const f16x8 kr = *(const f16x8*)(k + (size_t)(t0 + min(row, n - 1)) * qk_stride +
-                                             (size_t)hk * CK_K + k0 + 8 * c16);
-            kv[j] = row < n ? kr : (f16x8)(0);
-        }
-    };
-    // the K slice into LDS: row r's 32-byte half kb at kb ^ ((r / 4) % 2), so
-    // the transposed reads of phase C hit 16 distinct 32-byte bank groups
-    auto stage_k = [&]() {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int idx = l + 64 * j, row = idx >> 2, c16 = idx & 3;
-            const int pos = row * 64 + 32 * ((c16 >> 1) ^ ((row >> 2) & 1)) + 16 * (c16 & 1);
-            *(f16x8*)(ksl + pos) = kv[j];
-        }
-    };
-
+    const int g = l >> 4, i = l & 15;
+    const int vw0 = part * CS_VW, v0 = vw0 + 16 * w;
+    const uint32_t lds0 = (uint32_t)(uintptr_t)((__attribute__((address_space(3))) char*)smem);
+    const char* kb = uniform_ptr((const char*)(k + (size_t)hk * CK_K));
+    const char* qb = uniform_ptr((const char*)(q + (size_t)hk * CK_K));
+    const char* vb = uniform_ptr((const char*)(v + (size_t)hv * CK_V + vw0));
+    const int qk_bytes = 2 * qk_stride, v_bytes = 2 * v_stride;
     const int n_chunks = (T + CK_C - 1) / CK_C;
-    load_wq(0);
-    load_rest(0);
+    auto wblock = [&](int c) {
+        return uniform_ptr(work + ((size_t)c * n_vheads + hv) * CK_BLK);
+    };
+
+    // the state, st[kb][r] = S[v0 + i][16 kb + 4 g + r]: the result layout of
+    // the 16 x 16 blocks of S^T
+    float* Sv = S + ((size_t)hv * CK_V + v0 + i) * CK_K + 4 * g;
+    f32x4 st[8];
+#pragma unroll
+    for (int kb8 = 0; kb8 < 8; ++kb8) st[kb8] = *(const f32x4*)(Sv + 16 * kb8);
+
+    cs_issue(lds0, kb, qb, vb, wblock(0), 0, min(CK_C, T), qk_bytes, v_bytes, w, l);
     for (int c = 0; c < n_chunks; ++c) {
         const int t0 = c * CK_C;
         const int n = min(CK_C, T - t0);
-        const int par = c & 1;
+        const uint32_t sb = lds0 + (c & 1) * ST_BYTES;
+        // this wave's copies of the stage landed (after them it issued only the
+        // previous chunk's y stores), then every wave's, and every wave is
+        // done with the other stage, which the next copies refill
+        if (c == 0) {
+            WAIT_VMCNT(0);
+        } else {
+            WAIT_VMCNT(CS_NSTORE);
+        }
+        tile_done();
+        if (c + 1 < n_chunks)
+            cs_issue(lds0 + ((c + 1) & 1) * ST_BYTES, kb, qb, vb, wblock(c + 1), t0 + CK_C,
+                     min(CK_C, T - t0 - CK_C), qk_bytes, v_bytes, w, l);
+        const uint32_t sw_ = sb + ST_W;
+        const f32x4 sc = *(lds_f32x4*)(uintptr_t)(sw_ + WS_SC);   // e^{g_C}, 2^-tau, 2^-kappa
 
-        // A: this wave's partials of P = W S^T and QS = Q S^T
-        f32x4 p[4], qs[4];
+        // the state, scaled and split: B operands of the four k-steps
+        float ms = 0.f;
 #pragma unroll
-        for (int mb = 0; mb < 4; ++mb) p[mb] = qs[mb] = (f32x4)(0.f);
+        for (int kb8 = 0; kb8 < 8; ++kb8)
 #pragma unroll
-        for (int kq = 0; kq < 2; ++kq)
+            for (int r = 0; r < 4; ++r) ms = fmaxf(ms, fabsf(st[kb8][r]));
+        float s_inv;
+        const float s_sc = pow2_scale<7>(wave_max(ms), s_inv);
+        f16x8 sh[4], sl[4];
 #pragma unroll
-            for (int r = 0; r < 4; ++r)
-#pragma unroll
-                for (int mb = 0; mb < 4; ++mb) {
-                    p[mb] = mfma4(wf[mb][kq][r], st[kq][r], p[mb]);
-                    qs[mb] = mfma4((float)qf[mb][kq][r], st[kq][r], qs[mb]);
-                }
-        load_wq(min(c + 1, n_chunks - 1));   // unconditional: see load_rest below
-        f32x4* mine = part + par * (CS_PART) + w * (2 * 4 * 64);
-#pragma unroll
-        for (int mb = 0; mb < 4; ++mb) {
-            mine[mb * 64 + l] = p[mb];
-            mine[4 * 64 + mb * 64 + l] = qs[mb];
-        }
-        stage_k();   // this wave's own region: its reads of the previous slice came before
-        // The partials are LDS writes: wait for those alone, then the barrier
-        // (__syncthreads would first drain vmcnt, i.e. wait for the next
-        // chunk's W / Q loads just issued and the y stores, every chunk).
-        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-        const f32x4* all = part + par * (CS_PART);
-        f32x4 d[4];   // Delta rows tok = 16 mb + 4 kk + r, column v0 + m
-#pragma unroll
-        for (int mb = 0; mb < 4; ++mb) {
-            f32x4 s = all[mb * 64 + l];
-#pragma unroll
-            for (int ww = 1; ww < 4; ++ww) s += all[ww * (2 * 4 * 64) + mb * 64 + l];
-            d[mb] = u[mb] - s;
-        }
-        f32x4 qsw = all[4 * 64 + w * 64 + l];   // this wave's token block of QS
-#pragma unroll
-        for (int ww = 1; ww < 4; ++ww) qsw += all[ww * (2 * 4 * 64) + 4 * 64 + w * 64 + l];
+        for (int js = 0; js < 4; ++js) split8(st[2 * js], st[2 * js + 1], s_sc, sh[js], sl[js]);
 
-        // B: O for tokens 16 w .. 16 w + 15
-        f32x4 o;
+        // X = K S^T and Q S^T (two passes each), 64 tokens x 16 rows; the
+        // k-step's fragments read first, consecutive MFMAs on different
+        // accumulators
+        f32x4 x[4], qs[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) o[r] = eg[r] * qsw[r];
+        for (int mb = 0; mb < 4; ++mb) x[mb] = qs[mb] = (f32x4)(0.f);
 #pragma unroll
-        for (int kq = 0; kq < 4; ++kq) {
-            if (kq > w) break;   // QKm is zero above the diagonal
+        for (int js = 0; js < 4; ++js) {
+            f16x8 ka[4], qa[4];
 #pragma unroll
-            for (int r = 0; r < 4; ++r) o = mfma4(qkm[kq][r], d[kq][r], o);
-        }
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int i = 16 * w + 4 * kk + r;
-            if (i < n)
-                y[(size_t)(t0 + i) * y_stride + (size_t)hv * CK_V + v0 + m] = f16_sat(o[r] * out_scale);
-        }
-
-        // C: S^T = e^{g_C} S^T + Kd^T Delta over this wave's k range
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb) st[kb] *= eC;
-#pragma unroll
-        for (int kq = 0; kq < 4; ++kq) {
-            // lane m of group kk receives K[16 kq + 4 kk + e][k0 + 16 kb + m], e = 0..3
-            const int row = 16 * kq + 4 * kk + (m >> 2);
-            f32x4 ka[2];
-#pragma unroll
-            for (int kb = 0; kb < 2; ++kb) {
-                const int pos = row * 64 + 32 * (kb ^ ((row >> 2) & 1)) + 8 * (m & 3);
-                const s16x4 kt = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                    (lds_s16x4*)((lds_char*)(uintptr_t)ksl_lds + pos));
-                const f16x4 kh = __builtin_bit_cast(f16x4, kt);
-#pragma unroll
-                for (int r = 0; r < 4; ++r) ka[kb][r] = (float)kh[r] * dk[kq][r];
+            for (int mb = 0; mb < 4; ++mb) {
+                ka[mb] = row_frag(sb + ST_K, mb, js, g, i);
+                qa[mb] = row_frag(sb + ST_Q, mb, js, g, i);
             }
 #pragma unroll
-            for (int r = 0; r < 4; ++r)
+            for (int mb = 0; mb < 4; ++mb) x[mb] = mfma16(ka[mb], sh[js], x[mb]);
 #pragma unroll
-                for (int kb = 0; kb < 2; ++kb) st[kb] = mfma4(ka[kb][r], d[kq][r], st[kb]);
+            for (int mb = 0; mb < 4; ++mb) x[mb] = mfma16(ka[mb], sl[js], x[mb]);
+#pragma unroll
+            for (int mb = 0; mb < 4; ++mb) qs[mb] = mfma16(qa[mb], sh[js], qs[mb]);
+#pragma unroll
+            for (int mb = 0; mb < 4; ++mb) qs[mb] = mfma16(qa[mb], sl[js], qs[mb]);
         }
-        // Unconditional (the last chunk re-reads its own operands): under a
-        // branch the compiler's wait for the K slice before the barrier could
-        // not count the loads issued after it and drained them all.
-        load_rest(min(c + 1, n_chunks - 1));
+
+        // Y = beta (V - e^g X) at tokens 16 mb + 4 g + r, column v0 + i
+        f32x4 yv[4];
+        float my = 0.f;
+#pragma unroll
+        for (int mb = 0; mb < 4; ++mb) {
+            const int tok = 16 * mb + 4 * g;
+            const int vr = tok + (i >> 2);
+            const s16x4 vraw = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (lds_s16x4*)(uintptr_t)(sb + ST_V + vr * (CS_VW * 2) + 32 * w + 8 * (i & 3)));
+            const f16x4 vv = __builtin_bit_cast(f16x4, vraw);
+            const f32x4 be = *(lds_f32x4*)(uintptr_t)(sw_ + WS_BETA + 4 * tok);
+            const f32x4 eg = *(lds_f32x4*)(uintptr_t)(sw_ + WS_EG + 4 * tok);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                yv[mb][r] = be[r] * ((float)vv[r] - eg[r] * (x[mb][r] * s_inv));
+                my = fmaxf(my, fabsf(yv[mb][r]));
+            }
+        }
+        float y_inv;
+        const float y_sc = pow2_scale<7>(wave_max(my), y_inv);
+        f16x8 yh[2], yl[2];
+#pragma unroll
+        for (int kq = 0; kq < 2; ++kq) split8(yv[2 * kq], yv[2 * kq + 1], y_sc, yh[kq], yl[kq]);
+
+        // Delta = T Y (three passes; T is zero above the diagonal, so rows 0..31
+        // take no columns 32..63)
+        f32x4 dl[4];
+        float md = 0.f, mo = 0.f;
+        const float d_un = sc[1] * y_inv;
+#pragma unroll
+        for (int mb = 0; mb < 4; ++mb) dl[mb] = (f32x4)(0.f);
+#pragma unroll
+        for (int kq = 0; kq < 2; ++kq) {
+            f16x8 th[4], tl[4];
+#pragma unroll
+            for (int mb = kq * 2; mb < 4; ++mb) {
+                const uint32_t fo = ((mb * 2 + kq) * 64 + l) * 16;
+                th[mb] = *(lds_f16x8*)(uintptr_t)(sw_ + WS_T_HI + fo);
+                tl[mb] = *(lds_f16x8*)(uintptr_t)(sw_ + WS_T_LO + fo);
+            }
+#pragma unroll
+            for (int mb = kq * 2; mb < 4; ++mb) dl[mb] = mfma16(th[mb], yh[kq], dl[mb]);
+#pragma unroll
+            for (int mb = kq * 2; mb < 4; ++mb) dl[mb] = mfma16(th[mb], yl[kq], dl[mb]);
+#pragma unroll
+            for (int mb = kq * 2; mb < 4; ++mb) dl[mb] = mfma16(tl[mb], yh[kq], dl[mb]);
+        }
+#pragma unroll
+        for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                dl[mb][r] *= d_un;
+                mo = fmaxf(mo, fabsf(dl[mb][r]));
+            }
+        // Delta' = e^{g_C - g} Delta for the state update and Delta for the
+        // output, each scaled and split
+        f32x4 dp[4];
+#pragma unroll
+        for (int mb = 0; mb < 4; ++mb) {
+            const f32x4 dk = *(lds_f32x4*)(uintptr_t)(sw_ + WS_DK + 4 * (16 * mb + 4 * g));
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                dp[mb][r] = dk[r] * dl[mb][r];
+                md = fmaxf(md, fabsf(dp[mb][r]));
+            }
+        }
+        float p_inv, o_inv;
+        const float p_sc = pow2_scale<7>(wave_max(md), p_inv);
+        const float o_sc = pow2_scale<7>(wave_max(mo), o_inv);
+        f16x8 ph[2], pl[2], oh[2], ol[2];
+#pragma unroll
+        for (int kq = 0; kq < 2; ++kq) {
+            split8(dp[2 * kq], dp[2 * kq + 1], p_sc, ph[kq], pl[kq]);
+            split8(dl[2 * kq], dl[2 * kq + 1], o_sc, oh[kq], ol[kq]);
+        }
+
+        // S^T = e^{g_C} S^T + K^T Delta' (K exact: two passes), in two halves
+        // of 4 k blocks
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            f32x4 u[4];
+#pragma unroll
+            for (int b = 0; b < 4; ++b) u[b] = (f32x4)(0.f);
+#pragma unroll
+            for (int kq = 0; kq < 2; ++kq) {
+                f16x8 ka[4];
+#pragma unroll
+                for (int b = 0; b < 4; ++b) ka[b] = col_frag(sb + ST_K, 4 * h + b, kq, g, i);
+#pragma unroll
+                for (int b = 0; b < 4; ++b) u[b] = mfma16(ka[b], ph[kq], u[b]);
+#pragma unroll
+                for (int b = 0; b < 4; ++b) u[b] = mfma16(ka[b], pl[kq], u[b]);
+            }
+#pragma unroll
+            for (int b = 0; b < 4; ++b)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    st[4 * h + b][r] = sc[0] * st[4 * h + b][r] + u[b][r] * p_inv;
+        }
+
+        // O = e^g Q S^T + (M o QK^T) Delta (three passes), accumulated scaled
+        // by 2^(kappa + eps)
+        const float o_un = sc[2] * o_inv;
+        const float o_up = 1.f / o_un;   // a power of two: exact
+        f32x4 o[4];
+#pragma unroll
+        for (int mb = 0; mb < 4; ++mb) {
+            const f32x4 eg = *(lds_f32x4*)(uintptr_t)(sw_ + WS_EG + 4 * (16 * mb + 4 * g));
+#pragma unroll
+            for (int r = 0; r < 4; ++r) o[mb][r] = eg[r] * (qs[mb][r] * s_inv) * o_up;
+        }
+#pragma unroll
+        for (int kq = 0; kq < 2; ++kq) {
+            f16x8 qh[4], ql[4];
+#pragma unroll
+            for (int mb = kq * 2; mb < 4; ++mb) {
+                const uint32_t fo = ((mb * 2 + kq) * 64 + l) * 16;
+                qh[mb] = *(lds_f16x8*)(uintptr_t)(sw_ + WS_Q_HI + fo);
+                ql[mb] = *(lds_f16x8*)(uintptr_t)(sw_ + WS_Q_LO + fo);
+            }
+#pragma unroll
+            for (int mb = kq * 2; mb < 4; ++mb) o[mb] = mfma16(qh[mb], oh[kq], o[mb]);
+#pragma unroll
+            for (int mb = kq * 2; mb < 4; ++mb) o[mb] = mfma16(qh[mb], ol[kq], o[mb]);
+#pragma unroll
+            for (int mb = kq * 2; mb < 4; ++mb) o[mb] = mfma16(ql[mb], oh[kq], o[mb]);
+        }
+        // y through this wave's LDS tile: element (token 16 mb + 4 g + r, row
+        // i) in, then lane l stores token l's 16 rows (32 bytes) with two
+        // 16-byte stores
+        const uint32_t yt = lds0 + ST_Y + w * (CK_C * 32);
+        typedef __attribute__((address_space(3))) f16 lds_f16w;
+#pragma unroll
+        for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                *(lds_f16w*)(uintptr_t)(yt + (16 * mb + 4 * g + r) * 32 + 2 * i) =
+                    f16_sat(o[mb][r] * o_un * out_scale);
+        const f16x8 y0 = *(lds_f16x8*)(uintptr_t)(yt + l * 32);
+        const f16x8 y1 = *(lds_f16x8*)(uintptr_t)(yt + l * 32 + 16);
+        if (n == CK_C || l < n) {
+            f16* yo = y + (size_t)(t0 + l) * y_stride + (size_t)hv * CK_V + v0;
+            *(f16x8*)yo = y0;
+            *(f16x8*)(yo + 8) = y1;
+        }
     }
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) *(f32x4*)(Sv + 16 * kb) = st[kb];
+    for (int kb8 = 0; kb8 < 8; ++kb8) *(f32x4*)(Sv + 16 * kb8) = st[kb8];
 }
 
 // The state pass's dynamic LDS is above the 64 KiB default: raised once per
@@ -403,7 +619,7 @@ extern "C" {
 size_t fl_gdn_chunked_work_bytes(int T, int n_vheads, int K, int V, int chunk) {
     if (T < 1 || n_vheads < 1 || K != CK_K || V != CK_V || chunk != CK_C) return 0;
     const size_t n_chunks = (size_t)(T + CK_C - 1) / CK_C;
-    return n_chunks * n_vheads * CK_BLK * sizeof(float);
+    return n_chunks * n_vheads * CK_BLK;
 }
 
 int fl_gdn_prefill_chunked(const void* q, const void* k, const void* v, const float* beta,
@@ -416,9 +632,12 @@ int fl_gdn_prefill_chunked(const void* q, const void* k, const void* v, const fl
     FL_REQUIRE(chunk == CK_C, "chunk == 64");
     FL_REQUIRE(T >= 1, "T >= 1");
     FL_REQUIRE(group >= 1 && (n_vheads - 1) / group < n_kheads, "n_vheads / group <= n_kheads");
-    FL_REQUIRE(qk_stride % 8 == 0 && ((uintptr_t)q & 15u) == 0 && ((uintptr_t)k & 15u) == 0,
-               "16-byte aligned q / k rows");
-    FL_REQUIRE(((uintptr_t)S & 15u) == 0 && ((uintptr_t)work & 15u) == 0, "16-byte aligned S, work");
+    FL_REQUIRE(qk_stride % 8 == 0 && v_stride % 8 == 0 && ((uintptr_t)q & 15u) == 0 &&
+                   ((uintptr_t)k & 15u) == 0 && ((uintptr_t)v & 15u) == 0,
+               "16-byte aligned q / k / v rows");
+    FL_REQUIRE(((uintptr_t)S & 15u) == 0 && ((uintptr_t)work & 15u) == 0 &&
+                   ((uintptr_t)y & 15u) == 0 && y_stride % 8 == 0,
+               "16-byte aligned S, work and y rows");
     const size_t need = fl_gdn_chunked_work_bytes(T, n_vheads, K, V, chunk);
     if (work_bytes < need) {
         fl::set_error("work: %zu bytes, fl_gdn_chunked_work_bytes asks %zu", work_bytes, need);
@@ -426,15 +645,16 @@ int fl_gdn_prefill_chunked(const void* q, const void* k, const void* v, const fl
     }
     const int n_chunks = (T + CK_C - 1) / CK_C;
     hipLaunchKernelGGL(chunk_prep_kernel, dim3(n_chunks, n_vheads), dim3(256), 0,
-                       (hipStream_t)stream, (const f16*)q, (const f16*)k, (const f16*)v, beta,
-                       decay, T, n_vheads, qk_stride, v_stride, group, (float*)work);
+                       (hipStream_t)stream, (const f16*)q, (const f16*)k, beta, decay, T, n_vheads,
+                       qk_stride, group, (char*)work);
     int rc = fl::check_launch("gdn_chunk_prep");
     if (rc) return rc;
     rc = raise_state_lds_limit();
     if (rc) return rc;
-    hipLaunchKernelGGL(chunk_state_kernel, dim3(n_vheads, CK_V / CS_ROWS), dim3(256), CS_LDS,
-                       (hipStream_t)stream, (const f16*)q, (const f16*)k, S, (f16*)y, T, n_vheads,
-                       qk_stride, y_stride, out_scale, group, (const float*)work);
+    hipLaunchKernelGGL(chunk_state_kernel, dim3(n_vheads * (CK_V / CS_VW)), dim3(64 * CS_WAVES),
+                       CS_LDS, (hipStream_t)stream, (const f16*)q, (const f16*)k, (const f16*)v, S,
+                       (f16*)y, T, n_vheads, qk_stride, v_stride, y_stride, out_scale, group,
+                       (const char*)work);
     return fl::check_launch("gdn_chunk_state");
 }
 

@@ -362,9 +362,10 @@ int fl_rmsnorm_gated(const void* o, const void* z, const float* w, void* y, int 
  * between chunks; S in place, y as fl_gdn_scan. NOT in the reference (the
  * reference runs gdn_scan sequentially and names the chunked scan as undone,
  * kernels.cu:1788-1791); it replaces that call (runtime.py:3094-3100) for
- * prefill. work: caller scratch of fl_gdn_chunked_work_bytes(...) bytes (the
- * per-chunk W, U and decayed Q K^T of the WY form). chunk == 64,
- * K == V == 128. */
+ * prefill. work: caller scratch of fl_gdn_chunked_work_bytes(...) bytes (per
+ * chunk and v head, T = (I + A)^-1 and the decayed Q K^T of the WY form as
+ * fp16 MFMA operands, and the gates). chunk == 64, K == V == 128; q, k, v, S,
+ * work and the rows of y (y_stride % 8 == 0) 16-byte aligned. */
 size_t fl_gdn_chunked_work_bytes(int T, int n_vheads, int K, int V, int chunk);
 int fl_gdn_prefill_chunked(const void* q, const void* k, const void* v, const float* beta,
                            const float* decay, float* S, void* y, int T, int n_kheads,

@@ -344,6 +344,17 @@ def test_chunked_vs_recurrence(fl, dev, orc, T):
     assert rel_err(Sh, S_r) <= STATE_RTOL
     err, ok = close(y.cpu().numpy(), y_r, 2e-3, 1e-2)
     assert ok, f"T={T}: max|dy| {err}"
+    # y against each (token, head) row's RMS, beyond one fp16 ulp of rounding:
+    # the gated norm after the scan divides every row by its RMS, so an output
+    # error inside y's own tolerance but large in a row whose terms cancel
+    # would surface there. Emulated: fp32 products <= 1.3e-3, products on
+    # split fp16 halves <= 2e-4, the output on one fp16 pass 1.6e-3 - 5.3e-3.
+    yg = y.cpu().numpy().reshape(T, NV, 128).astype(np.float64)
+    yr = y_r.reshape(T, NV, 128).astype(np.float64)
+    rms = np.sqrt((yr ** 2).mean(axis=-1, keepdims=True)) + 1e-30
+    beyond = float((np.maximum(np.abs(yg - yr) - 2.0 ** -10 * np.abs(yr), 0) / rms).max())
+    print(f"chunked T={T}: y error against the row RMS beyond 1 ulp {beyond:.2e}")
+    assert beyond <= 1.5e-3, f"T={T}: y error against the row RMS {beyond:.2e}"
 
 
 # the 16-lanes-a-row kernel takes calls of >= 8192 rows with 16-byte aligned
