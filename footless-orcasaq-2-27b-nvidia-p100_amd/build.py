@@ -38,10 +38,13 @@ HIPCC_FLAGS = [
 # accumulators are AGPRs held by inline asm); no NaNs and IEEE mode off, so
 # the score max is plain v_max / v_max3 without NaN-quieting canonicalisation
 # (scores are finite or -inf). attn_decode: its accumulators (scores read by the
-# softmax, O rescaled in place) in VGPRs as well.
+# softmax, O rescaled in place) in VGPRs as well. gdn_chunk: the products'
+# results are split, scaled and fed back as operands by VALU code; in AGPRs
+# each would be copied out first.
 FILE_FLAGS = {
     "attn_prefill": ["-mllvm", "-amdgpu-mfma-vgpr-form", "-fno-honor-nans", "-mno-amdgpu-ieee"],
     "attn_decode": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+    "gdn_chunk": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
 }
 
 

@@ -21,10 +21,11 @@
 // Two launches. chunk_prep_kernel, every (chunk, v head) in parallel: K K^T
 // and Q K^T on MFMA, the prefix sums, A, T by forward substitution in fp32,
 // the gates, and T and M o QK^T written as fp16 MFMA operands.
-// chunk_state_kernel: one wavefront per 16 state rows (v) of a v head, all
-// 128 k columns of them in fp32 registers, sequential over the chunks with no
-// barrier or exchange on its own chain; the two wavefronts of a workgroup
-// share each chunk's operands, copied HBM -> LDS one chunk ahead.
+// chunk_state_kernel: a state wavefront per 16 state rows (v) of a v head,
+// all 128 k columns of them in fp32 registers, sequential over the chunks; a
+// paired output wavefront takes its Q S0^T and Delta through LDS a chunk later,
+// forms O and stores y, and issues the HBM -> LDS copies of the operands one
+// chunk ahead, so the state chain carries only its own products.
 //
 // Precision. Every product runs on v_mfma_f32_16x16x32_f16 (fp16 inputs,
 // fp32 accumulate: the product of two fp16 values is exact in fp32). K, Q and
@@ -275,133 +276,187 @@ chunk_prep_kernel(const f16* __restrict__ q, const f16* __restrict__ k,
 }
 
 // ---------------------------------------------------------------------------
-// chunk_state_kernel: CS_WAVES wavefronts a workgroup, 16 state rows each
+// chunk_state_kernel: 32 state rows (v) of a v head a workgroup, 4 wavefronts.
+// Waves 0 and 1 (state waves) each hold 16 rows of S and run the recurrence's
+// chain: X = K S^T and Q S^T, Y, Delta = T Y, the state update. Waves 2 and 3
+// (output waves) each take a state wave's Q S^T and Delta a chunk later, form
+// O and store y, and issue every HBM -> LDS copy, so the state waves' chain
+// carries neither.
 // ---------------------------------------------------------------------------
-constexpr int CS_WAVES = 4;
-constexpr int CS_VW = 16 * CS_WAVES;   // state rows (v) a workgroup
-// One LDS stage: K and Q rows [64][256 B] (16-byte chunk c of row r at
-// c ^ (r & 15)), the workgroup's V columns [64][CS_VW] fp16, then the
-// workspace block (T and M o QK^T operands, the gates) as it is in HBM.
-constexpr int ST_K = 0, ST_Q = 16384, ST_V = 32768, ST_W = ST_V + CK_C * CS_VW * 2;
-constexpr int ST_BYTES = ST_W + CK_BLK;
-// then each wave's y tile [64 tokens][16 rows] fp16, written in the result
-// layout and read back as rows for 16-byte stores
-constexpr int ST_Y = 2 * ST_BYTES;
-constexpr int CS_LDS = ST_Y + CS_WAVES * CK_C * 16 * 2;
-static_assert(CS_LDS <= 160 * 1024, "two stages and the y tiles in 160 KiB of LDS");
-// copy instructions (1 KiB each, 16 B a lane) of a stage
-constexpr int CP_K = 16, CP_V = CK_C * CS_VW * 2 / 1024, CP_W = CK_BLK / 1024;
-constexpr int CP_ALL = 2 * CP_K + CP_V + CP_W;
-static_assert(CK_BLK % 1024 == 0 && (CK_C * CS_VW * 2) % 1024 == 0, "whole copy instructions");
-// y stores a wavefront issues a chunk (the vmcnt wait for the next stage's
-// copies, issued before them, counts them)
+constexpr int CS_ROWS = 32;   // state rows (v) a workgroup
+// A stage (the state waves' operands of a chunk): K and Q rows [64][256 B]
+// (16-byte chunk c of row r at c ^ (r & 15)), V columns [64][CS_ROWS] fp16,
+// T's hi / lo operands and the gates KiB (workspace bytes 0 .. 16 KiB and
+// 32 .. 33 KiB, as in HBM)
+constexpr int SA_K = 0, SA_Q = 16384, SA_V = 32768, SA_T = SA_V + CK_C * CS_ROWS * 2,
+              SA_G = SA_T + 16384, SA_BYTES = SA_G + 1024;
+// B stage (the output waves'): M o QK^T's hi / lo operands (workspace bytes
+// 16 .. 32 KiB) and the gates KiB
+constexpr int SB_Q = 0, SB_G = 16384, SB_BYTES = SB_G + 1024;
+// offsets in the gates KiB: beta, e^g, e^{g_C - g} [64] f32, then e^{g_C},
+// 2^-tau, 2^-kappa
+constexpr int G_BETA = WS_BETA - WS_BETA, G_EG = WS_EG - WS_BETA, G_DK = WS_DK - WS_BETA,
+              G_SC = WS_SC - WS_BETA;
+static_assert(WS_T_HI == 0 && WS_T_LO == 8192 && WS_Q_HI == 16384 && WS_Q_LO == 24576 &&
+                  CK_BLK == WS_BETA + 1024,
+              "workspace block: T, then M o QK^T, then the gates KiB");
+// LDS: two A stages, two B stages, the hand-over (each state wave's Q S^T
+// 2^-s and Delta, [8][64 lanes] f32x4) and each output wave's y tile
+// [64 tokens][16 rows] fp16
+constexpr int L_A = 0, L_B = 2 * SA_BYTES, L_X = L_B + 2 * SB_BYTES, X_WAVE = 8 * 64 * 16,
+              L_Y = L_X + 2 * X_WAVE, CS_LDS = L_Y + 2 * CK_C * 16 * 2;
+static_assert(CS_LDS <= 160 * 1024, "the state pass's LDS fits 160 KiB");
+// y stores an output wave issues a chunk, after that chunk's copies
 constexpr int CS_NSTORE = 2;
 
-// The copies of chunk c's stage, instructions w, w + CS_WAVES, .. by wave w.
-// Rows past the chunk's last token repeat it (beta is 0 there). The LDS
-// destination (m0) is marked uniform: the compiler cannot prove it and would
-// wrap each copy in a loop over the distinct values.
-__device__ __forceinline__ void cs_issue(uint32_t dst, const char* kb, const char* qb,
-                                         const char* vb, const char* wb, int t0, int n,
-                                         int qk_bytes, int v_bytes, int w, int lane) {
-#pragma unroll
-    for (int j = 0; j < (CP_ALL + CS_WAVES - 1) / CS_WAVES; ++j) {
-        const int m = CS_WAVES * j + w;
-        if (m >= CP_ALL) break;
-        if (m < 2 * CP_K) {   // K (m < 16) or Q rows 4 (m % 16) .. + 3
-            const int isq = m >= CP_K, nn = isq ? m - CP_K : m;
-            const int r = 4 * nn + (lane >> 4), p = lane & 15;
-            const char* src = (isq ? qb : kb) + (size_t)(t0 + min(r, n - 1)) * qk_bytes +
-                              16 * (p ^ (r & 15));
-            copy16_v(src, __builtin_amdgcn_readfirstlane(dst + (isq ? ST_Q : ST_K) + 1024 * nn));
-        } else if (m < 2 * CP_K + CP_V) {   // V rows, CS_VW * 2 bytes each
-            constexpr int PR = CS_VW * 2 / 16;   // 16-byte pieces a row
-            const int nn = m - 2 * CP_K;
-            const int r = (64 / PR) * nn + lane / PR, p = lane % PR;
-            copy16_v(vb + (size_t)(t0 + min(r, n - 1)) * v_bytes + 16 * p,
-                     __builtin_amdgcn_readfirstlane(dst + ST_V + 1024 * nn));
-        } else {   // the workspace block, as it is
-            const int nn = m - 2 * CP_K - CP_V;
-            copy16_v(wb + 1024 * nn + 16 * lane, __builtin_amdgcn_readfirstlane(dst + ST_W + 1024 * nn));
-        }
-    }
+typedef __attribute__((address_space(3))) f32x4 lds_f32x4w;
+typedef __attribute__((address_space(3))) f16 lds_f16w;
+
+// Per-lane source offsets of output wave wb's copies of a 64-token chunk (the
+// base is scalar): K / Q copy n (n = 2 j + wb) brings rows 4 n .. 4 n + 3,
+// lane -> row 8 j + rr, rr = 4 wb + lane / 16, and 16-byte chunk
+// (lane % 16) ^ (row & 15), row & 15 = rr + 8 (j & 1); V copy n rows
+// 16 n + lane / 4, 16 bytes (lane % 4) of the workgroup's 64-byte slice; a
+// workspace copy 16 bytes a lane.
+struct CsOff {
+    uint32_t kq[2], v, w;
+};
+__device__ __forceinline__ CsOff cs_offsets(int qk_bytes, int v_bytes, int wb, int lane) {
+    const int rr = 4 * wb + (lane >> 4), p = lane & 15;
+    return {{(uint32_t)(rr * qk_bytes + 16 * (p ^ rr)),
+             (uint32_t)(rr * qk_bytes + 16 * (p ^ (rr + 8)))},
+            (uint32_t)((lane >> 2) * v_bytes + 16 * (lane & 3)), (uint32_t)(16 * lane)};
 }
 
-// A operand of X = K S^T (or Q S^T) for row block mb, k-step js: row
-// 16 mb + i at k = 32 js + kap(g, e): two 8-byte reads of the swizzled row
-__device__ __forceinline__ f16x8 row_frag(uint32_t base, int mb, int js, int g, int i) {
-    const int row = 16 * mb + i;
-    const uint32_t rb = base + row * 256 + 8 * (g & 1);
-    const f16x4 a = *(lds_f16x4*)(uintptr_t)(rb + 16 * ((4 * js + (g >> 1)) ^ (row & 15)));
-    const f16x4 b = *(lds_f16x4*)(uintptr_t)(rb + 16 * ((4 * js + 2 + (g >> 1)) ^ (row & 15)));
+// Output wave wb's half of the copies of chunk c's A stage into dst: 8 K, 8 Q,
+// 2 V and 8 T copies, and (wb = 0) the gates KiB. Rows past the last token
+// repeat it (beta is 0 there).
+__device__ __forceinline__ void cs_copy_a(uint32_t dst, const char* kb, const char* qb,
+                                          const char* vb, const char* wk, int t0, int T,
+                                          int qk_bytes, int v_bytes, int wb, int lane,
+                                          const CsOff& o) {
+    if (T - t0 >= CK_C) {
+        const char* kt = kb + (size_t)t0 * qk_bytes;
+        const char* qt = qb + (size_t)t0 * qk_bytes;
+        const char* vt = vb + (size_t)t0 * v_bytes;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int n = 2 * j + wb;
+            copy16(kt + (size_t)(8 * j) * qk_bytes, o.kq[j & 1], dst + SA_K + 1024 * n);
+            copy16(qt + (size_t)(8 * j) * qk_bytes, o.kq[j & 1], dst + SA_Q + 1024 * n);
+        }
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int n = 2 * j + wb;
+            copy16(vt + (size_t)(16 * n) * v_bytes, o.v, dst + SA_V + 1024 * n);
+        }
+    } else {
+        const int last = T - t0 - 1;
+        const int rr = 4 * wb + (lane >> 4), p = lane & 15;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int n = 2 * j + wb, r = 8 * j + rr;
+            const size_t ro = (size_t)(t0 + min(r, last)) * qk_bytes + 16 * (p ^ (r & 15));
+            copy16_v(kb + ro, __builtin_amdgcn_readfirstlane(dst + SA_K + 1024 * n));
+            copy16_v(qb + ro, __builtin_amdgcn_readfirstlane(dst + SA_Q + 1024 * n));
+        }
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int n = 2 * j + wb, r = 16 * n + (lane >> 2);
+            copy16_v(vb + (size_t)(t0 + min(r, last)) * v_bytes + 16 * (lane & 3),
+                     __builtin_amdgcn_readfirstlane(dst + SA_V + 1024 * n));
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int n = 2 * j + wb;
+        copy16(wk + 1024 * n, o.w, dst + SA_T + 1024 * n);
+    }
+    if (wb == 0) copy16(wk + WS_BETA, o.w, dst + SA_G);
+}
+
+// Output wave wb's half of the copies of chunk c's B stage: 8 M o QK^T copies
+// and (wb = 1) the gates KiB.
+__device__ __forceinline__ void cs_copy_b(uint32_t dst, const char* wk, int wb, const CsOff& o) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int n = 2 * j + wb;
+        copy16(wk + WS_Q_HI + 1024 * n, o.w, dst + SB_Q + 1024 * n);
+    }
+    if (wb == 1) copy16(wk + WS_BETA, o.w, dst + SB_G);
+}
+
+// The lane's parts of the swizzled K / Q row addresses, fixed for the kernel:
+// the A operand of X = K S^T (or Q S^T) for row block mb, k-step js holds row
+// 16 mb + i at k = 32 js + kap(g, e), two 8-byte reads at 16-byte chunks
+// (4 js + 2 h + (g >> 1)) ^ i, h = 0, 1 (row & 15 = i for every mb; mb adds
+// 16 rows = 4096 bytes)
+__device__ __forceinline__ void row_offsets(int g, int i, uint32_t (&ro)[8]) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+        ro[j] = i * 256 + 8 * (g & 1) + 16 * ((2 * j + (g >> 1)) ^ i);
+}
+// stage base (scalar) + lane part, once a chunk: an opaque vector sum, so the
+// constant parts of each read (row block, K or Q, k step) stay in the LDS
+// instruction's offset field instead of each read adding its own base
+__device__ __forceinline__ uint32_t lane_addr(uint32_t sbase, uint32_t lane_part) {
+    uint32_t r;
+    asm("v_add_u32 %0, %1, %2" : "=v"(r) : "s"(sbase), "v"(lane_part));
+    return r;
+}
+__device__ __forceinline__ f16x8 row_frag(const uint32_t (&ra)[8], uint32_t off, int mb, int js) {
+    const f16x4 a = *(lds_f16x4*)(uintptr_t)(ra[2 * js] + off + 4096 * mb);
+    const f16x4 b = *(lds_f16x4*)(uintptr_t)(ra[2 * js + 1] + off + 4096 * mb);
     return (f16x8){a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
 }
 
 // A operand of K^T Delta' for k rows 16 kb .., token step kq: lane 16 g + i
 // gets K[32 kq + kap(g, e)][16 kb + i] by two transposed reads (each: the
 // group's 16 lanes read a 4-row x 16-column block, lane i addressing row
-// i / 4, columns 4 (i % 4) .., and receiving column i of the four rows)
-__device__ __forceinline__ f16x8 col_frag(uint32_t base, int kb, int kq, int g, int i) {
-    const int c16 = 2 * kb + ((i & 3) >> 1), half = 8 * (i & 1);
-    const int r0 = 32 * kq + 4 * g + (i >> 2), r1 = r0 + 16;
-    const s16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-        (lds_s16x4*)(uintptr_t)(base + r0 * 256 + 16 * (c16 ^ (r0 & 15)) + half));
-    const s16x4 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-        (lds_s16x4*)(uintptr_t)(base + r1 * 256 + 16 * (c16 ^ (r1 & 15)) + half));
+// r = 32 kq + 4 g + i / 4 (+ 16), columns 4 (i % 4) .., and receiving column
+// i of the four rows). r & 15 = 4 g + i / 4 for both reads and every kq, so the
+// lane's part of the address is fixed per kb; kq and the second read add
+// 8192 and 4096 bytes.
+__device__ __forceinline__ void col_offsets(int g, int i, uint32_t (&co)[8]) {
+    const int rr = 4 * g + (i >> 2);
+#pragma unroll
+    for (int kb = 0; kb < 8; ++kb)
+        co[kb] = rr * 256 + 16 * ((2 * kb + ((i & 3) >> 1)) ^ rr) + 8 * (i & 1);
+}
+__device__ __forceinline__ f16x8 col_frag(const uint32_t (&ca)[8], int kb, int kq) {
+    const uint32_t a0 = ca[kb] + SA_K + 8192 * kq;
+    const s16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(uintptr_t)a0);
+    const s16x4 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(uintptr_t)(a0 + 4096));
     const f16x4 ah = __builtin_bit_cast(f16x4, a), bh = __builtin_bit_cast(f16x4, b);
     return (f16x8){ah[0], ah[1], ah[2], ah[3], bh[0], bh[1], bh[2], bh[3]};
 }
 
-__global__ void __launch_bounds__(64 * CS_WAVES)
-chunk_state_kernel(const f16* __restrict__ q, const f16* __restrict__ k,
-                   const f16* __restrict__ v, float* __restrict__ S, f16* __restrict__ y, int T,
-                   int n_vheads, int qk_stride, int v_stride, int y_stride, float out_scale,
-                   int group, const char* __restrict__ work) {
-    extern __shared__ __attribute__((aligned(16))) char smem[];
-    // a v head's workgroups are n_vheads apart in the flat id, so with
-    // n_vheads a multiple of 8 (48 here) they land on one XCD (dispatch goes
-    // round robin over the 8) and share its L2
-    const int hv = blockIdx.x % n_vheads, part = blockIdx.x / n_vheads, hk = hv / group;
-    const int tid = threadIdx.x, l = tid & 63;
-    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int g = l >> 4, i = l & 15;
-    const int vw0 = part * CS_VW, v0 = vw0 + 16 * w;
-    const uint32_t lds0 = (uint32_t)(uintptr_t)((__attribute__((address_space(3))) char*)smem);
-    const char* kb = uniform_ptr((const char*)(k + (size_t)hk * CK_K));
-    const char* qb = uniform_ptr((const char*)(q + (size_t)hk * CK_K));
-    const char* vb = uniform_ptr((const char*)(v + (size_t)hv * CK_V + vw0));
-    const int qk_bytes = 2 * qk_stride, v_bytes = 2 * v_stride;
-    const int n_chunks = (T + CK_C - 1) / CK_C;
-    auto wblock = [&](int c) {
-        return uniform_ptr(work + ((size_t)c * n_vheads + hv) * CK_BLK);
-    };
-
+// A state wave: 16 rows v0 .. v0 + 15 of the state, chunk after chunk.
+// Barriers (every wave of the workgroup passes the same sequence): E(-1),
+// then per chunk c: M(c-1) (the output wave has read the hand-over of c-1),
+// E(c) (the hand-over of c written; A stage c free for the copies of c + 2).
+__device__ __forceinline__ void cs_state_wave(float* __restrict__ S, uint32_t lds0, int hv, int v0,
+                                              int wa, int g, int i, int l, int n_chunks) {
+    uint32_t ro[8], co[8];
+    row_offsets(g, i, ro);
+    col_offsets(g, i, co);
     // the state, st[kb][r] = S[v0 + i][16 kb + 4 g + r]: the result layout of
     // the 16 x 16 blocks of S^T
     float* Sv = S + ((size_t)hv * CK_V + v0 + i) * CK_K + 4 * g;
     f32x4 st[8];
 #pragma unroll
     for (int kb8 = 0; kb8 < 8; ++kb8) st[kb8] = *(const f32x4*)(Sv + 16 * kb8);
-
-    cs_issue(lds0, kb, qb, vb, wblock(0), 0, min(CK_C, T), qk_bytes, v_bytes, w, l);
+    tile_done();   // E(-1): stages 0 and 1 landed
     for (int c = 0; c < n_chunks; ++c) {
-        const int t0 = c * CK_C;
-        const int n = min(CK_C, T - t0);
-        const uint32_t sb = lds0 + (c & 1) * ST_BYTES;
-        // this wave's copies of the stage landed (after them it issued only the
-        // previous chunk's y stores), then every wave's, and every wave is
-        // done with the other stage, which the next copies refill
-        if (c == 0) {
-            WAIT_VMCNT(0);
-        } else {
-            WAIT_VMCNT(CS_NSTORE);
+        const uint32_t sb = lds0 + L_A + (c & 1) * SA_BYTES;
+        const uint32_t sg = sb + SA_G;
+        uint32_t ra[8], ca[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            ra[j] = lane_addr(sb, ro[j]);
+            ca[j] = lane_addr(sb, co[j]);
         }
-        tile_done();
-        if (c + 1 < n_chunks)
-            cs_issue(lds0 + ((c + 1) & 1) * ST_BYTES, kb, qb, vb, wblock(c + 1), t0 + CK_C,
-                     min(CK_C, T - t0 - CK_C), qk_bytes, v_bytes, w, l);
-        const uint32_t sw_ = sb + ST_W;
-        const f32x4 sc = *(lds_f32x4*)(uintptr_t)(sw_ + WS_SC);   // e^{g_C}, 2^-tau, 2^-kappa
+        const f32x4 sc = *(lds_f32x4*)(uintptr_t)(sg + G_SC);   // e^{g_C}, 2^-tau, 2^-kappa
 
         // the state, scaled and split: B operands of the four k-steps
         float ms = 0.f;
@@ -426,8 +481,8 @@ chunk_state_kernel(const f16* __restrict__ q, const f16* __restrict__ k,
             f16x8 ka[4], qa[4];
 #pragma unroll
             for (int mb = 0; mb < 4; ++mb) {
-                ka[mb] = row_frag(sb + ST_K, mb, js, g, i);
-                qa[mb] = row_frag(sb + ST_Q, mb, js, g, i);
+                ka[mb] = row_frag(ra, SA_K, mb, js);
+                qa[mb] = row_frag(ra, SA_Q, mb, js);
             }
 #pragma unroll
             for (int mb = 0; mb < 4; ++mb) x[mb] = mfma16(ka[mb], sh[js], x[mb]);
@@ -447,10 +502,10 @@ chunk_state_kernel(const f16* __restrict__ q, const f16* __restrict__ k,
             const int tok = 16 * mb + 4 * g;
             const int vr = tok + (i >> 2);
             const s16x4 vraw = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                (lds_s16x4*)(uintptr_t)(sb + ST_V + vr * (CS_VW * 2) + 32 * w + 8 * (i & 3)));
+                (lds_s16x4*)(uintptr_t)(sb + SA_V + vr * (CS_ROWS * 2) + 32 * wa + 8 * (i & 3)));
             const f16x4 vv = __builtin_bit_cast(f16x4, vraw);
-            const f32x4 be = *(lds_f32x4*)(uintptr_t)(sw_ + WS_BETA + 4 * tok);
-            const f32x4 eg = *(lds_f32x4*)(uintptr_t)(sw_ + WS_EG + 4 * tok);
+            const f32x4 be = *(lds_f32x4*)(uintptr_t)(sg + G_BETA + 4 * tok);
+            const f32x4 eg = *(lds_f32x4*)(uintptr_t)(sg + G_EG + 4 * tok);
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 yv[mb][r] = be[r] * ((float)vv[r] - eg[r] * (x[mb][r] * s_inv));
@@ -466,7 +521,7 @@ chunk_state_kernel(const f16* __restrict__ q, const f16* __restrict__ k,
         // Delta = T Y (three passes; T is zero above the diagonal, so rows 0..31
         // take no columns 32..63)
         f32x4 dl[4];
-        float md = 0.f, mo = 0.f;
+        float md = 0.f;
         const float d_un = sc[1] * y_inv;
 #pragma unroll
         for (int mb = 0; mb < 4; ++mb) dl[mb] = (f32x4)(0.f);
@@ -476,8 +531,8 @@ chunk_state_kernel(const f16* __restrict__ q, const f16* __restrict__ k,
 #pragma unroll
             for (int mb = kq * 2; mb < 4; ++mb) {
                 const uint32_t fo = ((mb * 2 + kq) * 64 + l) * 16;
-                th[mb] = *(lds_f16x8*)(uintptr_t)(sw_ + WS_T_HI + fo);
-                tl[mb] = *(lds_f16x8*)(uintptr_t)(sw_ + WS_T_LO + fo);
+                th[mb] = *(lds_f16x8*)(uintptr_t)(sb + SA_T + WS_T_HI + fo);
+                tl[mb] = *(lds_f16x8*)(uintptr_t)(sb + SA_T + WS_T_LO + fo);
             }
 #pragma unroll
             for (int mb = kq * 2; mb < 4; ++mb) dl[mb] = mfma16(th[mb], yh[kq], dl[mb]);
@@ -486,34 +541,23 @@ chunk_state_kernel(const f16* __restrict__ q, const f16* __restrict__ k,
 #pragma unroll
             for (int mb = kq * 2; mb < 4; ++mb) dl[mb] = mfma16(tl[mb], yh[kq], dl[mb]);
         }
-#pragma unroll
-        for (int mb = 0; mb < 4; ++mb)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                dl[mb][r] *= d_un;
-                mo = fmaxf(mo, fabsf(dl[mb][r]));
-            }
-        // Delta' = e^{g_C - g} Delta for the state update and Delta for the
-        // output, each scaled and split
+        // Delta' = e^{g_C - g} Delta for the state update, scaled and split
         f32x4 dp[4];
 #pragma unroll
         for (int mb = 0; mb < 4; ++mb) {
-            const f32x4 dk = *(lds_f32x4*)(uintptr_t)(sw_ + WS_DK + 4 * (16 * mb + 4 * g));
+            const f32x4 dk = *(lds_f32x4*)(uintptr_t)(sg + G_DK + 4 * (16 * mb + 4 * g));
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
+                dl[mb][r] *= d_un;
                 dp[mb][r] = dk[r] * dl[mb][r];
                 md = fmaxf(md, fabsf(dp[mb][r]));
             }
         }
-        float p_inv, o_inv;
+        float p_inv;
         const float p_sc = pow2_scale<7>(wave_max(md), p_inv);
-        const float o_sc = pow2_scale<7>(wave_max(mo), o_inv);
-        f16x8 ph[2], pl[2], oh[2], ol[2];
+        f16x8 ph[2], pl[2];
 #pragma unroll
-        for (int kq = 0; kq < 2; ++kq) {
-            split8(dp[2 * kq], dp[2 * kq + 1], p_sc, ph[kq], pl[kq]);
-            split8(dl[2 * kq], dl[2 * kq + 1], o_sc, oh[kq], ol[kq]);
-        }
+        for (int kq = 0; kq < 2; ++kq) split8(dp[2 * kq], dp[2 * kq + 1], p_sc, ph[kq], pl[kq]);
 
         // S^T = e^{g_C} S^T + K^T Delta' (K exact: two passes), in two halves
         // of 4 k blocks
@@ -526,7 +570,7 @@ chunk_state_kernel(const f16* __restrict__ q, const f16* __restrict__ k,
             for (int kq = 0; kq < 2; ++kq) {
                 f16x8 ka[4];
 #pragma unroll
-                for (int b = 0; b < 4; ++b) ka[b] = col_frag(sb + ST_K, 4 * h + b, kq, g, i);
+                for (int b = 0; b < 4; ++b) ka[b] = col_frag(ca, 4 * h + b, kq);
 #pragma unroll
                 for (int b = 0; b < 4; ++b) u[b] = mfma16(ka[b], ph[kq], u[b]);
 #pragma unroll
@@ -539,16 +583,84 @@ chunk_state_kernel(const f16* __restrict__ q, const f16* __restrict__ k,
                     st[4 * h + b][r] = sc[0] * st[4 * h + b][r] + u[b][r] * p_inv;
         }
 
-        // O = e^g Q S^T + (M o QK^T) Delta (three passes), accumulated scaled
-        // by 2^(kappa + eps)
+        // hand Q S0^T and Delta to the output wave (after it has read the
+        // previous chunk's)
+        tile_done();   // M(c-1)
+        const uint32_t xo = lds0 + L_X + wa * X_WAVE + l * 16;
+#pragma unroll
+        for (int mb = 0; mb < 4; ++mb) {
+            *(lds_f32x4w*)(uintptr_t)(xo + 1024 * mb) = qs[mb] * s_inv;
+            *(lds_f32x4w*)(uintptr_t)(xo + 1024 * (4 + mb)) = dl[mb];
+        }
+        tile_done();   // E(c)
+    }
+#pragma unroll
+    for (int kb8 = 0; kb8 < 8; ++kb8) *(f32x4*)(Sv + 16 * kb8) = st[kb8];
+}
+
+// An output wave: the paired state wave's rows, a chunk behind it. y at token
+// t = 16 mb + 4 g + r, row v0 + i: O = e^g Q S0^T + (M o QK^T) Delta (three
+// passes), accumulated scaled by 2^(kappa + eps). Barriers: E(-1), M(-1), then
+// per chunk c: E(c), and M(c) but for the last chunk.
+__device__ __forceinline__ void cs_output_wave(const f16* q, const f16* k, const f16* v,
+                                               f16* __restrict__ y, const char* work,
+                                               uint32_t lds0, int T, int n_vheads, int hv, int hk,
+                                               int vw0, int v0, int wb, int g, int i, int l,
+                                               int n_chunks, int qk_bytes, int v_bytes,
+                                               int y_stride, float out_scale) {
+    const char* kb = uniform_ptr((const char*)(k + (size_t)hk * CK_K));
+    const char* qb = uniform_ptr((const char*)(q + (size_t)hk * CK_K));
+    const char* vb = uniform_ptr((const char*)(v + (size_t)hv * CK_V + vw0));
+    auto wblock = [&](int c) {
+        return uniform_ptr(work + ((size_t)c * n_vheads + hv) * CK_BLK);
+    };
+    const CsOff off = cs_offsets(qk_bytes, v_bytes, wb, l);
+    auto copy_a = [&](int c) {
+        cs_copy_a(lds0 + L_A + (c & 1) * SA_BYTES, kb, qb, vb, wblock(c), c * CK_C, T, qk_bytes,
+                  v_bytes, wb, l, off);
+    };
+    auto copy_b = [&](int c) { cs_copy_b(lds0 + L_B + (c & 1) * SB_BYTES, wblock(c), wb, off); };
+    copy_a(0);
+    copy_b(0);
+    if (n_chunks > 1) copy_a(1);
+    WAIT_VMCNT(0);
+    tile_done();   // E(-1)
+    tile_done();   // M(-1)
+    const uint32_t yt = lds0 + L_Y + wb * (CK_C * 32);
+    for (int c = 0; c < n_chunks; ++c) {
+        // this wave's copies for chunk c (B stage) and c + 1 (A stage) landed;
+        // only this wave's y stores of chunk c - 1 were issued after them
+        WAIT_VMCNT(CS_NSTORE);
+        tile_done();   // E(c)
+        if (c + 2 < n_chunks) copy_a(c + 2);
+        if (c + 1 < n_chunks) copy_b(c + 1);
+        const uint32_t xo = lds0 + L_X + wb * X_WAVE + l * 16;
+        const uint32_t sbb = lds0 + L_B + (c & 1) * SB_BYTES;
+        f32x4 qs[4], dl[4];
+#pragma unroll
+        for (int mb = 0; mb < 4; ++mb) {
+            qs[mb] = *(lds_f32x4*)(uintptr_t)(xo + 1024 * mb);
+            dl[mb] = *(lds_f32x4*)(uintptr_t)(xo + 1024 * (4 + mb));
+        }
+        const f32x4 sc = *(lds_f32x4*)(uintptr_t)(sbb + SB_G + G_SC);
+        float mo = 0.f;
+#pragma unroll
+        for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) mo = fmaxf(mo, fabsf(dl[mb][r]));
+        float o_inv;
+        const float o_sc = pow2_scale<7>(wave_max(mo), o_inv);
+        f16x8 oh[2], ol[2];
+#pragma unroll
+        for (int kq = 0; kq < 2; ++kq) split8(dl[2 * kq], dl[2 * kq + 1], o_sc, oh[kq], ol[kq]);
         const float o_un = sc[2] * o_inv;
         const float o_up = 1.f / o_un;   // a power of two: exact
         f32x4 o[4];
 #pragma unroll
         for (int mb = 0; mb < 4; ++mb) {
-            const f32x4 eg = *(lds_f32x4*)(uintptr_t)(sw_ + WS_EG + 4 * (16 * mb + 4 * g));
+            const f32x4 eg = *(lds_f32x4*)(uintptr_t)(sbb + SB_G + G_EG + 4 * (16 * mb + 4 * g));
 #pragma unroll
-            for (int r = 0; r < 4; ++r) o[mb][r] = eg[r] * (qs[mb][r] * s_inv) * o_up;
+            for (int r = 0; r < 4; ++r) o[mb][r] = eg[r] * qs[mb][r] * o_up;
         }
 #pragma unroll
         for (int kq = 0; kq < 2; ++kq) {
@@ -556,8 +668,8 @@ chunk_state_kernel(const f16* __restrict__ q, const f16* __restrict__ k,
 #pragma unroll
             for (int mb = kq * 2; mb < 4; ++mb) {
                 const uint32_t fo = ((mb * 2 + kq) * 64 + l) * 16;
-                qh[mb] = *(lds_f16x8*)(uintptr_t)(sw_ + WS_Q_HI + fo);
-                ql[mb] = *(lds_f16x8*)(uintptr_t)(sw_ + WS_Q_LO + fo);
+                qh[mb] = *(lds_f16x8*)(uintptr_t)(sbb + SB_Q + fo);
+                ql[mb] = *(lds_f16x8*)(uintptr_t)(sbb + SB_Q + 8192 + fo);
             }
 #pragma unroll
             for (int mb = kq * 2; mb < 4; ++mb) o[mb] = mfma16(qh[mb], oh[kq], o[mb]);
@@ -569,8 +681,6 @@ chunk_state_kernel(const f16* __restrict__ q, const f16* __restrict__ k,
         // y through this wave's LDS tile: element (token 16 mb + 4 g + r, row
         // i) in, then lane l stores token l's 16 rows (32 bytes) with two
         // 16-byte stores
-        const uint32_t yt = lds0 + ST_Y + w * (CK_C * 32);
-        typedef __attribute__((address_space(3))) f16 lds_f16w;
 #pragma unroll
         for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
@@ -579,14 +689,37 @@ chunk_state_kernel(const f16* __restrict__ q, const f16* __restrict__ k,
                     f16_sat(o[mb][r] * o_un * out_scale);
         const f16x8 y0 = *(lds_f16x8*)(uintptr_t)(yt + l * 32);
         const f16x8 y1 = *(lds_f16x8*)(uintptr_t)(yt + l * 32 + 16);
-        if (n == CK_C || l < n) {
+        const int t0 = c * CK_C;
+        if (T - t0 >= CK_C || l < T - t0) {
             f16* yo = y + (size_t)(t0 + l) * y_stride + (size_t)hv * CK_V + v0;
             *(f16x8*)yo = y0;
             *(f16x8*)(yo + 8) = y1;
         }
+        if (c + 1 < n_chunks) tile_done();   // M(c)
     }
-#pragma unroll
-    for (int kb8 = 0; kb8 < 8; ++kb8) *(f32x4*)(Sv + 16 * kb8) = st[kb8];
+}
+
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+chunk_state_kernel(const f16* __restrict__ q, const f16* __restrict__ k,
+                   const f16* __restrict__ v, float* __restrict__ S, f16* __restrict__ y, int T,
+                   int n_vheads, int qk_stride, int v_stride, int y_stride, float out_scale,
+                   int group, const char* __restrict__ work) {
+    extern __shared__ __attribute__((aligned(16))) char smem[];
+    // a v head's workgroups are n_vheads apart in the flat id, so with
+    // n_vheads a multiple of 8 (48 here) they land on one XCD (dispatch goes
+    // round robin over the 8) and share its L2
+    const int hv = blockIdx.x % n_vheads, part = blockIdx.x / n_vheads, hk = hv / group;
+    const int l = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int g = l >> 4, i = l & 15;
+    const int vw0 = part * CS_ROWS;
+    const uint32_t lds0 = (uint32_t)(uintptr_t)((__attribute__((address_space(3))) char*)smem);
+    const int n_chunks = (T + CK_C - 1) / CK_C;
+    if (w < 2)
+        cs_state_wave(S, lds0, hv, vw0 + 16 * w, w, g, i, l, n_chunks);
+    else
+        cs_output_wave(q, k, v, y, work, lds0, T, n_vheads, hv, hk, vw0, vw0 + 16 * (w - 2),
+                       w - 2, g, i, l, n_chunks, 2 * qk_stride, 2 * v_stride, y_stride, out_scale);
 }
 
 // The state pass's dynamic LDS is above the 64 KiB default: raised once per
@@ -651,7 +784,7 @@ int fl_gdn_prefill_chunked(const void* q, const void* k, const void* v, const fl
     if (rc) return rc;
     rc = raise_state_lds_limit();
     if (rc) return rc;
-    hipLaunchKernelGGL(chunk_state_kernel, dim3(n_vheads * (CK_V / CS_VW)), dim3(64 * CS_WAVES),
+    hipLaunchKernelGGL(chunk_state_kernel, dim3(n_vheads * (CK_V / CS_ROWS)), dim3(256),
                        CS_LDS, (hipStream_t)stream, (const f16*)q, (const f16*)k, (const f16*)v, S,
                        (f16*)y, T, n_vheads, qk_stride, v_stride, y_stride, out_scale, group,
                        (const char*)work);
