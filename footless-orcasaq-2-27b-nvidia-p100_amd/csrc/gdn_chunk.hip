@@ -101,16 +101,32 @@ __device__ __forceinline__ float pow2_scale(float m, float& inv) {
     return __uint_as_float((uint32_t)se << 23);
 }
 
-// x s = hi + lo, both fp16 (round to nearest): the B operand of a k-step from
-// the accumulators a (slots 0..3) and b (slots 4..7)
+// x s = hi + lo, both fp16 (round to nearest), for two values into packed
+// halves: v_fma_mix rounds x s (exact: s is a power of two) and x s - hi
+// (exact in fp32: hi is x s to 11 bits) to fp16 once each, reading hi back as
+// an fp16 source, so a value costs two instructions
+__device__ __forceinline__ void split2(float x0, float x1, float s, uint32_t& hi, uint32_t& lo) {
+    uint32_t h, e;
+    asm("v_fma_mixlo_f16 %0, %1, %2, 0" : "=v"(h) : "v"(x0), "v"(s));
+    asm("v_fma_mixhi_f16 %0, %1, %2, 0" : "+v"(h) : "v"(x1), "v"(s));
+    asm("v_fma_mixlo_f16 %0, %1, %2, -%3 op_sel_hi:[0,0,1]" : "=v"(e) : "v"(x0), "v"(s), "v"(h));
+    asm("v_fma_mixhi_f16 %0, %1, %2, -%3 op_sel:[0,0,1] op_sel_hi:[0,0,1]"
+        : "+v"(e) : "v"(x1), "v"(s), "v"(h));
+    hi = h;
+    lo = e;
+}
+
+// the B operand of a k-step from the accumulators a (slots 0..3) and b
+// (slots 4..7), scaled by s and split
 __device__ __forceinline__ void split8(f32x4 a, f32x4 b, float s, f16x8& hi, f16x8& lo) {
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-        const float x = (e < 4 ? a[e] : b[e - 4]) * s;
-        const f16 h = (f16)x;
-        hi[e] = h;
-        lo[e] = (f16)(x - (float)h);
-    }
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    uint32_t h0, h1, h2, h3, l0, l1, l2, l3;
+    split2(a[0], a[1], s, h0, l0);
+    split2(a[2], a[3], s, h1, l1);
+    split2(b[0], b[1], s, h2, l2);
+    split2(b[2], b[3], s, h3, l3);
+    hi = __builtin_bit_cast(f16x8, (u32x4){h0, h1, h2, h3});
+    lo = __builtin_bit_cast(f16x8, (u32x4){l0, l1, l2, l3});
 }
 
 // ---------------------------------------------------------------------------
@@ -405,8 +421,8 @@ __device__ __forceinline__ uint32_t lane_addr(uint32_t sbase, uint32_t lane_part
     return r;
 }
 __device__ __forceinline__ f16x8 row_frag(const uint32_t (&ra)[8], uint32_t off, int mb, int js) {
-    const f16x4 a = *(lds_f16x4*)(uintptr_t)(ra[2 * js] + off + 4096 * mb);
-    const f16x4 b = *(lds_f16x4*)(uintptr_t)(ra[2 * js + 1] + off + 4096 * mb);
+    const f16x4 a = *(volatile lds_f16x4*)(uintptr_t)(ra[2 * js] + off + 4096 * mb);
+    const f16x4 b = *(volatile lds_f16x4*)(uintptr_t)(ra[2 * js + 1] + off + 4096 * mb);
     return (f16x8){a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
 }
 
@@ -470,24 +486,28 @@ __device__ __forceinline__ void cs_state_wave(float* __restrict__ S, uint32_t ld
 #pragma unroll
         for (int js = 0; js < 4; ++js) split8(st[2 * js], st[2 * js + 1], s_sc, sh[js], sl[js]);
 
-        // X = K S^T and Q S^T (two passes each), 64 tokens x 16 rows; the
-        // k-step's fragments read first, consecutive MFMAs on different
-        // accumulators
+        // X = K S^T (two passes), 64 tokens x 16 rows, first: Y waits for it;
+        // then Q S^T, which only the output wave needs, under Y's vector work.
+        // The k-step's fragments read first, consecutive MFMAs on different
+        // accumulators.
         f32x4 x[4], qs[4];
 #pragma unroll
         for (int mb = 0; mb < 4; ++mb) x[mb] = qs[mb] = (f32x4)(0.f);
 #pragma unroll
         for (int js = 0; js < 4; ++js) {
-            f16x8 ka[4], qa[4];
+            f16x8 ka[4];
 #pragma unroll
-            for (int mb = 0; mb < 4; ++mb) {
-                ka[mb] = row_frag(ra, SA_K, mb, js);
-                qa[mb] = row_frag(ra, SA_Q, mb, js);
-            }
+            for (int mb = 0; mb < 4; ++mb) ka[mb] = row_frag(ra, SA_K, mb, js);
 #pragma unroll
             for (int mb = 0; mb < 4; ++mb) x[mb] = mfma16(ka[mb], sh[js], x[mb]);
 #pragma unroll
             for (int mb = 0; mb < 4; ++mb) x[mb] = mfma16(ka[mb], sl[js], x[mb]);
+        }
+#pragma unroll
+        for (int js = 0; js < 4; ++js) {
+            f16x8 qa[4];
+#pragma unroll
+            for (int mb = 0; mb < 4; ++mb) qa[mb] = row_frag(ra, SA_Q, mb, js);
 #pragma unroll
             for (int mb = 0; mb < 4; ++mb) qs[mb] = mfma16(qa[mb], sh[js], qs[mb]);
 #pragma unroll
@@ -508,7 +528,7 @@ __device__ __forceinline__ void cs_state_wave(float* __restrict__ S, uint32_t ld
             const f32x4 eg = *(lds_f32x4*)(uintptr_t)(sg + G_EG + 4 * tok);
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                yv[mb][r] = be[r] * ((float)vv[r] - eg[r] * (x[mb][r] * s_inv));
+                yv[mb][r] = be[r] * fmaf(-(eg[r] * s_inv), x[mb][r], (float)vv[r]);
                 my = fmaxf(my, fabsf(yv[mb][r]));
             }
         }
@@ -580,7 +600,7 @@ __device__ __forceinline__ void cs_state_wave(float* __restrict__ S, uint32_t ld
             for (int b = 0; b < 4; ++b)
 #pragma unroll
                 for (int r = 0; r < 4; ++r)
-                    st[4 * h + b][r] = sc[0] * st[4 * h + b][r] + u[b][r] * p_inv;
+                    st[4 * h + b][r] = fmaf(u[b][r], p_inv, sc[0] * st[4 * h + b][r]);
         }
 
         // hand Q S0^T and Delta to the output wave (after it has read the
