@@ -31,10 +31,11 @@
 // fp32 accumulate: the product of two fp16 values is exact in fp32). K, Q and
 // V are fp16 data. An fp32 operand x of the recurrence's products (the state,
 // Y, T, the decayed Delta) is scaled by a power of two 2^s chosen from its
-// block's maximum (max |x| 2^s in [128, 256)) and split x 2^s = hi + lo, both
-// fp16: two MFMAs (hi, lo) against an exact operand, three (hi.hi, hi.lo,
-// lo.hi) between two split operands, which leaves an error of ~2^-22 of the
-// block's maximum, fp32's order. The output's products need it too: one fp16
+// block's maximum (max |x| 2^s in [128, 256); a block is T or M o QK^T whole,
+// and one state row, i.e. one column of a B operand, for the state, Y and
+// Delta) and split x 2^s = hi + lo, both fp16: two MFMAs (hi, lo) against an
+// exact operand, three (hi.hi, hi.lo, lo.hi) between two split operands, which
+// leaves an error of ~2^-22 of the block's maximum, fp32's order. The output's products need it too: one fp16
 // pass leaves y within its own tolerance, but its two terms cancel in places
 // and the gated norm that follows divides each head's row by its RMS (7e-3 of
 // the row's RMS against 2e-3 for fp32 products). Emulated in numpy before the
@@ -64,12 +65,19 @@ constexpr int CK_K = 128;      // key dim
 constexpr int CK_V = 128;      // value dim
 
 // Workspace block of one (chunk, v head), bytes: T and M o QK^T, each as hi
-// and lo fp16 A operands [4 row blocks][2 k-steps][64 lanes][8] (8 KiB each),
+// and lo fp16 A operands [6 blocks][64 lanes][8] (6 KiB each; block f is row
+// block mb = f, k-step 0 for f < 4, and mb = f - 2, k-step 1 for f = 4, 5: both
+// matrices are lower triangular, so rows 0..31 take nothing from k-step 1),
 // then beta, e^{g} and e^{g_C - g} [64] f32 (beta 0 past the chunk's last
 // token), then e^{g_C}, 2^-tau and 2^-kappa (T's and M o QK^T's scales).
-constexpr int WS_T_HI = 0, WS_T_LO = 8192, WS_Q_HI = 16384, WS_Q_LO = 24576, WS_BETA = 32768,
-              WS_EG = 33024, WS_DK = 33280, WS_SC = 33536;
-constexpr int CK_BLK = 33792;
+constexpr int CK_NF = 6;
+__host__ __device__ constexpr int f_mb(int f) { return f < 4 ? f : f - 2; }
+__host__ __device__ constexpr int f_kq(int f) { return f < 4 ? 0 : 1; }
+constexpr int WS_OP = CK_NF * 1024;
+constexpr int WS_T_HI = 0, WS_T_LO = WS_OP, WS_Q_HI = 2 * WS_OP, WS_Q_LO = 3 * WS_OP,
+              WS_BETA = 4 * WS_OP, WS_EG = WS_BETA + 256, WS_DK = WS_BETA + 512,
+              WS_SC = WS_BETA + 768;
+constexpr int CK_BLK = WS_BETA + 1024;
 
 typedef __attribute__((address_space(3))) const f16x4 lds_f16x4;
 typedef __attribute__((address_space(3))) const f16x8 lds_f16x8;
@@ -86,6 +94,16 @@ __device__ __forceinline__ float wave_max(float v) {
     v = fmaxf(v, dpp_xor2(v));
     v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x124, 0xF, 0xF, true)));
     v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x128, 0xF, 0xF, true)));
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                    false);
+    return pair32_max(fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1])));
+}
+
+// max over the lanes l, l ^ 16, l ^ 32 and l ^ 48, the four lane groups that
+// hold one column of an MFMA B operand (or result): v_permlane16_swap with
+// both operands v returns v of the lane pair (l, l ^ 16), then
+// v_permlane32_swap the pair (l, l ^ 32)
+__device__ __forceinline__ float col_max(float v) {
     const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false,
                                                     false);
     return pair32_max(fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1])));
@@ -137,6 +155,44 @@ constexpr int PA_P = CK_C + 4;   // f32 pitch of the A / T and M o QK^T rows
 static_assert(CK_C * PA_P * 4 == CK_C * PK_P * 2, "A / QKm reuse the K / Q storage");
 
 __device__ __forceinline__ float safe_log(float d) { return logf(fmaxf(d, 1.17549435e-38f)); }
+
+// an empty use: the value is loaded unconditionally (every address read is in
+// bounds), instead of the load being moved under the select that keeps it
+__device__ __forceinline__ void keep(float& v) { asm volatile("" : "+v"(v)); }
+
+// v_mfma_f32_16x16x4_f32, lane l = 16 g + i: A holds X[i][g], B holds Y[g][i],
+// the result Z[4 g + r][i] in slot r
+__device__ __forceinline__ f32x4 mfma4(float a, float b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// T's block (bi, bj), bi > bj, from the blocks of T already in sA (kept
+// transposed above the diagonal, the diagonal blocks D with their zeros):
+// S = sum_k A_{bi,k} T_{k,bj} (k-step s takes k = 16 k + 4 s + g), then
+// T_{bi,bj} = -D_bi S with S's result slots as the B operand as they stand
+// (k-step s pairs lane group g with S's row 4 g + s, so D is read at column
+// 4 g + s)
+__device__ __forceinline__ void t_block(float (*sA)[CK_C + 4], int bi, int bj, int lane) {
+    const int g = lane >> 4, i = lane & 15;
+    f32x4 sm = (f32x4)(0.f);
+    for (int kb = bj; kb < bi; ++kb) {
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const int kk = 4 * s + g;
+            const float a = sA[16 * bi + i][16 * kb + kk];
+            // T_{kb,bj}[kk][i]: transposed at sA[16 bj + i][16 kb + kk] (D's
+            // zeros above its diagonal are stored)
+            sm = mfma4(a, sA[16 * bj + i][16 * kb + kk], sm);
+        }
+    }
+    f32x4 t = (f32x4)(0.f);
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+        const int kk = 4 * g + s;
+        t = mfma4(sA[16 * bi + kk][16 * bi + i], sm[s], t);   // D_bi[i][kk], transposed
+    }
+    *(f32x4*)&sA[16 * bj + i][16 * bi + 4 * g] = -t;
+}
 
 
 __global__ void __launch_bounds__(256)
@@ -211,43 +267,53 @@ chunk_prep_kernel(const f16* __restrict__ q, const f16* __restrict__ k,
     for (int r = 0; r < 16; ++r) {
         const int i = 32 * bi + 8 * (r >> 2) + 4 * hh + (r & 3);
         const int j = 32 * bj + ql;
-        const float ratio = j <= i ? fast_exp2((sG[i] - sG[j]) * FL_LOG2E) : 0.f;
+        // e^{g_i - g_j}, taken for every pair (above the diagonal it may be
+        // inf, and is not selected)
+        const float ratio = fast_exp2((sG[i] - sG[j]) * FL_LOG2E);
         sA[i][j] = j < i ? sB[i] * ratio * kk[r] : 0.f;
         sM[i][j] = j <= i ? ratio * qk[r] : 0.f;
     }
     __syncthreads();
 
-    // T = (I + A)^-1 by forward substitution in fp32, column j by thread j:
-    // x[i] = [i == j] - sum_{m < i} A[i][m] x[m] (x[m] = 0 above the
-    // diagonal), the sum over m in four interleaved chains (m mod 4)
-    float x[CK_C];
-    if (tid < CK_C) {
+    // T = (I + A)^-1 by blocks of 16, in fp32: T_ii = D_i = (I + A_ii)^-1 by
+    // forward substitution (wave i, lane j solving column j), then, a block
+    // diagonal at a time, T_ij = -D_i sum_{k = j .. i-1} A_ik T_kj on fp32
+    // MFMA. T is kept transposed in sA's upper triangle (T_ij[a][b] at
+    // sA[16 j + b][16 i + a]), clear of A below the diagonal.
+    if (lane < 16) {
+        const int o = 16 * w, j = lane;
+        float xd[16];
 #pragma unroll
-        for (int i = 0; i < CK_C; ++i) {
-            float acc[4] = {i == tid ? 1.f : 0.f, 0.f, 0.f, 0.f};
+        for (int i = 0; i < 16; ++i) {
+            float a0 = i == j ? 1.f : 0.f, a1 = 0.f;
 #pragma unroll
-            for (int m = 0; m < i; m += 4) {
-                const f32x4 a4 = *(const f32x4*)&sA[i][m];
-#pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    if (m + e < i) acc[e] = fmaf(-a4[e], x[m + e], acc[e]);
+            for (int m = 0; m < i; ++m) {
+                if (m & 1)
+                    a1 = fmaf(-sA[o + i][o + m], xd[m], a1);
+                else
+                    a0 = fmaf(-sA[o + i][o + m], xd[m], a0);
             }
-            x[i] = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+            xd[i] = a0 + a1;
         }
-    }
-    __syncthreads();   // every read of A done: T takes its storage
-    if (tid < CK_C) {
+        // every element, the zeros above D_w's diagonal included: they land
+        // on A_ww, which the remaining steps do not read
 #pragma unroll
-        for (int i = 0; i < CK_C; ++i) sA[i][tid] = x[i];
+        for (int i = 0; i < 16; ++i) sA[o + j][o + i] = xd[i];
     }
     __syncthreads();
-
+#pragma unroll
+    for (int lv = 1; lv < 4; ++lv) {
+        if (w < 4 - lv) t_block(sA, w + lv, w, lane);
+        __syncthreads();
+    }
     // the scales: block maxima of |T| and |M o QK^T|
     float mt = 0.f, mq = 0.f;
 #pragma unroll
     for (int m = 0; m < CK_C * CK_C / 256; ++m) {
         const int idx = tid + 256 * m, i = idx >> 6, j = idx & 63;
-        mt = fmaxf(mt, fabsf(sA[i][j]));
+        float tv = sA[j][i];   // T[i][j], transposed: A's values where j > i
+        keep(tv);
+        mt = fmaxf(mt, i >= j ? fabsf(tv) : 0.f);
         mq = fmaxf(mq, fabsf(sM[i][j]));
     }
     mt = wave_max(mt);
@@ -263,23 +329,29 @@ chunk_prep_kernel(const f16* __restrict__ q, const f16* __restrict__ k,
     const float t_sc = pow2_scale<7>(mt, t_inv);
     const float q_sc = pow2_scale<7>(mq, q_inv);
 
-    // the operands: slot (which: T hi, T lo, M o QK^T hi, lo; row block mb,
-    // k-step kq, lane l = 16 g + i) holds row 16 mb + i at columns
-    // 32 kq + kap(g, e)
+    // the operands: slot (T or M o QK^T; block f, lane l = 16 g + i) holds row
+    // 16 mb + i at columns 32 kq + kap(g, e), its hi and lo halves 6 KiB apart
 #pragma unroll
-    for (int m = 0; m < 8; ++m) {
+    for (int m = 0; m < 3; ++m) {
         const int s = tid + 256 * m;
-        const int which = s >> 9, mb = (s >> 7) & 3, kq = (s >> 6) & 1, l = s & 63;
-        const int g = l >> 4, row = 16 * mb + (l & 15);
-        f16x8 o;
+        const bool isq = s >= CK_NF * 64;
+        const int f = (s % (CK_NF * 64)) >> 6, l = s & 63;
+        const int g = l >> 4, row = 16 * f_mb(f) + (l & 15), kq = f_kq(f);
+        f16x8 hi, lo;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
             const int col = 32 * kq + (e < 4 ? 4 * g + e : 12 + 4 * g + e);
-            const float xs = which < 2 ? sA[row][col] * t_sc : sM[row][col] * q_sc;
+            float ta = sA[col][row];   // T[row][col], transposed
+            keep(ta);
+            const float mq_ = sM[row][col];
+            const float xs = isq ? mq_ * q_sc : (row >= col ? ta : 0.f) * t_sc;
             const f16 h = (f16)xs;
-            o[e] = (which & 1) == 0 ? h : (f16)(xs - (float)h);
+            hi[e] = h;
+            lo[e] = (f16)(xs - (float)h);
         }
-        *(f16x8*)(blk + 8192 * which + ((mb * 2 + kq) * 64 + l) * 16) = o;
+        char* dst = blk + (isq ? WS_Q_HI : WS_T_HI) + (f * 64 + l) * 16;
+        *(f16x8*)dst = hi;
+        *(f16x8*)(dst + WS_OP) = lo;
     }
     if (tid < CK_C) {
         const float gC = sG[CK_C - 1];
@@ -305,17 +377,18 @@ constexpr int CS_ROWS = 32;   // state rows (v) a workgroup
 // T's hi / lo operands and the gates KiB (workspace bytes 0 .. 16 KiB and
 // 32 .. 33 KiB, as in HBM)
 constexpr int SA_K = 0, SA_Q = 16384, SA_V = 32768, SA_T = SA_V + CK_C * CS_ROWS * 2,
-              SA_G = SA_T + 16384, SA_BYTES = SA_G + 1024;
+              SA_G = SA_T + 2 * WS_OP, SA_BYTES = SA_G + 1024;
 // B stage (the output waves'): M o QK^T's hi / lo operands (workspace bytes
 // 16 .. 32 KiB) and the gates KiB
-constexpr int SB_Q = 0, SB_G = 16384, SB_BYTES = SB_G + 1024;
+constexpr int SB_Q = 0, SB_G = 2 * WS_OP, SB_BYTES = SB_G + 1024;
 // offsets in the gates KiB: beta, e^g, e^{g_C - g} [64] f32, then e^{g_C},
 // 2^-tau, 2^-kappa
 constexpr int G_BETA = WS_BETA - WS_BETA, G_EG = WS_EG - WS_BETA, G_DK = WS_DK - WS_BETA,
               G_SC = WS_SC - WS_BETA;
-static_assert(WS_T_HI == 0 && WS_T_LO == 8192 && WS_Q_HI == 16384 && WS_Q_LO == 24576 &&
-                  CK_BLK == WS_BETA + 1024,
-              "workspace block: T, then M o QK^T, then the gates KiB");
+static_assert(WS_T_LO == WS_T_HI + WS_OP && WS_Q_HI == WS_T_LO + WS_OP &&
+                  WS_Q_LO == WS_Q_HI + WS_OP && WS_BETA == WS_Q_LO + WS_OP &&
+                  CK_BLK == WS_BETA + 1024 && WS_OP % 2048 == 0,
+              "workspace block: T, then M o QK^T, then the gates KiB, whole copy pairs");
 // LDS: two A stages, two B stages, the hand-over (each state wave's Q S^T
 // 2^-s and Delta, [8][64 lanes] f32x4) and each output wave's y tile
 // [64 tokens][16 rows] fp16
@@ -345,7 +418,7 @@ __device__ __forceinline__ CsOff cs_offsets(int qk_bytes, int v_bytes, int wb, i
 }
 
 // Output wave wb's half of the copies of chunk c's A stage into dst: 8 K, 8 Q,
-// 2 V and 8 T copies, and (wb = 0) the gates KiB. Rows past the last token
+// 2 V and 6 T copies, and (wb = 0) the gates KiB. Rows past the last token
 // repeat it (beta is 0 there).
 __device__ __forceinline__ void cs_copy_a(uint32_t dst, const char* kb, const char* qb,
                                           const char* vb, const char* wk, int t0, int T,
@@ -384,18 +457,18 @@ __device__ __forceinline__ void cs_copy_a(uint32_t dst, const char* kb, const ch
         }
     }
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
+    for (int j = 0; j < WS_OP / 1024; ++j) {
         const int n = 2 * j + wb;
-        copy16(wk + 1024 * n, o.w, dst + SA_T + 1024 * n);
+        copy16(wk + WS_T_HI + 1024 * n, o.w, dst + SA_T + 1024 * n);
     }
     if (wb == 0) copy16(wk + WS_BETA, o.w, dst + SA_G);
 }
 
-// Output wave wb's half of the copies of chunk c's B stage: 8 M o QK^T copies
+// Output wave wb's half of the copies of chunk c's B stage: 6 M o QK^T copies
 // and (wb = 1) the gates KiB.
 __device__ __forceinline__ void cs_copy_b(uint32_t dst, const char* wk, int wb, const CsOff& o) {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
+    for (int j = 0; j < WS_OP / 1024; ++j) {
         const int n = 2 * j + wb;
         copy16(wk + WS_Q_HI + 1024 * n, o.w, dst + SB_Q + 1024 * n);
     }
@@ -466,13 +539,19 @@ __device__ __forceinline__ void cs_state_wave(float* __restrict__ S, uint32_t ld
     for (int c = 0; c < n_chunks; ++c) {
         const uint32_t sb = lds0 + L_A + (c & 1) * SA_BYTES;
         const uint32_t sg = sb + SA_G;
-        uint32_t ra[8], ca[8];
+        uint32_t ra[8];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            ra[j] = lane_addr(sb, ro[j]);
-            ca[j] = lane_addr(sb, co[j]);
-        }
+        for (int j = 0; j < 8; ++j) ra[j] = lane_addr(sb, ro[j]);
+        // Each phase's LDS operands are read a phase ahead, behind a
+        // scheduling fence, so no phase waits on LDS latency. First X's K
+        // fragments, which do not wait for the state.
+        f16x8 kx[4][4];
+#pragma unroll
+        for (int js = 0; js < 4; ++js)
+#pragma unroll
+            for (int mb = 0; mb < 4; ++mb) kx[js][mb] = row_frag(ra, SA_K, mb, js);
         const f32x4 sc = *(lds_f32x4*)(uintptr_t)(sg + G_SC);   // e^{g_C}, 2^-tau, 2^-kappa
+        __builtin_amdgcn_sched_barrier(0);
 
         // the state, scaled and split: B operands of the four k-steps
         float ms = 0.f;
@@ -481,100 +560,132 @@ __device__ __forceinline__ void cs_state_wave(float* __restrict__ S, uint32_t ld
 #pragma unroll
             for (int r = 0; r < 4; ++r) ms = fmaxf(ms, fabsf(st[kb8][r]));
         float s_inv;
-        const float s_sc = pow2_scale<7>(wave_max(ms), s_inv);
+        const float s_sc = pow2_scale<7>(col_max(ms), s_inv);
         f16x8 sh[4], sl[4];
 #pragma unroll
         for (int js = 0; js < 4; ++js) split8(st[2 * js], st[2 * js + 1], s_sc, sh[js], sl[js]);
+        __builtin_amdgcn_sched_barrier(0);
 
-        // X = K S^T (two passes), 64 tokens x 16 rows, first: Y waits for it;
-        // then Q S^T, which only the output wave needs, under Y's vector work.
-        // The k-step's fragments read first, consecutive MFMAs on different
-        // accumulators.
+        // Y's inputs and Q S^T's first fragments, then X = K S^T (two
+        // passes), 64 tokens x 16 rows, on four accumulators
+        f16x4 vv[4];
+        f32x4 be[4], eg[4];
+#pragma unroll
+        for (int mb = 0; mb < 4; ++mb) {
+            const int tok = 16 * mb + 4 * g;
+            const int vr = tok + (i >> 2);
+            vv[mb] = __builtin_bit_cast(
+                f16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(uintptr_t)(
+                           sb + SA_V + vr * (CS_ROWS * 2) + 32 * wa + 8 * (i & 3))));
+            be[mb] = *(lds_f32x4*)(uintptr_t)(sg + G_BETA + 4 * tok);
+            eg[mb] = *(lds_f32x4*)(uintptr_t)(sg + G_EG + 4 * tok);
+        }
+        f16x8 qa[2][4];
+#pragma unroll
+        for (int m2 = 0; m2 < 4; ++m2) qa[0][m2] = row_frag(ra, SA_Q, m2, 0);
         f32x4 x[4], qs[4];
 #pragma unroll
         for (int mb = 0; mb < 4; ++mb) x[mb] = qs[mb] = (f32x4)(0.f);
 #pragma unroll
         for (int js = 0; js < 4; ++js) {
-            f16x8 ka[4];
 #pragma unroll
-            for (int mb = 0; mb < 4; ++mb) ka[mb] = row_frag(ra, SA_K, mb, js);
+            for (int mb = 0; mb < 4; ++mb) x[mb] = mfma16(kx[js][mb], sh[js], x[mb]);
 #pragma unroll
-            for (int mb = 0; mb < 4; ++mb) x[mb] = mfma16(ka[mb], sh[js], x[mb]);
-#pragma unroll
-            for (int mb = 0; mb < 4; ++mb) x[mb] = mfma16(ka[mb], sl[js], x[mb]);
+            for (int mb = 0; mb < 4; ++mb) x[mb] = mfma16(kx[js][mb], sl[js], x[mb]);
         }
-#pragma unroll
-        for (int js = 0; js < 4; ++js) {
-            f16x8 qa[4];
-#pragma unroll
-            for (int mb = 0; mb < 4; ++mb) qa[mb] = row_frag(ra, SA_Q, mb, js);
-#pragma unroll
-            for (int mb = 0; mb < 4; ++mb) qs[mb] = mfma16(qa[mb], sh[js], qs[mb]);
-#pragma unroll
-            for (int mb = 0; mb < 4; ++mb) qs[mb] = mfma16(qa[mb], sl[js], qs[mb]);
-        }
+        __builtin_amdgcn_sched_barrier(0);
 
-        // Y = beta (V - e^g X) at tokens 16 mb + 4 g + r, column v0 + i
+        // T's operands for Delta; then Q S^T, which only the output wave
+        // needs, issued between the blocks of Y = beta (V - e^g X) (tokens
+        // 16 mb + 4 g + r, column v0 + i), its next fragments read a k-step
+        // ahead
+        f16x8 th[CK_NF], tl[CK_NF];
+#pragma unroll
+        for (int f = 0; f < CK_NF; ++f) {
+            const uint32_t fo = (f * 64 + l) * 16;
+            th[f] = *(lds_f16x8*)(uintptr_t)(sb + SA_T + fo);
+            tl[f] = *(lds_f16x8*)(uintptr_t)(sb + SA_T + WS_OP + fo);
+        }
         f32x4 yv[4];
         float my = 0.f;
 #pragma unroll
         for (int mb = 0; mb < 4; ++mb) {
-            const int tok = 16 * mb + 4 * g;
-            const int vr = tok + (i >> 2);
-            const s16x4 vraw = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                (lds_s16x4*)(uintptr_t)(sb + SA_V + vr * (CS_ROWS * 2) + 32 * wa + 8 * (i & 3)));
-            const f16x4 vv = __builtin_bit_cast(f16x4, vraw);
-            const f32x4 be = *(lds_f32x4*)(uintptr_t)(sg + G_BETA + 4 * tok);
-            const f32x4 eg = *(lds_f32x4*)(uintptr_t)(sg + G_EG + 4 * tok);
+            if (mb < 3) {
+#pragma unroll
+                for (int m2 = 0; m2 < 4; ++m2) qa[(mb + 1) & 1][m2] = row_frag(ra, SA_Q, m2, mb + 1);
+            }
+#pragma unroll
+            for (int m2 = 0; m2 < 4; ++m2) qs[m2] = mfma16(qa[mb & 1][m2], sh[mb], qs[m2]);
+#pragma unroll
+            for (int m2 = 0; m2 < 4; ++m2) qs[m2] = mfma16(qa[mb & 1][m2], sl[mb], qs[m2]);
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                yv[mb][r] = be[r] * fmaf(-(eg[r] * s_inv), x[mb][r], (float)vv[r]);
+                yv[mb][r] = be[mb][r] * fmaf(-(eg[mb][r] * s_inv), x[mb][r], (float)vv[mb][r]);
                 my = fmaxf(my, fabsf(yv[mb][r]));
             }
         }
         float y_inv;
-        const float y_sc = pow2_scale<7>(wave_max(my), y_inv);
+        const float y_sc = pow2_scale<7>(col_max(my), y_inv);
         f16x8 yh[2], yl[2];
 #pragma unroll
         for (int kq = 0; kq < 2; ++kq) split8(yv[2 * kq], yv[2 * kq + 1], y_sc, yh[kq], yl[kq]);
+        __builtin_amdgcn_sched_barrier(0);
 
-        // Delta = T Y (three passes; T is zero above the diagonal, so rows 0..31
-        // take no columns 32..63)
+        // the state update's first K^T fragments and the decays; then
+        // Delta = T Y (three passes; T is zero above the diagonal, so rows
+        // 0..31 take no columns 32..63)
+        uint32_t ca[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) ca[j] = lane_addr(sb, co[j]);
+        f16x8 kt[2][2][4];
+#pragma unroll
+        for (int kq = 0; kq < 2; ++kq)
+#pragma unroll
+            for (int b = 0; b < 4; ++b) kt[0][kq][b] = col_frag(ca, b, kq);
+        f32x4 dk[4];
+#pragma unroll
+        for (int mb = 0; mb < 4; ++mb)
+            dk[mb] = *(lds_f32x4*)(uintptr_t)(sg + G_DK + 4 * (16 * mb + 4 * g));
         f32x4 dl[4];
-        float md = 0.f;
-        const float d_un = sc[1] * y_inv;
 #pragma unroll
         for (int mb = 0; mb < 4; ++mb) dl[mb] = (f32x4)(0.f);
 #pragma unroll
-        for (int kq = 0; kq < 2; ++kq) {
-            f16x8 th[4], tl[4];
-#pragma unroll
-            for (int mb = kq * 2; mb < 4; ++mb) {
-                const uint32_t fo = ((mb * 2 + kq) * 64 + l) * 16;
-                th[mb] = *(lds_f16x8*)(uintptr_t)(sb + SA_T + WS_T_HI + fo);
-                tl[mb] = *(lds_f16x8*)(uintptr_t)(sb + SA_T + WS_T_LO + fo);
-            }
-#pragma unroll
-            for (int mb = kq * 2; mb < 4; ++mb) dl[mb] = mfma16(th[mb], yh[kq], dl[mb]);
-#pragma unroll
-            for (int mb = kq * 2; mb < 4; ++mb) dl[mb] = mfma16(th[mb], yl[kq], dl[mb]);
-#pragma unroll
-            for (int mb = kq * 2; mb < 4; ++mb) dl[mb] = mfma16(tl[mb], yh[kq], dl[mb]);
+        for (int f = 0; f < CK_NF; ++f) {
+            const int mb = f_mb(f), kq = f_kq(f);
+            dl[mb] = mfma16(th[f], yh[kq], dl[mb]);
         }
-        // Delta' = e^{g_C - g} Delta for the state update, scaled and split
+#pragma unroll
+        for (int f = 0; f < CK_NF; ++f) {
+            const int mb = f_mb(f), kq = f_kq(f);
+            dl[mb] = mfma16(th[f], yl[kq], dl[mb]);
+        }
+#pragma unroll
+        for (int f = 0; f < CK_NF; ++f) {
+            const int mb = f_mb(f), kq = f_kq(f);
+            dl[mb] = mfma16(tl[f], yh[kq], dl[mb]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+
+        // the second half's K^T fragments; Delta' = e^{g_C - g} Delta for
+        // the state update, scaled and split
+#pragma unroll
+        for (int kq = 0; kq < 2; ++kq)
+#pragma unroll
+            for (int b = 0; b < 4; ++b) kt[1][kq][b] = col_frag(ca, 4 + b, kq);
+        const float d_un = sc[1] * y_inv;
+        float md = 0.f;
         f32x4 dp[4];
 #pragma unroll
         for (int mb = 0; mb < 4; ++mb) {
-            const f32x4 dk = *(lds_f32x4*)(uintptr_t)(sg + G_DK + 4 * (16 * mb + 4 * g));
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 dl[mb][r] *= d_un;
-                dp[mb][r] = dk[r] * dl[mb][r];
+                dp[mb][r] = dk[mb][r] * dl[mb][r];
                 md = fmaxf(md, fabsf(dp[mb][r]));
             }
         }
         float p_inv;
-        const float p_sc = pow2_scale<7>(wave_max(md), p_inv);
+        const float p_sc = pow2_scale<7>(col_max(md), p_inv);
         f16x8 ph[2], pl[2];
 #pragma unroll
         for (int kq = 0; kq < 2; ++kq) split8(dp[2 * kq], dp[2 * kq + 1], p_sc, ph[kq], pl[kq]);
@@ -588,13 +699,10 @@ __device__ __forceinline__ void cs_state_wave(float* __restrict__ S, uint32_t ld
             for (int b = 0; b < 4; ++b) u[b] = (f32x4)(0.f);
 #pragma unroll
             for (int kq = 0; kq < 2; ++kq) {
-                f16x8 ka[4];
 #pragma unroll
-                for (int b = 0; b < 4; ++b) ka[b] = col_frag(ca, 4 * h + b, kq);
+                for (int b = 0; b < 4; ++b) u[b] = mfma16(kt[h][kq][b], ph[kq], u[b]);
 #pragma unroll
-                for (int b = 0; b < 4; ++b) u[b] = mfma16(ka[b], ph[kq], u[b]);
-#pragma unroll
-                for (int b = 0; b < 4; ++b) u[b] = mfma16(ka[b], pl[kq], u[b]);
+                for (int b = 0; b < 4; ++b) u[b] = mfma16(kt[h][kq][b], pl[kq], u[b]);
             }
 #pragma unroll
             for (int b = 0; b < 4; ++b)
@@ -602,6 +710,7 @@ __device__ __forceinline__ void cs_state_wave(float* __restrict__ S, uint32_t ld
                 for (int r = 0; r < 4; ++r)
                     st[4 * h + b][r] = fmaf(u[b][r], p_inv, sc[0] * st[4 * h + b][r]);
         }
+        __builtin_amdgcn_sched_barrier(0);
 
         // hand Q S0^T and Delta to the output wave (after it has read the
         // previous chunk's)
@@ -669,12 +778,12 @@ __device__ __forceinline__ void cs_output_wave(const f16* q, const f16* k, const
 #pragma unroll
             for (int r = 0; r < 4; ++r) mo = fmaxf(mo, fabsf(dl[mb][r]));
         float o_inv;
-        const float o_sc = pow2_scale<7>(wave_max(mo), o_inv);
+        const float o_sc = pow2_scale<7>(col_max(mo), o_inv);
         f16x8 oh[2], ol[2];
 #pragma unroll
         for (int kq = 0; kq < 2; ++kq) split8(dl[2 * kq], dl[2 * kq + 1], o_sc, oh[kq], ol[kq]);
         const float o_un = sc[2] * o_inv;
-        const float o_up = 1.f / o_un;   // a power of two: exact
+        const float o_up = o_sc * __builtin_amdgcn_rcpf(sc[2]);   // 1 / o_un: powers of two, exact
         f32x4 o[4];
 #pragma unroll
         for (int mb = 0; mb < 4; ++mb) {
@@ -682,22 +791,19 @@ __device__ __forceinline__ void cs_output_wave(const f16* q, const f16* k, const
 #pragma unroll
             for (int r = 0; r < 4; ++r) o[mb][r] = eg[r] * qs[mb][r] * o_up;
         }
+        f16x8 qh[CK_NF], ql[CK_NF];
 #pragma unroll
-        for (int kq = 0; kq < 2; ++kq) {
-            f16x8 qh[4], ql[4];
-#pragma unroll
-            for (int mb = kq * 2; mb < 4; ++mb) {
-                const uint32_t fo = ((mb * 2 + kq) * 64 + l) * 16;
-                qh[mb] = *(lds_f16x8*)(uintptr_t)(sbb + SB_Q + fo);
-                ql[mb] = *(lds_f16x8*)(uintptr_t)(sbb + SB_Q + 8192 + fo);
-            }
-#pragma unroll
-            for (int mb = kq * 2; mb < 4; ++mb) o[mb] = mfma16(qh[mb], oh[kq], o[mb]);
-#pragma unroll
-            for (int mb = kq * 2; mb < 4; ++mb) o[mb] = mfma16(qh[mb], ol[kq], o[mb]);
-#pragma unroll
-            for (int mb = kq * 2; mb < 4; ++mb) o[mb] = mfma16(ql[mb], oh[kq], o[mb]);
+        for (int f = 0; f < CK_NF; ++f) {
+            const uint32_t fo = (f * 64 + l) * 16;
+            qh[f] = *(lds_f16x8*)(uintptr_t)(sbb + SB_Q + fo);
+            ql[f] = *(lds_f16x8*)(uintptr_t)(sbb + SB_Q + WS_OP + fo);
         }
+#pragma unroll
+        for (int f = 0; f < CK_NF; ++f) o[f_mb(f)] = mfma16(qh[f], oh[f_kq(f)], o[f_mb(f)]);
+#pragma unroll
+        for (int f = 0; f < CK_NF; ++f) o[f_mb(f)] = mfma16(qh[f], ol[f_kq(f)], o[f_mb(f)]);
+#pragma unroll
+        for (int f = 0; f < CK_NF; ++f) o[f_mb(f)] = mfma16(ql[f], oh[f_kq(f)], o[f_mb(f)]);
         // y through this wave's LDS tile: element (token 16 mb + 4 g + r, row
         // i) in, then lane l stores token l's 16 rows (32 bytes) with two
         // 16-byte stores

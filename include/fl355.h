@@ -363,8 +363,8 @@ int fl_rmsnorm_gated(const void* o, const void* z, const float* w, void* y, int 
  * reference runs gdn_scan sequentially and names the chunked scan as undone,
  * kernels.cu:1788-1791); it replaces that call (runtime.py:3094-3100) for
  * prefill. work: caller scratch of fl_gdn_chunked_work_bytes(...) bytes (per
- * chunk and v head, T = (I + A)^-1 and the decayed Q K^T of the WY form as
- * fp16 MFMA operands, and the gates). chunk == 64, K == V == 128; q, k, v, S,
+ * chunk and v head 25,600: T = (I + A)^-1 and the decayed Q K^T of the WY form
+ * as fp16 hi / lo MFMA operands of their nonzero blocks, and the gates). chunk == 64, K == V == 128; q, k, v, S,
  * work and the rows of y (y_stride % 8 == 0) 16-byte aligned. */
 size_t fl_gdn_chunked_work_bytes(int T, int n_vheads, int K, int V, int chunk);
 int fl_gdn_prefill_chunked(const void* q, const void* k, const void* v, const float* beta,

@@ -69,12 +69,13 @@ def test_argument_checks_refuse_before_launch(fl):
 def test_work_size_queries(fl):
     lib = fl._lib.lib()
     assert lib.fl_attn_decode_work_bytes(4, 3, 24, 256, 64) == 4 * 3 * 24 * 64 * (256 + 2) * 4
-    # per (chunk, v head): T and M o QK^T as hi / lo fp16 MFMA operands
-    # (4 x 64 x 64 x 2 bytes), beta / e^g / e^{g_C - g} (3 x 64 f32) and a
-    # 64-float block of scalars
+    # per (chunk, v head): T and M o QK^T as hi / lo fp16 MFMA operands of
+    # their 6 nonzero 16 x 32 blocks (4 x 6 x 16 x 32 x 2 bytes: both are lower
+    # triangular, the blocks above the diagonal are left out), beta / e^g /
+    # e^{g_C - g} (3 x 64 f32) and a 64-float block of scalars
     n_chunks = (8192 + 63) // 64
     assert lib.fl_gdn_chunked_work_bytes(8192, 48, 128, 128, 64) == \
-        n_chunks * 48 * (4 * 64 * 64 * 2 + 4 * 64 * 4)
+        n_chunks * 48 * (4 * 6 * 16 * 32 * 2 + 4 * 64 * 4)
     assert lib.fl_gdn_chunked_work_bytes(8192, 48, 128, 128, 32) == 0
 
 
