@@ -195,6 +195,22 @@ __device__ __forceinline__ void t_block(float (*sA)[CK_C + 4], int bi, int bj, i
 }
 
 
+// inclusive prefix sum over the 64 lanes of a wavefront: DPP row shifts by 1,
+// 2, 4 and 8 (zero fill at the row start), then the row totals carried by
+// row_bcast:15 and row_bcast:31
+__device__ __forceinline__ float wave_prefix_sum(float v) {
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x111, 0xF, 0xF, false));
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x112, 0xF, 0xF, false));
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x114, 0xF, 0xF, false));
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x118, 0xF, 0xF, false));
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x142, 0xA, 0xF, false));
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x143, 0xC, 0xF, false));
+    return v;
+}
+
+// One workgroup of 4 waves a (chunk, k head): K and Q are loaded and K K^T,
+// Q K^T formed once, then each v head of the group in turn gets its A, T and
+// M o QK^T from them with its own gates.
 __global__ void __launch_bounds__(256)
 chunk_prep_kernel(const f16* __restrict__ q, const f16* __restrict__ k,
                   const float* __restrict__ beta, const float* __restrict__ decay, int T,
@@ -206,16 +222,16 @@ chunk_prep_kernel(const f16* __restrict__ q, const f16* __restrict__ k,
     float(*sA)[PA_P] = (float(*)[PA_P])smem;                     // after the products
     float(*sM)[PA_P] = (float(*)[PA_P])(smem + CK_C * PA_P * 4);
 
-    const int c = blockIdx.x, hv = blockIdx.y, hk = hv / group;
+    const int c = blockIdx.x, hk = blockIdx.y;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int ql = lane & 31, hh = lane >> 5;
     const int t0 = c * CK_C;
     const int n = min(CK_C, T - t0);
-    char* blk = work + ((size_t)c * n_vheads + hv) * CK_BLK;
+    const int hv0 = hk * group, hv_end = min(hv0 + group, n_vheads);
 
     // Every global load issued up front and unconditionally, rows clamped to
     // the chunk's last token, past-the-end rows zeroed by a select: K and Q
-    // (4 rows x 16 B a thread), beta and decay.
+    // (4 rows x 16 B a thread), the first v head's beta and decay.
     f16x8 kv8[4], qv8[4];
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
@@ -224,34 +240,17 @@ chunk_prep_kernel(const f16* __restrict__ q, const f16* __restrict__ k,
         kv8[m] = *(const f16x8*)(k + off);
         qv8[m] = *(const f16x8*)(q + off);
     }
-    const int tg = min(tid & (CK_C - 1), n - 1);
-    const float dec = decay[(size_t)(t0 + tg) * n_vheads + hv];
-    const float bet = beta[(size_t)(t0 + tg) * n_vheads + hv];
+    const size_t gt = (size_t)(t0 + min(lane, n - 1)) * n_vheads;
+    float dec = decay[gt + hv0], bet = beta[gt + hv0];
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
         const int idx = tid + 256 * m, i = idx >> 4, c8 = (idx & 15) * 8;
         *(f16x8*)&sK[i][c8] = i < n ? kv8[m] : (f16x8)(0);
         *(f16x8*)&sQ[i][c8] = i < n ? qv8[m] : (f16x8)(0);
     }
-    if (tid < CK_C) {   // decay 1 and beta 0 past the end: g stays at the last token's
-        sG[tid] = tid < n ? safe_log(dec) : 0.f;
-        sB[tid] = tid < n ? bet : 0.f;
-    }
-    __syncthreads();
-    if (tid == 0) {   // the in-chunk prefix sums of log decay, in token order
-        float gs[CK_C];
-#pragma unroll
-        for (int i = 0; i < CK_C; ++i) gs[i] = sG[i];
-        float a = 0.f;
-#pragma unroll
-        for (int i = 0; i < CK_C; ++i) {
-            a += gs[i];
-            sG[i] = a;
-        }
-    }
     __syncthreads();
 
-    // K K^T and Q K^T: wave w the 32 x 32 block (bi, bj)
+    // K K^T and Q K^T: wave w the 32 x 32 block (bi, bj), kept in registers
     const int bi = w >> 1, bj = w & 1;
     f32x16 kk = (f32x16)(0.f), qk = (f32x16)(0.f);
 #pragma unroll
@@ -262,104 +261,126 @@ chunk_prep_kernel(const f16* __restrict__ q, const f16* __restrict__ k,
         kk = __builtin_amdgcn_mfma_f32_32x32x16_f16(ak, bk, kk, 0, 0, 0);
         qk = __builtin_amdgcn_mfma_f32_32x32x16_f16(aq, bk, qk, 0, 0, 0);
     }
-    __syncthreads();   // every K / Q read done: A and M o QK^T take their storage
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-        const int i = 32 * bi + 8 * (r >> 2) + 4 * hh + (r & 3);
-        const int j = 32 * bj + ql;
-        // e^{g_i - g_j}, taken for every pair (above the diagonal it may be
-        // inf, and is not selected)
-        const float ratio = fast_exp2((sG[i] - sG[j]) * FL_LOG2E);
-        sA[i][j] = j < i ? sB[i] * ratio * kk[r] : 0.f;
-        sM[i][j] = j <= i ? ratio * qk[r] : 0.f;
-    }
-    __syncthreads();
 
-    // T = (I + A)^-1 by blocks of 16, in fp32: T_ii = D_i = (I + A_ii)^-1 by
-    // forward substitution (wave i, lane j solving column j), then, a block
-    // diagonal at a time, T_ij = -D_i sum_{k = j .. i-1} A_ik T_kj on fp32
-    // MFMA. T is kept transposed in sA's upper triangle (T_ij[a][b] at
-    // sA[16 j + b][16 i + a]), clear of A below the diagonal.
-    if (lane < 16) {
-        const int o = 16 * w, j = lane;
-        float xd[16];
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            float a0 = i == j ? 1.f : 0.f, a1 = 0.f;
-#pragma unroll
-            for (int m = 0; m < i; ++m) {
-                if (m & 1)
-                    a1 = fmaf(-sA[o + i][o + m], xd[m], a1);
-                else
-                    a0 = fmaf(-sA[o + i][o + m], xd[m], a0);
-            }
-            xd[i] = a0 + a1;
+    for (int hv = hv0; hv < hv_end; ++hv) {
+        char* blk = work + ((size_t)c * n_vheads + hv) * CK_BLK;
+        // this head's gates (decay 1 and beta 0 past the end: g stays at the
+        // last token's), the in-chunk prefix sums of log decay on wave 0; the
+        // next head's gates loaded meanwhile
+        if (w == 0) {
+            const float gs = wave_prefix_sum(lane < n ? safe_log(dec) : 0.f);
+            sG[lane] = gs;
+            sB[lane] = lane < n ? bet : 0.f;
         }
-        // every element, the zeros above D_w's diagonal included: they land
-        // on A_ww, which the remaining steps do not read
+        if (hv + 1 < hv_end) {
+            dec = decay[gt + hv + 1];
+            bet = beta[gt + hv + 1];
+        }
+        __syncthreads();   // the gates in; every K / Q read (or T / M o QK^T
+                           // read of the previous head) done
+
+        // A = strictly lower beta_i e^{g_i - g_j} k_i.k_j and M o QK^T
 #pragma unroll
-        for (int i = 0; i < 16; ++i) sA[o + j][o + i] = xd[i];
-    }
-    __syncthreads();
-#pragma unroll
-    for (int lv = 1; lv < 4; ++lv) {
-        if (w < 4 - lv) t_block(sA, w + lv, w, lane);
+        for (int r = 0; r < 16; ++r) {
+            const int i = 32 * bi + 8 * (r >> 2) + 4 * hh + (r & 3);
+            const int j = 32 * bj + ql;
+            // e^{g_i - g_j}, taken for every pair (above the diagonal it may be
+            // inf, and is not selected)
+            const float ratio = fast_exp2((sG[i] - sG[j]) * FL_LOG2E);
+            sA[i][j] = j < i ? sB[i] * ratio * kk[r] : 0.f;
+            sM[i][j] = j <= i ? ratio * qk[r] : 0.f;
+        }
         __syncthreads();
-    }
-    // the scales: block maxima of |T| and |M o QK^T|
-    float mt = 0.f, mq = 0.f;
-#pragma unroll
-    for (int m = 0; m < CK_C * CK_C / 256; ++m) {
-        const int idx = tid + 256 * m, i = idx >> 6, j = idx & 63;
-        float tv = sA[j][i];   // T[i][j], transposed: A's values where j > i
-        keep(tv);
-        mt = fmaxf(mt, i >= j ? fabsf(tv) : 0.f);
-        mq = fmaxf(mq, fabsf(sM[i][j]));
-    }
-    mt = wave_max(mt);
-    mq = wave_max(mq);
-    if (lane == 0) {
-        sRed[w] = mt;
-        sRed[4 + w] = mq;
-    }
-    __syncthreads();
-    mt = fmaxf(fmaxf(sRed[0], sRed[1]), fmaxf(sRed[2], sRed[3]));
-    mq = fmaxf(fmaxf(sRed[4], sRed[5]), fmaxf(sRed[6], sRed[7]));
-    float t_inv, q_inv;
-    const float t_sc = pow2_scale<7>(mt, t_inv);
-    const float q_sc = pow2_scale<7>(mq, q_inv);
 
-    // the operands: slot (T or M o QK^T; block f, lane l = 16 g + i) holds row
-    // 16 mb + i at columns 32 kq + kap(g, e), its hi and lo halves 6 KiB apart
+        // T = (I + A)^-1 by blocks of 16, in fp32: T_ii = D_i = (I + A_ii)^-1
+        // by forward substitution (wave i, lane j solving column j), then, a
+        // block diagonal at a time, T_ij = -D_i sum_{k = j .. i-1} A_ik T_kj on
+        // fp32 MFMA. T is kept transposed in sA's upper triangle
+        // (T_ij[a][b] at sA[16 j + b][16 i + a]), clear of A below the diagonal.
+        if (lane < 16) {
+            const int o = 16 * w, j = lane;
+            float xd[16];
 #pragma unroll
-    for (int m = 0; m < 3; ++m) {
-        const int s = tid + 256 * m;
-        const bool isq = s >= CK_NF * 64;
-        const int f = (s % (CK_NF * 64)) >> 6, l = s & 63;
-        const int g = l >> 4, row = 16 * f_mb(f) + (l & 15), kq = f_kq(f);
-        f16x8 hi, lo;
+            for (int i = 0; i < 16; ++i) {
+                float a0 = i == j ? 1.f : 0.f, a1 = 0.f;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const int col = 32 * kq + (e < 4 ? 4 * g + e : 12 + 4 * g + e);
-            float ta = sA[col][row];   // T[row][col], transposed
-            keep(ta);
-            const float mq_ = sM[row][col];
-            const float xs = isq ? mq_ * q_sc : (row >= col ? ta : 0.f) * t_sc;
-            const f16 h = (f16)xs;
-            hi[e] = h;
-            lo[e] = (f16)(xs - (float)h);
+                for (int m = 0; m < i; ++m) {
+                    if (m & 1)
+                        a1 = fmaf(-sA[o + i][o + m], xd[m], a1);
+                    else
+                        a0 = fmaf(-sA[o + i][o + m], xd[m], a0);
+                }
+                xd[i] = a0 + a1;
+            }
+            // every element, the zeros above D_w's diagonal included: they land
+            // on A_ww, which the remaining steps do not read
+#pragma unroll
+            for (int i = 0; i < 16; ++i) sA[o + j][o + i] = xd[i];
         }
-        char* dst = blk + (isq ? WS_Q_HI : WS_T_HI) + (f * 64 + l) * 16;
-        *(f16x8*)dst = hi;
-        *(f16x8*)(dst + WS_OP) = lo;
-    }
-    if (tid < CK_C) {
-        const float gC = sG[CK_C - 1];
-        ((float*)(blk + WS_BETA))[tid] = sB[tid];
-        ((float*)(blk + WS_EG))[tid] = expf(sG[tid]);
-        ((float*)(blk + WS_DK))[tid] = expf(gC - sG[tid]);
-        if (tid < 4)
-            ((float*)(blk + WS_SC))[tid] = tid == 0 ? expf(gC) : tid == 1 ? t_inv : tid == 2 ? q_inv : 0.f;
+        __syncthreads();
+#pragma unroll
+        for (int lv = 1; lv < 4; ++lv) {
+            if (w < 4 - lv) t_block(sA, w + lv, w, lane);
+            __syncthreads();
+        }
+
+        // the scales: block maxima of |T| and |M o QK^T|
+        float mt = 0.f, mq = 0.f;
+#pragma unroll
+        for (int m = 0; m < CK_C * CK_C / 256; ++m) {
+            const int idx = tid + 256 * m, i = idx >> 6, j = idx & 63;
+            float tv = sA[j][i];   // T[i][j], transposed: A's values where j > i
+            keep(tv);
+            mt = fmaxf(mt, i >= j ? fabsf(tv) : 0.f);
+            mq = fmaxf(mq, fabsf(sM[i][j]));
+        }
+        mt = wave_max(mt);
+        mq = wave_max(mq);
+        if (lane == 0) {
+            sRed[w] = mt;
+            sRed[4 + w] = mq;
+        }
+        __syncthreads();
+        mt = fmaxf(fmaxf(sRed[0], sRed[1]), fmaxf(sRed[2], sRed[3]));
+        mq = fmaxf(fmaxf(sRed[4], sRed[5]), fmaxf(sRed[6], sRed[7]));
+        float t_inv, q_inv;
+        const float t_sc = pow2_scale<7>(mt, t_inv);
+        const float q_sc = pow2_scale<7>(mq, q_inv);
+
+        // the operands: slot (T or M o QK^T; block f, lane l = 16 g + i) holds
+        // row 16 mb + i at columns 32 kq + kap(g, e), its hi and lo halves
+        // 6 KiB apart
+#pragma unroll
+        for (int m = 0; m < 3; ++m) {
+            const int s = tid + 256 * m;
+            const bool isq = s >= CK_NF * 64;
+            const int f = (s % (CK_NF * 64)) >> 6, l = s & 63;
+            const int g = l >> 4, row = 16 * f_mb(f) + (l & 15), kq = f_kq(f);
+            f16x8 hi, lo;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int col = 32 * kq + (e < 4 ? 4 * g + e : 12 + 4 * g + e);
+                float ta = sA[col][row];   // T[row][col], transposed
+                keep(ta);
+                const float mq_ = sM[row][col];
+                const float xs = isq ? mq_ * q_sc : (row >= col ? ta : 0.f) * t_sc;
+                const f16 h = (f16)xs;
+                hi[e] = h;
+                lo[e] = (f16)(xs - (float)h);
+            }
+            char* dst = blk + (isq ? WS_Q_HI : WS_T_HI) + (f * 64 + l) * 16;
+            *(f16x8*)dst = hi;
+            *(f16x8*)(dst + WS_OP) = lo;
+        }
+        if (tid < CK_C) {
+            const float gC = sG[CK_C - 1];
+            ((float*)(blk + WS_BETA))[tid] = sB[tid];
+            ((float*)(blk + WS_EG))[tid] = expf(sG[tid]);
+            ((float*)(blk + WS_DK))[tid] = expf(gC - sG[tid]);
+            if (tid < 4)
+                ((float*)(blk + WS_SC))[tid] =
+                    tid == 0 ? expf(gC) : tid == 1 ? t_inv : tid == 2 ? q_inv : 0.f;
+        }
     }
 }
 
@@ -903,7 +924,7 @@ int fl_gdn_prefill_chunked(const void* q, const void* k, const void* v, const fl
         return FL_ESCRATCH;
     }
     const int n_chunks = (T + CK_C - 1) / CK_C;
-    hipLaunchKernelGGL(chunk_prep_kernel, dim3(n_chunks, n_vheads), dim3(256), 0,
+    hipLaunchKernelGGL(chunk_prep_kernel, dim3(n_chunks, (n_vheads + group - 1) / group), dim3(256), 0,
                        (hipStream_t)stream, (const f16*)q, (const f16*)k, beta, decay, T, n_vheads,
                        qk_stride, group, (char*)work);
     int rc = fl::check_launch("gdn_chunk_prep");
