@@ -1031,6 +1031,37 @@ int split_policy(int T, int pos0, int n_q_heads, int n_kv_heads) {
     return best;
 }
 
+// The int8 cache's rows [0, rows) as fp16(byte * scale), the values the int8
+// kernel builds in LDS, into a staging copy [rows][n_kv][256] of K then V:
+// thread i converts 16-byte chunk i of a K row and of a V row (16 values of
+// one 32-value scale block) into two 16-byte stores each. HBM-bound; the
+// long prefill then runs the 64-rows-a-wave kernel on the copy.
+__global__ void __launch_bounds__(256)
+q8_stage_kernel(const uint4* __restrict__ kc, const uint4* __restrict__ vc,
+                const f16* __restrict__ ksc, const f16* __restrict__ vsc, f16x8* __restrict__ ko,
+                f16x8* __restrict__ vo, int n_chunks) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= n_chunks) return;
+    const uint4 kb = kc[i], vb = vc[i];
+    const f16 ks = ksc[i >> 1], vs = vsc[i >> 1];   // 16 chunks, 8 scales a row of 256
+    ko[2 * i] = deq8(kb.x, kb.y, ks);
+    ko[2 * i + 1] = deq8(kb.z, kb.w, ks);
+    vo[2 * i] = deq8(vb.x, vb.y, vs);
+    vo[2 * i + 1] = deq8(vb.z, vb.w, vs);
+}
+
+// Bytes of that staging copy for a long prefill over an int8 cache (the rows
+// [0, pos0 + T) every query reads, fp16 K and V), 0 where the 64-rows-a-wave
+// kernel does not run (short prompts, the KV-split chunk).
+size_t q8_stage_bytes(int T, int pos0, int n_q_heads, int n_kv_heads, int head_dim) {
+    if (T < 1 || pos0 < 0 || n_kv_heads < 1 || n_q_heads < 1 || n_q_heads % n_kv_heads != 0 ||
+        head_dim != PF_HD)
+        return 0;
+    if (split_policy(T, pos0, n_q_heads, n_kv_heads) != 1 || !use_r64(T, n_q_heads, n_kv_heads))
+        return 0;
+    return 2 * (size_t)(pos0 + T) * n_kv_heads * head_dim * sizeof(f16);
+}
+
 size_t split_work_bytes(int T, int n_q_heads, int head_dim, int split) {
     return (size_t)T * n_q_heads * split * ((size_t)head_dim * 4 + 8);
 }
@@ -1087,7 +1118,25 @@ int prefill(const void* q, int q_pitch, const void* k_new, const void* v_new, vo
     }
     const int rows = T * (n_q_heads / n_kv_heads);
     const int r64_tiles = (rows + R64_BQ - 1) / R64_BQ;
-    if (!Q8 && split == 1 && use_r64(T, n_q_heads, n_kv_heads)) {
+    // over an int8 cache with room in `work` for the fp16 staging copy: stage,
+    // then the fp16 path below on the copy
+    const size_t stage = Q8 && split == 1 ? q8_stage_bytes(T, pos0, n_q_heads, n_kv_heads, head_dim)
+                                          : 0;
+    const bool staged = stage > 0 && work != nullptr && aligned16(work) && work_bytes >= stage;
+    if (staged) {
+        const size_t cache_rows = (size_t)(pos0 + T) * n_kv_heads;
+        const int n_chunks = (int)(cache_rows * (PF_HD / 16));
+        f16* ko = (f16*)work;
+        f16* vo = ko + cache_rows * PF_HD;
+        hipLaunchKernelGGL(q8_stage_kernel, dim3((n_chunks + 255) / 256), dim3(256), 0,
+                           (hipStream_t)stream, (const uint4*)kc, (const uint4*)vc, ksc, vsc,
+                           (f16x8*)ko, (f16x8*)vo, n_chunks);
+        rc = fl::check_launch("attn_prefill q8 staging");
+        if (rc) return rc;
+        kc = ko;
+        vc = vo;
+    }
+    if ((!Q8 || staged) && split == 1 && use_r64(T, n_q_heads, n_kv_heads)) {
         R64Plan plan;
         const int G = n_q_heads / n_kv_heads;
         const int bins = r64_plan(T, pos0, G, n_kv_heads, n_cu, plan) > 0 ? n_cu / n_kv_heads : 0;
@@ -1155,6 +1204,11 @@ extern "C" int fl_attention_prefill_plan(int T, int pos0, int n_q_heads, int n_k
 
 extern "C" int fl_attention_prefill_split_count(int T, int pos0, int n_q_heads, int n_kv_heads) {
     return split_policy(T, pos0, n_q_heads, n_kv_heads);
+}
+
+extern "C" size_t fl_attention_prefill_q8_stage_bytes(int T, int pos0, int n_q_heads,
+                                                     int n_kv_heads, int head_dim) {
+    return q8_stage_bytes(T, pos0, n_q_heads, n_kv_heads, head_dim);
 }
 
 extern "C" size_t fl_attention_prefill_work_bytes(int T, int n_q_heads, int head_dim, int split) {

@@ -396,7 +396,9 @@ def attention_prefill_q8(q, kcache, vcache, *, pos0: int, max_pos: int, T: int |
                          n_kv_heads: int = N_KV, q_pitch: int | None = None,
                          scale: float = ATTN_SCALE, split: int | None = None, work=None):
     """attention_prefill_fh_q8 (kernels.cu:2778-2786) over an int8 cache, with
-    kv_store_q8 of k_new / v_new fused in front when given."""
+    kv_store_q8 of k_new / v_new fused in front when given. Long prompts run
+    the fp16 long-prompt kernel on an fp16 copy of the cache rows made first
+    (in `work`, allocated here when not given or too small)."""
     T = q.shape[0] if T is None else T
     q_pitch = q.shape[-1] if q_pitch is None else q_pitch
     row = n_kv_heads * HEAD_DIM
@@ -409,7 +411,16 @@ def attention_prefill_q8(q, kcache, vcache, *, pos0: int, max_pos: int, T: int |
             _kv8(vcache, "vcache", max_pos, n_kv_heads, HEAD_DIM), 0, n_q_heads, n_kv_heads,
             HEAD_DIM, pos0, max_pos, float(scale), T)
     zargs = (_ptr(z, F16, "z", T * n_q_heads * z.shape[-1]), z.shape[-1])
+    stage = 0
     if split == 1:
+        stage = int(_lib.lib().fl_attention_prefill_q8_stage_bytes(T, pos0, n_q_heads, n_kv_heads,
+                                                                   HEAD_DIM))
+    if split == 1 and stage > 0:
+        if work is None or work.numel() < stage:
+            work = torch.empty(stage, dtype=torch.uint8, device=q.device)
+        _lib.call("fl_attention_prefill_kv_q8", *args, 1, *zargs,
+                  _ptr(work, torch.uint8, "work", stage), work.numel(), _stream())
+    elif split == 1:
         _lib.call("fl_attention_prefill_q8", *args, *zargs, _stream())
     else:
         _lib.call("fl_attention_prefill_kv_q8", *args, split, *zargs,

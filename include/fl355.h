@@ -260,7 +260,13 @@ int fl_attention_prefill_kv(const void* q, int q_pitch, const void* k_new, const
                             int head_dim, int pos0, int max_pos, float scale, int T, int split,
                             void* z, int z_pitch, void* work, size_t work_bytes,
                             fl_stream_t stream);
-/* ... over an int8 cache (attention_prefill_fh_q8, kernels.cu:2778-2786). */
+/* ... over an int8 cache (attention_prefill_fh_q8, kernels.cu:2778-2786).
+ * With split 1 and `work` of at least fl_attention_prefill_q8_stage_bytes
+ * bytes (nonzero for long prompts), the rows [0, pos0 + T) are first
+ * converted to fp16 (byte * scale, the values the int8 kernel forms) into
+ * `work`, and the long-prompt fp16 kernel runs on that copy. */
+size_t fl_attention_prefill_q8_stage_bytes(int T, int pos0, int n_q_heads, int n_kv_heads,
+                                           int head_dim);
 int fl_attention_prefill_kv_q8(const void* q, int q_pitch, const void* k_new, const void* v_new,
                                void* kcache, void* vcache, int layer, int n_q_heads,
                                int n_kv_heads, int head_dim, int pos0, int max_pos, float scale,

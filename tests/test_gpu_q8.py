@@ -226,6 +226,35 @@ def test_prefill_q8_vs_oracle(fl, dev, orc, rng, T, pos0):
     assert ok, f"T={T} pos0={pos0}: max|err| {err}"
 
 
+def test_prefill_q8_staged_equals_direct(fl, dev, orc, rng):
+    """A long prompt over an int8 cache two ways: the fp16 staging copy with the
+    long-prompt kernel (what attention_prefill_q8 picks here) and the int8
+    kernel reading the cache directly (fl_attention_prefill_q8): the same fp16
+    values enter both, so they agree to the kernels' rounding (the staged path
+    is checked against the oracle by the 8k sampled-row test below)."""
+    T, pos0 = 4096, 512   # 384 row tiles of 64: the long-prompt kernel's shape
+    L = pos0 + T
+    k, v, kc8, vc8 = oracle_cache(orc, rng, L, L)
+    qg = rand_qg(rng, T)
+    kd, vd = fl.ops.kv8_cache(L), fl.ops.kv8_cache(L)
+    fl.ops.kv_store_q8(to_dev(k, dev), to_dev(v, dev), kd, vd, pos0=0, max_pos=L)
+    lib = fl._lib.lib()
+    stage = lib.fl_attention_prefill_q8_stage_bytes(T, pos0, 24, 4, 256)
+    assert stage == 2 * L * 4 * 256 * 2
+    assert lib.fl_attention_prefill_q8_stage_bytes(T, pos0, 24, 4, 128) == 0
+    assert lib.fl_attention_prefill_q8_stage_bytes(64, pos0, 24, 4, 256) == 0   # short: no copy
+    qd = to_dev(qg, dev)
+    z_st = fl.ops.attention_prefill_q8(qd, kd, vd, pos0=pos0, max_pos=L)
+    z_di = torch.empty_like(z_st)
+    fl._lib.call("fl_attention_prefill_q8", qd.data_ptr(), 512, None, None, kd.data_ptr(),
+                 vd.data_ptr(), 0, 24, 4, 256, pos0, L, float(SCALE), T, z_di.data_ptr(), 256,
+                 None)
+    torch.cuda.synchronize()
+    a, b = z_st.float().cpu().numpy(), z_di.float().cpu().numpy()
+    err, ok = close(a, b, ATOL, RTOL)
+    assert ok, f"staged vs direct: max|err| {err}"
+
+
 @pytest.mark.parametrize("L", [8192])
 def test_prefill_q8_config3_sampled_rows(fl, dev, orc, L):
     """Config 3's shape over an int8 cache: sampled rows against the float64
