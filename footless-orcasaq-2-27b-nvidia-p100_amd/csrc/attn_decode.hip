@@ -78,22 +78,34 @@ struct DecSeqs {
 // split_rows, 1, split) splits over its nt = ceil(seqlen / 32) tiles, split s
 // taking tiles [nt s / St, nt (s+1) / St) (the reference's per-token rule,
 // kernels.cu:535-544, on tile boundaries). Empty (lo == hi == 0) for s >= St.
-__host__ __device__ __forceinline__ int split_count(int seqlen, int split_rows, int split) {
+// With floor_splits > 0 a token gets at least min(seqlen / 64, floor_splits)
+// splits (still at most `split`): short contexts are cut into 64-row splits
+// up to that floor, so they spread over more CUs; longer ones keep
+// split_rows rows a split, so the partials stay a small part of the bytes.
+// Either way St is a function of the token's own length.
+constexpr int DEC_FINE_ROWS = 64;
+
+__host__ __device__ __forceinline__ int split_count(int seqlen, int split_rows, int split,
+                                                    int floor_splits) {
     int st = seqlen / split_rows;
+    const int fine = seqlen / DEC_FINE_ROWS;
+    const int lo = fine < floor_splits ? fine : floor_splits;
+    st = st > lo ? st : lo;
     return st < 1 ? 1 : (st > split ? split : st);
 }
 
 __host__ __device__ __forceinline__ void split_range(int seqlen, int s, int split_rows, int split,
-                                                     int& lo, int& hi) {
-    const int st = split_count(seqlen, split_rows, split);
+                                                     int floor_splits, int& lo, int& hi) {
+    const int st = split_count(seqlen, split_rows, split, floor_splits);
     if (s >= st) {
         lo = 0;
         hi = 0;
         return;
     }
-    const int nt = (seqlen + DEC_TILE - 1) / DEC_TILE;
-    const int t0 = (int)((long long)nt * s / st);
-    const int t1 = (int)((long long)nt * (s + 1) / st);
+    // nt (s + 1) < 2^32 (split_math_fits): 32-bit unsigned products
+    const unsigned nt = (unsigned)(seqlen + DEC_TILE - 1) / DEC_TILE;
+    const int t0 = (int)(nt * (unsigned)s / (unsigned)st);
+    const int t1 = (int)(nt * (unsigned)(s + 1) / (unsigned)st);
     lo = t0 * DEC_TILE;
     hi = t1 * DEC_TILE < seqlen ? t1 * DEC_TILE : seqlen;
 }
@@ -116,9 +128,9 @@ __host__ __device__ __forceinline__ void dec_split_range(int len, int s, int tmi
         hi = 0;
         return;
     }
-    const int nkt = (len + 63) / 64;
-    lo = (int)((long long)nkt * s / st) * 64;
-    const int e = (int)((long long)nkt * (s + 1) / st) * 64;
+    const unsigned nkt = (unsigned)(len + 63) / 64;   // nkt (s + 1) < 2^32
+    lo = (int)(nkt * (unsigned)s / (unsigned)st) * 64;
+    const int e = (int)(nkt * (unsigned)(s + 1) / (unsigned)st) * 64;
     hi = e < len ? e : len;
 }
 
@@ -251,7 +263,8 @@ template <int NBUF, bool NT_V, bool Q8, bool DEC>
 __global__ void __launch_bounds__(DEC_THREADS)
 attn_decode_split_kernel(const f16* __restrict__ qg, DecSeqs seqs, float* __restrict__ pacc,
                          float* __restrict__ pm, float* __restrict__ pd, int n_q_heads,
-                         int n_kv, int q_pitch, int T, int split, int split_rows, float sl2) {
+                         int n_kv, int q_pitch, int T, int split, int split_rows,
+                         int split_floor, float sl2) {
     __shared__ __attribute__((aligned(16))) f32x4 s_part[2][DEC_WAVES][4][64];
     __shared__ __attribute__((aligned(16))) f16 s_vt[DEC_WAVES][64][VT_PITCH];
 
@@ -272,7 +285,7 @@ attn_decode_split_kernel(const f16* __restrict__ qg, DecSeqs seqs, float* __rest
         if constexpr (DEC)
             dec_split_range(len, s, split_rows, split, lo, hi);
         else
-            split_range(len, s, split_rows, split, lo, hi);
+            split_range(len, s, split_rows, split, split_floor, lo, hi);
     };
 
     // the union of the launch's tokens' ranges for this split
@@ -445,16 +458,22 @@ attn_decode_split_kernel(const f16* __restrict__ qg, DecSeqs seqs, float* __rest
 
 // ---------------------------------------------------------------------------
 // merge (+ gate): attention_merge (kernels.cu:1387-1424) with attn_gate
-// (kernels.cu:1572-1600) fused. M = max_s m_s, z = f16_sat(sum_s e_s acc_s /
-// sum_s e_s d_s), e_s = e^(m_s - M), then z = f16_sat(z * sigmoid(g)).
-// One block of 256 threads a (row, q head). Thread tid owns the float4 of
-// dims 4c..4c+3 (c = tid % C, C = head_dim / 4) for the splits s = j, j + J,
-// ... (j = tid / C, J = 256 / C), eight partials in flight; the J group sums
-// are added in j order through LDS. Empty partials (m = -1e30, d = 0, acc =
-// 0) contribute exact zeros, so the result does not depend on how many
-// empty splits follow a token's own.
+// (kernels.cu:1572-1600) fused. z = f16_sat(sum_s e_s acc_s / sum_s e_s d_s),
+// e_s = e^(m_s - M) with M = max_s m_s, then z = f16_sat(z * sigmoid(g)).
+// One block of 256 threads a (row, q head), one pass over the partials:
+// thread tid owns the float4 of dims 4c..4c+3 (c = tid % C, C = head_dim / 4)
+// for the splits s = j, j + J, ... (j = tid / C, J = 256 / C), read in
+// batches of eight with every load issued before any is used (indices past
+// the last split clamped, their values replaced by an empty partial). Each
+// thread weighs its splits by e^(m_s - M_j) against its own running max M_j
+// (rescaled when a batch raises it); the J group sums are then weighed by
+// e^(M_j - M) and added in j order through LDS. The gate is read before the
+// partials. Empty partials (m = -1e30, d = 0, acc = 0) contribute exact
+// zeros, so the result does not depend on how many empty splits follow a
+// token's own.
 // ---------------------------------------------------------------------------
 constexpr int MG_THREADS = 256;
+constexpr int MG_BATCH = 8;
 
 __global__ void __launch_bounds__(MG_THREADS)
 attn_merge_kernel(const float* __restrict__ pacc, const float* __restrict__ pm,
@@ -463,73 +482,86 @@ attn_merge_kernel(const float* __restrict__ pacc, const float* __restrict__ pm,
                   int g_pitch, int g_off, int split) {
     __shared__ f32x4 s_num[MG_THREADS];
     __shared__ float s_den[MG_THREADS];
-    __shared__ float s_max[MG_THREADS / 64];
+    __shared__ float s_mx[MG_THREADS];
     const int head = blockIdx.x, row = blockIdx.y, tid = threadIdx.x;
     const int C = head_dim >> 2, J = MG_THREADS / C;
     const int c = tid % C, j = tid / C;
-    const size_t p0 = ((size_t)row * n_q_heads + head) * split;
+    const size_t rh = (size_t)row * n_q_heads + head;
+    const size_t p0 = rh * split;
     const float* pmr = pm + p0;
     const float* pdr = pd + p0;
 
-    float M = -1e30f;
-    for (int s = tid; s < split; s += MG_THREADS) M = fmaxf(M, pmr[s]);
+    float gv[4] = {0.f, 0.f, 0.f, 0.f};
+    if (gate != nullptr && tid < C) {
+        const f16* gr = gate + rh * g_pitch + g_off + 4 * tid;
 #pragma unroll
-    for (int d = 32; d >= 1; d >>= 1) M = fmaxf(M, lane_xor(M, d));
-    if ((tid & 63) == 0) s_max[tid >> 6] = M;
-    __syncthreads();
-    M = fmaxf(fmaxf(s_max[0], s_max[1]), fmaxf(s_max[2], s_max[3]));
+        for (int e = 0; e < 4; ++e) gv[e] = (float)gr[e];
+    }
 
     f32x4 num = (f32x4)(0.f);
-    float den = 0.f;
+    float den = 0.f, M = -1e30f;
     if (j < J) {
         const f32x4* acc = (const f32x4*)(pacc + p0 * head_dim) + c;
-        auto add = [&](float m, float dv, const f32x4& a) {
-            const float e = fast_exp2((m - M) * FL_LOG2E);
-            num[0] = fmaf(e, a[0], num[0]);
-            num[1] = fmaf(e, a[1], num[1]);
-            num[2] = fmaf(e, a[2], num[2]);
-            num[3] = fmaf(e, a[3], num[3]);
-            den = fmaf(e, dv, den);
-        };
-        int s = j;
-        for (; s + 7 * J < split; s += 8 * J) {
-            float mv[8], dv[8];
-            f32x4 av[8];
+        for (int s = j; s < split; s += MG_BATCH * J) {
+            float mv[MG_BATCH], dv[MG_BATCH];
+            f32x4 av[MG_BATCH];
 #pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                mv[u] = pmr[s + u * J];
-                dv[u] = pdr[s + u * J];
-                av[u] = acc[(size_t)(s + u * J) * C];
+            for (int u = 0; u < MG_BATCH; ++u) {
+                const int si = min(s + u * J, split - 1);
+                mv[u] = pmr[si];
+                dv[u] = pdr[si];
+                av[u] = acc[(size_t)si * C];
+            }
+            float bm = M;
+#pragma unroll
+            for (int u = 0; u < MG_BATCH; ++u) {
+                const bool ok = s + u * J < split;
+                mv[u] = ok ? mv[u] : -1e30f;
+                dv[u] = ok ? dv[u] : 0.f;
+                av[u] = ok ? av[u] : (f32x4)(0.f);
+                bm = fmaxf(bm, mv[u]);
+            }
+            if (bm > M) {
+                const float corr = fast_exp2((M - bm) * FL_LOG2E);
+                num *= corr;
+                den *= corr;
+                M = bm;
             }
 #pragma unroll
-            for (int u = 0; u < 8; ++u) add(mv[u], dv[u], av[u]);
+            for (int u = 0; u < MG_BATCH; ++u) {
+                const float e = fast_exp2((mv[u] - M) * FL_LOG2E);
+                num[0] = fmaf(e, av[u][0], num[0]);
+                num[1] = fmaf(e, av[u][1], num[1]);
+                num[2] = fmaf(e, av[u][2], num[2]);
+                num[3] = fmaf(e, av[u][3], num[3]);
+                den = fmaf(e, dv[u], den);
+            }
         }
-        for (; s < split; s += J) add(pmr[s], pdr[s], acc[(size_t)s * C]);
     }
     s_num[tid] = num;
     s_den[tid] = den;
+    s_mx[tid] = M;
     __syncthreads();
     if (tid < C) {
-        f32x4 n = s_num[tid];
-        float dsum = s_den[tid];
-        for (int jj = 1; jj < J; ++jj) {
+        float Mg = s_mx[tid];
+        for (int jj = 1; jj < J; ++jj) Mg = fmaxf(Mg, s_mx[jj * C + tid]);
+        f32x4 n = (f32x4)(0.f);
+        float dsum = 0.f;
+        for (int jj = 0; jj < J; ++jj) {
+            const float e = fast_exp2((s_mx[jj * C + tid] - Mg) * FL_LOG2E);
             const f32x4 o = s_num[jj * C + tid];
-            n[0] += o[0];
-            n[1] += o[1];
-            n[2] += o[2];
-            n[3] += o[3];
-            dsum += s_den[jj * C + tid];
+            n[0] = fmaf(e, o[0], n[0]);
+            n[1] = fmaf(e, o[1], n[1]);
+            n[2] = fmaf(e, o[2], n[2]);
+            n[3] = fmaf(e, o[3], n[3]);
+            dsum = fmaf(e, s_den[jj * C + tid], dsum);
         }
         const float inv = 1.f / dsum;
-        const size_t rh = (size_t)row * n_q_heads + head;
         f16* zr = z + rh * z_pitch + 4 * tid;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             f16 zv = f16_sat(n[e] * inv);
-            if (gate != nullptr) {
-                const float g = (float)gate[rh * g_pitch + g_off + 4 * tid + e];
-                zv = f16_sat((float)zv * sigmoid_f(g));
-            }
+            if (gate != nullptr) zv = f16_sat((float)zv * sigmoid_f(gv[e]));
             zr[e] = zv;
         }
     }
@@ -575,20 +607,30 @@ __global__ void attn_gate_kernel(f16* __restrict__ z, const f16* __restrict__ g,
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
+// The batched decode's split floor (split_count): on MI355X a 4k-row B = 1
+// decode with 16 splits of 256 rows leaves 192 of 256 CUs idle; 32 splits of
+// 64-128 rows run it 1.3x faster, while 4-sequence verify launches at 8k and
+// beyond keep their 256-row splits (more splits there cost more in partial
+// traffic than the wider grid gains).
+#ifndef DEC_SPLIT_FLOOR
+#define DEC_SPLIT_FLOOR 32
+#endif
+
 #ifndef DEC_NBUF_Q8
 #define DEC_NBUF_Q8 3
 #endif
 
-// grid_split blocks a (sequence, kv head); `split` the partials' stride.
+// grid_split blocks a (sequence, kv head); `split` the partials' stride;
+// split_floor the floor of split_count (0: the reference's rule).
 template <bool Q8, bool DEC>
 int launch_split(const f16* qg, const DecSeqs& seqs, float* pacc, float* pm, float* pd, int B,
                  int T, int n_q_heads, int n_kv, int q_pitch, int grid_split, int split,
-                 int split_rows, float sl2, hipStream_t stream) {
+                 int split_rows, float sl2, hipStream_t stream, int split_floor = 0) {
     dim3 grid(grid_split, n_kv, B);
     constexpr int NBUF = Q8 ? DEC_NBUF_Q8 : DEC_NBUF;
     hipLaunchKernelGGL((attn_decode_split_kernel<NBUF, DEC_NT_V, Q8, DEC>), grid, dim3(DEC_THREADS),
                        0, stream, qg, seqs, pacc, pm, pd, n_q_heads, n_kv, q_pitch, T, split,
-                       split_rows, sl2);
+                       split_rows, split_floor, sl2);
     return fl::check_launch("attn_decode_split");
 }
 
@@ -607,6 +649,12 @@ void set_q8_seq(DecSeqs& seqs, int b, const void* kc, const void* vc, int max_po
 // (or sequence's) base.
 bool cache_fits(int max_pos, int n_kv, int bytes_per_elem) {
     return (uint64_t)max_pos * n_kv * DEC_HD * bytes_per_elem < (1ull << 31);
+}
+
+// The split ranges are formed with 32-bit unsigned products of a token's
+// tile count and a split index.
+bool split_math_fits(int max_pos, int split) {
+    return (uint64_t)(max_pos / DEC_TILE + 1) * (uint64_t)(split + 1) < (1ull << 32);
 }
 
 int check_decode_geometry(int T, int n_q_heads, int n_kv, int head_dim, int q_pitch, int split,
@@ -645,6 +693,7 @@ int attn_decode_batched(const void* qg, int q_pitch, const void* const* kcache,
         FL_REQUIRE(aligned16(kcache[b]) && aligned16(vcache[b]), "16-byte aligned caches");
         FL_REQUIRE(pos0[b] >= 0 && pos0[b] + T <= cap[b], "pos0[b] + T <= cap[b]");
         FL_REQUIRE(cache_fits(cap[b], n_kv_heads, Q8 ? 1 : 2), "a cache of at most 2 GiB");
+        FL_REQUIRE(split_math_fits(cap[b], split), "(cap / 32 + 1) * (split + 1) < 2^32");
         if (Q8)
             set_q8_seq(seqs, b, kcache[b], vcache[b], cap[b], n_kv_heads, pos0[b]);
         else {
@@ -652,7 +701,7 @@ int attn_decode_batched(const void* qg, int q_pitch, const void* const* kcache,
             seqs.v[b] = (const f16*)vcache[b];
             seqs.pos0[b] = pos0[b];
         }
-        const int st = split_count(pos0[b] + T, split_rows, split);
+        const int st = split_count(pos0[b] + T, split_rows, split, DEC_SPLIT_FLOOR);
         grid_split = st > grid_split ? st : grid_split;
     }
     const size_t parts = (size_t)B * T * n_q_heads * grid_split;
@@ -661,7 +710,7 @@ int attn_decode_batched(const void* qg, int q_pitch, const void* const* kcache,
     float* pd = pm + parts;
     rc = launch_split<Q8, false>((const f16*)qg, seqs, pacc, pm, pd, B, T, n_q_heads, n_kv_heads,
                                  q_pitch, grid_split, grid_split, split_rows, scale * FL_LOG2E,
-                                 (hipStream_t)stream);
+                                 (hipStream_t)stream, DEC_SPLIT_FLOOR);
     if (rc) return rc;
     hipLaunchKernelGGL(attn_merge_kernel, dim3(n_q_heads, B * T), dim3(MG_THREADS), 0,
                        (hipStream_t)stream, pacc, pm, pd, (f16*)z, (const f16*)gate, n_q_heads,
@@ -742,6 +791,7 @@ int fl_attention_split_gqa(const void* q, const void* kcache, const void* vcache
     FL_REQUIRE(q && kcache && vcache && pacc && pm && pd, "null pointer");
     FL_REQUIRE(pos0 >= 0 && layer >= 0 && pos0 + T <= max_pos, "pos0 + T <= max_pos");
     FL_REQUIRE(cache_fits(max_pos, n_kv_heads, 2), "a layer cache of at most 2 GiB");
+    FL_REQUIRE(split_math_fits(max_pos, split), "(max_pos / 32 + 1) * (split + 1) < 2^32");
     FL_REQUIRE(aligned16(q) && aligned16(kcache) && aligned16(vcache) && aligned16(pacc),
                "16-byte aligned buffers");
     DecSeqs seqs = {};
@@ -764,6 +814,7 @@ int fl_attention_split_gqa_q8(const void* q, const void* kcache, const void* vca
     FL_REQUIRE(layer == 0, "an int8 cache is one buffer a layer: layer must be 0");
     FL_REQUIRE(pos0 >= 0 && pos0 + T <= max_pos, "pos0 + T <= max_pos");
     FL_REQUIRE(cache_fits(max_pos, n_kv_heads, 1), "a cache of at most 2 GiB");
+    FL_REQUIRE(split_math_fits(max_pos, split), "(max_pos / 32 + 1) * (split + 1) < 2^32");
     FL_REQUIRE(aligned16(q) && aligned16(kcache) && aligned16(vcache) && aligned16(pacc),
                "16-byte aligned buffers");
     DecSeqs seqs = {};
@@ -782,6 +833,7 @@ int fl_attention_dec_q8(const void* q, const void* kcache, const void* vcache, f
     FL_REQUIRE(tmin >= 1, "tmin >= 1");
     FL_REQUIRE(pos0 >= 0 && pos0 + T <= max_pos, "pos0 + T <= max_pos");
     FL_REQUIRE(cache_fits(max_pos, n_kv_heads, 1), "a cache of at most 2 GiB");
+    FL_REQUIRE(split_math_fits(max_pos, smax), "(max_pos / 32 + 1) * (smax + 1) < 2^32");
     FL_REQUIRE(aligned16(q) && aligned16(kcache) && aligned16(vcache) && aligned16(pacc),
                "16-byte aligned buffers");
     DecSeqs seqs = {};

@@ -26,13 +26,16 @@ L2_EPS = 1e-6           #                                 runtime.py:116
 GDN_NORM_EPS = 1e-6     # GDN output RMSNormGated          runtime.py:113
 
 # Decode / verify split policy on MI355X. A token's split count is
-# clamp(seqlen / SPLIT_ROWS, 1, SPLIT_MAX) (the reference's per-token rule,
-# kernels.cu:535-544, with its ATT_SPLIT = 32 / ATT_GQA_ROWS = 32 of
-# runtime.py:213-219 re-chosen): at 4 sequences x 4 kv heads, 64 splits a
-# long sequence give 1024 workgroups for 256 CUs, while a split keeps at least
-# 256 rows (8 tiles) so the partials stay a small fraction of the KV bytes
-# (measured on MI355X: 256 beats 512 and 1024 at 4k / 8k / 32k contexts and
-# ties at 100k).
+# clamp(max(seqlen / SPLIT_ROWS, min(seqlen / 64, 32)), 1, SPLIT_MAX): the
+# reference's per-token rule (kernels.cu:535-544, with its ATT_SPLIT = 32 /
+# ATT_GQA_ROWS = 32 of runtime.py:213-219 re-chosen) plus a floor of 32
+# splits of 64 rows and up for short contexts (the library's batched decode
+# applies it). At 4 sequences x 4 kv heads, 64 splits a long sequence give
+# 1024 workgroups for 256 CUs, while a split keeps at least 256 rows (8
+# tiles) so the partials stay a small fraction of the KV bytes (measured on
+# MI355X: 256 beats 512 and 1024 at 8k / 32k contexts and ties at 100k); a
+# 4k-row single sequence, 16 splits of 256 rows (64 workgroups), runs 1.3x
+# faster as 32 splits of 128.
 SPLIT_ROWS = 256
 SPLIT_MAX = 64
 # The largest T the decode attention takes (MTP verify rows; runtime.py:299).

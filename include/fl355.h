@@ -125,6 +125,9 @@ int fl_attn_gate(void* z, const void* g, int n_heads, int head_dim, int z_pitch,
  * [cap[b]][n_kv_heads][head_dim] f16; pos0[b], cap[b] host arrays.
  * z [B][T][n_q_heads][z_pitch] f16. work: caller scratch of at least
  * fl_attn_decode_work_bytes(B, T, n_q_heads, head_dim, split) bytes.
+ * A token of length len gets clamp(max(len / split_rows, min(len / 64, 32)),
+ * 1, split) splits: the reference's rule (kernels.cu:535-544) with a floor of
+ * 64-row splits for short contexts, up to 32 of them.
  * Each token's values equal a T = 1 call at its own position, bit for bit
  * (the split depends on the token's own length only; runtime.py:2062-2069).
  * Replaces the per-sequence loop of runtime.py:2865-2878 / 2828-2862. */

@@ -79,8 +79,11 @@ def test_config2_decode_verify_vs_oracle(fl, dev, orc, Lmax):
         assert ok, f"Lmax={Lmax} seq {b} (L={lens[b]}): max|err| {err}"
 
 
-def test_verify_rows_equal_t1_calls_bit_exact(fl, dev, rng):
-    L = 40000
+@pytest.mark.parametrize("L", [40000, 2050, 8450])
+def test_verify_rows_equal_t1_calls_bit_exact(fl, dev, rng, L):
+    """Each row of a T = 4 verify equals the T = 1 call at its position, bit for
+    bit -- also where the rows' split counts differ: lengths 2047..2050 cross
+    the 64-row floor's 31 -> 32 splits, 8447..8450 the 256-row rule's 32 -> 33."""
     kc, vc = rand_cache(rng, L)
     qg = rand_qg(rng, 4)
     kd, vd = to_dev(kc, dev), to_dev(vc, dev)
