@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the MI355X attention / Gated DeltaNet hot path.
 
-Primary line (BASELINE.json's metric on configs[1]): the fused GDN decode
+Primary line (the headline metric on the GDN decode config): the fused GDN decode
 step of 4 sequences (conv + L2 norm + gates + delta rule, one launch per
 step), states of 48 GDN layers rotated (604 MB, past the 256 MB Infinity
 Cache) as a decode through the model does. A step is one launch over one
@@ -96,7 +96,7 @@ def measure(torch, g, calls, samples, min_ms=2.0, warm_ms=200.0):
             "replays_per_region": reps, "calls_per_replay": calls}
 
 
-# BASELINE.md's measurement rule: the median of >= 50 timed iterations for
+# The measurement rule: the median of >= 50 timed iterations for
 # decode-shaped work and >= 10 for prefill-shaped work
 DECODE_SAMPLES = 50
 PREFILL_SAMPLES = 10

@@ -18,9 +18,11 @@
 // matrix cores.) The decay ratios are formed as e^{g_i - g_j} with j <= i
 // (never 1 / gamma_j, which overflows over a chunk of strong decay).
 //
-// Two launches. chunk_prep_kernel, every (chunk, v head) in parallel: K K^T
-// and Q K^T on MFMA, the prefix sums, A, T by forward substitution in fp32,
-// the gates, and T and M o QK^T written as fp16 MFMA operands.
+// Two launches. chunk_prep_kernel, every (chunk, k head) in parallel: K K^T
+// and Q K^T on MFMA once, then for each v head of the group the prefix sums,
+// A, T in fp32 by blocks of 16 (the diagonal blocks by forward substitution,
+// the others on fp32 MFMA), the gates, and T and M o QK^T written as fp16
+// MFMA operands.
 // chunk_state_kernel: a state wavefront per 16 state rows (v) of a v head,
 // all 128 k columns of them in fp32 registers, sequential over the chunks; a
 // paired output wavefront takes its Q S0^T and Delta through LDS a chunk later,
@@ -148,7 +150,7 @@ __device__ __forceinline__ void split8(f32x4 a, f32x4 b, float s, f16x8& hi, f16
 }
 
 // ---------------------------------------------------------------------------
-// chunk_prep_kernel: one workgroup of 4 waves a (chunk, v head)
+// chunk_prep_kernel: one workgroup of 4 waves a (chunk, k head)
 // ---------------------------------------------------------------------------
 constexpr int PK_P = CK_K + 8;   // f16 pitch of staged K / Q rows
 constexpr int PA_P = CK_C + 4;   // f32 pitch of the A / T and M o QK^T rows

@@ -14,7 +14,7 @@
  * Storage types: "f16" = IEEE binary16 (uint16_t bits), "f32" = float.
  * Each declaration names the reference launch it replaces: the kernel
  * (kernels.cu:line) and the runtime call site (runtime.py:line) that a
- * maintainer rebinds (INTEGRATION.md shows the ctypes stub).
+ * maintainer rebinds through a ctypes binding of this header.
  */
 #ifndef FL355_H
 #define FL355_H
@@ -93,7 +93,8 @@ int fl_attn_prep(void* qg, int q_pitch, void* k, const void* v, const float* wq,
  * (the reference's partial contract, kernels.cu:93-99).
  * Replaces kernels.cu:820-835 (+ 522-680), runtime.py:2830-2837.
  * Supported: head_dim == 256, T * n_q_heads / n_kv_heads <= 32,
- * split_rows >= 32. */
+ * split_rows >= 32, a layer cache under 2 GiB and (max_pos / 32 + 1) *
+ * (split + 1) < 2^32. */
 int fl_attention_split_gqa(const void* q, const void* kcache, const void* vcache,
                            float* pacc, float* pm, float* pd, int layer, int n_q_heads,
                            int n_kv_heads, int head_dim, int q_pitch, int pos0, int max_pos,

@@ -3,8 +3,8 @@ baseline only).
 
 The same ops as the reference kernels (model/footless/cuda_sm60/kernels.cu),
 vectorised over sequences and heads in fp32 with the reference's fp16
-rounding points, for running on the host's cores: BASELINE.md's CPU baseline
-is this module timed by bench.py. tests/test_oracle_torch.py checks it
+rounding points, for running on the host's cores: bench.py's CPU baseline
+is this module, timed. tests/test_oracle_torch.py checks it
 against the C oracle (fl_oracle.c). Never imported by the product.
 """
 from __future__ import annotations

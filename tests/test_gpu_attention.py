@@ -1,8 +1,8 @@
 """GPU parity of the full-attention path against the CPU oracle.
 
-Bar: attention outputs within max-abs 2e-3 / rel 1e-2 of the
-reference math in fp16; the KV store bit-exact. Size-independent properties
-at BASELINE's full sizes: a verify row equals the T = 1 call at its position
+Bar: attention outputs within max-abs 2e-3 / rel 1e-2 of the reference math
+in fp16; the KV store bit-exact. Size-independent properties at the
+benchmark's full sizes: a verify row equals the T = 1 call at its position
 bit for bit, a batched call equals per-sequence calls bit for bit, the split
 count does not change the result beyond rounding.
 """

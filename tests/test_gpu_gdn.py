@@ -1,6 +1,6 @@
 """GPU parity of the Gated DeltaNet path against the CPU oracle.
 
-Bar (BASELINE.json): GDN recurrent state within rel 1e-4 (fp32) after 1024
+Bar: GDN recurrent state within rel 1e-4 (fp32) after 1024
 decode steps (config 1); outputs y within max-abs 2e-3 / rel 1e-2 (fp16);
 conv states bit-exact (they are fp16 copies of inputs). The chunked WY scan
 (config 4) against the step-by-step recurrence.
