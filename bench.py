@@ -380,6 +380,53 @@ def bench_gdn_out_norm(torch, fl, T, iters=50):
             "hbm_frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 3)}
 
 
+def bench_gdn_prefill_front(torch, fl, T, which, iters=20):
+    """The GDN prefill's steps before the chunked scan, as the runtime launches
+    them (runtime.py:3035-3038, 3070-3076): the causal conv over T tokens x
+    10240 channels (which = "conv": x read, y written, the weights and the
+    ring), the L2 norm over the conv'd rows as 80 head-sized rows a token
+    ("l2norm": read + written), or the gates of 48 v heads ("scalars")."""
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(T + 2)
+    row = 10240
+    if which == "conv":
+        nbytes = 2 * T * row * 2 + row * 4 * 2 + 2 * row * 3 * 2
+    elif which == "l2norm":
+        nbytes = 2 * T * row * 2
+    else:
+        nbytes = 4 * T * 48 * 4 + 2 * 48 * 4
+    n_sets = min(64, max(1, -(-600_000_000 // nbytes)))
+    if which == "scalars":
+        sets = [(torch.randn((T, 48), generator=g, device=dev),
+                 torch.randn((T, 48), generator=g, device=dev)) for _ in range(n_sets)]
+        A_log = torch.zeros(48, device=dev)
+        dt_bias = torch.zeros(48, device=dev)
+        beta = torch.empty((T, 48), device=dev)
+        decay = torch.empty_like(beta)
+
+        def call(i):
+            a, b = sets[i % n_sets]
+            fl.ops.gdn_scalars(a, b, A_log, dt_bias, beta, decay, T=T)
+    else:
+        sets = [torch.randn((T, row), generator=g, device=dev).half() for _ in range(n_sets)]
+        out = torch.empty((T, row), dtype=torch.float16, device=dev)
+        w = (torch.randn((row, 4), generator=g, device=dev) * 0.5).half()
+        rings = torch.randn((2, row, 3), generator=g, device=dev).half()
+
+        def call(i):
+            x = sets[i % n_sets]
+            if which == "conv":
+                fl.ops.conv1d_causal(x, w, rings[0], out, rings[1], T=T, pos0=4096)
+            else:
+                fl.ops.l2norm_scaled(x, out, rows=row // 128, T=T)
+
+    gr = graph_of(torch, call, iters)
+    us = measure(torch, gr, iters, PREFILL_SAMPLES)["us"]
+    return {"config": f"gdn_prefill_{which}_T{T}", "us": round(us, 2),
+            "GBs": round(nbytes / (us * 1e-6) / 1e9, 1),
+            "hbm_frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 3)}
+
+
 def bench_gdn_verify(torch, fl, T=3, steps=96, warmup=16):
     """The GDN step of an MTP verify (runtime.py:3040-3053, gdn_scan_rows_f):
     B = 4 sequences, T = 3 conv'd rows each, the state updated over the three
@@ -666,6 +713,9 @@ EXTRA_CONFIGS = {
     "prefill8_L8192": (bench_prefill, {"L": 8192, "kv8": True}),
     "prefill8_L32768": (bench_prefill, {"L": 32768, "kv8": True}),
     "gdn_chunked_L8192": (bench_chunked, {}),
+    "gdn_prefill_conv_T8192": (bench_gdn_prefill_front, {"T": 8192, "which": "conv"}),
+    "gdn_prefill_l2norm_T8192": (bench_gdn_prefill_front, {"T": 8192, "which": "l2norm"}),
+    "gdn_prefill_scalars_T8192": (bench_gdn_prefill_front, {"T": 8192, "which": "scalars"}),
     "gdn_verify_B4_T3": (bench_gdn_verify, {}),
     "attn_prep_T1": (bench_attn_prep, {"T": 1}),
     "attn_prep_T8192": (bench_attn_prep, {"T": 8192, "iters": 20}),

@@ -818,6 +818,52 @@ rmsnorm_gated_rows_kernel(const f16* __restrict__ o, const f16* __restrict__ z,
     }
 }
 
+// l2norm_scaled on 128-element rows at 16-byte-aligned pitch: 16 lanes a row
+// (lane j of the row holds x[8 j .. 8 j + 7], one 16-byte load), 4 rows a
+// wave. The reference's block of 128 threads sums the squares by warp
+// (elements 32 w'.. 32 w' + 31, a __shfl_down tree over offsets 16, 8, 4, 2,
+// 1) and then (r0 + r2) + (r1 + r3) (kernels.cu:373-391): here warp w' is
+// lanes 4 w'.. 4 w' + 3, offsets 16 and 8 are the lane exchanges at distance
+// 2 and 1 (butterflies: every lane of the four holds the tree's sum, a + b ==
+// b + a), 4, 2, 1 the in-lane pairs, and the warp sums combine by exchanges
+// at distance 8 and 4 -- the same additions in the same order, so the same
+// bits as the one-row-a-workgroup kernel above.
+constexpr int L2_ROWS_PER_WG = (GR_THREADS / 64) * 4;
+__global__ void __launch_bounds__(GR_THREADS)
+l2norm_rows_kernel(const f16* __restrict__ x, f16* __restrict__ y, int rows, int pitch,
+                   int n_rows, float eps, float scale) {
+    typedef _Float16 f16x8v __attribute__((ext_vector_type(8)));
+    const int lane = threadIdx.x & 63, j = lane & 15;
+    const int rid = (blockIdx.x * (GR_THREADS / 64) + (threadIdx.x >> 6)) * 4 + (lane >> 4);
+    const bool ok = rid < n_rows;
+    const int rr = ok ? rid : n_rows - 1;   // rows past the end read the last, store nothing
+    const int t = rr / rows, r = rr - t * rows;
+    const size_t base = ((size_t)t * rows + r) * pitch + 8 * j;
+    const f16x8v xv = *(const f16x8v*)(x + base);
+    float xf[8], sq[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        xf[i] = (float)xv[i];
+        sq[i] = fmaf(xf[i], xf[i], 0.f);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) sq[i] += dpp_xor2(sq[i]);   // offset 16
+#pragma unroll
+    for (int i = 0; i < 8; ++i) sq[i] += dpp_xor1(sq[i]);   // offset 8
+    float t4[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) t4[i] = sq[i] + sq[i + 4];        // offset 4
+    const float t2a = t4[0] + t4[2], t2b = t4[1] + t4[3];         // offset 2
+    float ss = t2a + t2b;                                          // offset 1: warp sum
+    ss += lane_xor(ss, 8);                                         // r0 + r2, r1 + r3
+    ss += lane_xor(ss, 4);                                         // (r0 + r2) + (r1 + r3)
+    const float den = sqrtf(ss + eps);
+    f16x8v out;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) out[i] = f16_sat((xf[i] / den) * scale);
+    if (ok) *(f16x8v*)(y + base) = out;
+}
+
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 }  // namespace
@@ -881,8 +927,16 @@ int fl_l2norm_scaled(const void* x, void* y, int n, int rows, int pitch, float e
                      int T, fl_stream_t stream) {
     FL_REQUIRE(x && y, "null pointer");
     FL_REQUIRE(n >= 1 && n <= 1024 && pitch >= n && rows >= 1 && T >= 1, "n, rows, pitch, T");
-    hipLaunchKernelGGL(l2norm_kernel, dim3(rows, T), dim3(128), 0, (hipStream_t)stream,
-                       (const f16*)x, (f16*)y, n, rows, pitch, eps, scale);
+    const long long n_rows = (long long)rows * T;
+    if (n == GR_K && pitch % 8 == 0 && aligned16(x) && aligned16(y) && n_rows < (1ll << 31)) {
+        const long long wgs = (n_rows + L2_ROWS_PER_WG - 1) / L2_ROWS_PER_WG;
+        hipLaunchKernelGGL(l2norm_rows_kernel, dim3((unsigned)wgs), dim3(GR_THREADS), 0,
+                           (hipStream_t)stream, (const f16*)x, (f16*)y, rows, pitch,
+                           (int)n_rows, eps, scale);
+    } else {
+        hipLaunchKernelGGL(l2norm_kernel, dim3(rows, T), dim3(128), 0, (hipStream_t)stream,
+                           (const f16*)x, (f16*)y, n, rows, pitch, eps, scale);
+    }
     return fl::check_launch("l2norm_scaled");
 }
 

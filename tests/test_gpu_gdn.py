@@ -167,6 +167,35 @@ def test_l2norm_and_gates_vs_oracle(fl, dev, orc, rng):
     assert np.abs(decay.cpu().numpy() - d_r).max() / d_r.max() <= 2e-6
 
 
+@pytest.mark.parametrize("T,rows", [(7, 3), (5, 80), (1, 1)])
+def test_l2norm_row_layouts(fl, dev, orc, rng, T, rows):
+    """Rows at 16-byte-aligned pitch 136 (16 lanes a row, 4 rows a wave) and
+    at pitch 130 (a workgroup a row) give the same bits, the oracle's within
+    1 ulp, leave the padding after each row untouched, and run in place;
+    row counts that leave a wave's last rows empty."""
+    x = (rng.standard_normal((T, rows, 128)) * 3).astype(np.float16)
+    x[0, 0, :] = 0
+    want = orc.l2norm_scaled(x.reshape(T, rows * 128), n=128, rows=rows, pitch=128, eps=1e-6,
+                             scale=0.5, T=T).reshape(T, rows, 128)
+    outs = []
+    for pitch in (136, 130):
+        xp = np.zeros((T, rows, pitch), np.float16)
+        xp[..., :128] = x
+        y = torch.full((T, rows, pitch), 7.0, dtype=torch.float16, device=dev)
+        fl.ops.l2norm_scaled(torch.from_numpy(xp).to(dev), y, rows=rows, pitch=pitch,
+                             scale=0.5, T=T)
+        torch.cuda.synchronize()
+        yh = y.cpu().numpy()
+        assert (yh[..., 128:] == 7.0).all(), f"pitch {pitch}: wrote past the row"
+        outs.append(yh[..., :128])
+    assert np.array_equal(outs[0].view(np.int16), outs[1].view(np.int16))
+    assert ulp16_diff(outs[0], want) <= 1
+    xi = torch.from_numpy(np.ascontiguousarray(x)).to(dev)
+    fl.ops.l2norm_scaled(xi, xi, rows=rows, scale=0.5, T=T)
+    torch.cuda.synchronize()
+    assert np.array_equal(xi.cpu().numpy().view(np.int16), outs[0].view(np.int16))
+
+
 def _scan_inputs(rng, T):
     c = rng.standard_normal((T, ROW)).astype(np.float16)
     ln = np.zeros_like(c)
