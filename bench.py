@@ -380,6 +380,29 @@ def bench_gdn_out_norm(torch, fl, T, iters=50):
             "hbm_frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 3)}
 
 
+def bench_attn_gate(torch, fl, T, iters=20):
+    """The full-attention layer's output gate after a prefill (runtime.py:
+    2860-2862 applied to the prefill's z): z = f16_sat(z * sigmoid(g)) over T
+    tokens x 24 heads x 256, g the gate half of each head's q | gate row (HBM:
+    z read and written, g read)."""
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(T + 3)
+    nbytes = 3 * T * 24 * 256 * 2
+    n_sets = min(64, max(1, -(-600_000_000 // nbytes)))
+    sets = [(torch.randn((T, 24, 256), generator=g, device=dev).half(),
+             torch.randn((T, 24, 512), generator=g, device=dev).half()) for _ in range(n_sets)]
+
+    def call(i):
+        z, qg = sets[i % n_sets]
+        fl.ops.attn_gate(z, qg, T=T)
+
+    gr = graph_of(torch, call, iters)
+    us = measure(torch, gr, iters, PREFILL_SAMPLES)["us"]
+    return {"config": f"attn_gate_T{T}", "us": round(us, 2),
+            "GBs": round(nbytes / (us * 1e-6) / 1e9, 1),
+            "hbm_frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 3)}
+
+
 def bench_gdn_prefill_front(torch, fl, T, which, iters=20):
     """The GDN prefill's steps before the chunked scan, as the runtime launches
     them (runtime.py:3035-3038, 3070-3076): the causal conv over T tokens x
@@ -713,6 +736,7 @@ EXTRA_CONFIGS = {
     "prefill8_L8192": (bench_prefill, {"L": 8192, "kv8": True}),
     "prefill8_L32768": (bench_prefill, {"L": 32768, "kv8": True}),
     "gdn_chunked_L8192": (bench_chunked, {}),
+    "attn_gate_T8192": (bench_attn_gate, {"T": 8192}),
     "gdn_prefill_conv_T8192": (bench_gdn_prefill_front, {"T": 8192, "which": "conv"}),
     "gdn_prefill_l2norm_T8192": (bench_gdn_prefill_front, {"T": 8192, "which": "l2norm"}),
     "gdn_prefill_scalars_T8192": (bench_gdn_prefill_front, {"T": 8192, "which": "scalars"}),

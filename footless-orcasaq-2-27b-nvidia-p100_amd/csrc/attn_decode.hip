@@ -605,6 +605,26 @@ __global__ void attn_gate_kernel(f16* __restrict__ z, const f16* __restrict__ g,
     }
 }
 
+// The gate with 8 elements a lane (one 16-byte load of z and of g, one store
+// of z), for head_dim, the pitches and g_off multiples of 8 and 16-byte
+// aligned z / g: the same sigmoid_f and roundings as attn_gate_kernel, so the
+// same bits. chunks = T n_heads head_dim / 8 lanes in all.
+__global__ void __launch_bounds__(256)
+attn_gate_vec_kernel(f16* __restrict__ z, const f16* __restrict__ g, int n_heads, int head_dim,
+                     int z_pitch, int g_pitch, int g_off, long long chunks) {
+    const long long c = (long long)blockIdx.x * 256 + threadIdx.x;
+    if (c >= chunks) return;
+    const int per_row = head_dim >> 3;
+    const long long row = c / per_row;                  // (token, head)
+    const int d = (int)(c - row * per_row) * 8;
+    f16x8* zp = (f16x8*)(z + row * z_pitch + d);
+    const f16x8 gv = *(const f16x8*)(g + row * g_pitch + g_off + d);
+    f16x8 zv = *zp;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) zv[e] = f16_sat((float)zv[e] * sigmoid_f((float)gv[e]));
+    *zp = zv;
+}
+
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 // The batched decode's split floor (split_count): on MI355X a 4k-row B = 1
@@ -897,10 +917,18 @@ int fl_attn_gate(void* z, const void* g, int n_heads, int head_dim, int z_pitch,
     FL_REQUIRE(z && g, "null pointer");
     FL_REQUIRE(T >= 1 && n_heads >= 1 && head_dim >= 1, "T, n_heads, head_dim >= 1");
     FL_REQUIRE(z_pitch >= head_dim && g_off + head_dim <= g_pitch, "pitches");
-    const int n = n_heads * head_dim;
-    hipLaunchKernelGGL(attn_gate_kernel, dim3((n + 255) / 256, T), dim3(256), 0,
-                       (hipStream_t)stream, (f16*)z, (const f16*)g, n_heads, head_dim, z_pitch,
-                       g_pitch, g_off);
+    if (head_dim % 8 == 0 && z_pitch % 8 == 0 && g_pitch % 8 == 0 && g_off % 8 == 0 &&
+        aligned16(z) && aligned16(g)) {
+        const long long chunks = (long long)T * n_heads * (head_dim / 8);
+        hipLaunchKernelGGL(attn_gate_vec_kernel, dim3((unsigned)((chunks + 255) / 256)),
+                           dim3(256), 0, (hipStream_t)stream, (f16*)z, (const f16*)g, n_heads,
+                           head_dim, z_pitch, g_pitch, g_off, chunks);
+    } else {
+        const int n = n_heads * head_dim;
+        hipLaunchKernelGGL(attn_gate_kernel, dim3((n + 255) / 256, T), dim3(256), 0,
+                           (hipStream_t)stream, (f16*)z, (const f16*)g, n_heads, head_dim,
+                           z_pitch, g_pitch, g_off);
+    }
     return fl::check_launch("attn_gate");
 }
 

@@ -129,6 +129,35 @@ def test_gate_is_sigmoid(fl, dev, rng):
     assert torch.equal(zg, want)
 
 
+@pytest.mark.parametrize("T", [1, 37])
+def test_attn_gate_layouts(fl, dev, rng, T):
+    """fl_attn_gate over the runtime's layout (z pitch 256, the gate at 256 of
+    a 512-wide q | gate row: 8 elements a lane) and over pitches that take the
+    element-a-thread kernel (z pitch 260, gate pitch 516 at 258) gives the
+    same bits, within fp16 rounding of f16(z * sigmoid(g)) in fp32, and
+    leaves the rest of each row untouched."""
+    z = (rng.standard_normal((T, 24, 256)) * 2).astype(np.float16)
+    g = (rng.standard_normal((T, 24, 256)) * 4).astype(np.float16)
+    g[0, 0, :4] = [0.0, 30.0, -30.0, 88.0]
+    outs = []
+    for zp, gp, goff in ((256, 512, 256), (260, 516, 258)):
+        zb = np.full((T, 24, zp), 5.0, np.float16)
+        zb[..., :256] = z
+        gb = np.zeros((T, 24, gp), np.float16)
+        gb[..., goff:goff + 256] = g
+        zd = torch.from_numpy(zb).to(dev)
+        fl.ops.attn_gate(zd, torch.from_numpy(gb).to(dev), z_pitch=zp, g_pitch=gp, g_off=goff,
+                         T=T)
+        torch.cuda.synchronize()
+        zh = zd.cpu().numpy()
+        assert (zh[..., 256:] == 5.0).all()
+        outs.append(zh[..., :256])
+    assert np.array_equal(outs[0].view(np.int16), outs[1].view(np.int16))
+    want = (z.astype(np.float32) / (1 + np.exp(-g.astype(np.float32)))).astype(np.float16)
+    err, ok = close(outs[0], want.astype(np.float64), ATOL, RTOL)
+    assert ok, err
+
+
 def test_decode_rejects_bad_geometry(fl, dev, rng):
     kc, vc = rand_cache(rng, 64)
     kd, vd = to_dev(kc, dev), to_dev(vc, dev)
