@@ -19,13 +19,19 @@
 // One workgroup a (token, group of 4 RPW heads), a wavefront RPW rows (all
 // loaded before any is processed). The rotation's cos / sin depend only on
 // (position, pair), so the workgroup computes the rope_dim / 2 pairs once
-// (fp64 pow and sincos, as the reference does for every row) into LDS. A lane holds 4 consecutive
+// into LDS: the fp64 frequencies theta^(-2j / rope_dim), which do not depend
+// on the position, formed once on the host (std::pow) and passed in the
+// kernel arguments, the angle and its sincos in fp64, as the reference does
+// for every row. A lane holds 4 consecutive
 // elements of a row (one 8-byte load): the reference's warp w' (elements
 // 32 w'..32 w' + 31) is lanes 8 w'..8 w' + 7, and its __shfl_down tree over
 // offsets 16, 8, 4, 2, 1 becomes lane exchanges at distance 4, 2, 1 followed
 // by the in-lane pairs (c, c + 2) and (0, 1) -- the same additions in the same
 // order. The 8 warp sums are then combined as block_reduce_sum's second stage.
 #include "fl_common.hpp"
+
+#include <cmath>
+#include <mutex>
 
 // Products and sums round separately (no fma contraction), as the oracle's
 // restatement does, so the two agree bit for bit.
@@ -37,6 +43,13 @@ constexpr int PR_HD = 256;
 constexpr int PR_WAVES = 4;
 constexpr int PR_MAXPAIRS = PR_HD / 2;
 
+// The rotation's frequencies theta^(-2j / rope_dim), j < rope_dim / 2, in
+// fp64: they do not depend on the position, so the host forms them once per
+// (theta, rope_dim) and they ride in the kernel arguments.
+struct RopeFreqs {
+    double f[PR_MAXPAIRS];
+};
+
 // flags: bit 0 norm, bit 1 rope, bit 2 KV store (k rows and their v rows),
 // bit 3 the store in the int8 format (caches of capacity max_pos); RPW rows a
 // wavefront
@@ -45,8 +58,8 @@ __global__ void __launch_bounds__(64 * PR_WAVES)
 attn_prep_kernel(const f16* q, f16* qo, int q_pitch, f16* k, int k_pitch,
                  const f16* __restrict__ v, const float* __restrict__ wq,
                  const float* __restrict__ wk, void* __restrict__ kc, void* __restrict__ vc,
-                 int n_q_heads, int n_kv_heads, int pos0, int max_pos, int rope_dim, double theta,
-                 float eps) {
+                 int n_q_heads, int n_kv_heads, int pos0, int max_pos, int rope_dim,
+                 const RopeFreqs freqs, float eps) {
     __shared__ float scs[PR_MAXPAIRS], ssn[PR_MAXPAIRS];
     __shared__ __attribute__((aligned(16))) f16 srow[PR_WAVES][PR_HD];
     constexpr bool NORM = FLAGS & 1, ROPE = FLAGS & 2, STORE = FLAGS & 4, Q8 = FLAGS & 8;
@@ -56,8 +69,7 @@ attn_prep_kernel(const f16* q, f16* qo, int q_pitch, f16* k, int k_pitch,
     const int half_r = rope_dim >> 1;
     if (ROPE) {
         for (int j = threadIdx.x; j < half_r; j += 64 * PR_WAVES) {
-            const double invf = pow(theta, -2.0 * (double)j / (double)rope_dim);
-            const double ang = (double)pos * invf;
+            const double ang = (double)pos * freqs.f[j];
             double sn, cs;
             sincos(ang, &sn, &cs);
             scs[j] = (float)cs;
@@ -153,23 +165,42 @@ attn_prep_kernel(const f16* q, f16* qo, int q_pitch, f16* k, int k_pitch,
 // rows); large T: 7 rows a wavefront -- a token's 28 heads in one workgroup,
 // its cos / sin computed once (measured at T = 8192: 2 rows a wave 118 us,
 // 7 rows a wave 97 us, the fp64 sincos per workgroup being the difference).
+// theta^(-2j / rope_dim) for j < rope_dim / 2; the last (theta, rope_dim)'s
+// are kept (a mutex: callers may come from several threads).
+std::mutex g_freq_mu;
+float g_freq_theta = 0.f;
+int g_freq_dim = 0;
+RopeFreqs g_freqs;
+void rope_freqs(float theta, int rope_dim, RopeFreqs& out) {
+    std::lock_guard<std::mutex> lock(g_freq_mu);
+    if (theta != g_freq_theta || rope_dim != g_freq_dim) {
+        for (int j = 0; j < rope_dim / 2; ++j)
+            g_freqs.f[j] = std::pow((double)theta, -2.0 * (double)j / (double)rope_dim);
+        g_freq_theta = theta;
+        g_freq_dim = rope_dim;
+    }
+    out = g_freqs;
+}
+
 template <int FLAGS>
 int launch_prep(const f16* q, f16* qo, int q_pitch, f16* k, int k_pitch, const f16* v,
                 const float* wq, const float* wk, void* kc, void* vc, int n_q_heads, int n_kv_heads,
                 int pos0, int max_pos, int T, int rope_dim, float theta, float eps,
                 fl_stream_t stream) {
     const int heads = n_q_heads + n_kv_heads;
+    RopeFreqs freqs = {};
+    if (FLAGS & 2) rope_freqs(theta, rope_dim, freqs);
     if (T < 256) {
         hipLaunchKernelGGL((attn_prep_kernel<FLAGS, 1>),
                            dim3(T, (heads + PR_WAVES - 1) / PR_WAVES), dim3(64 * PR_WAVES), 0,
                            (hipStream_t)stream, q, qo, q_pitch, k, k_pitch, v, wq, wk, kc, vc,
-                           n_q_heads, n_kv_heads, pos0, max_pos, rope_dim, (double)theta, eps);
+                           n_q_heads, n_kv_heads, pos0, max_pos, rope_dim, freqs, eps);
     } else {
         hipLaunchKernelGGL((attn_prep_kernel<FLAGS, 7>),
                            dim3(T, (heads + 7 * PR_WAVES - 1) / (7 * PR_WAVES)),
                            dim3(64 * PR_WAVES), 0, (hipStream_t)stream, q, qo, q_pitch, k,
                            k_pitch, v, wq, wk, kc, vc, n_q_heads, n_kv_heads, pos0, max_pos,
-                           rope_dim, (double)theta, eps);
+                           rope_dim, freqs, eps);
     }
     return fl::check_launch("attn_prep");
 }
