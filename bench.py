@@ -728,6 +728,7 @@ EXTRA_CONFIGS = {
     "prefill_L32768": (bench_prefill, {"L": 32768}),
     "prefill_T1024_pos98k": (bench_prefill_chunk, {}),
     "prefill_T1024_pos98k_split1": (bench_prefill_chunk, {"split": 1}),
+    "decode8_verify_B1_T1_L4096": (bench_attn_decode, {"Lmax": 4096, "Bq": 1, "T": 1, "kv8": True}),
     "decode8_verify_B4_T3_L8192": (bench_attn_decode, {"Lmax": 8192, "kv8": True}),
     "decode8_verify_B4_T3_L32768": (bench_attn_decode, {"Lmax": 32768, "kv8": True}),
     "decode8_verify_B4_T3_L102400": (bench_attn_decode, {"Lmax": 102400, "kv8": True}),

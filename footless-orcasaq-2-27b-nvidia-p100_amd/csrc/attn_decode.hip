@@ -229,6 +229,82 @@ __device__ __forceinline__ DecTileRegs dec_dequant(const DecTileQ8& q, int lane)
     return r;
 }
 
+// int8 tiles are copied HBM -> LDS (global_load_lds) into stages of
+// Q8_STAGE_B bytes: K rows [32][256] at Q8_K_OFF, V rows at Q8_V_OFF, then
+// one 1 KiB block of scales a wave at Q8_S_OFF + 1024 w -- the tile's 32 rows
+// of K scales (16 bytes a row: the 8 blocks) and then its 32 rows of V scales
+// (every wave copies them all, for its own reads). A row's 16-byte chunk c is stored at c ^ q8_sw(row): a copy
+// instruction reads 4 whole rows (16 lanes a row, each 128-byte line from
+// one instruction), and the fragment reads below hit distinct banks -- the K
+// operand (one row a lane, 16 rows at one chunk) and the V slice (rows 4k + i,
+// k = 0..7, at chunks c and c ^ 1, 8 bytes a lane).
+constexpr int Q8_K_OFF = 0;
+constexpr int Q8_V_OFF = DEC_TILE * DEC_HD;
+constexpr int Q8_S_OFF = 2 * DEC_TILE * DEC_HD;
+constexpr int Q8_STAGE_B = Q8_S_OFF + DEC_WAVES * 1024;   // 20 KiB
+constexpr int Q8_COPIES = 5;   // copy instructions a wave a tile (2 K, 2 V, scales)
+
+__device__ __forceinline__ int q8_sw(int r) {
+    return (r & 1) | (((r >> 2) & 3) << 1) | ((((r >> 1) ^ (r >> 4)) & 1) << 3);
+}
+
+typedef __attribute__((address_space(3))) const char lds_cchar;
+
+// Copy tile jt (rows past uhi clamped to uhi - 1) into the stage at LDS
+// address sb: wave w copies rows 8w .. 8w + 7 of K and V and its own scales.
+// copy_off[c]: this lane's offset in row 8w + 4c + lane / 16 (its swizzled
+// chunk); sc: this lane's scale row 0 (K for lanes < 32, V above).
+__device__ __forceinline__ void q8_issue(uint32_t sb, const char* kb, const char* vb,
+                                         const char* sc, uint32_t rs, int jt, int uhi, int w,
+                                         int lane, const uint32_t (&copy_off)[2]) {
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+        const uint32_t row = (uint32_t)min(jt * DEC_TILE + 8 * w + 4 * c + (lane >> 4), uhi - 1);
+        const uint32_t lds = __builtin_amdgcn_readfirstlane(sb + (8 * w + 4 * c) * DEC_HD);
+        copy16(kb, row * rs + copy_off[c], lds + Q8_K_OFF);
+        copy16(vb, row * rs + copy_off[c], lds + Q8_V_OFF);
+    }
+    const uint32_t srow = (uint32_t)min(jt * DEC_TILE + (lane & 31), uhi - 1);
+    copy16_v(sc + (size_t)srow * (rs / 16), __builtin_amdgcn_readfirstlane(sb + Q8_S_OFF + 1024 * w));
+}
+
+// The staged int8 tile as the fp16 tile the MFMAs read (DecTileRegs):
+// fp16(byte * scale), each value once.
+__device__ __forceinline__ DecTileRegs q8_stage_tile(lds_cchar* S, int lane, int w) {
+    const int ql = lane & 31, hh = lane >> 5;
+    DecTileRegs r;
+    typedef __attribute__((address_space(3))) const u32x4 lds_u32x4;
+    typedef __attribute__((address_space(3))) const u32x2 lds_u32x2;
+    typedef __attribute__((address_space(3))) const f16 lds_f16;
+    lds_cchar* krow = S + Q8_K_OFF + ql * DEC_HD;
+    const u32x4 k0 = *(lds_u32x4*)(krow + 16 * ((4 * w + 2 * hh) ^ q8_sw(ql)));
+    const u32x4 k1 = *(lds_u32x4*)(krow + 16 * ((4 * w + 2 * hh + 1) ^ q8_sw(ql)));
+    lds_cchar* scl = S + Q8_S_OFF + 1024 * w + 2 * (2 * w + hh);   // block 2 w + hh of row 0
+    const f16 ksh = *(lds_f16*)(scl + 16 * ql);
+    const f16x2 ks2 = {ksh, ksh};
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+        const u32x4 b = ks < 2 ? k0 : k1;
+        const f16x4 lo = q8_deq4((ks & 1) ? b.z : b.x, ks2);
+        const f16x4 hi = q8_deq4((ks & 1) ? b.w : b.y, ks2);
+        r.k[ks] = (f16x8){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    }
+    // V rows 4 (l & 7) + i, dims 64 w + 8 (l >> 3) .. + 7: chunk 4 w + l / 16,
+    // its half (l >> 3) & 1; scale block 2 w + hh
+    const int vr = 4 * (lane & 7), vc = 4 * w + (lane >> 4), vhalf = 8 * ((lane >> 3) & 1);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const u32x2 bv =
+            *(lds_u32x2*)(S + Q8_V_OFF + (vr + i) * DEC_HD + 16 * (vc ^ q8_sw(vr + i)) + vhalf);
+        const f16 vsh = *(lds_f16*)(scl + 16 * (32 + vr + i));
+        const f16x2 vs2 = {vsh, vsh};
+        const f16x4 lo = q8_deq4(bv.x, vs2);
+        const f16x4 hi = q8_deq4(bv.y, vs2);
+        r.v[i] = (f16x8){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    }
+    return r;
+}
+
 template <bool NT_V>
 __device__ __forceinline__ void dec_load_tile(DecTileRegs& r, const f16* __restrict__ kbase,
                                               const f16* __restrict__ vbase, size_t row_stride,
@@ -259,7 +335,7 @@ __device__ __forceinline__ void lds_barrier() {
 // DEC: attention_dec_q8's split rule and partials -- (split, split_rows) are
 // (smax, tmin), pm in log2 units, no partial written for s >= St; otherwise
 // attention_split_gqa's -- pm in natural-log units, empty partials written.
-template <int NBUF, bool NT_V, bool Q8, bool DEC>
+template <int NBUF, bool NT_V, bool Q8, bool DEC, bool STAGE>
 __global__ void __launch_bounds__(DEC_THREADS)
 attn_decode_split_kernel(const f16* __restrict__ qg, DecSeqs seqs, float* __restrict__ pacc,
                          float* __restrict__ pm, float* __restrict__ pd, int n_q_heads,
@@ -267,6 +343,7 @@ attn_decode_split_kernel(const f16* __restrict__ qg, DecSeqs seqs, float* __rest
                          int split_floor, float sl2) {
     __shared__ __attribute__((aligned(16))) f32x4 s_part[2][DEC_WAVES][4][64];
     __shared__ __attribute__((aligned(16))) f16 s_vt[DEC_WAVES][64][VT_PITCH];
+    __shared__ __attribute__((aligned(16))) char s_stage[STAGE ? NBUF * Q8_STAGE_B : 16];
 
     const int s = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
@@ -306,16 +383,18 @@ attn_decode_split_kernel(const f16* __restrict__ qg, DecSeqs seqs, float* __rest
     if (qvalid) range(pos0 + tq + 1, qlo, qhi);
 
     f16x8 qreg[4];
-    {
+    auto load_q = [&] {
         const f16* qrow = qg + (((size_t)b * T + tq) * n_q_heads + h * G + gq) * q_pitch + 64 * w + 32 * hh;
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) qreg[ks] = qvalid ? *(const f16x8*)(qrow + 8 * ks) : (f16x8)(0);
-    }
+    };
+    if constexpr (!STAGE) load_q();
 
     f32x16 o0 = (f32x16)(0.f), o1 = (f32x16)(0.f);
     float m_run = -1e30f, l_run = 0.f;
 
-    auto body = [&](const DecTileRegs& r, int j) {
+    // at_barrier: run before the mid-tile barrier (pre) and after it (post)
+    auto body = [&](const DecTileRegs& r, int j, auto&& pre, auto&& post) {
         // partial scores of this wave's 64 dims
         f32x16 sacc = (f32x16)(0.f);
 #pragma unroll
@@ -332,7 +411,9 @@ attn_decode_split_kernel(const f16* __restrict__ qg, DecSeqs seqs, float* __rest
             const f16x4 col = {r.v[0][e], r.v[1][e], r.v[2][e], r.v[3][e]};
             *(f16x4*)&s_vt[w][8 * (lane >> 3) + e][4 * (lane & 7)] = col;
         }
+        pre();
         lds_barrier();
+        post();
         // full scores, summed in wave order
         float sc[16];
 #pragma unroll
@@ -403,20 +484,64 @@ attn_decode_split_kernel(const f16* __restrict__ qg, DecSeqs seqs, float* __rest
         }
     };
 
-    typedef typename std::conditional<Q8, DecTileQ8, DecTileRegs>::type Raw;
-    auto load = [&](Raw& r, int j) {
-        if constexpr (Q8)
-            dec_load_tile<NT_V>(r, kbase8, vbase8, ksb, vsb, row_stride, j, uhi, lane, w);
-        else
-            dec_load_tile<NT_V>(r, kbase, vbase, row_stride, j, uhi, lane, w);
-    };
-    if (uhi > ulo) {
+    auto none = [] {};
+    if constexpr (STAGE) {
+        static_assert(Q8, "the staged tiles are int8");
+        if (uhi > ulo) {
+            // NBUF stages, copied NBUF - 1 tiles ahead of the one computed.
+            // Tile j's copies are waited for (each wave its own, then the
+            // mid-tile barrier of tile j - 1) before tile j is read; stage j
+            // is refilled after tile j's barrier, when every wave is past
+            // reading it. Copies past the last tile re-copy it (clamped), so
+            // every wave issues Q8_COPIES a tile and the waits are constants.
+            const int j0 = ulo / DEC_TILE;
+            const int j1 = (uhi + DEC_TILE - 1) / DEC_TILE;
+            const uint32_t rs = (uint32_t)row_stride;   // bytes between rows; caches < 2 GiB
+            const char* kb = uniform_ptr(kbase8);
+            const char* vb = uniform_ptr(vbase8);
+            const char* sc = (const char*)(hh ? vsb : ksb);
+            uint32_t copy_off[2];
+#pragma unroll
+            for (int c = 0; c < 2; ++c)
+                copy_off[c] = 16 * ((lane & 15) ^ q8_sw(8 * w + 4 * c + (lane >> 4)));
+            const uint32_t stage0 = (uint32_t)(uintptr_t)((__attribute__((address_space(3))) char*)s_stage);
+#pragma unroll
+            for (int p = 0; p < NBUF; ++p)
+                q8_issue(stage0 + p * Q8_STAGE_B, kb, vb, sc, rs, j0 + p, uhi, w, lane, copy_off);
+            // q after the copies, then one wait for all of them: the compiler
+            // does not see the copies, so a wait it placed for q would land in
+            // the loop and drain every tile's copies
+            asm volatile("" ::: "memory");
+            load_q();
+            WAIT_VMCNT(0);
+            tile_ready();
+            int st = 0;
+            for (int j = j0; j < j1; ++j) {
+                const DecTileRegs r = q8_stage_tile((lds_cchar*)s_stage + st * Q8_STAGE_B, lane, w);
+                const int sn = st;
+                body(r, j, [] { WAIT_VMCNT((NBUF - 2) * Q8_COPIES); },
+                     [&] {
+                         q8_issue(stage0 + sn * Q8_STAGE_B, kb, vb, sc, rs, j + NBUF, uhi, w, lane,
+                                  copy_off);
+                     });
+                st = st == NBUF - 1 ? 0 : st + 1;
+            }
+            WAIT_VMCNT(0);   // no copy into LDS outlives the workgroup
+        }
+    } else if (uhi > ulo) {
         // NBUF register tile buffers: the loads of tile j + NBUF - 1 are issued
         // before the math of tile j. Every load is issued unconditionally (rows
         // and tiles clamped into the range: a row past uhi reads row uhi - 1,
         // masked to p = 0; a tile past the end re-reads the last one), so the
         // compiler's wait before tile j's math counts exactly the loads of the
         // tiles behind it instead of draining them all.
+        typedef typename std::conditional<Q8, DecTileQ8, DecTileRegs>::type Raw;
+        auto load = [&](Raw& r, int j) {
+            if constexpr (Q8)
+                dec_load_tile<NT_V>(r, kbase8, vbase8, ksb, vsb, row_stride, j, uhi, lane, w);
+            else
+                dec_load_tile<NT_V>(r, kbase, vbase, row_stride, j, uhi, lane, w);
+        };
         const int j0 = ulo / DEC_TILE;
         const int j1 = (uhi + DEC_TILE - 1) / DEC_TILE;
         Raw rbuf[NBUF];
@@ -429,9 +554,9 @@ attn_decode_split_kernel(const f16* __restrict__ qg, DecSeqs seqs, float* __rest
                 load(rbuf[(u + NBUF - 1) % NBUF], min(jj + NBUF - 1, j1 - 1));
                 if (jj < j1) {
                     if constexpr (Q8)
-                        body(dec_dequant(rbuf[u], lane), jj);
+                        body(dec_dequant(rbuf[u], lane), jj, none, none);
                     else
-                        body(rbuf[u], jj);
+                        body(rbuf[u], jj, none, none);
                 }
             }
         }
@@ -640,6 +765,16 @@ bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 #define DEC_NBUF_Q8 3
 #endif
 
+// int8 grids of at most one workgroup a CU take the LDS-staged tiles (2
+// stages of Q8_STAGE_B: 92 KiB of LDS, one workgroup a CU): whole-line
+// copies and no registers held by tiles in flight. Measured on MI355X, B = 1
+// at 4k (128 workgroups) 14.9 -> 12.6 us; larger grids keep the register
+// tiles, whose two workgroups a CU overlap each other's barriers (B = 4, T =
+// 3 at ~8k / ~100k: 33.3 / 223 us against 34.4 / 235 staged). Both give the
+// same bits.
+constexpr int DEC_STAGE_MAX_WGS = 256;
+constexpr int DEC_NBUF_STAGE = 2;
+
 // grid_split blocks a (sequence, kv head); `split` the partials' stride;
 // split_floor the floor of split_count (0: the reference's rule).
 template <bool Q8, bool DEC>
@@ -647,10 +782,15 @@ int launch_split(const f16* qg, const DecSeqs& seqs, float* pacc, float* pm, flo
                  int T, int n_q_heads, int n_kv, int q_pitch, int grid_split, int split,
                  int split_rows, float sl2, hipStream_t stream, int split_floor = 0) {
     dim3 grid(grid_split, n_kv, B);
-    constexpr int NBUF = Q8 ? DEC_NBUF_Q8 : DEC_NBUF;
-    hipLaunchKernelGGL((attn_decode_split_kernel<NBUF, DEC_NT_V, Q8, DEC>), grid, dim3(DEC_THREADS),
-                       0, stream, qg, seqs, pacc, pm, pd, n_q_heads, n_kv, q_pitch, T, split,
-                       split_rows, split_floor, sl2);
+    if (Q8 && (long long)grid_split * n_kv * B <= DEC_STAGE_MAX_WGS)
+        hipLaunchKernelGGL((attn_decode_split_kernel<DEC_NBUF_STAGE, false, true, DEC, true>),
+                           grid, dim3(DEC_THREADS), 0, stream, qg, seqs, pacc, pm, pd, n_q_heads,
+                           n_kv, q_pitch, T, split, split_rows, split_floor, sl2);
+    else
+        hipLaunchKernelGGL((attn_decode_split_kernel<Q8 ? DEC_NBUF_Q8 : DEC_NBUF, DEC_NT_V, Q8, DEC,
+                                                     false>),
+                           grid, dim3(DEC_THREADS), 0, stream, qg, seqs, pacc, pm, pd, n_q_heads,
+                           n_kv, q_pitch, T, split, split_rows, split_floor, sl2);
     return fl::check_launch("attn_decode_split");
 }
 

@@ -122,7 +122,6 @@ __device__ __forceinline__ void copy16(const char* sbase, uint32_t voff, uint32_
 __device__ __forceinline__ void copy16_v(const char* vptr, uint32_t lds) {
     asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(vptr), "{m0}"(lds));
 }
-
 // p as a wave-uniform (scalar) value: the copies take their row base in SGPRs
 __device__ __forceinline__ const char* uniform_ptr(const char* p) {
     const uint64_t v = (uint64_t)(uintptr_t)p;

@@ -140,6 +140,10 @@ def test_dec_q8_verify_rows_equal_t1_calls_bit_exact(fl, dev, orc, rng):
 
 
 def test_decode_q8_batched_vs_single_and_oracle(fl, dev, orc, rng):
+    """The batched launch (35 splits x 4 kv heads x 4 sequences = 560
+    workgroups) runs the register tiles, each single call (at most 140
+    workgroups) the LDS-staged ones: equal bits pin the two tile paths to each
+    other as well as batched == single."""
     lens = [3000, 17, 9000, 1]
     caps = [L + 64 for L in lens]
     caches = [oracle_cache(orc, rng, L, c) for L, c in zip(lens, caps)]
