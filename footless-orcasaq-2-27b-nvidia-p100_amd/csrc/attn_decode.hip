@@ -38,7 +38,12 @@
 //     and each value becomes fp16(byte * scale) in registers -- the
 //     reference's prefill dequantizes V the same way (kernels.cu:2500-2509);
 //     its decode keeps byte * scale in fp32, so scores and outputs differ
-//     from it by fp16 rounding, far below the int8 format's own error.
+//     from it by fp16 rounding, far below the int8 format's own error. An
+//     int8 row of a kv head is two 128-byte lines, so the int8 tiles split
+//     the work otherwise: wave w takes 16 rows and 128 dims (S^T on 16x16x32
+//     MFMAs, two partials a score summed through LDS) and reads whole lines;
+//     its V^T lands in the owning waves' LDS slices (double-buffered). Grids
+//     of at most one workgroup a CU copy the int8 tiles HBM -> LDS instead.
 //   * Tiles are 32-row aligned in absolute position and every tile a token's
 //     range does not cover is an exact no-op for that token (masked scores,
 //     p = 0, corr = 1), so a token's partial is the same bits whichever other
@@ -58,6 +63,9 @@ constexpr int DEC_HD = 256;
 constexpr int DEC_WAVES = 4;
 constexpr int DEC_THREADS = 64 * DEC_WAVES;
 constexpr int VT_PITCH = 40;   // halves per d row of the transposed V slice (32 + 8 pad)
+// the int8 layout's pitch: its V^T writes (8 d rows 8 apart x 4 kv groups a
+// store) spread over 32 banks at 18 dwords a row, 8 at 20
+constexpr int VT_PITCH_Q8 = 36;
 constexpr float RESCALE_LOG2 = 8.f;
 #ifndef DEC_NBUF
 #define DEC_NBUF 2                // register tile buffers (prefetch depth + 1)
@@ -171,9 +179,16 @@ struct DecTileRegs {
     f16x8 v[4];   // V[row 4(l&7) + i][64w + 8(l>>3) + 0..7], i = 0..3
 };
 
+// int8 tiles use their own split of the work (the int8 layout): wave w
+// takes kv rows 16 (w & 1) .. + 15 and dims 128 (w >> 1) .. + 127, so each
+// wave reads whole 128-byte lines of its K and V rows (4 lanes a K row, 16
+// lanes a V row), where the fp16 layout reads each line in two halves from
+// two waves. In DecTileRegs, lane l = 16 g + i:
+//   k[ks] = K[row 16 (w & 1) + i][128 (w >> 1) + 32 g + 8 ks + 0..7]
+//   v[i'] = V[row 16 (w & 1) + 4 (l & 3) + i'][128 (w >> 1) + 8 (l >> 2) + 0..7]
 // One int8 tile in flight: the same elements as bytes, plus one dword of
-// scales a lane -- lane l < 32: row l's K scales of blocks 2w, 2w + 1 (this
-// wave's dims); lane l >= 32: row l - 32's V scales.
+// scales a lane -- rows 16 (w & 1) + (l & 15), blocks 4 (w >> 1) + 2 ((l >>
+// 4) & 1) + 0, 1; K for l < 32, V above.
 struct DecTileQ8 {
     u32x4 k[2];
     u32x2 v[4];
@@ -186,28 +201,31 @@ __device__ __forceinline__ void dec_load_tile(DecTileQ8& r, const char* __restri
                                               const f16* __restrict__ ksb,
                                               const f16* __restrict__ vsb, size_t row_stride,
                                               int j, int uhi, int lane, int w) {
-    const int ql = lane & 31, hh = lane >> 5;
+    const int hh = lane >> 5;
     const uint32_t rs = (uint32_t)row_stride;   // bytes between rows; caches < 2 GiB
-    const uint32_t krow = (uint32_t)min(j * DEC_TILE + ql, uhi - 1);
-    const u32x4* src = (const u32x4*)(kbase + (krow * rs + 64 * w + 32 * hh));
+    const int r0 = j * DEC_TILE + 16 * (w & 1), cb = 128 * (w >> 1);
+    const uint32_t krow = (uint32_t)min(r0 + (lane & 15), uhi - 1);
+    const u32x4* src = (const u32x4*)(kbase + (krow * rs + cb + 32 * ((lane >> 4) & 3)));
     r.k[0] = src[0];
     r.k[1] = src[1];
     const char* sb = (const char*)(hh ? vsb : ksb);
-    r.sc = *(const uint32_t*)(sb + (krow * (rs / 16) + 4 * w));
+    r.sc = *(const uint32_t*)(sb + (krow * (rs / 16) + 2 * (4 * (w >> 1) + 2 * ((lane >> 4) & 1))));
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const uint32_t vrow = (uint32_t)min(j * DEC_TILE + 4 * (lane & 7) + i, uhi - 1);
-        const u32x2* vsrc = (const u32x2*)(vbase + (vrow * rs + 64 * w + 8 * (lane >> 3)));
+        const uint32_t vrow = (uint32_t)min(r0 + 4 * (lane & 3) + i, uhi - 1);
+        const u32x2* vsrc = (const u32x2*)(vbase + (vrow * rs + cb + 8 * (lane >> 2)));
         r.v[i] = NT_V ? __builtin_nontemporal_load(vsrc) : *vsrc;
     }
 }
 
 // The int8 tile as the fp16 tile the MFMAs read: fp16(byte * scale).
 __device__ __forceinline__ DecTileRegs dec_dequant(const DecTileQ8& q, int lane) {
-    const int ql = lane & 31, hh = lane >> 5;
     DecTileRegs r;
-    const uint32_t kp = (uint32_t)__builtin_amdgcn_ds_bpermute(ql << 2, (int)q.sc);
-    const f16 ksh = __builtin_bit_cast(f16x2, kp)[hh];
+    // K: row (l & 15), block 4 (w >> 1) + l / 16 -- lane (l & 15) + 16 (l / 32)'s
+    // dword, half (l / 16) & 1; V row 4 (l & 3) + i, the same block -- lane 32 + that
+    const int bh = (lane >> 4) & 1, bl = 16 * (lane >> 5);
+    const uint32_t kp = (uint32_t)__builtin_amdgcn_ds_bpermute(((lane & 15) + bl) << 2, (int)q.sc);
+    const f16 ksh = __builtin_bit_cast(f16x2, kp)[bh];
     const f16x2 ks2 = {ksh, ksh};
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
@@ -218,9 +236,9 @@ __device__ __forceinline__ DecTileRegs dec_dequant(const DecTileQ8& q, int lane)
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const uint32_t vp =
-            (uint32_t)__builtin_amdgcn_ds_bpermute((32 + 4 * (lane & 7) + i) << 2, (int)q.sc);
-        const f16 vsh = __builtin_bit_cast(f16x2, vp)[hh];
+        const uint32_t vp = (uint32_t)__builtin_amdgcn_ds_bpermute(
+            (32 + bl + 4 * (lane & 3) + i) << 2, (int)q.sc);
+        const f16 vsh = __builtin_bit_cast(f16x2, vp)[bh];
         const f16x2 vs2 = {vsh, vsh};
         const f16x4 lo = q8_deq4(q.v[i].x, vs2);
         const f16x4 hi = q8_deq4(q.v[i].y, vs2);
@@ -271,16 +289,19 @@ __device__ __forceinline__ void q8_issue(uint32_t sb, const char* kb, const char
 // The staged int8 tile as the fp16 tile the MFMAs read (DecTileRegs):
 // fp16(byte * scale), each value once.
 __device__ __forceinline__ DecTileRegs q8_stage_tile(lds_cchar* S, int lane, int w) {
-    const int ql = lane & 31, hh = lane >> 5;
     DecTileRegs r;
     typedef __attribute__((address_space(3))) const u32x4 lds_u32x4;
     typedef __attribute__((address_space(3))) const u32x2 lds_u32x2;
     typedef __attribute__((address_space(3))) const f16 lds_f16;
-    lds_cchar* krow = S + Q8_K_OFF + ql * DEC_HD;
-    const u32x4 k0 = *(lds_u32x4*)(krow + 16 * ((4 * w + 2 * hh) ^ q8_sw(ql)));
-    const u32x4 k1 = *(lds_u32x4*)(krow + 16 * ((4 * w + 2 * hh + 1) ^ q8_sw(ql)));
-    lds_cchar* scl = S + Q8_S_OFF + 1024 * w + 2 * (2 * w + hh);   // block 2 w + hh of row 0
-    const f16 ksh = *(lds_f16*)(scl + 16 * ql);
+    // the int8 layout: K row 16 (w & 1) + (l & 15), chunks 8 (w >> 1) + 2 (l /
+    // 16) + 0, 1; V rows 16 (w & 1) + 4 (l & 3) + i, chunk 8 (w >> 1) + l / 8,
+    // half (l / 4) & 1; scales of block 4 (w >> 1) + l / 16
+    const int kr = 16 * (w & 1) + (lane & 15), kc = 8 * (w >> 1) + 2 * (lane >> 4);
+    lds_cchar* krow = S + Q8_K_OFF + kr * DEC_HD;
+    const u32x4 k0 = *(lds_u32x4*)(krow + 16 * (kc ^ q8_sw(kr)));
+    const u32x4 k1 = *(lds_u32x4*)(krow + 16 * ((kc + 1) ^ q8_sw(kr)));
+    lds_cchar* scl = S + Q8_S_OFF + 1024 * w + 2 * (4 * (w >> 1) + (lane >> 4));
+    const f16 ksh = *(lds_f16*)(scl + 16 * kr);
     const f16x2 ks2 = {ksh, ksh};
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
@@ -289,9 +310,8 @@ __device__ __forceinline__ DecTileRegs q8_stage_tile(lds_cchar* S, int lane, int
         const f16x4 hi = q8_deq4((ks & 1) ? b.w : b.y, ks2);
         r.k[ks] = (f16x8){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
     }
-    // V rows 4 (l & 7) + i, dims 64 w + 8 (l >> 3) .. + 7: chunk 4 w + l / 16,
-    // its half (l >> 3) & 1; scale block 2 w + hh
-    const int vr = 4 * (lane & 7), vc = 4 * w + (lane >> 4), vhalf = 8 * ((lane >> 3) & 1);
+    const int vr = 16 * (w & 1) + 4 * (lane & 3), vc = 8 * (w >> 1) + (lane >> 3),
+              vhalf = 8 * ((lane >> 2) & 1);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const u32x2 bv =
@@ -341,8 +361,13 @@ attn_decode_split_kernel(const f16* __restrict__ qg, DecSeqs seqs, float* __rest
                          float* __restrict__ pm, float* __restrict__ pd, int n_q_heads,
                          int n_kv, int q_pitch, int T, int split, int split_rows,
                          int split_floor, float sl2) {
-    __shared__ __attribute__((aligned(16))) f32x4 s_part[2][DEC_WAVES][4][64];
-    __shared__ __attribute__((aligned(16))) f16 s_vt[DEC_WAVES][64][VT_PITCH];
+    // partial scores: 4 writers a row (fp16 layout: a wave's 64 dims) or 2
+    // (int8 layout: a wave's 128 dims of 16 rows); V^T in the owner wave's
+    // region, double-buffered in the int8 layout (written across waves)
+    constexpr int SP_W = Q8 ? 2 : DEC_WAVES;
+    constexpr int VTP = Q8 ? VT_PITCH_Q8 : VT_PITCH;
+    __shared__ __attribute__((aligned(16))) f32x4 s_part[2][SP_W][4][64];
+    __shared__ __attribute__((aligned(16))) f16 s_vt[Q8 ? 2 : 1][DEC_WAVES][64][VTP];
     __shared__ __attribute__((aligned(16))) char s_stage[STAGE ? NBUF * Q8_STAGE_B : 16];
 
     const int s = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
@@ -382,11 +407,28 @@ attn_decode_split_kernel(const f16* __restrict__ qg, DecSeqs seqs, float* __rest
     int qlo = 0, qhi = 0;
     if (qvalid) range(pos0 + tq + 1, qlo, qhi);
 
-    f16x8 qreg[4];
+    // fp16 layout: qreg[ks] = Q[column ql][64 w + 32 hh + 8 ks + 0..7]; int8
+    // layout: qreg[4 nb + ks] = Q[column 16 nb + (l & 15)][128 (w >> 1) + 32 (l
+    // / 16) + 8 ks + 0..7], the B operand of the 16x16x32 products
+    f16x8 qreg[Q8 ? 8 : 4];
     auto load_q = [&] {
-        const f16* qrow = qg + (((size_t)b * T + tq) * n_q_heads + h * G + gq) * q_pitch + 64 * w + 32 * hh;
+        if constexpr (Q8) {
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) qreg[ks] = qvalid ? *(const f16x8*)(qrow + 8 * ks) : (f16x8)(0);
+            for (int nb = 0; nb < 2; ++nb) {
+                const int c = 16 * nb + (lane & 15);
+                const bool ok = c < R;
+                const int t = ok ? c / G : 0, g = ok ? c - t * G : 0;
+                const f16* qrow = qg + (((size_t)b * T + t) * n_q_heads + h * G + g) * q_pitch +
+                                  128 * (w >> 1) + 32 * (lane >> 4);
+#pragma unroll
+                for (int ks = 0; ks < 4; ++ks)
+                    qreg[4 * nb + ks] = ok ? *(const f16x8*)(qrow + 8 * ks) : (f16x8)(0);
+            }
+        } else {
+            const f16* qrow = qg + (((size_t)b * T + tq) * n_q_heads + h * G + gq) * q_pitch + 64 * w + 32 * hh;
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) qreg[ks] = qvalid ? *(const f16x8*)(qrow + 8 * ks) : (f16x8)(0);
+        }
     };
     if constexpr (!STAGE) load_q();
 
@@ -395,21 +437,47 @@ attn_decode_split_kernel(const f16* __restrict__ qg, DecSeqs seqs, float* __rest
 
     // at_barrier: run before the mid-tile barrier (pre) and after it (post)
     auto body = [&](const DecTileRegs& r, int j, auto&& pre, auto&& post) {
-        // partial scores of this wave's 64 dims
-        f32x16 sacc = (f32x16)(0.f);
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks)
-            sacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(r.k[ks], qreg[ks], sacc, 0, 0, 0);
         const int buf = j & 1;
+        const int vb = Q8 ? buf : 0;
+        if constexpr (Q8) {
+            // partial scores of 16 rows x 32 columns over this wave's 128 dims
+            // (16x16x32: lane 16 g + i holds rows 4 g .. + 3 of column i), stored
+            // where the 32x32 layout below reads rows 8 r4 + 4 hh .. + 3 of
+            // column ql: r4 = 2 (w & 1) + g / 2, hh = g & 1
+            f32x4 c0 = (f32x4)(0.f), c1 = (f32x4)(0.f);
 #pragma unroll
-        for (int r4 = 0; r4 < 4; ++r4)
-            s_part[buf][w][r4][lane] =
-                (f32x4){sacc[4 * r4], sacc[4 * r4 + 1], sacc[4 * r4 + 2], sacc[4 * r4 + 3]};
-        // V slice, transposed to [d][kv] in this wave's LDS region
+            for (int ks = 0; ks < 4; ++ks) {
+                c0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(r.k[ks], qreg[ks], c0, 0, 0, 0);
+                c1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(r.k[ks], qreg[4 + ks], c1, 0, 0, 0);
+            }
+            const int g = lane >> 4, lp = (lane & 15) + 32 * (g & 1);
+            s_part[buf][w >> 1][2 * (w & 1) + (g >> 1)][lp] = c0;
+            s_part[buf][w >> 1][2 * (w & 1) + (g >> 1)][lp + 16] = c1;
+            // V slice, transposed to [d][kv] in the region of the wave that
+            // owns dims 64 w' .. (w' = 2 (w >> 1) + l / 32)
+            const int own = 2 * (w >> 1) + (lane >> 5), d0 = 8 * ((lane >> 2) & 7);
+            const int kv0 = 16 * (w & 1) + 4 * (lane & 3);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const f16x4 col = {r.v[0][e], r.v[1][e], r.v[2][e], r.v[3][e]};
-            *(f16x4*)&s_vt[w][8 * (lane >> 3) + e][4 * (lane & 7)] = col;
+            for (int e = 0; e < 8; ++e) {
+                const f16x4 col = {r.v[0][e], r.v[1][e], r.v[2][e], r.v[3][e]};
+                *(f16x4*)&s_vt[vb][own][d0 + e][kv0] = col;
+            }
+        } else {
+            // partial scores of this wave's 64 dims
+            f32x16 sacc = (f32x16)(0.f);
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks)
+                sacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(r.k[ks], qreg[ks], sacc, 0, 0, 0);
+#pragma unroll
+            for (int r4 = 0; r4 < 4; ++r4)
+                s_part[buf][w][r4][lane] =
+                    (f32x4){sacc[4 * r4], sacc[4 * r4 + 1], sacc[4 * r4 + 2], sacc[4 * r4 + 3]};
+            // V slice, transposed to [d][kv] in this wave's LDS region
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const f16x4 col = {r.v[0][e], r.v[1][e], r.v[2][e], r.v[3][e]};
+                *(f16x4*)&s_vt[0][w][8 * (lane >> 3) + e][4 * (lane & 7)] = col;
+            }
         }
         pre();
         lds_barrier();
@@ -418,9 +486,14 @@ attn_decode_split_kernel(const f16* __restrict__ qg, DecSeqs seqs, float* __rest
         float sc[16];
 #pragma unroll
         for (int r4 = 0; r4 < 4; ++r4) {
-            const f32x4 a0 = s_part[buf][0][r4][lane], a1 = s_part[buf][1][r4][lane];
-            const f32x4 a2 = s_part[buf][2][r4][lane], a3 = s_part[buf][3][r4][lane];
-            const f32x4 t4 = ((a0 + a1) + a2) + a3;
+            f32x4 t4;
+            if constexpr (Q8) {
+                t4 = s_part[buf][0][r4][lane] + s_part[buf][1][r4][lane];
+            } else {
+                const f32x4 a0 = s_part[buf][0][r4][lane], a1 = s_part[buf][1][r4][lane];
+                const f32x4 a2 = s_part[buf][2][r4][lane], a3 = s_part[buf][3][r4][lane];
+                t4 = ((a0 + a1) + a2) + a3;
+            }
             sc[4 * r4] = t4[0];
             sc[4 * r4 + 1] = t4[1];
             sc[4 * r4 + 2] = t4[2];
@@ -470,14 +543,14 @@ attn_decode_split_kernel(const f16* __restrict__ qg, DecSeqs seqs, float* __rest
         for (int ks = 0; ks < 2; ++ks) {
             const f16x8 pb = ks ? pk1 : pk0;
             {
-                const f16x4 lo4 = *(const f16x4*)&s_vt[w][ql][16 * ks + 4 * hh];
-                const f16x4 hi4 = *(const f16x4*)&s_vt[w][ql][16 * ks + 8 + 4 * hh];
+                const f16x4 lo4 = *(const f16x4*)&s_vt[vb][w][ql][16 * ks + 4 * hh];
+                const f16x4 hi4 = *(const f16x4*)&s_vt[vb][w][ql][16 * ks + 8 + 4 * hh];
                 const f16x8 a = {lo4[0], lo4[1], lo4[2], lo4[3], hi4[0], hi4[1], hi4[2], hi4[3]};
                 o0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pb, o0, 0, 0, 0);
             }
             {
-                const f16x4 lo4 = *(const f16x4*)&s_vt[w][32 + ql][16 * ks + 4 * hh];
-                const f16x4 hi4 = *(const f16x4*)&s_vt[w][32 + ql][16 * ks + 8 + 4 * hh];
+                const f16x4 lo4 = *(const f16x4*)&s_vt[vb][w][32 + ql][16 * ks + 4 * hh];
+                const f16x4 hi4 = *(const f16x4*)&s_vt[vb][w][32 + ql][16 * ks + 8 + 4 * hh];
                 const f16x8 a = {lo4[0], lo4[1], lo4[2], lo4[3], hi4[0], hi4[1], hi4[2], hi4[3]};
                 o1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pb, o1, 0, 0, 0);
             }
