@@ -639,11 +639,15 @@ __device__ __forceinline__ void r64_vfrags(s16x4 (&vb)[8], const char* vt,
         vb[i] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vt + b[i] + imm));
 }
 
+// SPLIT: blockIdx.z is the KV split (tile grid only, bins == 0): the
+// workgroup walks tiles [n s / S, n (s + 1) / S) of its causal range (n
+// tiles) and leaves the partials in `sp`, as attn_prefill_kernel<Q8, true>.
+template <bool SPLIT>
 __global__ void __launch_bounds__(PF_THREADS)
 attn_prefill_r64_kernel(const f16* __restrict__ q, int q_pitch, const f16* __restrict__ kc,
                         const f16* __restrict__ vc, f16* __restrict__ z, int z_pitch,
                         int n_q_heads, int n_kv, int pos0, int T, float sl2, int n_row_tiles,
-                        int bins, const R64Plan plan) {
+                        int bins, const R64Plan plan, PfSplit sp) {
     extern __shared__ __attribute__((aligned(16))) char smem[];
 
     // This workgroup's row tiles: one, of a grid of row tiles x kv heads
@@ -706,12 +710,36 @@ attn_prefill_r64_kernel(const f16* __restrict__ q, int q_pitch, const f16* __res
         const int wqmin = __builtin_amdgcn_readfirstlane(pos0 + wfirst / G);
         const int blast = min(R0 + R64_BQ - 1, RT - 1);
         const int kv_end = __builtin_amdgcn_readfirstlane(pos0 + blast / G + 1);
-        const int n_tiles = (kv_end + R64_BK - 1) / R64_BK;
+        // this item's tiles [j_lo, j_lo + n_tiles): all, or split s's share
+        const int n_all = (kv_end + R64_BK - 1) / R64_BK;
+        const int s_idx = SPLIT ? (int)blockIdx.z : 0;
+        const int j_lo = SPLIT ? __builtin_amdgcn_readfirstlane(n_all * s_idx / sp.n) : 0;
+        const int n_tiles =
+            SPLIT ? __builtin_amdgcn_readfirstlane(n_all * (s_idx + 1) / sp.n) - j_lo : n_all;
+        if constexpr (SPLIT) {
+            if (n_tiles == 0) {   // an empty split: the empty partial (uniform exit)
+#pragma unroll
+                for (int nb = 0; nb < 2; ++nb) {
+                    if (!rvalid[nb]) continue;
+                    const size_t part = ((size_t)t[nb] * n_q_heads + h * G + g[nb]) * sp.n + s_idx;
+                    float* acc = sp.pacc + part * PF_HD + 4 * hh;
+#pragma unroll
+                    for (int i = 0; i < 32; ++i) *(f32x4*)(acc + 8 * i) = (f32x4)(0.f);
+                    if (hh == 0) {
+                        sp.pm[part] = -1e30f;
+                        sp.pd[part] = 0.f;
+                    }
+                }
+                continue;
+            }
+        }
 
 
 #pragma unroll
         for (int d = 0; d < R64_DIST; ++d)
-            if (d < n_tiles) r64_issue(lds_base + d * R64_STAGE, kb, vb, rsb, d * R64_BK, kv_end, w, lane, loff);
+            if (d < n_tiles)
+                r64_issue(lds_base + d * R64_STAGE, kb, vb, rsb, (j_lo + d) * R64_BK, kv_end, w,
+                          lane, loff);
 
         f16x8 qreg[2][16];   // Q[row nb][128 hh + 8 ks + 0..7]
 #pragma unroll
@@ -744,10 +772,10 @@ attn_prefill_r64_kernel(const f16* __restrict__ q, int q_pitch, const f16* __res
             tile_done();   // every wave is past tile j - 1: its stage can be refilled
             if (j + R64_DIST < n_tiles) {
                 const int sn = st == 0 ? R64_NST - 1 : st - 1;   // (j + DIST) % NST == (j - 1) % NST
-                r64_issue(lds_base + sn * R64_STAGE, kb, vb, rsb, (j + R64_DIST) * R64_BK, kv_end, w,
-                          lane, loff);
+                r64_issue(lds_base + sn * R64_STAGE, kb, vb, rsb, (j_lo + j + R64_DIST) * R64_BK,
+                          kv_end, w, lane, loff);
             }
-            const int kv0 = j * R64_BK;
+            const int kv0 = (j_lo + j) * R64_BK;
             if (kv0 <= wqmax) {
                 const uint32_t kst = koff + st * R64_STAGE;
                 f32x16 s[2] = {(f32x16)(0.f), (f32x16)(0.f)};
@@ -792,6 +820,27 @@ attn_prefill_r64_kernel(const f16* __restrict__ q, int q_pitch, const f16* __res
 
         acc_settle(o[0]);
         acc_settle(o[1]);
+        if constexpr (SPLIT) {
+            // dims 32 mb + 8 r4 + 4 hh + 0..3 of O, unnormalised; m in natural-log units
+#pragma unroll
+            for (int nb = 0; nb < 2; ++nb) {
+                if (!rvalid[nb]) continue;
+                const size_t part = ((size_t)t[nb] * n_q_heads + h * G + g[nb]) * sp.n + s_idx;
+                float* acc = sp.pacc + part * PF_HD + 4 * hh;
+#pragma unroll
+                for (int mb = 0; mb < 8; ++mb)
+#pragma unroll
+                    for (int r4 = 0; r4 < 4; ++r4)
+                        *(f32x4*)(acc + 32 * mb + 8 * r4) =
+                            (f32x4){o[nb][mb][4 * r4], o[nb][mb][4 * r4 + 1], o[nb][mb][4 * r4 + 2],
+                                    o[nb][mb][4 * r4 + 3]};
+                if (hh == 0) {
+                    sp.pm[part] = l_run[nb] > 0.f ? m_run[nb] * FL_LN2 : -1e30f;
+                    sp.pd[part] = l_run[nb];
+                }
+            }
+            continue;
+        }
 #pragma unroll
         for (int nb = 0; nb < 2; ++nb) {
             if (!rvalid[nb]) continue;
@@ -839,11 +888,14 @@ int prefill_device_setup(int& n_cu) {
             fl::set_error("attn_prefill: cannot raise the dynamic LDS limit to %d bytes", LDS_B);
             return FL_ELAUNCH;
         }
-    if (hipFuncSetAttribute((const void*)attn_prefill_r64_kernel,
-                            hipFuncAttributeMaxDynamicSharedMemorySize, R64_LDS) != hipSuccess) {
-        fl::set_error("attn_prefill: cannot raise the dynamic LDS limit to %d bytes", R64_LDS);
-        return FL_ELAUNCH;
-    }
+    const void* fns64[] = {(const void*)attn_prefill_r64_kernel<false>,
+                           (const void*)attn_prefill_r64_kernel<true>};
+    for (const void* f : fns64)
+        if (hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, R64_LDS) !=
+            hipSuccess) {
+            fl::set_error("attn_prefill: cannot raise the dynamic LDS limit to %d bytes", R64_LDS);
+            return FL_ELAUNCH;
+        }
     if (hipDeviceGetAttribute(&g_cus[dev], hipDeviceAttributeMultiprocessorCount, dev) !=
         hipSuccess) {
         fl::set_error("attn_prefill: cannot read the CU count of device %d", dev);
@@ -1006,29 +1058,50 @@ bool use_r64(int T, int n_q_heads, int n_kv_heads) {
 constexpr int PF_SPLIT_MAX = 16;
 constexpr int PF_CUS = 256;         // MI355X: 256 CUs, one 128 KiB-LDS workgroup each
 constexpr int PF_SPLIT_OVH = 2;     // a split's fixed cost in tile units: prologue, partials, merge
+// The 64-rows-a-wave kernel takes a KV split (fp16 caches) from this many
+// 256-row workgroups a split; a split's fixed cost there, in its 32-row tiles.
+constexpr int R64_SPLIT_MIN_WGS = 64;
+constexpr int R64_SPLIT_OVH = 4;
 
-// The KV split of a prefill call whose 128-row workgroups are too few to fill
-// the CUs (a short chunk deep into a long prompt, runtime.py:196 / 2932-2941):
-// the count that minimises (rounds of one workgroup a CU) x (tiles the
-// heaviest workgroup walks + a split's fixed cost). 1 where the 64-rows-a-wave
-// kernel runs or the grid already fills the chip.
-int split_policy(int T, int pos0, int n_q_heads, int n_kv_heads) {
-    if (T < 1 || pos0 < 0 || n_kv_heads < 1 || n_q_heads % n_kv_heads != 0) return 1;
-    if (use_r64(T, n_q_heads, n_kv_heads)) return 1;
-    const int wgs = n_kv_heads * ((T * (n_q_heads / n_kv_heads) + PF_BQ - 1) / PF_BQ);
-    if (wgs >= PF_CUS) return 1;
-    const int nkt = (pos0 + T + PF_BK - 1) / PF_BK;
+bool use_r64_split(int T, int n_q_heads, int n_kv_heads) {
+    const int rows = T * (n_q_heads / n_kv_heads);
+    return (rows + R64_BQ - 1) / R64_BQ * n_kv_heads >= R64_SPLIT_MIN_WGS;
+}
+
+// The count S minimising (rounds of one workgroup a CU) x (tiles a split
+// walks + a split's fixed cost), S <= PF_SPLIT_MAX.
+int best_split(int wgs, int nkt, int ovh) {
     int best = 1;
     long long best_cost = -1;
     for (int S = 1; S <= PF_SPLIT_MAX && S <= nkt; ++S) {
         const long long rounds = ((long long)wgs * S + PF_CUS - 1) / PF_CUS;
-        const long long cost = rounds * ((nkt + S - 1) / S + PF_SPLIT_OVH);
+        const long long cost = rounds * ((nkt + S - 1) / S + ovh);
         if (best_cost < 0 || cost < best_cost) {
             best_cost = cost;
             best = S;
         }
     }
     return best;
+}
+
+// The KV split of a prefill call whose workgroups are too few to fill the
+// CUs (a short chunk deep into a long prompt, runtime.py:196 / 2932-2941),
+// by best_split over the kernel that runs: fp16 caches with at least
+// R64_SPLIT_MIN_WGS 256-row workgroups take the 64-rows-a-wave kernel's split
+// (a 1024-token chunk at 24 / 4 heads: 96 workgroups a split), the rest the
+// 128-row kernel's. 1 where the unsplit 64-rows-a-wave kernel runs or the
+// 128-row grid already fills the chip.
+int split_policy(int T, int pos0, int n_q_heads, int n_kv_heads, bool q8 = false) {
+    if (T < 1 || pos0 < 0 || n_kv_heads < 1 || n_q_heads % n_kv_heads != 0) return 1;
+    if (use_r64(T, n_q_heads, n_kv_heads)) return 1;
+    const int G = n_q_heads / n_kv_heads;
+    if (!q8 && use_r64_split(T, n_q_heads, n_kv_heads)) {
+        const int wgs64 = n_kv_heads * ((T * G + R64_BQ - 1) / R64_BQ);
+        return best_split(wgs64, (pos0 + T + R64_BK - 1) / R64_BK, R64_SPLIT_OVH);
+    }
+    const int wgs = n_kv_heads * ((T * G + PF_BQ - 1) / PF_BQ);
+    if (wgs >= PF_CUS) return 1;
+    return best_split(wgs, (pos0 + T + PF_BK - 1) / PF_BK, PF_SPLIT_OVH);
 }
 
 // The int8 cache's rows [0, rows) as fp16(byte * scale), the values the int8
@@ -1141,11 +1214,28 @@ int prefill(const void* q, int q_pitch, const void* k_new, const void* v_new, vo
         const int G = n_q_heads / n_kv_heads;
         const int bins = r64_plan(T, pos0, G, n_kv_heads, n_cu, plan) > 0 ? n_cu / n_kv_heads : 0;
         const dim3 grid = bins > 0 ? dim3(n_cu) : dim3(r64_tiles, n_kv_heads);
-        hipLaunchKernelGGL(attn_prefill_r64_kernel, grid, dim3(PF_THREADS), R64_LDS,
+        hipLaunchKernelGGL(attn_prefill_r64_kernel<false>, grid, dim3(PF_THREADS), R64_LDS,
                            (hipStream_t)stream, (const f16*)q, q_pitch, (const f16*)kc,
                            (const f16*)vc, (f16*)z, z_pitch, n_q_heads, n_kv_heads, pos0, T,
-                           scale * FL_LOG2E, r64_tiles, bins, plan);
+                           scale * FL_LOG2E, r64_tiles, bins, plan,
+                           PfSplit{nullptr, nullptr, nullptr, 1});
         return fl::check_launch("attn_prefill_r64");
+    }
+    if (!Q8 && split > 1 && use_r64_split(T, n_q_heads, n_kv_heads)) {
+        const size_t parts = (size_t)T * n_q_heads * split;
+        PfSplit sp = {(float*)work, nullptr, nullptr, split};
+        sp.pm = sp.pacc + parts * PF_HD;
+        sp.pd = sp.pm + parts;
+        R64Plan plan;
+        plan.v[0] = 0;
+        hipLaunchKernelGGL(attn_prefill_r64_kernel<true>, dim3(r64_tiles, n_kv_heads, split),
+                           dim3(PF_THREADS), R64_LDS, (hipStream_t)stream, (const f16*)q, q_pitch,
+                           (const f16*)kc, (const f16*)vc, (f16*)z, z_pitch, n_q_heads,
+                           n_kv_heads, pos0, T, scale * FL_LOG2E, r64_tiles, 0, plan, sp);
+        rc = fl::check_launch("attn_prefill_r64 (kv split)");
+        if (rc) return rc;
+        return fl_attention_merge(sp.pacc, sp.pm, sp.pd, z, n_q_heads, head_dim, z_pitch, T,
+                                  split, nullptr, 0, 0, stream);
     }
     const int n_row_tiles = (rows + PF_BQ - 1) / PF_BQ;
     if (split == 1) {
@@ -1234,7 +1324,7 @@ extern "C" int fl_attention_prefill_kv_q8(const void* q, int q_pitch, const void
                                           int pos0, int max_pos, float scale, int T, int split,
                                           void* z, int z_pitch, void* work, size_t work_bytes,
                                           fl_stream_t stream) {
-    if (split == 0) split = split_policy(T, pos0, n_q_heads, n_kv_heads);
+    if (split == 0) split = split_policy(T, pos0, n_q_heads, n_kv_heads, true);
     return prefill<true>(q, q_pitch, k_new, v_new, kcache, vcache, layer, n_q_heads, n_kv_heads,
                          head_dim, pos0, max_pos, scale, T, z, z_pitch, split, work, work_bytes,
                          stream);

@@ -253,10 +253,12 @@ size_t fl_attn_decode_noalloc_max_bytes(void);
  * _fh_split, runtime.py:2932-2959): split s of every workgroup walks a share
  * of its causal KV tiles and leaves partials in `work` (the reference's `pt`
  * arena: pacc [T][n_q_heads][S][head_dim], pm (natural log) and pd
- * [T][n_q_heads][S], f32); one merge writes z. For calls whose 128-row
- * workgroups are too few to fill the CUs -- a 1024-token chunk deep into a
- * long prompt (runtime.py:196). split 0: fl_attention_prefill_split_count's
- * choice; split 1: fl_attention_prefill (no work needed). */
+ * [T][n_q_heads][S], f32); one merge writes z. For calls whose workgroups
+ * are too few to fill the CUs -- a 1024-token chunk deep into a long prompt
+ * (runtime.py:196): the 64-rows-a-wave kernel splits from 64 workgroups of
+ * 256 rows (fp16 caches), the 128-row kernel below that and over int8 caches.
+ * split 0: fl_attention_prefill_split_count's choice; split 1:
+ * fl_attention_prefill (no work needed). */
 int fl_attention_prefill_split_count(int T, int pos0, int n_q_heads, int n_kv_heads);
 size_t fl_attention_prefill_work_bytes(int T, int n_q_heads, int head_dim, int split);
 int fl_attention_prefill_kv(const void* q, int q_pitch, const void* k_new, const void* v_new,

@@ -347,12 +347,15 @@ def test_prefill_long_sampled_rows(fl, dev, orc, T, pos0, ramp):
 # --------------------------------------------------------------------------
 
 @pytest.mark.parametrize("T,pos0,split", [(300, 500, 2), (300, 500, 3), (129, 1000, 7),
-                                          (40, 3, 4), (1, 70, 5), (700, 0, 16)])
+                                          (40, 3, 4), (1, 70, 5), (700, 0, 16), (683, 300, 3)])
 def test_prefill_kv_split_vs_oracle(fl, dev, orc, rng, T, pos0, split):
     """Forced KV splits against the C oracle, every row: splits that leave some
     workgroups' shares empty (40 tokens from pos0 3 are one or two 64-row
     tiles for 4 splits; 16 splits of a fresh 700-token prompt), one query
-    token, and the fused kv_store in front."""
+    token, and the fused kv_store in front. From 64 workgroups of 256 rows
+    (T >= 683 at 24 / 4 heads: 700 and 683 here, 683 leaving 2 rows in its
+    last row tile) the 64-rows-a-wave kernel takes the split, below it the
+    128-row kernel."""
     L = pos0 + T
     kc, vc = rand_cache(rng, L)
     qg = rand_qg(rng, T)
@@ -371,14 +374,15 @@ def test_prefill_kv_split_vs_oracle(fl, dev, orc, rng, T, pos0, split):
 
 def test_prefill_kv_split_chunk_deep_in_prompt(fl, dev):
     """The reference's own prefill shape: a 1024-token chunk (MAX_CHUNK,
-    runtime.py:196) at pos0 = 98000, where the 128-row workgroups (192) are
-    fewer than the CUs and the policy splits the KV range 4 ways. Every row
-    against oracle/torch_ref.attention_prefill (fp32 on the GPU), and the
-    unsplit call within the same bar."""
+    runtime.py:196) at pos0 = 98000, where the 256-row workgroups (96) are
+    fewer than the CUs and the policy splits the KV range 8 ways (768
+    workgroups of the 64-rows-a-wave kernel). Every row against
+    oracle/torch_ref.attention_prefill (fp32 on the GPU), and the unsplit call
+    (the 128-row kernel) within the same bar."""
     from oracle import torch_ref as tr
 
     T, pos0 = 1024, 98000
-    assert fl.ops.prefill_split_count(T, pos0) == 4
+    assert fl.ops.prefill_split_count(T, pos0) == 8
     L = pos0 + T
     g = torch.Generator(device=dev).manual_seed(98)
     q = (torch.randn((T, 24, 256), generator=g, device=dev) / 16).half()
@@ -389,7 +393,7 @@ def test_prefill_kv_split_chunk_deep_in_prompt(fl, dev):
     want = tr.attention_prefill(q, kd, vd, pos0, 1.0, block=256)
     torch.cuda.synchronize()
     scale_out = float(want.float().abs().max())
-    for name, got in (("split 4", z), ("split 1", z1)):
+    for name, got in (("split 8", z), ("split 1", z1)):
         err = (got.float() - want.float()).abs()
         bad = int((err > ATOL + RTOL * want.float().abs()).sum())
         print(f"T={T} pos0={pos0} {name}: max|err| {float(err.max()):.2e} "
