@@ -1084,9 +1084,9 @@ int best_split(int wgs, int nkt, int ovh) {
     return best;
 }
 
-// The KV split of a prefill call whose workgroups are too few to fill the
-// CUs (a short chunk deep into a long prompt, runtime.py:196 / 2932-2941),
-// by best_split over the kernel that runs: fp16 caches with at least
+// The KV split of a prefill call whose 128-row workgroups are too few to
+// fill the CUs (a short chunk deep into a long prompt, runtime.py:196 /
+// 2932-2941), by best_split over the kernel that runs: fp16 caches with at least
 // R64_SPLIT_MIN_WGS 256-row workgroups take the 64-rows-a-wave kernel's split
 // (a 1024-token chunk at 24 / 4 heads: 96 workgroups a split), the rest the
 // 128-row kernel's. 1 where the unsplit 64-rows-a-wave kernel runs or the
@@ -1095,12 +1095,12 @@ int split_policy(int T, int pos0, int n_q_heads, int n_kv_heads, bool q8 = false
     if (T < 1 || pos0 < 0 || n_kv_heads < 1 || n_q_heads % n_kv_heads != 0) return 1;
     if (use_r64(T, n_q_heads, n_kv_heads)) return 1;
     const int G = n_q_heads / n_kv_heads;
+    const int wgs = n_kv_heads * ((T * G + PF_BQ - 1) / PF_BQ);
+    if (wgs >= PF_CUS) return 1;   // e.g. a fresh 2k prompt: 384 workgroups, unsplit
     if (!q8 && use_r64_split(T, n_q_heads, n_kv_heads)) {
         const int wgs64 = n_kv_heads * ((T * G + R64_BQ - 1) / R64_BQ);
         return best_split(wgs64, (pos0 + T + R64_BK - 1) / R64_BK, R64_SPLIT_OVH);
     }
-    const int wgs = n_kv_heads * ((T * G + PF_BQ - 1) / PF_BQ);
-    if (wgs >= PF_CUS) return 1;
     return best_split(wgs, (pos0 + T + PF_BK - 1) / PF_BK, PF_SPLIT_OVH);
 }
 

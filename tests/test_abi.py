@@ -116,13 +116,15 @@ def test_noalloc_decode_refuses_beyond_its_static_scratch(fl):
 def test_prefill_split_policy(fl):
     """The KV split the prefill takes: none where the grid fills the CUs (an 8k
     or 2k fresh prompt, a 4k chunk deep in a prompt: the 64-rows-a-wave kernel
-    or 384+ workgroups), 4 for the reference's 1024-token chunk at pos0 98k
-    (192 workgroups on 256 CUs), more for shorter chunks; the work it needs."""
+    or 384+ workgroups of 128 rows), 8 for the reference's 1024-token chunk at
+    pos0 98k (192 workgroups of 128 rows on 256 CUs; the 64-rows-a-wave
+    kernel's 96 a split x 8 = 3 rounds), 8 for a 512-token chunk (the 128-row
+    kernel's split); the work it needs."""
     lib = fl._lib.lib()
     assert lib.fl_attention_prefill_split_count(8192, 0, 24, 4) == 1
     assert lib.fl_attention_prefill_split_count(2048, 0, 24, 4) == 1
     assert lib.fl_attention_prefill_split_count(4096, 98000, 24, 4) == 1
-    assert lib.fl_attention_prefill_split_count(1024, 98000, 24, 4) == 4
+    assert lib.fl_attention_prefill_split_count(1024, 98000, 24, 4) == 8
     assert lib.fl_attention_prefill_split_count(512, 98000, 24, 4) == 8
     assert lib.fl_attention_prefill_work_bytes(1024, 24, 256, 4) == 1024 * 24 * 4 * (256 * 4 + 8)
     assert lib.fl_attention_prefill_work_bytes(1024, 24, 256, 1) == 0
