@@ -1059,13 +1059,19 @@ constexpr int PF_SPLIT_MAX = 16;
 constexpr int PF_CUS = 256;         // MI355X: 256 CUs, one 128 KiB-LDS workgroup each
 constexpr int PF_SPLIT_OVH = 2;     // a split's fixed cost in tile units: prologue, partials, merge
 // The 64-rows-a-wave kernel takes a KV split (fp16 caches) from this many
-// 256-row workgroups a split; a split's fixed cost there, in its 32-row tiles.
+// 256-row workgroups a split and a causal range of this many rows (a chunk
+// deep in a prompt); a split's fixed cost there, in its 32-row tiles.
+// Same-box A/B at T = 1024, the 128-row kernel's split against it: pos0 0
+// 49 against 82 us, 1024 116 / 121, 3072 and 8000 equal, 30000 836 / 776,
+// 98000 2716 / 2264.
 constexpr int R64_SPLIT_MIN_WGS = 64;
+constexpr int R64_SPLIT_MIN_ROWS = 16384;
 constexpr int R64_SPLIT_OVH = 4;
 
-bool use_r64_split(int T, int n_q_heads, int n_kv_heads) {
+bool use_r64_split(int T, int pos0, int n_q_heads, int n_kv_heads) {
     const int rows = T * (n_q_heads / n_kv_heads);
-    return (rows + R64_BQ - 1) / R64_BQ * n_kv_heads >= R64_SPLIT_MIN_WGS;
+    return (rows + R64_BQ - 1) / R64_BQ * n_kv_heads >= R64_SPLIT_MIN_WGS &&
+           (long long)pos0 + T >= R64_SPLIT_MIN_ROWS;
 }
 
 // The count S minimising (rounds of one workgroup a CU) x (tiles a split
@@ -1087,9 +1093,9 @@ int best_split(int wgs, int nkt, int ovh) {
 // The KV split of a prefill call whose 128-row workgroups are too few to
 // fill the CUs (a short chunk deep into a long prompt, runtime.py:196 /
 // 2932-2941), by best_split over the kernel that runs: fp16 caches with at least
-// R64_SPLIT_MIN_WGS 256-row workgroups take the 64-rows-a-wave kernel's split
-// (a 1024-token chunk at 24 / 4 heads: 96 workgroups a split), the rest the
-// 128-row kernel's. 1 where the unsplit 64-rows-a-wave kernel runs or the
+// R64_SPLIT_MIN_WGS 256-row workgroups and R64_SPLIT_MIN_ROWS rows take the
+// 64-rows-a-wave kernel's split (a 1024-token chunk at 24 / 4 heads from
+// pos0 15360: 96 workgroups a split), the rest the 128-row kernel's. 1 where the unsplit 64-rows-a-wave kernel runs or the
 // 128-row grid already fills the chip.
 int split_policy(int T, int pos0, int n_q_heads, int n_kv_heads, bool q8 = false) {
     if (T < 1 || pos0 < 0 || n_kv_heads < 1 || n_q_heads % n_kv_heads != 0) return 1;
@@ -1097,7 +1103,7 @@ int split_policy(int T, int pos0, int n_q_heads, int n_kv_heads, bool q8 = false
     const int G = n_q_heads / n_kv_heads;
     const int wgs = n_kv_heads * ((T * G + PF_BQ - 1) / PF_BQ);
     if (wgs >= PF_CUS) return 1;   // e.g. a fresh 2k prompt: 384 workgroups, unsplit
-    if (!q8 && use_r64_split(T, n_q_heads, n_kv_heads)) {
+    if (!q8 && use_r64_split(T, pos0, n_q_heads, n_kv_heads)) {
         const int wgs64 = n_kv_heads * ((T * G + R64_BQ - 1) / R64_BQ);
         return best_split(wgs64, (pos0 + T + R64_BK - 1) / R64_BK, R64_SPLIT_OVH);
     }
@@ -1221,7 +1227,7 @@ int prefill(const void* q, int q_pitch, const void* k_new, const void* v_new, vo
                            PfSplit{nullptr, nullptr, nullptr, 1});
         return fl::check_launch("attn_prefill_r64");
     }
-    if (!Q8 && split > 1 && use_r64_split(T, n_q_heads, n_kv_heads)) {
+    if (!Q8 && split > 1 && use_r64_split(T, pos0, n_q_heads, n_kv_heads)) {
         const size_t parts = (size_t)T * n_q_heads * split;
         PfSplit sp = {(float*)work, nullptr, nullptr, split};
         sp.pm = sp.pacc + parts * PF_HD;

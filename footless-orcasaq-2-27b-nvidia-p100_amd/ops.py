@@ -262,9 +262,10 @@ def attention_prefill(q, kcache, vcache, *, pos0: int, T: int | None = None, z=N
 def prefill_split_count(T: int, pos0: int, n_q_heads: int = N_HEADS,
                         n_kv_heads: int = N_KV) -> int:
     """The KV split the prefill takes for T queries at pos0 (runtime.py:
-    2932-2941's role): 1 unless the workgroups are too few for the CUs (the
-    64-rows-a-wave kernel's split from 64 workgroups of 256 rows, the 128-row
-    kernel's below). The int8 prefill takes the same count."""
+    2932-2941's role): 1 unless the 128-row workgroups are too few for the
+    CUs (the 64-rows-a-wave kernel's split from 64 workgroups of 256 rows
+    and 16384 cache rows, the 128-row kernel's otherwise). The int8 prefill
+    takes the same count."""
     return int(_lib.lib().fl_attention_prefill_split_count(T, pos0, n_q_heads, n_kv_heads))
 
 

@@ -256,7 +256,8 @@ size_t fl_attn_decode_noalloc_max_bytes(void);
  * [T][n_q_heads][S], f32); one merge writes z. For calls whose workgroups
  * are too few to fill the CUs -- a 1024-token chunk deep into a long prompt
  * (runtime.py:196): the 64-rows-a-wave kernel splits from 64 workgroups of
- * 256 rows (fp16 caches), the 128-row kernel below that and over int8 caches.
+ * 256 rows and 16384 cache rows (fp16 caches), the 128-row kernel otherwise
+ * and over int8 caches.
  * split 0: fl_attention_prefill_split_count's choice; split 1:
  * fl_attention_prefill (no work needed). */
 int fl_attention_prefill_split_count(int T, int pos0, int n_q_heads, int n_kv_heads);

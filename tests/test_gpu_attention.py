@@ -347,15 +347,12 @@ def test_prefill_long_sampled_rows(fl, dev, orc, T, pos0, ramp):
 # --------------------------------------------------------------------------
 
 @pytest.mark.parametrize("T,pos0,split", [(300, 500, 2), (300, 500, 3), (129, 1000, 7),
-                                          (40, 3, 4), (1, 70, 5), (700, 0, 16), (683, 300, 3)])
+                                          (40, 3, 4), (1, 70, 5), (700, 0, 16)])
 def test_prefill_kv_split_vs_oracle(fl, dev, orc, rng, T, pos0, split):
-    """Forced KV splits against the C oracle, every row: splits that leave some
-    workgroups' shares empty (40 tokens from pos0 3 are one or two 64-row
-    tiles for 4 splits; 16 splits of a fresh 700-token prompt), one query
-    token, and the fused kv_store in front. From 64 workgroups of 256 rows
-    (T >= 683 at 24 / 4 heads: 700 and 683 here, 683 leaving 2 rows in its
-    last row tile) the 64-rows-a-wave kernel takes the split, below it the
-    128-row kernel."""
+    """Forced KV splits (the 128-row kernel's) against the C oracle, every
+    row: splits that leave some workgroups' shares empty (40 tokens from pos0
+    3 are one or two 64-row tiles for 4 splits; 16 splits of a fresh
+    700-token prompt), one query token, and the fused kv_store in front."""
     L = pos0 + T
     kc, vc = rand_cache(rng, L)
     qg = rand_qg(rng, T)
@@ -370,6 +367,31 @@ def test_prefill_kv_split_vs_oracle(fl, dev, orc, rng, T, pos0, split):
     want = orc.attention_prefill(qg, kc, vc, q_pitch=512, pos0=pos0, max_pos=L, scale=SCALE, T=T)
     err, ok = close(z.cpu().numpy(), want, ATOL, RTOL)
     assert ok, f"T={T} pos0={pos0} split={split}: max|err| {err}"
+
+
+@pytest.mark.parametrize("T,pos0,split", [(683, 16000, 5), (700, 15700, 16)])
+def test_prefill_r64_kv_split_vs_fp32(fl, dev, T, pos0, split):
+    """The 64-rows-a-wave kernel's KV split (>= 64 workgroups of 256 rows and
+    >= 16384 cache rows): 683 tokens leave 2 rows in the last row tile, 16
+    splits of 16400 rows leave some shares of the first row tiles' ranges
+    short. Every row against oracle/torch_ref.attention_prefill (fp32 on the
+    GPU) and the unsplit call, the attention bar."""
+    from oracle import torch_ref as tr
+
+    L = pos0 + T
+    g = torch.Generator(device=dev).manual_seed(T + split)
+    q = (torch.randn((T, 24, 256), generator=g, device=dev) / 16).half()
+    kd = torch.randn((L, 4, 256), generator=g, device=dev).half()
+    vd = torch.randn((L, 4, 256), generator=g, device=dev).half()
+    z = fl.ops.attention_prefill(q, kd, vd, pos0=pos0, scale=1.0, split=split)
+    z1 = fl.ops.attention_prefill(q, kd, vd, pos0=pos0, scale=1.0, split=1)
+    want = tr.attention_prefill(q, kd, vd, pos0, 1.0, block=256)
+    torch.cuda.synchronize()
+    for name, got in ((f"split {split}", z), ("split 1", z1)):
+        err = (got.float() - want.float()).abs()
+        bad = int((err > ATOL + RTOL * want.float().abs()).sum())
+        assert torch.isfinite(got.float()).all() and bad == 0, (name, float(err.max()))
+        assert float(err.max()) <= 1e-2 * float(want.float().abs().max()), name
 
 
 def test_prefill_kv_split_chunk_deep_in_prompt(fl, dev):
