@@ -834,8 +834,11 @@ bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 #define DEC_SPLIT_FLOOR 32
 #endif
 
+// int8 register tiles: 2 buffers (168 VGPRs, three waves a SIMD) -- in the
+// int8 layout 3 buffers (two waves a SIMD) measured 83.4 / 30.9 us at ~32k /
+// ~8k against 77.5 / 28.0, 4 and 5 slower still
 #ifndef DEC_NBUF_Q8
-#define DEC_NBUF_Q8 3
+#define DEC_NBUF_Q8 2
 #endif
 
 // int8 grids of at most one workgroup a CU take the LDS-staged tiles (2
