@@ -843,11 +843,13 @@ bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 // int8 grids of at most one workgroup a CU take the LDS-staged tiles (2
 // stages of Q8_STAGE_B: 92 KiB of LDS, one workgroup a CU): whole-line
-// copies and no registers held by tiles in flight. Measured on MI355X, B = 1
-// at 4k (128 workgroups) 14.9 -> 12.6 us; larger grids keep the register
-// tiles, whose two workgroups a CU overlap each other's barriers (B = 4, T =
-// 3 at ~8k / ~100k: 33.3 / 223 us against 34.4 / 235 staged). Both give the
-// same bits.
+// copies and no registers held by tiles in flight. Measured on MI355X: the
+// per-sequence launches of attention_dec_q8 (112 workgroups, ~100k rows
+// each) 478 against 525 us a step for the register tiles; B = 1 at 4k-16k
+// within 3 % of them (12.2 at 4k either way); larger grids keep the register
+// tiles, whose workgroups (three a CU) overlap each other's barriers (B = 4,
+// T = 3 at ~8k / ~100k: 33.3 / 223 us against 34.4 / 235 staged, measured
+// before the int8 layout). Both give the same bits.
 constexpr int DEC_STAGE_MAX_WGS = 256;
 constexpr int DEC_NBUF_STAGE = 2;
 
