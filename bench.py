@@ -408,7 +408,9 @@ def bench_gdn_prefill_front(torch, fl, T, which, iters=20):
     them (runtime.py:3035-3038, 3070-3076): the causal conv over T tokens x
     10240 channels (which = "conv": x read, y written, the weights and the
     ring), the L2 norm over the conv'd rows as 80 head-sized rows a token
-    ("l2norm": read + written), or the gates of 48 v heads ("scalars")."""
+    ("l2norm": read + written, the reference's launch), over only the 32 q and
+    k rows the scan reads ("l2norm_qk": the runtime's), or the gates of 48 v
+    heads ("scalars")."""
     dev = torch.device("cuda:0")
     g = torch.Generator(device=dev).manual_seed(T + 2)
     row = 10240
@@ -416,6 +418,8 @@ def bench_gdn_prefill_front(torch, fl, T, which, iters=20):
         nbytes = 2 * T * row * 2 + row * 4 * 2 + 2 * row * 3 * 2
     elif which == "l2norm":
         nbytes = 2 * T * row * 2
+    elif which == "l2norm_qk":
+        nbytes = 2 * T * 32 * 128 * 2
     else:
         nbytes = 4 * T * 48 * 4 + 2 * 48 * 4
     n_sets = min(64, max(1, -(-600_000_000 // nbytes)))
@@ -440,6 +444,8 @@ def bench_gdn_prefill_front(torch, fl, T, which, iters=20):
             x = sets[i % n_sets]
             if which == "conv":
                 fl.ops.conv1d_causal(x, w, rings[0], out, rings[1], T=T, pos0=4096)
+            elif which == "l2norm_qk":
+                fl.ops.l2norm_scaled_strided(x, out, rows=32, token_stride=row, T=T)
             else:
                 fl.ops.l2norm_scaled(x, out, rows=row // 128, T=T)
 
@@ -740,6 +746,7 @@ EXTRA_CONFIGS = {
     "attn_gate_T8192": (bench_attn_gate, {"T": 8192}),
     "gdn_prefill_conv_T8192": (bench_gdn_prefill_front, {"T": 8192, "which": "conv"}),
     "gdn_prefill_l2norm_T8192": (bench_gdn_prefill_front, {"T": 8192, "which": "l2norm"}),
+    "gdn_prefill_l2norm_qk_T8192": (bench_gdn_prefill_front, {"T": 8192, "which": "l2norm_qk"}),
     "gdn_prefill_scalars_T8192": (bench_gdn_prefill_front, {"T": 8192, "which": "scalars"}),
     "gdn_verify_B4_T3": (bench_gdn_verify, {}),
     "attn_prep_T1": (bench_attn_prep, {"T": 1}),

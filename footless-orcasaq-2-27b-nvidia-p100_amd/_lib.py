@@ -66,6 +66,7 @@ SIGNATURES = {
     "fl_conv1d_causal": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P]),
     "fl_conv1d_causal_rows": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P]),
     "fl_l2norm_scaled": (_I, [_P, _P, _I, _I, _I, _F, _F, _I, _P]),
+    "fl_l2norm_scaled_strided": (_I, [_P, _P, _I, _I, _LL, _F, _F, _I, _P]),
     "fl_rmsnorm_gated": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _F, _P]),
     "fl_gdn_scalars": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P]),
     "fl_gdn_scan": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _F, _I, _P,

@@ -831,14 +831,16 @@ rmsnorm_gated_rows_kernel(const f16* __restrict__ o, const f16* __restrict__ z,
 constexpr int L2_ROWS_PER_WG = (GR_THREADS / 64) * 4;
 __global__ void __launch_bounds__(GR_THREADS)
 l2norm_rows_kernel(const f16* __restrict__ x, f16* __restrict__ y, int rows, int pitch,
-                   int n_rows, float eps, float scale) {
+                   long long tstride, int n_rows, float eps, float scale) {
     typedef _Float16 f16x8v __attribute__((ext_vector_type(8)));
     const int lane = threadIdx.x & 63, j = lane & 15;
     const int rid = (blockIdx.x * (GR_THREADS / 64) + (threadIdx.x >> 6)) * 4 + (lane >> 4);
     const bool ok = rid < n_rows;
     const int rr = ok ? rid : n_rows - 1;   // rows past the end read the last, store nothing
     const int t = rr / rows, r = rr - t * rows;
-    const size_t base = ((size_t)t * rows + r) * pitch + 8 * j;
+    // tstride: elements between tokens' first rows (rows * pitch when a
+    // token's rows are all normalised)
+    const size_t base = (size_t)t * tstride + (size_t)r * pitch + 8 * j;
     const f16x8v xv = *(const f16x8v*)(x + base);
     float xf[8], sq[8];
 #pragma unroll
@@ -932,12 +934,29 @@ int fl_l2norm_scaled(const void* x, void* y, int n, int rows, int pitch, float e
         const long long wgs = (n_rows + L2_ROWS_PER_WG - 1) / L2_ROWS_PER_WG;
         hipLaunchKernelGGL(l2norm_rows_kernel, dim3((unsigned)wgs), dim3(GR_THREADS), 0,
                            (hipStream_t)stream, (const f16*)x, (f16*)y, rows, pitch,
-                           (int)n_rows, eps, scale);
+                           (long long)rows * pitch, (int)n_rows, eps, scale);
     } else {
         hipLaunchKernelGGL(l2norm_kernel, dim3(rows, T), dim3(128), 0, (hipStream_t)stream,
                            (const f16*)x, (f16*)y, n, rows, pitch, eps, scale);
     }
     return fl::check_launch("l2norm_scaled");
+}
+
+int fl_l2norm_scaled_strided(const void* x, void* y, int rows, int pitch,
+                             long long token_stride, float eps, float scale, int T,
+                             fl_stream_t stream) {
+    FL_REQUIRE(x && y, "null pointer");
+    FL_REQUIRE(rows >= 1 && T >= 1 && pitch >= GR_K && pitch % 8 == 0, "rows, T, pitch");
+    FL_REQUIRE(token_stride >= (long long)rows * pitch && token_stride % 8 == 0,
+               "token_stride >= rows * pitch, a multiple of 8");
+    FL_REQUIRE(aligned16(x) && aligned16(y), "16-byte aligned x / y");
+    const long long n_rows = (long long)rows * T;
+    FL_REQUIRE(n_rows < (1ll << 31), "rows * T < 2^31");
+    const long long wgs = (n_rows + L2_ROWS_PER_WG - 1) / L2_ROWS_PER_WG;
+    hipLaunchKernelGGL(l2norm_rows_kernel, dim3((unsigned)wgs), dim3(GR_THREADS), 0,
+                       (hipStream_t)stream, (const f16*)x, (f16*)y, rows, pitch, token_stride,
+                       (int)n_rows, eps, scale);
+    return fl::check_launch("l2norm_scaled_strided");
 }
 
 int fl_gdn_scalars(const float* a, const float* b, const float* A_log, const float* dt_bias,

@@ -464,6 +464,18 @@ def l2norm_scaled(x, y, *, n: int = GDN_K, rows: int, pitch: int = GDN_K, eps: f
               pitch, float(eps), float(scale), T, _stream())
 
 
+def l2norm_scaled_strided(x, y, *, rows: int, token_stride: int, pitch: int = GDN_K,
+                          eps: float = L2_EPS, scale: float = 1.0, T: int):
+    """l2norm_scaled (n = 128) over the first `rows` head-sized rows of each
+    token, token t starting at element t * token_stride (no reference
+    counterpart: the GDN prefill needs only the q and k rows of the 80 the
+    reference normalises, runtime.py:3068-3072); the other rows of y are not
+    written."""
+    span = (T - 1) * token_stride + (rows - 1) * pitch + GDN_K
+    _lib.call("fl_l2norm_scaled_strided", _ptr(x, F16, "x", span), _ptr(y, F16, "y", span), rows,
+              pitch, int(token_stride), float(eps), float(scale), T, _stream())
+
+
 def rmsnorm_gated(o, z, w, y=None, *, T: int | None = None, rows: int = GDN_V_HEADS,
                   n: int = GDN_V, pitch: int = GDN_V, eps: float = GDN_NORM_EPS):
     """kernels.cu:335-358 (runtime.py:3063-3065): the GDN output norm

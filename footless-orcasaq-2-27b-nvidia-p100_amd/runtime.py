@@ -350,10 +350,11 @@ class HybridRuntime:
         else:
             c = torch.empty_like(qkv)
             ops.conv1d_causal(qkv, wt.conv_w, cin, c, cout, T=T, pos0=pos0)
-            # the L2 norm over the whole row as head-sized rows, as the
-            # reference launches it (runtime.py:3070); q and k are read back
+            # the L2 norm of the q and k head rows (the reference launches it
+            # over all 80 head-sized rows of the conv'd row, runtime.py:3070,
+            # and reads back only these 32: the same bits for them)
             ln = torch.empty_like(c)
-            ops.l2norm_scaled(c, ln, rows=QKV_ROWS // GDN_K, T=T)
+            ops.l2norm_scaled_strided(c, ln, rows=2 * GDN_K_HEADS, token_stride=QKV_ROWS, T=T)
             beta = torch.empty((T, GDN_V_HEADS), dtype=F32, device=qkv.device)
             decay = torch.empty_like(beta)
             ops.gdn_scalars(a, b, wt.A_log, wt.dt_bias, beta, decay, T=T)

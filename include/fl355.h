@@ -311,6 +311,15 @@ int fl_conv1d_causal_rows(const void* x, const void* w, const void* st_in, void*
  * Replaces kernels.cu:373-391, runtime.py:3070-3071. */
 int fl_l2norm_scaled(const void* x, void* y, int n, int rows, int pitch, float eps, float scale,
                      int T, fl_stream_t stream);
+/* No counterpart in the reference: l2norm_scaled (n = 128) over the first
+ * `rows` rows of each token, token t's rows starting at t * token_stride
+ * elements -- for callers that need only some of a token's rows (the GDN
+ * prefill reads back q and k, 32 of the 80 head-sized rows the reference
+ * normalises, runtime.py:3068-3072). The same bits as fl_l2norm_scaled for
+ * those rows; the others are not touched. pitch and token_stride multiples
+ * of 8, x / y 16-byte aligned. */
+int fl_l2norm_scaled_strided(const void* x, void* y, int rows, int pitch, long long token_stride,
+                             float eps, float scale, int T, fl_stream_t stream);
 
 /* ---- GDN gates ------------------------------------------------------------
  * gdn_scalars: beta = sigmoid(b), decay = exp(-exp(A_log[h]) *

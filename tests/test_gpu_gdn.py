@@ -167,6 +167,22 @@ def test_l2norm_and_gates_vs_oracle(fl, dev, orc, rng):
     assert np.abs(decay.cpu().numpy() - d_r).max() / d_r.max() <= 2e-6
 
 
+@pytest.mark.parametrize("T", [1, 37, 300])
+def test_l2norm_strided_equals_full_rows(fl, dev, rng, T):
+    """fl_l2norm_scaled_strided over the q and k rows (32 of a token's 80
+    head-sized rows, the GDN prefill's use) gives the bits fl_l2norm_scaled
+    gives them over all 80, and leaves the other 48 rows untouched; 37 x 32
+    rows leave the last wave ragged."""
+    x = torch.from_numpy((rng.standard_normal((T, 80, 128)) * 0.8).astype(np.float16)).to(dev)
+    full = torch.empty_like(x)
+    fl.ops.l2norm_scaled(x, full, rows=80, T=T)
+    part = torch.full_like(x, 5.0)
+    fl.ops.l2norm_scaled_strided(x, part, rows=32, token_stride=80 * 128, T=T)
+    torch.cuda.synchronize()
+    assert torch.equal(part[:, :32].view(torch.int16), full[:, :32].view(torch.int16))
+    assert (part[:, 32:] == 5.0).all()
+
+
 @pytest.mark.parametrize("T,rows", [(7, 3), (5, 80), (1, 1)])
 def test_l2norm_row_layouts(fl, dev, orc, rng, T, rows):
     """Rows at 16-byte-aligned pitch 136 (16 lanes a row, 4 rows a wave) and
