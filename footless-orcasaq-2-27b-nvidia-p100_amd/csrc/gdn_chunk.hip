@@ -18,11 +18,12 @@
 // matrix cores.) The decay ratios are formed as e^{g_i - g_j} with j <= i
 // (never 1 / gamma_j, which overflows over a chunk of strong decay).
 //
-// Two launches. chunk_prep_kernel, every (chunk, k head) in parallel: K K^T
-// and Q K^T on MFMA once, then for each v head of the group the prefix sums,
-// A, T in fp32 by blocks of 16 (the diagonal blocks by forward substitution,
-// the others on fp32 MFMA), the gates, and T and M o QK^T written as fp16
-// MFMA operands.
+// Two launches. chunk_prep_kernel, every (chunk, v head) in parallel: K K^T
+// and Q K^T of the v head's k head on MFMA (the three v heads of a k head
+// each form them: one workgroup walking the three in turn measured 5 us
+// slower at 8k), then the prefix sums, A, T in fp32 by blocks of 16 (the
+// diagonal blocks by forward substitution, the others on fp32 MFMA), the
+// gates, and T and M o QK^T written as fp16 MFMA operands.
 // chunk_state_kernel: a state wavefront per 16 state rows (v) of a v head,
 // all 128 k columns of them in fp32 registers, sequential over the chunks; a
 // paired output wavefront takes its Q S0^T and Delta through LDS a chunk later,
@@ -150,7 +151,7 @@ __device__ __forceinline__ void split8(f32x4 a, f32x4 b, float s, f16x8& hi, f16
 }
 
 // ---------------------------------------------------------------------------
-// chunk_prep_kernel: one workgroup of 4 waves a (chunk, k head)
+// chunk_prep_kernel: one workgroup of 4 waves a (chunk, v head)
 // ---------------------------------------------------------------------------
 constexpr int PK_P = CK_K + 8;   // f16 pitch of staged K / Q rows
 constexpr int PA_P = CK_C + 4;   // f32 pitch of the A / T and M o QK^T rows
@@ -224,12 +225,12 @@ chunk_prep_kernel(const f16* __restrict__ q, const f16* __restrict__ k,
     float(*sA)[PA_P] = (float(*)[PA_P])smem;                     // after the products
     float(*sM)[PA_P] = (float(*)[PA_P])(smem + CK_C * PA_P * 4);
 
-    const int c = blockIdx.x, hk = blockIdx.y;
+    const int c = blockIdx.x, hv_blk = blockIdx.y, hk = hv_blk / group;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int ql = lane & 31, hh = lane >> 5;
     const int t0 = c * CK_C;
     const int n = min(CK_C, T - t0);
-    const int hv0 = hk * group, hv_end = min(hv0 + group, n_vheads);
+    const int hv0 = hv_blk;
 
     // Every global load issued up front and unconditionally, rows clamped to
     // the chunk's last token, past-the-end rows zeroed by a select: K and Q
@@ -264,19 +265,15 @@ chunk_prep_kernel(const f16* __restrict__ q, const f16* __restrict__ k,
         qk = __builtin_amdgcn_mfma_f32_32x32x16_f16(aq, bk, qk, 0, 0, 0);
     }
 
-    for (int hv = hv0; hv < hv_end; ++hv) {
+    {
+        const int hv = hv0;
         char* blk = work + ((size_t)c * n_vheads + hv) * CK_BLK;
         // this head's gates (decay 1 and beta 0 past the end: g stays at the
-        // last token's), the in-chunk prefix sums of log decay on wave 0; the
-        // next head's gates loaded meanwhile
+        // last token's), the in-chunk prefix sums of log decay on wave 0
         if (w == 0) {
             const float gs = wave_prefix_sum(lane < n ? safe_log(dec) : 0.f);
             sG[lane] = gs;
             sB[lane] = lane < n ? bet : 0.f;
-        }
-        if (hv + 1 < hv_end) {
-            dec = decay[gt + hv + 1];
-            bet = beta[gt + hv + 1];
         }
         __syncthreads();   // the gates in; every K / Q read (or T / M o QK^T
                            // read of the previous head) done
@@ -926,7 +923,7 @@ int fl_gdn_prefill_chunked(const void* q, const void* k, const void* v, const fl
         return FL_ESCRATCH;
     }
     const int n_chunks = (T + CK_C - 1) / CK_C;
-    hipLaunchKernelGGL(chunk_prep_kernel, dim3(n_chunks, (n_vheads + group - 1) / group), dim3(256), 0,
+    hipLaunchKernelGGL(chunk_prep_kernel, dim3(n_chunks, n_vheads), dim3(256), 0,
                        (hipStream_t)stream, (const f16*)q, (const f16*)k, beta, decay, T, n_vheads,
                        qk_stride, group, (char*)work);
     int rc = fl::check_launch("gdn_chunk_prep");
