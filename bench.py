@@ -670,7 +670,8 @@ def run_counter_workloads(torch, fl, names):
     WRITE_SIZE), gdn (config 1: 96 fused decode steps, 48 layer states
     rotated), prefill8k (config 3 at 8k, 3 launches), decode100k (config 2
     at 100k, B=4 T=3, 10 launches), decode4k_B1 / decode8k / decode32k
-    (configs 0 and 2, 10 eager launches), chunked (config 4 at 8k, 3
+    (configs 0 and 2, 10 eager launches), decode8_100k (config 2 at 100k
+    over int8 caches, 10 eager launches), chunked (config 4 at 8k, 3
     launches)."""
     dev = torch.device("cuda:0")
     for name in names:
@@ -715,6 +716,8 @@ def run_counter_workloads(torch, fl, names):
             L, Bq, T = {"decode4k_B1": (4096, 1, 1), "decode8k": (8192, 4, 3),
                         "decode32k": (32768, 4, 3)}[name]
             bench_attn_decode(torch, fl, L, Bq=Bq, T=T, eager=10)
+        elif name == "decode8_100k":
+            bench_attn_decode(torch, fl, 102400, kv8=True, eager=10)
         elif name == "chunked":
             bench_chunked(torch, fl, 8192, eager=3)
         else:
