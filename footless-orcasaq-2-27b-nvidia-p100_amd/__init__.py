@@ -11,6 +11,7 @@ from . import geometry  # noqa: F401
 from . import ops  # noqa: F401
 from . import state_blob  # noqa: F401
 from . import runtime  # noqa: F401
+from . import backend  # noqa: F401
 from ._lib import FlError, LIB_PATH  # noqa: F401
 
-__all__ = ["geometry", "ops", "runtime", "state_blob", "FlError", "LIB_PATH"]
+__all__ = ["geometry", "ops", "runtime", "backend", "state_blob", "FlError", "LIB_PATH"]

@@ -46,6 +46,7 @@ SIGNATURES = {
     "fl_attn_decode_noalloc_max_bytes": (_SZ, []),
     "fl_attention_prefill_plan": (_I, [_I, _I, _I, _I, _I, _P, _I]),
     "fl_attention_prefill_split_count": (_I, [_I, _I, _I, _I]),
+    "fl_attention_prefill_split_count_q8": (_I, [_I, _I, _I, _I]),
     "fl_attention_prefill_work_bytes": (_SZ, [_I, _I, _I, _I]),
     "fl_attention_prefill_q8_stage_bytes": (_SZ, [_I, _I, _I, _I, _I]),
     "fl_attention_prefill_kv": (_I, [_P, _I, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _I, _I,

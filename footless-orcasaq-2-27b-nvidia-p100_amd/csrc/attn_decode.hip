@@ -673,11 +673,17 @@ attn_decode_split_kernel(const f16* __restrict__ qg, DecSeqs seqs, float* __rest
 constexpr int MG_THREADS = 256;
 constexpr int MG_BATCH = 8;
 
+//
+// DEC: attention_dec_merge's contract (kernels.cu:1336-1385) -- pm in log2
+// units and only the first St = dec_split_count(pos0 + row + 1, tmin,
+// split) partials of a row written (the rest are never read); otherwise pm
+// in natural-log units and all `split` partials read.
+template <bool DEC>
 __global__ void __launch_bounds__(MG_THREADS)
 attn_merge_kernel(const float* __restrict__ pacc, const float* __restrict__ pm,
                   const float* __restrict__ pd, f16* __restrict__ z,
                   const f16* __restrict__ gate, int n_q_heads, int head_dim, int z_pitch,
-                  int g_pitch, int g_off, int split) {
+                  int g_pitch, int g_off, int split, int pos0, int tmin) {
     __shared__ f32x4 s_num[MG_THREADS];
     __shared__ float s_den[MG_THREADS];
     __shared__ float s_mx[MG_THREADS];
@@ -688,6 +694,8 @@ attn_merge_kernel(const float* __restrict__ pacc, const float* __restrict__ pm,
     const size_t p0 = rh * split;
     const float* pmr = pm + p0;
     const float* pdr = pd + p0;
+    const int ns = DEC ? dec_split_count(pos0 + row + 1, tmin, split) : split;
+    const float units = DEC ? 1.f : FL_LOG2E;   // m_s to log2 units
 
     float gv[4] = {0.f, 0.f, 0.f, 0.f};
     if (gate != nullptr && tid < C) {
@@ -700,12 +708,12 @@ attn_merge_kernel(const float* __restrict__ pacc, const float* __restrict__ pm,
     float den = 0.f, M = -1e30f;
     if (j < J) {
         const f32x4* acc = (const f32x4*)(pacc + p0 * head_dim) + c;
-        for (int s = j; s < split; s += MG_BATCH * J) {
+        for (int s = j; s < ns; s += MG_BATCH * J) {
             float mv[MG_BATCH], dv[MG_BATCH];
             f32x4 av[MG_BATCH];
 #pragma unroll
             for (int u = 0; u < MG_BATCH; ++u) {
-                const int si = min(s + u * J, split - 1);
+                const int si = min(s + u * J, ns - 1);
                 mv[u] = pmr[si];
                 dv[u] = pdr[si];
                 av[u] = acc[(size_t)si * C];
@@ -713,21 +721,21 @@ attn_merge_kernel(const float* __restrict__ pacc, const float* __restrict__ pm,
             float bm = M;
 #pragma unroll
             for (int u = 0; u < MG_BATCH; ++u) {
-                const bool ok = s + u * J < split;
+                const bool ok = s + u * J < ns;
                 mv[u] = ok ? mv[u] : -1e30f;
                 dv[u] = ok ? dv[u] : 0.f;
                 av[u] = ok ? av[u] : (f32x4)(0.f);
                 bm = fmaxf(bm, mv[u]);
             }
             if (bm > M) {
-                const float corr = fast_exp2((M - bm) * FL_LOG2E);
+                const float corr = fast_exp2((M - bm) * units);
                 num *= corr;
                 den *= corr;
                 M = bm;
             }
 #pragma unroll
             for (int u = 0; u < MG_BATCH; ++u) {
-                const float e = fast_exp2((mv[u] - M) * FL_LOG2E);
+                const float e = fast_exp2((mv[u] - M) * units);
                 num[0] = fmaf(e, av[u][0], num[0]);
                 num[1] = fmaf(e, av[u][1], num[1]);
                 num[2] = fmaf(e, av[u][2], num[2]);
@@ -746,7 +754,7 @@ attn_merge_kernel(const float* __restrict__ pacc, const float* __restrict__ pm,
         f32x4 n = (f32x4)(0.f);
         float dsum = 0.f;
         for (int jj = 0; jj < J; ++jj) {
-            const float e = fast_exp2((s_mx[jj * C + tid] - Mg) * FL_LOG2E);
+            const float e = fast_exp2((s_mx[jj * C + tid] - Mg) * units);
             const f32x4 o = s_num[jj * C + tid];
             n[0] = fmaf(e, o[0], n[0]);
             n[1] = fmaf(e, o[1], n[1]);
@@ -765,48 +773,24 @@ attn_merge_kernel(const float* __restrict__ pacc, const float* __restrict__ pm,
     }
 }
 
-// attention_dec_merge (kernels.cu:1336-1385): the first St partials of the
-// token (dec rule), exp2 weights, z = f16_sat(num / den), then the gate if
-// given. One block of 256 threads a (q head, token).
-__global__ void attn_dec_merge_kernel(const float* __restrict__ pacc, const float* __restrict__ pm,
-                                      const float* __restrict__ pd, f16* __restrict__ z,
-                                      const f16* __restrict__ gate, int n_q_heads, int z_pitch,
-                                      int g_pitch, int g_off, int pos0, int tmin, int smax) {
-    const int head = blockIdx.x, t = blockIdx.y, d = threadIdx.x;
-    const int st = dec_split_count(pos0 + t + 1, tmin, smax);
-    const size_t p0 = ((size_t)t * n_q_heads + head) * smax;
-    float M = -INFINITY;
-    for (int s = 0; s < st; ++s) M = fmaxf(M, pm[p0 + s]);
-    float num = 0.f, den = 0.f;
-    for (int s = 0; s < st; ++s) {
-        const float e = fast_exp2(pm[p0 + s] - M);
-        num = fmaf(e, pacc[(p0 + s) * DEC_HD + d], num);
-        den = fmaf(e, pd[p0 + s], den);
-    }
-    f16 zv = f16_sat(num / den);
-    if (gate != nullptr) {
-        const float g = (float)gate[((size_t)t * n_q_heads + head) * g_pitch + g_off + d];
-        zv = f16_sat((float)zv * sigmoid_f(g));
-    }
-    z[((size_t)t * n_q_heads + head) * z_pitch + d] = zv;
-}
-
-__global__ void attn_gate_kernel(f16* __restrict__ z, const f16* __restrict__ g, int n_heads,
-                                 int head_dim, int z_pitch, int g_pitch, int g_off) {
-    const int t = blockIdx.y;
-    const int n = n_heads * head_dim;
-    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
-        const int hd = i / head_dim, dd = i - hd * head_dim;
-        const float gv = (float)g[((size_t)t * n_heads + hd) * g_pitch + g_off + dd];
-        f16* p = z + ((size_t)t * n_heads + hd) * z_pitch + dd;
-        *p = f16_sat((float)*p * sigmoid_f(gv));
-    }
+// The output gate for layouts the 8-a-lane kernel below does not take (odd
+// head_dim, pitches or offsets, unaligned buffers): one wavefront a (token,
+// head) row, lane l taking elements l, l + 64, ... of it, with the same
+// sigmoid_f and roundings.
+__global__ void __launch_bounds__(64)
+attn_gate_row_kernel(f16* __restrict__ z, const f16* __restrict__ g, int head_dim, int z_pitch,
+                     int g_pitch, int g_off) {
+    const size_t row = blockIdx.x;                      // token n_heads + head
+    f16* zr = z + row * z_pitch;
+    const f16* gr = g + row * g_pitch + g_off;
+    for (int d = threadIdx.x; d < head_dim; d += 64)
+        zr[d] = f16_sat((float)zr[d] * sigmoid_f((float)gr[d]));
 }
 
 // The gate with 8 elements a lane (one 16-byte load of z and of g, one store
 // of z), for head_dim, the pitches and g_off multiples of 8 and 16-byte
-// aligned z / g: the same sigmoid_f and roundings as attn_gate_kernel, so the
-// same bits. chunks = T n_heads head_dim / 8 lanes in all.
+// aligned z / g: the same sigmoid_f and roundings as attn_gate_row_kernel,
+// so the same bits. chunks = T n_heads head_dim / 8 lanes in all.
 __global__ void __launch_bounds__(256)
 attn_gate_vec_kernel(f16* __restrict__ z, const f16* __restrict__ g, int n_heads, int head_dim,
                      int z_pitch, int g_pitch, int g_off, long long chunks) {
@@ -950,9 +934,9 @@ int attn_decode_batched(const void* qg, int q_pitch, const void* const* kcache,
                                  q_pitch, grid_split, grid_split, split_rows, scale * FL_LOG2E,
                                  (hipStream_t)stream, DEC_SPLIT_FLOOR);
     if (rc) return rc;
-    hipLaunchKernelGGL(attn_merge_kernel, dim3(n_q_heads, B * T), dim3(MG_THREADS), 0,
+    hipLaunchKernelGGL(attn_merge_kernel<false>, dim3(n_q_heads, B * T), dim3(MG_THREADS), 0,
                        (hipStream_t)stream, pacc, pm, pd, (f16*)z, (const f16*)gate, n_q_heads,
-                       head_dim, z_pitch, g_pitch, g_off, grid_split);
+                       head_dim, z_pitch, g_pitch, g_off, grid_split, 0, 1);
     return fl::check_launch("attn_merge");
 }
 
@@ -1089,9 +1073,10 @@ int fl_attention_dec_merge(const float* pacc, const float* pm, const float* pd, 
     FL_REQUIRE(n_q_heads >= 1 && T >= 1 && pos0 >= 0, "n_q_heads, T >= 1, pos0 >= 0");
     FL_REQUIRE(tmin >= 1 && smax >= 1 && z_pitch >= DEC_HD, "tmin, smax >= 1, z_pitch >= 256");
     FL_REQUIRE(gate == nullptr || g_off + DEC_HD <= g_pitch, "g_off + 256 <= g_pitch");
-    hipLaunchKernelGGL(attn_dec_merge_kernel, dim3(n_q_heads, T), dim3(DEC_HD), 0,
+    FL_REQUIRE(aligned16(pacc), "16-byte aligned pacc");
+    hipLaunchKernelGGL(attn_merge_kernel<true>, dim3(n_q_heads, T), dim3(MG_THREADS), 0,
                        (hipStream_t)stream, pacc, pm, pd, (f16*)z, (const f16*)gate, n_q_heads,
-                       z_pitch, g_pitch, g_off, pos0, tmin, smax);
+                       DEC_HD, z_pitch, g_pitch, g_off, smax, pos0, tmin);
     return fl::check_launch("attn_dec_merge");
 }
 
@@ -1124,9 +1109,9 @@ int fl_attention_merge(const float* pacc, const float* pm, const float* pd, void
     FL_REQUIRE(T >= 1 && split >= 1 && n_q_heads >= 1, "T, split, n_q_heads >= 1");
     FL_REQUIRE(gate == nullptr || g_off + head_dim <= g_pitch, "g_off + head_dim <= g_pitch");
     FL_REQUIRE(aligned16(pacc), "16-byte aligned pacc");
-    hipLaunchKernelGGL(attn_merge_kernel, dim3(n_q_heads, T), dim3(MG_THREADS), 0,
+    hipLaunchKernelGGL(attn_merge_kernel<false>, dim3(n_q_heads, T), dim3(MG_THREADS), 0,
                        (hipStream_t)stream, pacc, pm, pd, (f16*)z, (const f16*)gate, n_q_heads,
-                       head_dim, z_pitch, g_pitch, g_off, split);
+                       head_dim, z_pitch, g_pitch, g_off, split, 0, 1);
     return fl::check_launch("attn_merge");
 }
 
@@ -1142,10 +1127,11 @@ int fl_attn_gate(void* z, const void* g, int n_heads, int head_dim, int z_pitch,
                            dim3(256), 0, (hipStream_t)stream, (f16*)z, (const f16*)g, n_heads,
                            head_dim, z_pitch, g_pitch, g_off, chunks);
     } else {
-        const int n = n_heads * head_dim;
-        hipLaunchKernelGGL(attn_gate_kernel, dim3((n + 255) / 256, T), dim3(256), 0,
-                           (hipStream_t)stream, (f16*)z, (const f16*)g, n_heads, head_dim,
-                           z_pitch, g_pitch, g_off);
+        const long long rows = (long long)T * n_heads;
+        FL_REQUIRE(rows < (1ll << 31), "T * n_heads < 2^31");
+        hipLaunchKernelGGL(attn_gate_row_kernel, dim3((unsigned)rows), dim3(64), 0,
+                           (hipStream_t)stream, (f16*)z, (const f16*)g, head_dim, z_pitch,
+                           g_pitch, g_off);
     }
     return fl::check_launch("attn_gate");
 }

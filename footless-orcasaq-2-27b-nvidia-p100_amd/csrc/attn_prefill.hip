@@ -1302,6 +1302,11 @@ extern "C" int fl_attention_prefill_split_count(int T, int pos0, int n_q_heads, 
     return split_policy(T, pos0, n_q_heads, n_kv_heads);
 }
 
+extern "C" int fl_attention_prefill_split_count_q8(int T, int pos0, int n_q_heads,
+                                                   int n_kv_heads) {
+    return split_policy(T, pos0, n_q_heads, n_kv_heads, true);
+}
+
 extern "C" size_t fl_attention_prefill_q8_stage_bytes(int T, int pos0, int n_q_heads,
                                                      int n_kv_heads, int head_dim) {
     return q8_stage_bytes(T, pos0, n_q_heads, n_kv_heads, head_dim);

@@ -319,24 +319,41 @@ void conv_launch(bool vec, bool rows, dim3 grid_tok, const f16* x, const f16* w,
 }
 
 // ---------------------------------------------------------------------------
-// L2 norm, one 128-thread block a (row, token)
+// L2 norm for any row length n <= 1024 and pitch (the layouts the 16-lane row
+// kernel below does not take): one wavefront a row, four rows a workgroup, no
+// LDS and no barrier. The reference's 128-thread block (kernels.cu:373-391)
+// lets thread v sum x[v], x[v + 128], ... in order, reduces each warp by a
+// shuffle-down tree and combines the warp sums as (r0 + r2) + (r1 + r3).
+// Lane l here runs two of those threads, l and l + 64, as two running sums;
+// the warp trees become butterflies inside each 32-lane half (a lane and its
+// partner add the same two values, a + b == b + a, so every lane ends with
+// its half's tree sum), after which a lane below 32 holds r0 and r2, a lane
+// above r1 and r3; their sums meet in one exchange at distance 32. The same
+// additions in the same order, so the bits of the row kernel and the oracle.
 // ---------------------------------------------------------------------------
-__global__ void l2norm_kernel(const f16* __restrict__ x, f16* __restrict__ y, int n, int rows,
-                              int pitch, float eps, float scale) {
-    __shared__ float red[4];
-    const int t = blockIdx.y, r = blockIdx.x;
-    const f16* xr = x + ((size_t)t * rows + r) * pitch;
-    f16* yr = y + ((size_t)t * rows + r) * pitch;
-    float ss = 0.f;
-    for (int i = threadIdx.x; i < n; i += blockDim.x) {
-        const float v = (float)xr[i];
-        ss = fmaf(v, v, ss);
+__global__ void __launch_bounds__(256)
+l2norm_wave_kernel(const f16* __restrict__ x, f16* __restrict__ y, int n, int rows, int pitch,
+                   int n_rows, float eps, float scale) {
+    const int lane = threadIdx.x & 63;
+    const int rid = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (rid >= n_rows) return;                        // wave-uniform
+    const size_t off = (size_t)rid * pitch;           // rid = t rows + r
+    const f16* xr = x + off;
+    f16* yr = y + off;
+    float lo = 0.f, hi = 0.f;                         // threads `lane` and `lane + 64`
+    for (int i = lane; i < n; i += 128) {
+        const float a = (float)xr[i];
+        lo = fmaf(a, a, lo);
+        if (i + 64 < n) {
+            const float b = (float)xr[i + 64];
+            hi = fmaf(b, b, hi);
+        }
     }
-    ss = warp32_tree(ss);
-    if ((threadIdx.x & 31) == 0) red[threadIdx.x >> 5] = ss;
-    __syncthreads();
-    const float den = sqrtf(((red[0] + red[2]) + (red[1] + red[3])) + eps);
-    for (int i = threadIdx.x; i < n; i += blockDim.x) yr[i] = f16_sat(((float)xr[i] / den) * scale);
+    lo = warp32_tree(lo);                             // r0 (lanes < 32) or r1
+    hi = warp32_tree(hi);                             // r2 or r3
+    const float pair = lo + hi;
+    const float den = sqrtf((pair + lane_xor(pair, 32)) + eps);
+    for (int i = lane; i < n; i += 64) yr[i] = f16_sat(((float)xr[i] / den) * scale);
 }
 
 // ---------------------------------------------------------------------------
@@ -827,7 +844,7 @@ rmsnorm_gated_rows_kernel(const f16* __restrict__ o, const f16* __restrict__ z,
 // 2 and 1 (butterflies: every lane of the four holds the tree's sum, a + b ==
 // b + a), 4, 2, 1 the in-lane pairs, and the warp sums combine by exchanges
 // at distance 8 and 4 -- the same additions in the same order, so the same
-// bits as the one-row-a-workgroup kernel above.
+// bits as the one-row-a-wavefront kernel above.
 constexpr int L2_ROWS_PER_WG = (GR_THREADS / 64) * 4;
 __global__ void __launch_bounds__(GR_THREADS)
 l2norm_rows_kernel(const f16* __restrict__ x, f16* __restrict__ y, int rows, int pitch,
@@ -936,8 +953,10 @@ int fl_l2norm_scaled(const void* x, void* y, int n, int rows, int pitch, float e
                            (hipStream_t)stream, (const f16*)x, (f16*)y, rows, pitch,
                            (long long)rows * pitch, (int)n_rows, eps, scale);
     } else {
-        hipLaunchKernelGGL(l2norm_kernel, dim3(rows, T), dim3(128), 0, (hipStream_t)stream,
-                           (const f16*)x, (f16*)y, n, rows, pitch, eps, scale);
+        FL_REQUIRE(n_rows < (1ll << 31), "rows * T < 2^31");
+        hipLaunchKernelGGL(l2norm_wave_kernel, dim3((unsigned)((n_rows + 3) / 4)), dim3(256), 0,
+                           (hipStream_t)stream, (const f16*)x, (f16*)y, n, rows, pitch,
+                           (int)n_rows, eps, scale);
     }
     return fl::check_launch("l2norm_scaled");
 }

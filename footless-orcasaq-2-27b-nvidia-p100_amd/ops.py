@@ -265,13 +265,21 @@ def prefill_split_count(T: int, pos0: int, n_q_heads: int = N_HEADS,
     2932-2941's role): 1 unless the 128-row workgroups are too few for the
     CUs (the 64-rows-a-wave kernel's split from 64 workgroups of 256 rows
     and 16384 cache rows, the 128-row kernel's otherwise). The int8 prefill
-    takes the same count."""
+    takes prefill_split_count_q8's."""
     return int(_lib.lib().fl_attention_prefill_split_count(T, pos0, n_q_heads, n_kv_heads))
 
 
-def _prefill_split(T, pos0, n_q_heads, n_kv_heads, head_dim, split, work, device):
+def prefill_split_count_q8(T: int, pos0: int, n_q_heads: int = N_HEADS,
+                           n_kv_heads: int = N_KV) -> int:
+    """prefill_split_count for an int8 cache: the 128-row int8 kernel's split
+    (what fl_attention_prefill_kv_q8 takes for split 0)."""
+    return int(_lib.lib().fl_attention_prefill_split_count_q8(T, pos0, n_q_heads, n_kv_heads))
+
+
+def _prefill_split(T, pos0, n_q_heads, n_kv_heads, head_dim, split, work, device, q8=False):
     if split is None:
-        split = prefill_split_count(T, pos0, n_q_heads, n_kv_heads)
+        split = (prefill_split_count_q8 if q8 else prefill_split_count)(T, pos0, n_q_heads,
+                                                                          n_kv_heads)
     if split > 1 and work is None:
         need = int(_lib.lib().fl_attention_prefill_work_bytes(T, n_q_heads, head_dim, split))
         work = torch.empty(need, dtype=torch.uint8, device=device)
@@ -407,7 +415,8 @@ def attention_prefill_q8(q, kcache, vcache, *, pos0: int, max_pos: int, T: int |
     row = n_kv_heads * HEAD_DIM
     if z is None:
         z = torch.empty((T, n_q_heads, HEAD_DIM), dtype=F16, device=q.device)
-    split, work = _prefill_split(T, pos0, n_q_heads, n_kv_heads, HEAD_DIM, split, work, q.device)
+    split, work = _prefill_split(T, pos0, n_q_heads, n_kv_heads, HEAD_DIM, split, work, q.device,
+                                 q8=True)
     args = (_ptr(q, F16, "q", T * n_q_heads * q_pitch), q_pitch,
             _ptr(k_new, F16, "k_new", T * row), _ptr(v_new, F16, "v_new", T * row),
             _kv8(kcache, "kcache", max_pos, n_kv_heads, HEAD_DIM),

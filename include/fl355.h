@@ -217,8 +217,8 @@ int fl_attention_dec_q8(const void* q, const void* kcache, const void* vcache, f
 /* attention_dec_merge (+ gate when gate != NULL): z = f16_sat(sum_s 2^(m_s -
  * M) acc_s / sum_s 2^(m_s - M) d_s) over token t's first St partials, then
  * z = f16_sat(z * sigmoid(gate[t][h][g_off + d])). z [T][n_q_heads][z_pitch].
- * Replaces kernels.cu:1336-1385 attention_dec_merge / _gate,
- * runtime.py:2917-2920. */
+ * pacc 16-byte aligned. Replaces kernels.cu:1336-1385 attention_dec_merge /
+ * _gate, runtime.py:2917-2920. */
 int fl_attention_dec_merge(const float* pacc, const float* pm, const float* pd, void* z,
                            int n_q_heads, int z_pitch, int pos0, int tmin, int smax, int T,
                            const void* gate, int g_pitch, int g_off, fl_stream_t stream);
@@ -261,6 +261,10 @@ size_t fl_attn_decode_noalloc_max_bytes(void);
  * split 0: fl_attention_prefill_split_count's choice; split 1:
  * fl_attention_prefill (no work needed). */
 int fl_attention_prefill_split_count(int T, int pos0, int n_q_heads, int n_kv_heads);
+/* The same choice for an int8 cache (_fh_split's role for
+ * attention_prefill_fh_q8, runtime.py:2932-2941): always the 128-row int8
+ * kernel's split, what fl_attention_prefill_kv_q8 takes for split 0. */
+int fl_attention_prefill_split_count_q8(int T, int pos0, int n_q_heads, int n_kv_heads);
 size_t fl_attention_prefill_work_bytes(int T, int n_q_heads, int head_dim, int split);
 int fl_attention_prefill_kv(const void* q, int q_pitch, const void* k_new, const void* v_new,
                             void* kcache, void* vcache, int layer, int n_q_heads, int n_kv_heads,

@@ -859,10 +859,16 @@ ORC_API void orc_l2norm_scaled(const uint16_t* x, uint16_t* y, int n, int rows, 
         for (int r = 0; r < rows; r++) {
             const uint16_t* xr = x + ((size_t)t * rows + r) * pitch;
             uint16_t* yr = y + ((size_t)t * rows + r) * pitch;
+            /* thread v of the 128-thread block sums x[v], x[v + 128], ...
+             * in order (kernels.cu:384-387) */
             float lanes[128];
-            for (int i = 0; i < 128; i++) {
-                const float v = i < n ? orc_h2f(xr[i]) : 0.f;
-                lanes[i] = fmaf(v, v, 0.f);
+            for (int v = 0; v < 128; v++) {
+                float acc = 0.f;
+                for (int i = v; i < n; i += 128) {
+                    const float xv = orc_h2f(xr[i]);
+                    acc = fmaf(xv, xv, acc);
+                }
+                lanes[v] = acc;
             }
             float wsum[32] = {0};
             for (int wi = 0; wi < 4; wi++) wsum[wi] = tree_down(lanes + 32 * wi, 32);

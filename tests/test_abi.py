@@ -126,6 +126,10 @@ def test_prefill_split_policy(fl):
     assert lib.fl_attention_prefill_split_count(4096, 98000, 24, 4) == 1
     assert lib.fl_attention_prefill_split_count(1024, 98000, 24, 4) == 8
     assert lib.fl_attention_prefill_split_count(512, 98000, 24, 4) == 8
+    # over an int8 cache the 128-row int8 kernel always runs: its own cost model
+    assert lib.fl_attention_prefill_split_count_q8(1024, 98000, 24, 4) == 4
+    assert lib.fl_attention_prefill_split_count_q8(512, 98000, 24, 4) == 8
+    assert lib.fl_attention_prefill_split_count_q8(8192, 0, 24, 4) == 1
     assert lib.fl_attention_prefill_work_bytes(1024, 24, 256, 4) == 1024 * 24 * 4 * (256 * 4 + 8)
     assert lib.fl_attention_prefill_work_bytes(1024, 24, 256, 1) == 0
 

@@ -10,7 +10,7 @@ import numpy as np
 import pytest
 import torch
 
-from conftest import close, rand_cache, rand_qg
+from conftest import close_rel, rand_cache, rand_qg
 
 pytestmark = pytest.mark.gpu
 
@@ -55,18 +55,23 @@ def test_split_and_merge_vs_oracle(fl, dev, orc, rng, L, T):
     fl.ops.attention_merge(pacc, pm, pd, z, T=T, split=split, gate=qd)
     torch.cuda.synchronize()
     want = orc.attention_decode(qg, kc, vc, pos0, max_pos=L, scale=SCALE)
-    err, ok = close(z.cpu().numpy(), want, ATOL, RTOL)
+    err, ok = close_rel(z.cpu().numpy(), want, ATOL, RTOL)
     assert ok, f"L={L} T={T}: max|err| {err}"
 
 
-@pytest.mark.parametrize("Lmax", [8192, 32768, 102400])
-def test_config2_decode_verify_vs_oracle(fl, dev, orc, Lmax):
-    """Config 2: B=4, T=3 verify rows, lengths seeded-uniform in [0.9 Lmax, Lmax]."""
-    rng = np.random.default_rng(Lmax)
+@pytest.mark.parametrize("Lmax,q_scale", [(8192, 1 / 16), (32768, 1 / 16), (102400, 1 / 16),
+                                           (102400, 1.0)])
+def test_config2_decode_verify_vs_oracle(fl, dev, orc, Lmax, q_scale):
+    """Config 2: B=4, T=3 verify rows, lengths seeded-uniform in [0.9 Lmax, Lmax].
+    Bar: max-abs 2e-3 / rel 1e-2 and max|err| <= 1e-2 max|want|; at ~100k the
+    second rejects one lost split of 64 or one lost 32-row tile, which the first
+    alone accepts (tests/test_parity_bar.py). q_scale 1 gives scores of std 1
+    (peaked softmax) where config 2's q / 16 gives a nearly flat one."""
+    rng = np.random.default_rng(Lmax + int(q_scale * 16))
     B, T = 4, 3
     lens = rng.integers(int(np.ceil(0.9 * Lmax)), Lmax + 1, size=B)
     caches = [rand_cache(rng, int(L)) for L in lens]
-    qg = np.stack([rand_qg(rng, T) for _ in range(B)])
+    qg = np.stack([rand_qg(rng, T, q_scale=q_scale) for _ in range(B)])
     pos0s = [int(L) - T for L in lens]
     z = fl.ops.attn_decode(to_dev(qg, dev), [to_dev(c[0], dev) for c in caches],
                            [to_dev(c[1], dev) for c in caches], pos0s)
@@ -75,7 +80,9 @@ def test_config2_decode_verify_vs_oracle(fl, dev, orc, Lmax):
     for b in range(B):
         want = orc.attention_decode(qg[b], caches[b][0], caches[b][1], pos0s[b],
                                     max_pos=int(lens[b]), scale=SCALE)
-        err, ok = close(zh[b], want, ATOL, RTOL)
+        err, ok = close_rel(zh[b], want, ATOL, RTOL)
+        print(f"Lmax={Lmax} q_scale={q_scale} seq {b}: max|err| {err:.2e} "
+              f"max|want| {np.abs(want).max():.2e}")
         assert ok, f"Lmax={Lmax} seq {b} (L={lens[b]}): max|err| {err}"
 
 
@@ -106,15 +113,22 @@ def test_batched_equals_single_bit_exact(fl, dev, rng):
         assert torch.equal(zb[b], z1[0]), b
 
 
-def test_split_count_independence(fl, dev, rng):
+def test_split_count_independence(fl, dev, orc, rng):
+    """4 splits and 300 splits of the same ~20k rows agree with each other and
+    with the oracle, within the relative bar (a split lost or counted twice
+    moves z by ~1/4 of its own size at 4 splits)."""
     L = 20000
     kc, vc = rand_cache(rng, L)
     qg = rand_qg(rng, 2)
     kd, vd, qd = to_dev(kc, dev), to_dev(vc, dev), to_dev(qg[None], dev)
     za = fl.ops.attn_decode(qd, [kd], [vd], [L - 2], split_rows=32, split=4)
     zb = fl.ops.attn_decode(qd, [kd], [vd], [L - 2], split_rows=64, split=300)
-    err, ok = close(za.cpu().numpy(), zb.cpu().numpy().astype(np.float64), 1e-3, 1e-2)
+    err, ok = close_rel(za.cpu().numpy(), zb.cpu().numpy().astype(np.float64), 1e-3, 1e-2)
     assert ok, err
+    want = orc.attention_decode(qg, kc, vc, L - 2, max_pos=L, scale=SCALE)
+    for name, z in (("4 splits", za), ("300 splits", zb)):
+        err, ok = close_rel(z[0].cpu().numpy(), want, ATOL, RTOL)
+        assert ok, (name, err)
 
 
 def test_gate_is_sigmoid(fl, dev, rng):
@@ -154,7 +168,7 @@ def test_attn_gate_layouts(fl, dev, rng, T):
         outs.append(zh[..., :256])
     assert np.array_equal(outs[0].view(np.int16), outs[1].view(np.int16))
     want = (z.astype(np.float32) / (1 + np.exp(-g.astype(np.float32)))).astype(np.float16)
-    err, ok = close(outs[0], want.astype(np.float64), ATOL, RTOL)
+    err, ok = close_rel(outs[0], want.astype(np.float64), ATOL, RTOL)
     assert ok, err
 
 
@@ -188,7 +202,7 @@ def test_prefill_vs_oracle(fl, dev, orc, rng, T, pos0):
     torch.cuda.synchronize()
     assert np.array_equal(kd.cpu().numpy(), kc) and np.array_equal(vd.cpu().numpy(), vc)
     want = orc.attention_prefill(qg, kc, vc, q_pitch=512, pos0=pos0, max_pos=L, scale=SCALE, T=T)
-    err, ok = close(z.cpu().numpy(), want, ATOL, RTOL)
+    err, ok = close_rel(z.cpu().numpy(), want, ATOL, RTOL)
     assert ok, f"T={T} pos0={pos0}: max|err| {err}"
 
 
@@ -209,7 +223,7 @@ def test_prefill_growing_scores(fl, dev, orc, rng, T, pos0):
     z = fl.ops.attention_prefill(to_dev(qg, dev), kd, vd, pos0=pos0)
     torch.cuda.synchronize()
     want = orc.attention_prefill(qg, kc, vc, q_pitch=512, pos0=pos0, max_pos=L, scale=SCALE, T=T)
-    err, ok = close(z.cpu().numpy(), want, ATOL, RTOL)
+    err, ok = close_rel(z.cpu().numpy(), want, ATOL, RTOL)
     assert ok, f"T={T} pos0={pos0}: max|err| {err}"
 
 
@@ -227,7 +241,7 @@ def test_prefill_config3_scaling_full_rows_2k(fl, dev, orc):
                                  k_new=to_dev(kc, dev), v_new=to_dev(vc, dev))
     torch.cuda.synchronize()
     want = orc.attention_prefill(q, kc, vc, q_pitch=256, pos0=0, max_pos=L, scale=1.0, T=L)
-    err, ok = close(z.cpu().numpy(), want, ATOL, RTOL)
+    err, ok = close_rel(z.cpu().numpy(), want, ATOL, RTOL)
     assert ok, f"max|err| {err}"
 
 
@@ -278,7 +292,7 @@ def test_prefill_config3_sampled_rows(fl, dev, orc, L):
                      *rng.integers(0, L, 4).tolist()}):
         want = orc.attention_exact(q[t:t + 1], kc, vc, q_pitch=256, pos0=t, max_pos=L,
                                    scale=1.0, T=1)
-        err, ok = close(zh[t:t + 1], want, ATOL, RTOL)
+        err, ok = close_rel(zh[t:t + 1], want, ATOL, RTOL)
         assert ok, f"L={L} row {t}: max|err| {err}"
 
 
@@ -305,13 +319,13 @@ def test_prefill_kv_head_counts(fl, dev, orc, n_kv, G, T):
     if T <= 512:
         want = orc.attention_prefill(q, kc, vc, n_q_heads=n_q, n_kv_heads=n_kv, q_pitch=256,
                                      pos0=0, max_pos=T, scale=1.0, T=T)
-        err, ok = close(zh, want, ATOL, RTOL)
+        err, ok = close_rel(zh, want, ATOL, RTOL)
         assert ok, f"n_kv={n_kv} T={T}: max|err| {err}"
         return
     for t in sorted({0, 1, 85, 86, T // 2, T - 2, T - 1, *rng.integers(0, T, 4).tolist()}):
         want = orc.attention_exact(q[t:t + 1], kc, vc, n_q_heads=n_q, n_kv_heads=n_kv,
                                    q_pitch=256, pos0=t, max_pos=T, scale=1.0, T=1)
-        err, ok = close(zh[t:t + 1], want, ATOL, RTOL)
+        err, ok = close_rel(zh[t:t + 1], want, ATOL, RTOL)
         assert ok, f"n_kv={n_kv} T={T} row {t}: max|err| {err}"
 
 
@@ -339,7 +353,7 @@ def test_prefill_long_sampled_rows(fl, dev, orc, T, pos0, ramp):
                      *rng.integers(0, T, 5).tolist()}):
         want = orc.attention_exact(qg[t:t + 1], kc, vc, q_pitch=512, pos0=pos0 + t, max_pos=L,
                                    scale=SCALE, T=1)
-        err, ok = close(zh[t:t + 1], want, ATOL, RTOL)
+        err, ok = close_rel(zh[t:t + 1], want, ATOL, RTOL)
         assert ok, f"T={T} pos0={pos0} row {t}: max|err| {err}"
 
 # --------------------------------------------------------------------------
@@ -365,7 +379,7 @@ def test_prefill_kv_split_vs_oracle(fl, dev, orc, rng, T, pos0, split):
     torch.cuda.synchronize()
     assert np.array_equal(kd.cpu().numpy(), kc) and np.array_equal(vd.cpu().numpy(), vc)
     want = orc.attention_prefill(qg, kc, vc, q_pitch=512, pos0=pos0, max_pos=L, scale=SCALE, T=T)
-    err, ok = close(z.cpu().numpy(), want, ATOL, RTOL)
+    err, ok = close_rel(z.cpu().numpy(), want, ATOL, RTOL)
     assert ok, f"T={T} pos0={pos0} split={split}: max|err| {err}"
 
 
@@ -441,5 +455,5 @@ def test_prefill_q8_kv_split_vs_oracle(fl, dev, orc, rng, T, pos0, split):
     torch.cuda.synchronize()
     want = orc.attention_prefill_q8(qg, kc8, vc8, q_pitch=512, pos0=pos0, max_pos=L, scale=SCALE,
                                     T=T)
-    err, ok = close(z.cpu().numpy(), want, ATOL, RTOL)
+    err, ok = close_rel(z.cpu().numpy(), want, ATOL, RTOL)
     assert ok, f"T={T} pos0={pos0} split={split}: max|err| {err}"

@@ -212,6 +212,30 @@ def test_l2norm_row_layouts(fl, dev, orc, rng, T, rows):
     assert np.array_equal(xi.cpu().numpy().view(np.int16), outs[0].view(np.int16))
 
 
+@pytest.mark.parametrize("n,pitch,rows,T", [(64, 64, 3, 5), (200, 203, 2, 4), (1024, 1024, 1, 3),
+                                             (129, 129, 7, 1)])
+def test_l2norm_other_row_lengths(fl, dev, orc, rng, n, pitch, rows, T):
+    """Row lengths other than 128 (one wavefront a row): within 1 ulp of the
+    oracle's block order (thread v sums x[v], x[v + 128], ...; warp trees;
+    (r0 + r2) + (r1 + r3)), the padding after each row untouched, in place
+    the same bits."""
+    x = (rng.standard_normal((T, rows, pitch)) * 2).astype(np.float16)
+    x[0, 0, :] = 0
+    want = orc.l2norm_scaled(x.reshape(T, rows * pitch), n=n, rows=rows, pitch=pitch, eps=1e-6,
+                             scale=0.75, T=T).reshape(T, rows, pitch)
+    y = torch.full((T, rows, pitch), 7.0, dtype=torch.float16, device=dev)
+    fl.ops.l2norm_scaled(torch.from_numpy(x).to(dev), y, n=n, rows=rows, pitch=pitch, scale=0.75,
+                         T=T)
+    xi = torch.from_numpy(x).to(dev)
+    fl.ops.l2norm_scaled(xi, xi, n=n, rows=rows, pitch=pitch, scale=0.75, T=T)
+    torch.cuda.synchronize()
+    yh = y.cpu().numpy()
+    assert (yh[..., n:] == 7.0).all()
+    assert ulp16_diff(yh[..., :n], want[..., :n]) <= 1
+    assert not yh[0, 0, :n].any()
+    assert np.array_equal(xi.cpu().numpy()[..., :n].view(np.int16), yh[..., :n].view(np.int16))
+
+
 def _scan_inputs(rng, T):
     c = rng.standard_normal((T, ROW)).astype(np.float16)
     ln = np.zeros_like(c)

@@ -12,7 +12,7 @@ import numpy as np
 import pytest
 import torch
 
-from conftest import close, f16, rand_qg
+from conftest import close, close_rel, f16, rand_qg
 from test_oracle_q8 import LOG2E, rand_kv
 
 pytestmark = pytest.mark.gpu
@@ -97,7 +97,7 @@ def test_dec_q8_and_merge_vs_oracle(fl, dev, orc, rng, L, T, tmin, smax):
     opa, opm, opd = orc.attention_dec_q8(qg, kc8, vc8, pos0=pos0, max_pos=max_pos,
                                          sl2=SCALE * LOG2E, tmin=tmin, smax=smax, T=T)
     want = orc.attention_dec_merge(opa, opm, opd, pos0=pos0, tmin=tmin, smax=smax, T=T, gate=qg)
-    err, ok = close(z.cpu().numpy(), want, ATOL, RTOL)
+    err, ok = close_rel(z.cpu().numpy(), want, ATOL, RTOL)
     assert ok, f"L={L} T={T}: max|err| {err}"
     gpa, gpm, gpd = pacc.cpu().numpy(), pm.cpu().numpy(), pd.cpu().numpy()
     for t in range(T):
@@ -158,14 +158,19 @@ def test_decode_q8_batched_vs_single_and_oracle(fl, dev, orc, rng):
         assert torch.equal(zb[b], z1[0]), b
         want = orc.attention_decode_q8(qg[b], caches[b][2], caches[b][3], L - 1, max_pos=caps[b],
                                        scale=SCALE)
-        err, ok = close(zb[b].cpu().numpy(), want, ATOL, RTOL)
+        err, ok = close_rel(zb[b].cpu().numpy(), want, ATOL, RTOL)
         assert ok, f"seq {b} L={L}: {err}"
 
 
-def test_decode_q8_config2_vs_oracle(fl, dev, orc):
-    """Config 2's shape at 8k: B = 4, T = 3 verify rows over int8 caches."""
-    rng = np.random.default_rng(8192)
-    B, T, Lmax = 4, 3, 8192
+@pytest.mark.parametrize("B,T,Lmax", [(4, 3, 8192), (4, 3, 32768), (4, 3, 102400),
+                                      (1, 1, 102400)])
+def test_decode_q8_config2_vs_oracle(fl, dev, orc, B, T, Lmax):
+    """Config 2's shape (B = 4, T = 3 verify rows) over int8 caches at the
+    lengths the bench reports, and one sequence at ~100k (64 splits x 4 kv
+    heads = 256 workgroups: the LDS-staged int8 tiles). Bar: max-abs 2e-3 /
+    rel 1e-2 and max|err| <= 1e-2 max|want|, which rejects one lost split of
+    64 at ~100k (tests/test_parity_bar.py)."""
+    rng = np.random.default_rng(Lmax + B)
     lens = rng.integers(int(0.9 * Lmax), Lmax + 1, size=B)
     caches = [oracle_cache(orc, rng, int(L), int(L)) for L in lens]
     qg = np.stack([rand_qg(rng, T) for _ in range(B)])
@@ -177,7 +182,7 @@ def test_decode_q8_config2_vs_oracle(fl, dev, orc):
     for b in range(B):
         want = orc.attention_decode_q8(qg[b], caches[b][2], caches[b][3], pos0s[b],
                                        max_pos=int(lens[b]), scale=SCALE)
-        err, ok = close(zh[b], want, ATOL, RTOL)
+        err, ok = close_rel(zh[b], want, ATOL, RTOL)
         assert ok, f"seq {b}: {err}"
 
 
@@ -226,7 +231,7 @@ def test_prefill_q8_vs_oracle(fl, dev, orc, rng, T, pos0):
     assert np.array_equal(kd.cpu().numpy(), kc8) and np.array_equal(vd.cpu().numpy(), vc8)
     want = orc.attention_prefill_q8(qg, kc8, vc8, q_pitch=512, pos0=pos0, max_pos=L, scale=SCALE,
                                     T=T)
-    err, ok = close(z.cpu().numpy(), want, ATOL, RTOL)
+    err, ok = close_rel(z.cpu().numpy(), want, ATOL, RTOL)
     assert ok, f"T={T} pos0={pos0}: max|err| {err}"
 
 
@@ -255,7 +260,7 @@ def test_prefill_q8_staged_equals_direct(fl, dev, orc, rng):
                  None)
     torch.cuda.synchronize()
     a, b = z_st.float().cpu().numpy(), z_di.float().cpu().numpy()
-    err, ok = close(a, b, ATOL, RTOL)
+    err, ok = close_rel(a, b, ATOL, RTOL)
     assert ok, f"staged vs direct: max|err| {err}"
 
 
@@ -277,5 +282,5 @@ def test_prefill_q8_config3_sampled_rows(fl, dev, orc, L):
                      *rng.integers(0, L, 4).tolist()}):
         want = orc.attention_exact_q8(q[t:t + 1], kc8, vc8, q_pitch=256, pos0=t, max_pos=L,
                                       scale=1.0, T=1)
-        err, ok = close(zh[t:t + 1], want, ATOL, RTOL)
+        err, ok = close_rel(zh[t:t + 1], want, ATOL, RTOL)
         assert ok, f"L={L} row {t}: max|err| {err}"

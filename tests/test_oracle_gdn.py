@@ -110,15 +110,23 @@ def test_conv_rows_equals_t1_calls(orc, rng, T):
         assert np.array_equal(y1[0], y[t]) and np.array_equal(s, sts[t])
 
 
-def test_l2norm(orc, rng):
-    x = rng.standard_normal((2, 3, 128)).astype(np.float16)
+@pytest.mark.parametrize("n", [128, 64, 200, 1024])
+def test_l2norm(orc, rng, n):
+    """||y|| = scale ||x|| / sqrt(||x||^2 + eps) and each y_i = scale x_i / that
+    denominator in fp64, within fp16 rounding; a zero row gives 0. Row lengths
+    beyond the reference block's 128 threads make each thread sum several
+    elements: a sum that dropped them fails the per-element bound."""
+    x = rng.standard_normal((2, 3, n)).astype(np.float16)
     x[1, 2] = 0
     for scale in (1.0, QS):
-        y = orc.l2norm_scaled(x, n=128, rows=3, pitch=128, eps=1e-6, scale=scale, T=2)
-        xn = np.linalg.norm(x.astype(np.float64), axis=-1)
+        y = orc.l2norm_scaled(x, n=n, rows=3, pitch=n, eps=1e-6, scale=scale, T=2)
+        x64 = x.astype(np.float64)
+        xn = np.linalg.norm(x64, axis=-1)
         yn = np.linalg.norm(y.astype(np.float64), axis=-1)
         want = scale * xn / np.sqrt(xn ** 2 + 1e-6)
         assert np.abs(yn - want).max() < 2e-3 * scale
+        ye = scale * x64 / np.sqrt(xn ** 2 + 1e-6)[..., None]
+        assert np.abs(y.astype(np.float64) - ye).max() <= 2 ** -10 * np.abs(ye).max()
         assert not y[1, 2].any()
 
 
