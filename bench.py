@@ -532,6 +532,86 @@ def bench_chunked(torch, fl, L=8192, iters=1, eager=0):
 
 
 # ---------------------------------------------------------------------------
+# the reference's prefill flow: a prompt in 1024-token sub-chunks, 64 layers
+# ---------------------------------------------------------------------------
+
+class _FlowProj:
+    """The Projections seam for timing: one set of seeded inputs of a chunk's
+    size, handed to every layer (their values do not change the work)."""
+
+    def __init__(self, torch, T, dev, seed=5):
+        g = torch.Generator(device=dev).manual_seed(seed)
+        self.qg = torch.randn((T, 24, 512), generator=g, device=dev).half()
+        self.k = torch.randn((T, 4, 256), generator=g, device=dev).half()
+        self.v = torch.randn((T, 4, 256), generator=g, device=dev).half()
+        self.qkv = torch.randn((T, 10240), generator=g, device=dev).half()
+        self.z = torch.randn((T, 48, 128), generator=g, device=dev).half()
+        self.a = torch.randn((T, 48), generator=g, device=dev)
+        self.b = torch.randn((T, 48), generator=g, device=dev)
+
+    def full_attn_in(self, layer, T):
+        return self.qg[:T], self.k[:T], self.v[:T]
+
+    def gdn_in(self, layer, T):
+        return self.qkv[:T], self.z[:T], self.a[:T], self.b[:T]
+
+    def layer_out(self, layer, out):
+        pass
+
+
+def bench_prefill_flow(torch, fl, L, kv8=True, chunk=1024, reps=3):
+    """The reference's prefill flow for an L-token prompt (the engine's CHUNK
+    of 4096, engine.py:28-31, re-cut by the backend into MAX_CHUNK = 1024
+    sub-chunks at increasing pos0, runtime.py:1939-1966) through the model's
+    64 layers (16 full attention, 48 GDN) on HybridRuntime: per sub-chunk and
+    attention layer the prep, the prefill attention (KV split for chunks deep
+    in the prompt) and the gate; per GDN layer the conv, the q / k L2 norm,
+    the gates, the chunked WY scan and the gated output norm. The KV cache is
+    grown to the prompt once before the timed region (the reference grows
+    once a step); eager launches, timed with HIP events on the launch stream,
+    median of `reps` prompts. Also timed: the 16 attention layers alone and
+    the 48 GDN layers alone. MFMA fraction: the attention's 12288 L (L + 1)
+    FLOPs a layer and the chunked scan's 7.1e10 a layer per 8192 tokens."""
+    rtm = fl.runtime
+    dev = torch.device("cuda:0")
+    proj = _FlowProj(torch, chunk, dev)
+    out = {"config": f"prefill_flow_L{L}" + ("_kv8" if kv8 else ""), "chunk": chunk}
+    scheds = {"all": rtm.LAYER_TYPES, "attn": ("full_attention",) * 16,
+              "gdn": ("linear_attention",) * 48}
+    att_fl = 12288 * L * (L + 1)
+    gdn_fl = -(-L // 64) * 48 * (10 * 64 * 64 * 128 + 6 * 64 * 128 * 128)
+    for name, types in scheds.items():
+        rt = rtm.HybridRuntime(rtm.random_weights(types, seed=2, device=dev), layer_types=types,
+                               kv8=kv8, device=dev)
+        times = []
+        for rep in range(reps + 1):
+            st = rt.new_state()
+            rt.grow(st, L)
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for p0 in range(0, L, chunk):
+                n = min(chunk, L - p0)
+                rt.forward(st, proj, range(p0, p0 + n))
+            e1.record()
+            torch.cuda.synchronize()
+            if rep:
+                times.append(e0.elapsed_time(e1) * 1e3)
+            rt.free_state(st)
+            del st
+        times.sort()
+        us = times[len(times) // 2]
+        fl_n = {"all": 16 * att_fl + 48 * gdn_fl, "attn": 16 * att_fl, "gdn": 48 * gdn_fl}[name]
+        key = "" if name == "all" else name + "_"
+        out[key + "us"] = round(us, 1)
+        out[key + "tok_s"] = round(L / (us * 1e-6))
+        out[key + "mfma_frac"] = round(fl_n / (us * 1e-6) / 1e12 / MFMA_F16_PEAK_TFLOPS, 4)
+        del rt
+        torch.cuda.empty_cache()
+    return out
+
+
+# ---------------------------------------------------------------------------
 # CPU baseline: PyTorch fp32 on the host's cores
 # ---------------------------------------------------------------------------
 
@@ -756,6 +836,9 @@ EXTRA_CONFIGS = {
     "attn_prep_T8192": (bench_attn_prep, {"T": 8192, "iters": 20}),
     "gdn_out_norm_T4": (bench_gdn_out_norm, {"T": 4}),
     "gdn_out_norm_T8192": (bench_gdn_out_norm, {"T": 8192, "iters": 20}),
+    "prefill_flow_L8192_kv8": (bench_prefill_flow, {"L": 8192}),
+    "prefill_flow_L32768_kv8": (bench_prefill_flow, {"L": 32768, "reps": 1}),
+    "prefill_flow_L8192": (bench_prefill_flow, {"L": 8192, "kv8": False}),
 }
 
 

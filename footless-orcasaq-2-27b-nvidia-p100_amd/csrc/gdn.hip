@@ -594,7 +594,7 @@ gdn_decode_kernel(const f16* __restrict__ x, int x_stride, const f16* __restrict
                   int ab_stride, const float* __restrict__ A_log,
                   const float* __restrict__ dt_bias, f16* __restrict__ y, int y_stride,
                   long long ck_step, int T, int n_kheads, int n_vheads, int V, float out_scale,
-                  float l2eps, int group) {
+                  float l2eps, int group, int delay_loads) {
     __shared__ __attribute__((aligned(16))) float ssq[8];   // k's, q's 32-channel sums of squares
     __shared__ __attribute__((aligned(16))) float snorm[2 * GR_K];         // k | q, normalised
     __shared__ float sv[GR_ROWS];   // the rows' v values
@@ -611,7 +611,7 @@ gdn_decode_kernel(const f16* __restrict__ x, int x_stride, const f16* __restrict
     asm volatile("" ::"s"(Sb), "s"(cst_in), "s"(cst_out), "s"(Ck), "s"(pos0), "s"(x), "s"(conv_w),
                  "s"(ga), "s"(gb), "s"(A_log), "s"(dt_bias), "s"(x_stride), "s"(ab_stride), "s"(T),
                  "s"(n_kheads), "s"(V), "s"(group), "s"(y), "s"(y_stride), "s"(out_scale),
-                 "s"(l2eps), "s"(ck_step));
+                 "s"(l2eps), "s"(ck_step), "s"(delay_loads));
     __builtin_amdgcn_sched_barrier(0);
     const int hk = hv / group;
     const int tid = threadIdx.x, lane = tid & 63;
@@ -645,13 +645,12 @@ gdn_decode_kernel(const f16* __restrict__ x, int x_stride, const f16* __restrict
     const float dtb = dt_bias[hv + vz], A = A_log[hv + vz];
     const size_t ab0 = (size_t)b * T * ab_stride + hv + vz;
     const float ga0 = ga[ab0], gb0 = gb[ab0];
-    // The state loads wait ~512 clocks behind the small loads above. The grid's
-    // 768 workgroups (B = 4) are dispatched over ~0.3 us; issued at once, the
-    // first workgroups' state reads (16 KiB each) queue ahead of the later
-    // ones' conv inputs, which head the chain to every store. Measured over
-    // s_sleep 4..16 at B = 4: 8 and 9 best (6.45 -> 6.25 us a step). Small
-    // grids do not wait.
-    if (gridDim.x * gridDim.y * gridDim.z >= 512) __builtin_amdgcn_s_sleep(8);
+    // The state loads wait ~512 clocks behind the small loads above when the
+    // host asks (delay_loads: grids of 2 to 3 workgroups a CU, all resident and
+    // dispatched at once): issued at once, the first workgroups' state reads
+    // (16 KiB each) queue ahead of the later ones' conv inputs, which head the
+    // chain to every store. Measured at s_sleep 4..16 (B = 4): 8 and 9 best.
+    if (delay_loads) __builtin_amdgcn_s_sleep(8);
     __builtin_amdgcn_sched_barrier(0);
     float reg[16];
     load_row16_nt(reg, Srow);
@@ -885,6 +884,21 @@ l2norm_rows_kernel(const f16* __restrict__ x, f16* __restrict__ y, int rows, int
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
+// The current device's compute-unit count, looked up once per device.
+int gdn_cu_count() {
+    static int cached[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cached[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            n <= 0)
+            n = 256;
+        cached[dev] = n;
+    }
+    return cached[dev];
+}
+
 }  // namespace
 
 extern "C" {
@@ -1045,16 +1059,23 @@ int fl_gdn_decode(const void* x, int x_stride, int conv_fused, const void* conv_
         }
     }
     const dim3 grid(V / GR_ROWS, n_vheads, B);
+    // the state loads held behind the small ones for grids of 2 to 3
+    // workgroups a CU (B = 3, 4 at 48 v heads on 256 CUs: 5.96 / 6.33 us a
+    // step against 6.07 / 6.63 without); beyond that the delay costs (B = 5..8:
+    // ~0.1 us a step), below it changes nothing
+    const long long wgs = (long long)grid.x * grid.y * grid.z;
+    const int cus = gdn_cu_count();
+    const int delay = wgs >= 2LL * cus && wgs <= 3LL * cus;
     if (conv_fused)
         hipLaunchKernelGGL(gdn_decode_kernel<true>, grid, dim3(GR_THREADS), 0, (hipStream_t)stream,
                            (const f16*)x, x_stride, (const f16*)conv_w, seqs, a, b, ab_stride,
                            A_log, dt_bias, (f16*)y, y_stride, ck_step, T, n_kheads, n_vheads, V,
-                           out_scale, l2eps, n_vheads / n_kheads);
+                           out_scale, l2eps, n_vheads / n_kheads, delay);
     else
         hipLaunchKernelGGL(gdn_decode_kernel<false>, grid, dim3(GR_THREADS), 0,
                            (hipStream_t)stream, (const f16*)x, x_stride, (const f16*)conv_w, seqs,
                            a, b, ab_stride, A_log, dt_bias, (f16*)y, y_stride, ck_step, T,
-                           n_kheads, n_vheads, V, out_scale, l2eps, n_vheads / n_kheads);
+                           n_kheads, n_vheads, V, out_scale, l2eps, n_vheads / n_kheads, delay);
     return fl::check_launch("gdn_decode");
 }
 

@@ -214,7 +214,7 @@ class HybridRuntime:
                 self._kv_copy(k, cap, st.kk[li], old, old)
                 self._kv_copy(v, cap, st.kv[li], old, old)
             st.kk[li], st.kv[li], st.lcap[li] = k, v, cap
-        st.cap = min(st.lcap)
+        st.cap = min(st.lcap) if st.lcap else cap   # a schedule without attention layers
 
     def clone_state(self, st: SeqState) -> SeqState:
         c = SeqState()
