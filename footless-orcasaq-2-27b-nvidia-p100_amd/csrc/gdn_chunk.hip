@@ -211,9 +211,10 @@ __device__ __forceinline__ float wave_prefix_sum(float v) {
     return v;
 }
 
-// One workgroup of 4 waves a (chunk, k head): K and Q are loaded and K K^T,
-// Q K^T formed once, then each v head of the group in turn gets its A, T and
-// M o QK^T from them with its own gates.
+// One workgroup of 4 waves a (chunk, v head), a grid of chunks x v heads: it
+// loads its k head's K and Q rows of the chunk, forms K K^T and Q K^T (wave w
+// the 32 x 32 block (w / 2, w % 2)), then its v head's A, T and M o QK^T from
+// them with that head's gates, into the head's block of the workspace.
 __global__ void __launch_bounds__(256)
 chunk_prep_kernel(const f16* __restrict__ q, const f16* __restrict__ k,
                   const float* __restrict__ beta, const float* __restrict__ decay, int T,
