@@ -76,18 +76,21 @@ class GpuProj:
 
 
 class OracleStack:
-    """The same layers on the CPU oracle, one sequence."""
+    """The same layers on the CPU oracle, one sequence; kv8: int8 caches (the
+    reference's attn_prep_q8 and int8 attention, runtime.py:2907-2959)."""
 
-    def __init__(self, orc, rt, cap):
-        self.orc, self.rt, self.cap = orc, rt, cap
+    def __init__(self, orc, rt, cap, kv8=False):
+        self.orc, self.rt, self.cap, self.kv8 = orc, rt, cap, kv8
         self.w = {i: tuple(_np(t) for t in (w.q_norm, w.k_norm)) if i in rt.full_ord else
                   tuple(_np(t) for t in (w.conv_w, w.A_log, w.dt_bias, w.norm_w))
                   for i, w in rt.w.items()}
         self.S = {g: np.zeros((48, 128, 128), np.float32) for g in rt.gdn_ord.values()}
         self.conv = {g: [np.zeros((10240, 3), np.float16) for _ in range(2)]
                      for g in rt.gdn_ord.values()}
-        self.kc = {li: np.zeros((cap, 4, 256), np.float16) for li in rt.full_ord.values()}
-        self.vc = {li: np.zeros((cap, 4, 256), np.float16) for li in rt.full_ord.values()}
+        buf = (lambda: orc.kv8_buffer(cap)) if kv8 else \
+            (lambda: np.zeros((cap, 4, 256), np.float16))
+        self.kc = {li: buf() for li in rt.full_ord.values()}
+        self.vc = {li: buf() for li in rt.full_ord.values()}
         self.n, self.phase = 0, 0
 
     def step(self, inp):
@@ -97,14 +100,17 @@ class OracleStack:
                 li = self.rt.full_ord[i]
                 qg, k, v = (a.copy() for a in inp.d[i])
                 wq, wk = self.w[i]
-                qr, _ = orc.attn_prep(qg, k, v, wq, wk, self.kc[li], self.vc[li], pos0=pos0, T=T,
-                                      max_pos=self.cap)
+                prep = orc.attn_prep_q8 if self.kv8 else orc.attn_prep
+                qr, _ = prep(qg, k, v, wq, wk, self.kc[li], self.vc[li], pos0=pos0, T=T,
+                             max_pos=self.cap)
                 if T <= 4:
-                    z = orc.attention_decode(qr, self.kc[li], self.vc[li], pos0,
-                                             max_pos=self.cap, scale=ATTN_SCALE)
+                    dec = orc.attention_decode_q8 if self.kv8 else orc.attention_decode
+                    z = dec(qr, self.kc[li], self.vc[li], pos0, max_pos=self.cap,
+                            scale=ATTN_SCALE)
                 else:
-                    z = orc.attention_prefill(qr, self.kc[li], self.vc[li], q_pitch=512,
-                                              pos0=pos0, max_pos=self.cap, scale=ATTN_SCALE, T=T)
+                    pre = orc.attention_prefill_q8 if self.kv8 else orc.attention_prefill
+                    z = pre(qr, self.kc[li], self.vc[li], q_pitch=512, pos0=pos0,
+                            max_pos=self.cap, scale=ATTN_SCALE, T=T)
                     orc.attn_gate(z, qr, 24, 256, 256, 512, 256, T)
                 out[i] = z
             else:
@@ -148,8 +154,15 @@ def _check_state(rt, st, ref, what):
     n = len(st.tokens)
     assert n == ref.n
     for li in ref.kc:
-        assert np.array_equal(_np(st.kk[li][:n]), ref.kc[li][:n]), f"{what}: K of layer {li}"
-        assert np.array_equal(_np(st.kv[li][:n]), ref.vc[li][:n]), f"{what}: V of layer {li}"
+        for name, got, want in (("K", st.kk[li], ref.kc[li]), ("V", st.kv[li], ref.vc[li])):
+            if ref.kv8:   # values and block scales, each buffer at its own capacity
+                gv, gs = ref.orc.kv8_split(_np(got), st.lcap[li])
+                wv, ws = ref.orc.kv8_split(want, ref.cap)
+                same = np.array_equal(gv[:n], wv[:n]) and \
+                    np.array_equal(gs[:n].view(np.int16), ws[:n].view(np.int16))
+            else:
+                same = np.array_equal(_np(got[:n]), want[:n])
+            assert same, f"{what}: {name} of layer {li}"
     print(f"{what}: {n} positions, state rel {worst:.2e}")
 
 
@@ -203,6 +216,39 @@ def test_runtime_stack_prefill_decode_verify(fl, dev, orc):
     torch.cuda.synchronize()
     _check_outputs(p.out, ref.step(inp), "decode after reject")
     _check_state(rt, st, ref, "final")
+
+
+@pytest.mark.parametrize("kv8", [False, True])
+def test_runtime_stack_continuation_prefill(fl, dev, orc, kv8):
+    """A prompt fed as two prefills, the reference's sub-chunked prompt in
+    small (runtime.py:1939-1966): 40 tokens, then 200 at pos0 40 -- the GDN
+    layers' chunked scan over chunks of 64 + 64 + 64 + 8 from the state the
+    first call left, the conv ring carried across the calls; the attention
+    layers' prefill over the 40 rows already cached -- then two decode steps,
+    each against the oracle stack. fp16 and int8 caches; the runtime's caches
+    grow from 64 to 256 positions between the calls (int8: values and scales
+    moved as two regions)."""
+    rt_mod = fl.runtime
+    rt = rt_mod.HybridRuntime(rt_mod.random_weights(seed=7), device=dev, kv8=kv8)
+    st = rt.new_state()
+    ref = OracleStack(orc, rt, cap=256, kv8=kv8)
+    types = rt.layer_types
+    for T, seed, what in ((40, 60, "prefill 40"), (200, 61, "prefill 200 at pos0 40")):
+        inp = Inputs(types, T, seed=seed)
+        p = GpuProj(inp, dev)
+        pos = len(st.tokens)
+        rt.forward(st, p, list(range(pos, pos + T)))
+        torch.cuda.synchronize()
+        _check_outputs(p.out, ref.step(inp), what)
+        _check_state(rt, st, ref, what)
+    assert min(st.lcap) == 256
+    for s in range(2):
+        inp = Inputs(types, 1, seed=62 + s)
+        p = GpuProj(inp, dev)
+        rt.forward(st, p, [600 + s])
+        torch.cuda.synchronize()
+        _check_outputs(p.out, ref.step(inp), f"decode {s}")
+    _check_state(rt, st, ref, "after decode")
 
 
 @pytest.mark.parametrize("kv8", [False, True])
