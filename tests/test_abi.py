@@ -32,6 +32,30 @@ def test_library_exports_every_declared_symbol(fl):
     assert set(declared_entry_points()) <= set(fl._lib.SIGNATURES)
 
 
+def test_op_layer_fails_loudly_without_the_library(tmp_path):
+    """With libfl355.so absent the op layer raises instead of computing
+    anything another way (there is no CPU path), in a fresh process so the
+    library this session loaded stays in place."""
+    import subprocess
+    import sys
+    code = (
+        "import sys; from pathlib import Path\n"
+        f"sys.path.insert(0, {str(REPO)!r})\n"
+        "import __graft_entry__ as ge\n"
+        "fl = ge.load_package()\n"
+        "fl._lib._lib = None\n"
+        f"fl._lib.LIB_PATH = Path({str(tmp_path / 'absent.so')!r})\n"
+        "try:\n"
+        "    fl.ops.prefill_split_count(1024, 98000)\n"
+        "except ImportError as e:\n"
+        "    print('raised:', e)\n"
+        "    sys.exit(0)\n"
+        "sys.exit(3)\n")
+    r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert "absent.so is missing" in r.stdout
+
+
 def test_status_strings(fl):
     lib = fl._lib.lib()
     assert lib.fl_abi_version() == 1
