@@ -122,6 +122,11 @@ __device__ __forceinline__ float pow2_scale(float m, float& inv) {
     return __uint_as_float((uint32_t)se << 23);
 }
 
+// 1 / x for a power of two x = 2^e with -126 <= e <= 126, exactly
+__device__ __forceinline__ float pow2_inv(float x) {
+    return __uint_as_float((254u - (__float_as_uint(x) >> 23)) << 23);
+}
+
 // x s = hi + lo, both fp16 (round to nearest), for two values into packed
 // halves: v_fma_mix rounds x s (exact: s is a power of two) and x s - hi
 // (exact in fp32: hi is x s to 11 bits) to fp16 once each, reading hi back as
@@ -799,7 +804,17 @@ __device__ __forceinline__ void cs_output_wave(const f16* q, const f16* k, const
 #pragma unroll
             for (int r = 0; r < 4; ++r) mo = fmaxf(mo, fabsf(dl[mb][r]));
         float o_inv;
-        const float o_sc = pow2_scale<7>(col_max(mo), o_inv);
+        float o_sc = pow2_scale<7>(col_max(mo), o_inv);
+        // o_up below brings e^g Q S0^T into the accumulator's scale. Chosen
+        // from Delta alone, that scale overflows it for a zero (or nearly
+        // zero) Delta row -- a chunk with beta = 0 throughout -- or a zero M o
+        // QK^T block (2^-kappa = 2^-126): at most 2^64 2^-kappa, where
+        // Delta's own term is below 2^-40 of y
+        const float o_cap = 0x1p64f * sc[2];
+        if (o_sc > o_cap) {
+            o_sc = o_cap;
+            o_inv = pow2_inv(o_cap);
+        }
         f16x8 oh[2], ol[2];
 #pragma unroll
         for (int kq = 0; kq < 2; ++kq) split8(dl[2 * kq], dl[2 * kq + 1], o_sc, oh[kq], ol[kq]);

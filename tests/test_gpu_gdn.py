@@ -426,6 +426,32 @@ def test_chunked_vs_recurrence(fl, dev, orc, T):
     assert beyond <= 1.5e-3, f"T={T}: y error against the row RMS {beyond:.2e}"
 
 
+def test_chunked_degenerate_chunks_vs_recurrence(fl, dev, orc):
+    """Chunks whose operands vanish: tokens 64-127 with q = 0 (their M o QK^T
+    block is zero) and tokens 192-255 with beta = 0 (their Delta is zero):
+    the output's accumulator scale, chosen from Delta, once overflowed there
+    and saturated y. Against the oracle's recurrence, as the other chunked
+    cases."""
+    T = 300
+    rng = np.random.default_rng(300)
+    ln, beta, decay, S0 = _scan_inputs(rng, T)
+    ln[64:128, :2048] = 0
+    beta[192:256] = 0
+    lnd = to_dev(ln, dev)
+    S = to_dev(S0, dev)
+    y = fl.ops.gdn_prefill_chunked(lnd[:, :2048], lnd[:, 2048:4096], lnd[:, 4096:],
+                                   to_dev(beta, dev), to_dev(decay, dev), S, T=T)
+    torch.cuda.synchronize()
+    S_r = S0.copy()
+    y_r = orc.gdn_scan(ln[:, :2048], ln[:, 2048:4096], ln[:, 4096:], beta, decay, S_r, T=T,
+                       qk_stride=ROW, v_stride=ROW, out_scale=QS)
+    assert rel_err(S.cpu().numpy(), S_r) <= STATE_RTOL
+    yh = y.cpu().numpy()
+    assert np.isfinite(yh.astype(np.float32)).all()
+    err, ok = close(yh, y_r, 2e-3, 1e-2)
+    assert ok, f"max|dy| {err}"
+
+
 # the 16-lanes-a-row kernel takes calls of >= 8192 rows with 16-byte aligned
 # rows: 171 x 48 = 8208 and 8193 x 1 rows reach it with a ragged last wave
 # (8208 % 16 == 0 but 8193 % 16 == 1; 8211 = 1173 x 7 leaves 3 rows in the last
