@@ -452,6 +452,75 @@ def test_chunked_degenerate_chunks_vs_recurrence(fl, dev, orc):
     assert ok, f"max|dy| {err}"
 
 
+@pytest.mark.parametrize("regime", ["strong", "none", "mixed"])
+def test_scans_extreme_decay_vs_recurrence(fl, dev, orc, regime):
+    """Decay at its ends, for the recurrent and the chunked scan against the
+    oracle's recurrence over 200 tokens: 'strong' ~e^-12 a token (the in-chunk
+    ratios e^{g_i - g_j} underflow to 0 after a few tokens and the state is
+    all but erased every step), 'none' exactly 1, 'mixed' alternating heads of
+    the two with beta also at 0 and 1 for some tokens."""
+    T = 200
+    rng = np.random.default_rng({"strong": 11, "none": 12, "mixed": 13}[regime])
+    ln, beta, decay, S0 = _scan_inputs(rng, T)
+    if regime == "strong":
+        decay[:] = np.exp(-rng.uniform(10, 14, decay.shape)).astype(np.float32)
+    elif regime == "none":
+        decay[:] = 1.0
+    else:
+        decay[:, 0::2] = np.exp(-rng.uniform(10, 14, decay[:, 0::2].shape)).astype(np.float32)
+        decay[:, 1::2] = 1.0
+        beta[::7] = 0.0
+        beta[3::11] = 1.0
+    S_r = S0.copy()
+    y_r = orc.gdn_scan(ln[:, :2048], ln[:, 2048:4096], ln[:, 4096:], beta, decay, S_r, T=T,
+                       qk_stride=ROW, v_stride=ROW, out_scale=QS)
+    lnd = to_dev(ln, dev)
+    for form in ("recurrent", "chunked"):
+        S = to_dev(S0, dev)
+        if form == "recurrent":
+            y = torch.empty((T, NV * 128), dtype=torch.float16, device=dev)
+            fl.ops.gdn_scan(lnd[:, :2048], lnd[:, 2048:4096], lnd[:, 4096:], to_dev(beta, dev),
+                            to_dev(decay, dev), S, y, T=T)
+        else:
+            y = fl.ops.gdn_prefill_chunked(lnd[:, :2048], lnd[:, 2048:4096], lnd[:, 4096:],
+                                           to_dev(beta, dev), to_dev(decay, dev), S, T=T)
+        torch.cuda.synchronize()
+        yh, Sh = y.cpu().numpy(), S.cpu().numpy()
+        assert np.isfinite(yh.astype(np.float32)).all() and np.isfinite(Sh).all(), form
+        assert rel_err(Sh, S_r) <= STATE_RTOL, f"{regime} {form}: state rel {rel_err(Sh, S_r):.2e}"
+        err, ok = close(yh, y_r, 2e-3, 1e-2)
+        assert ok, f"{regime} {form}: max|dy| {err}"
+
+
+def test_decode_beta_zero_is_pure_decay(fl, dev, rng):
+    """Config 1's shape (B = 4, 48 v heads, conv fused) with b = -1000, so
+    beta = 1 / (1 + e^1000) = 0 exactly: every state is decay * S_0 (one fp32
+    product, bit for bit) with decay the gates kernel's value for the same
+    inputs."""
+    B = 4
+    w, A_log, dt = _decode_weights(rng)
+    S0 = (rng.standard_normal((B, NV, 128, 128)) * 0.02).astype(np.float32)
+    S_d = [to_dev(S0[b], dev) for b in range(B)]
+    x = rng.standard_normal((B, 1, ROW)).astype(np.float16)
+    a = rng.standard_normal((B, 1, NV)).astype(np.float32)
+    bb = np.full((B, 1, NV), -1000.0, np.float32)
+    rings = [[torch.zeros((ROW, 3), dtype=torch.float16, device=dev) for _ in range(2)]
+             for _ in range(B)]
+    fl.ops.gdn_decode(to_dev(x, dev), S_d, to_dev(a, dev), to_dev(bb, dev), to_dev(A_log, dev),
+                      to_dev(dt, dev), T=1, pos0s=[5] * B, conv_fused=True, conv_w=to_dev(w, dev),
+                      cst_in=[r[0] for r in rings], cst_out=[r[1] for r in rings])
+    beta = torch.empty((B, NV), dtype=torch.float32, device=dev)
+    decay = torch.empty_like(beta)
+    fl.ops.gdn_scalars(to_dev(a[:, 0], dev), to_dev(bb[:, 0], dev), to_dev(A_log, dev),
+                       to_dev(dt, dev), beta, decay, T=B)
+    torch.cuda.synchronize()
+    assert not beta.cpu().numpy().any()
+    dh = decay.cpu().numpy()
+    for b in range(B):
+        want = (dh[b][:, None, None] * S0[b]).astype(np.float32)
+        assert np.array_equal(S_d[b].cpu().numpy(), want), f"sequence {b}"
+
+
 # the 16-lanes-a-row kernel takes calls of >= 8192 rows with 16-byte aligned
 # rows: 171 x 48 = 8208 and 8193 x 1 rows reach it with a ragged last wave
 # (8208 % 16 == 0 but 8193 % 16 == 1; 8211 = 1173 x 7 leaves 3 rows in the last
