@@ -440,6 +440,44 @@ def test_prefill_kv_split_chunk_deep_in_prompt(fl, dev):
         assert float(err.max()) <= 1e-2 * scale_out, name
 
 
+@pytest.mark.parametrize("kind", ["decode", "decode_q8", "prefill", "prefill_split"])
+def test_peaked_scores_vs_oracle(fl, dev, orc, rng, kind):
+    """Scores of std ~30 (q ~ N(0,1) x 2 at scale 1/16): every row's softmax is
+    dominated by a few keys, its running max moves by far more than the lazy
+    rescale's 2^8 threshold several times, and P spans the whole fp16 range.
+    Decode / verify (fp16 and int8 caches) and the causal prefill, unsplit and
+    KV-split, against the oracle, to the attention bar and 1e-2 max|want|."""
+    from test_gpu_q8 import oracle_cache
+
+    L, T = 2000, 3 if kind.startswith("decode") else 200
+    pos0 = L - T
+    if kind == "decode_q8":
+        k, v, kc8, vc8 = oracle_cache(orc, rng, L, L)
+    else:
+        k, v = rand_cache(rng, L)
+    qg = rand_qg(rng, T, q_scale=2.0)
+    if kind == "decode":
+        z = fl.ops.attn_decode(to_dev(qg[None], dev), [to_dev(k, dev)], [to_dev(v, dev)],
+                               [pos0])[0]
+        want = orc.attention_decode(qg, k, v, pos0, max_pos=L, scale=SCALE)
+    elif kind == "decode_q8":
+        kd, vd = fl.ops.kv8_cache(L), fl.ops.kv8_cache(L)
+        fl.ops.kv_store_q8(to_dev(k, dev), to_dev(v, dev), kd, vd, pos0=0, max_pos=L)
+        z = fl.ops.attn_decode_q8(to_dev(qg[None], dev), [kd], [vd], [pos0], [L])[0]
+        want = orc.attention_decode_q8(qg, kc8, vc8, pos0, max_pos=L, scale=SCALE)
+    else:
+        split = 4 if kind == "prefill_split" else 1
+        z = fl.ops.attention_prefill(to_dev(qg, dev), to_dev(k, dev), to_dev(v, dev),
+                                     pos0=pos0, split=split)
+        want = orc.attention_prefill(qg, k, v, q_pitch=512, pos0=pos0, max_pos=L, scale=SCALE,
+                                     T=T)
+    torch.cuda.synchronize()
+    zh = z.cpu().numpy()
+    assert np.isfinite(zh.astype(np.float32)).all()
+    err, ok = close_rel(zh, want, ATOL, RTOL)
+    assert ok, f"{kind}: max|err| {err}"
+
+
 @pytest.mark.parametrize("T,pos0,split", [(200, 700, 3), (64, 100, 6)])
 def test_prefill_q8_kv_split_vs_oracle(fl, dev, orc, rng, T, pos0, split):
     """The KV split over the int8 cache (attention_prefill_fh_q8 with
