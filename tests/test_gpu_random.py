@@ -1,0 +1,153 @@
+"""Seeded random shapes through the HIP path against the oracle: the shapes a
+hand-picked list misses (ragged lengths, one-row contexts, capacities beyond
+the length, batches of up to 10 sequences at unrelated positions, forced KV
+splits from 1 to 9, verify rows 1..5, scan lengths 1..300). Each case prints
+its shape before it runs, and every comparison uses the attention bar with the
+relative-to-max check, the state bar for the scans."""
+import numpy as np
+import pytest
+import torch
+
+from conftest import close, close_rel, rand_cache, rand_qg
+
+pytestmark = pytest.mark.gpu
+
+SCALE = 256 ** -0.5
+QS = 128 ** -0.5
+ATOL, RTOL = 2e-3, 1e-2
+ROW, NV = 10240, 48
+
+
+def to_dev(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_random_decode_batches(fl, dev, orc, seed):
+    rng = np.random.default_rng(1000 + seed)
+    for case in range(4):
+        B = int(rng.integers(1, 11))
+        T = int(rng.integers(1, 6))
+        lens = [int(x) for x in rng.integers(T, 3001, size=B)]
+        caps = [L + int(rng.integers(0, 41)) for L in lens]
+        print(f"seed {seed} case {case}: B={B} T={T} lens={lens}", flush=True)
+        caches = [rand_cache(rng, cap) for cap in caps]
+        qg = np.stack([rand_qg(rng, T, q_scale=float(rng.choice([1 / 16, 0.5]))) for _ in range(B)])
+        pos0s = [L - T for L in lens]
+        z = fl.ops.attn_decode(to_dev(qg, dev), [to_dev(c[0], dev) for c in caches],
+                               [to_dev(c[1], dev) for c in caches], pos0s)
+        torch.cuda.synchronize()
+        zh = z.cpu().numpy()
+        for b in range(B):
+            want = orc.attention_decode(qg[b], caches[b][0], caches[b][1], pos0s[b],
+                                        max_pos=caps[b], scale=SCALE)
+            err, ok = close_rel(zh[b], want, ATOL, RTOL)
+            assert ok, f"seed {seed} case {case} sequence {b}: max|err| {err}"
+
+
+@pytest.mark.parametrize("seed", range(3))
+def test_random_decode_q8_batches(fl, dev, orc, seed):
+    from test_gpu_q8 import oracle_cache
+
+    rng = np.random.default_rng(2000 + seed)
+    for case in range(3):
+        B = int(rng.integers(1, 9))
+        T = int(rng.integers(1, 6))
+        lens = [int(x) for x in rng.integers(T, 3001, size=B)]
+        caps = [L + int(rng.integers(0, 41)) for L in lens]
+        print(f"seed {seed} case {case}: B={B} T={T} lens={lens}", flush=True)
+        caches = [oracle_cache(orc, rng, L, cap) for L, cap in zip(lens, caps)]
+        qg = np.stack([rand_qg(rng, T) for _ in range(B)])
+        pos0s = [L - T for L in lens]
+        kd, vd = [], []
+        for (k, v, _, _), L, cap in zip(caches, lens, caps):
+            a, b_ = fl.ops.kv8_cache(cap), fl.ops.kv8_cache(cap)
+            fl.ops.kv_store_q8(to_dev(k, dev), to_dev(v, dev), a, b_, pos0=0, max_pos=cap)
+            kd.append(a), vd.append(b_)
+        z = fl.ops.attn_decode_q8(to_dev(qg, dev), kd, vd, pos0s, caps)
+        torch.cuda.synchronize()
+        zh = z.cpu().numpy()
+        for b in range(B):
+            want = orc.attention_decode_q8(qg[b], caches[b][2], caches[b][3], pos0s[b],
+                                           max_pos=caps[b], scale=SCALE)
+            err, ok = close_rel(zh[b], want, ATOL, RTOL)
+            assert ok, f"seed {seed} case {case} sequence {b}: max|err| {err}"
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_random_prefill(fl, dev, orc, seed):
+    rng = np.random.default_rng(3000 + seed)
+    for case in range(4):
+        T = int(rng.integers(1, 301))
+        pos0 = int(rng.integers(0, 2001))
+        cap = pos0 + T + int(rng.integers(0, 33))
+        split = [None, 1, int(rng.integers(2, 10))][int(rng.integers(0, 3))]
+        print(f"seed {seed} case {case}: T={T} pos0={pos0} cap={cap} split={split}", flush=True)
+        k, v = rand_cache(rng, cap)
+        qg = rand_qg(rng, T, q_scale=float(rng.choice([1 / 16, 0.5])))
+        z = fl.ops.attention_prefill(to_dev(qg, dev), to_dev(k, dev), to_dev(v, dev), pos0=pos0,
+                                     split=split)
+        torch.cuda.synchronize()
+        want = orc.attention_prefill(qg, k, v, q_pitch=512, pos0=pos0, max_pos=cap, scale=SCALE,
+                                     T=T)
+        err, ok = close_rel(z.cpu().numpy(), want, ATOL, RTOL)
+        assert ok, f"seed {seed} case {case}: max|err| {err}"
+
+
+@pytest.mark.parametrize("seed", range(2))
+def test_random_prefill_q8(fl, dev, orc, seed):
+    from test_gpu_q8 import oracle_cache
+
+    rng = np.random.default_rng(4000 + seed)
+    for case in range(3):
+        T = int(rng.integers(1, 301))
+        pos0 = int(rng.integers(0, 2001))
+        cap = pos0 + T + int(rng.integers(0, 33))
+        split = [None, 1, int(rng.integers(2, 10))][int(rng.integers(0, 3))]
+        print(f"seed {seed} case {case}: T={T} pos0={pos0} cap={cap} split={split}", flush=True)
+        k, v, kc8, vc8 = oracle_cache(orc, rng, pos0 + T, cap)
+        qg = rand_qg(rng, T)
+        kd, vd = fl.ops.kv8_cache(cap), fl.ops.kv8_cache(cap)
+        fl.ops.kv_store_q8(to_dev(k, dev), to_dev(v, dev), kd, vd, pos0=0, max_pos=cap)
+        z = fl.ops.attention_prefill_q8(to_dev(qg, dev), kd, vd, pos0=pos0, max_pos=cap,
+                                        split=split)
+        torch.cuda.synchronize()
+        want = orc.attention_prefill_q8(qg, kc8, vc8, q_pitch=512, pos0=pos0, max_pos=cap,
+                                        scale=SCALE, T=T)
+        err, ok = close_rel(z.cpu().numpy(), want, ATOL, RTOL)
+        assert ok, f"seed {seed} case {case}: max|err| {err}"
+
+
+@pytest.mark.parametrize("seed", range(3))
+def test_random_scans(fl, dev, orc, seed):
+    rng = np.random.default_rng(5000 + seed)
+    for case in range(3):
+        T = int(rng.integers(1, 301))
+        print(f"seed {seed} case {case}: T={T}", flush=True)
+        c = rng.standard_normal((T, ROW)).astype(np.float16)
+        ln = c.copy()
+        qk = c[:, :4096].astype(np.float64).reshape(T, 32, 128)
+        ln[:, :4096] = (qk / np.linalg.norm(qk, axis=-1, keepdims=True)).reshape(T, 4096)
+        beta = (1 / (1 + np.exp(-rng.standard_normal((T, NV)) * 2))).astype(np.float32)
+        decay = np.exp(-np.log1p(np.exp(rng.standard_normal((T, NV)) * 2))).astype(np.float32)
+        S0 = (rng.standard_normal((NV, 128, 128)) * float(rng.choice([0.0, 0.02, 0.5]))).astype(
+            np.float32)
+        S_r = S0.copy()
+        y_r = orc.gdn_scan(ln[:, :2048], ln[:, 2048:4096], ln[:, 4096:], beta, decay, S_r, T=T,
+                           qk_stride=ROW, v_stride=ROW, out_scale=QS)
+        lnd = to_dev(ln, dev)
+        for form in ("recurrent", "chunked"):
+            S = to_dev(S0, dev)
+            if form == "recurrent":
+                y = torch.empty((T, NV * 128), dtype=torch.float16, device=dev)
+                fl.ops.gdn_scan(lnd[:, :2048], lnd[:, 2048:4096], lnd[:, 4096:],
+                                to_dev(beta, dev), to_dev(decay, dev), S, y, T=T)
+            else:
+                y = fl.ops.gdn_prefill_chunked(lnd[:, :2048], lnd[:, 2048:4096], lnd[:, 4096:],
+                                               to_dev(beta, dev), to_dev(decay, dev), S, T=T)
+            torch.cuda.synchronize()
+            Sh = S.cpu().numpy().astype(np.float64)
+            rel = float(np.abs(Sh - S_r).max() / max(np.abs(S_r).max(), 1e-30))
+            assert rel <= 1e-4, f"seed {seed} case {case} {form}: state rel {rel:.2e}"
+            err, ok = close(y.cpu().numpy(), y_r, ATOL, RTOL)
+            assert ok, f"seed {seed} case {case} {form}: max|dy| {err}"
