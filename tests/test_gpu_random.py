@@ -1,7 +1,8 @@
 """Seeded random shapes through the HIP path against the oracle: the shapes a
 hand-picked list misses (ragged lengths, one-row contexts, capacities beyond
 the length, batches of up to 10 sequences at unrelated positions, forced KV
-splits from 1 to 9, verify rows 1..5, scan lengths 1..300). Each case prints
+splits from 1 to 9, verify rows 1..5, scan lengths 1..300, GDN decode batches
+of up to 12 with the conv fused or verify rows with checkpoints). Each case prints
 its shape before it runs, and every comparison uses the attention bar with the
 relative-to-max check, the state bar for the scans."""
 import numpy as np
@@ -151,3 +152,65 @@ def test_random_scans(fl, dev, orc, seed):
             assert rel <= 1e-4, f"seed {seed} case {case} {form}: state rel {rel:.2e}"
             err, ok = close(y.cpu().numpy(), y_r, ATOL, RTOL)
             assert ok, f"seed {seed} case {case} {form}: max|dy| {err}"
+
+
+@pytest.mark.parametrize("seed", range(3))
+def test_random_gdn_decode(fl, dev, orc, seed):
+    """The fused GDN decode over random batches: T = 1 with the conv fused
+    (the plain decode step) or T = 2..3 verify rows after the conv rows, with
+    checkpoints, at random positions and gates, each sequence against the
+    oracle."""
+    rng = np.random.default_rng(6000 + seed)
+    for case in range(3):
+        B = int(rng.integers(1, 13))
+        T = int(rng.integers(1, 4))
+        pos0s = [int(x) for x in rng.integers(0, 5000, size=B)]
+        print(f"seed {seed} case {case}: B={B} T={T} pos0s={pos0s}", flush=True)
+        w = (rng.standard_normal((ROW, 4)) * 0.5).astype(np.float16)
+        A_log = (rng.standard_normal(NV) * 0.3).astype(np.float32)
+        dt = (rng.standard_normal(NV) * 0.3).astype(np.float32)
+        x = rng.standard_normal((B, T, ROW)).astype(np.float16)
+        a = rng.standard_normal((B, T, NV)).astype(np.float32)
+        bb = rng.standard_normal((B, T, NV)).astype(np.float32)
+        S0 = (rng.standard_normal((B, NV, 128, 128)) * 0.02).astype(np.float32)
+        st = rng.standard_normal((B, ROW, 3)).astype(np.float16)
+        S_d = [to_dev(S0[b], dev) for b in range(B)]
+        wd, Ad, dtd = to_dev(w, dev), to_dev(A_log, dev), to_dev(dt, dev)
+        if T == 1:
+            rin = [to_dev(st[b], dev) for b in range(B)]
+            rout = [torch.empty((ROW, 3), dtype=torch.float16, device=dev) for _ in range(B)]
+            y = fl.ops.gdn_decode(to_dev(x, dev), S_d, to_dev(a, dev), to_dev(bb, dev), Ad, dtd,
+                                  T=1, pos0s=pos0s, conv_fused=True, conv_w=wd, cst_in=rin,
+                                  cst_out=rout)
+            cks = None
+        else:
+            c = torch.empty((B, T, ROW), dtype=torch.float16, device=dev)
+            for b in range(B):
+                sts = [torch.empty((ROW, 3), dtype=torch.float16, device=dev) for _ in range(3)]
+                fl.ops.conv1d_causal_rows(to_dev(x[b], dev), wd, to_dev(st[b], dev), c[b],
+                                          *sts[:T], T=T, pos0=pos0s[b])
+            cks = [torch.zeros((T - 1, NV, 128, 128), dtype=torch.float32, device=dev)
+                   for _ in range(B)]
+            y = fl.ops.gdn_decode(c, S_d, to_dev(a, dev), to_dev(bb, dev), Ad, dtd, T=T,
+                                  pos0s=pos0s, ck=cks, ck_step=NV * 128 * 128)
+        torch.cuda.synchronize()
+        yh = y.cpu().numpy()
+        for b in range(B):
+            S_r = S0[b].copy()
+            if T == 1:
+                ring = np.zeros((ROW, 3), np.float16)
+                y_r = orc.gdn_decode(None, S_r, a[b], bb[b], A_log, dt, T=1, out_scale=QS,
+                                     cx=x[b], cw=w, cst_in=st[b], cst_out=ring, pos0=pos0s[b])
+                assert np.array_equal(rout[b].cpu().numpy(), ring), f"case {case} ring {b}"
+            else:
+                y_c, _ = orc.conv1d_causal_rows(x[b], w, st[b], dim=ROW, T=T, pos0=pos0s[b],
+                                                row_stride=ROW)
+                ck_r = np.zeros((T - 1, NV, 128, 128), np.float32)
+                y_r = orc.gdn_decode(y_c, S_r, a[b], bb[b], A_log, dt, T=T, out_scale=QS,
+                                     ck=ck_r, ck_step=NV * 128 * 128)
+                ckh = cks[b].cpu().numpy().astype(np.float64)
+                assert np.abs(ckh - ck_r).max() / np.abs(ck_r).max() <= 1e-4, f"case {case} ck {b}"
+            Sh = S_d[b].cpu().numpy().astype(np.float64)
+            assert np.abs(Sh - S_r).max() / np.abs(S_r).max() <= 1e-4, f"case {case} state {b}"
+            err, ok = close(yh[b], y_r, ATOL, RTOL)
+            assert ok, f"seed {seed} case {case} sequence {b}: max|dy| {err}"
