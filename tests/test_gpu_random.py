@@ -2,7 +2,9 @@
 hand-picked list misses (ragged lengths, one-row contexts, capacities beyond
 the length, batches of up to 10 sequences at unrelated positions, forced KV
 splits from 1 to 9, verify rows 1..5, scan lengths 1..300, GDN decode batches
-of up to 12 with the conv fused or verify rows with checkpoints). Each case prints
+of up to 12 with the conv fused or verify rows with checkpoints, the fused
+attention prep at positions up to ~200k, conv1d over odd channel counts and
+widths 1..8). Each case prints
 its shape before it runs, and every comparison uses the attention bar with the
 relative-to-max check, the state bar for the scans."""
 import numpy as np
@@ -214,3 +216,77 @@ def test_random_gdn_decode(fl, dev, orc, seed):
             assert np.abs(Sh - S_r).max() / np.abs(S_r).max() <= 1e-4, f"case {case} state {b}"
             err, ok = close(yh[b], y_r, ATOL, RTOL)
             assert ok, f"seed {seed} case {case} sequence {b}: max|dy| {err}"
+
+
+def _ulps(a, b):
+    ai = np.asarray(a).view(np.int16).astype(np.int32)
+    bi = np.asarray(b).view(np.int16).astype(np.int32)
+    ai = np.where(ai < 0, -32768 - ai, ai)
+    bi = np.where(bi < 0, -32768 - bi, bi)
+    return int(np.abs(ai - bi).max())
+
+
+@pytest.mark.parametrize("seed", range(2))
+def test_random_attn_prep(fl, dev, orc, seed):
+    """The fused prep (norms, partial RoPE, KV store; fp16 and int8 caches) at
+    random positions up to ~200k and 1..64 tokens: q and k within 1 fp16 ulp of
+    the oracle, the cache rows (int8: values and scales) bit for bit, nothing
+    written outside them."""
+    rng = np.random.default_rng(7000 + seed)
+    for case in range(4):
+        T = int(rng.integers(1, 65))
+        pos0 = int(rng.integers(0, 200000))
+        cap = pos0 + T + int(rng.integers(0, 9))
+        kv8 = bool(case & 1)
+        print(f"seed {seed} case {case}: T={T} pos0={pos0} kv8={kv8}", flush=True)
+        qg = rng.standard_normal((T, 24, 512)).astype(np.float16)
+        k = (rng.standard_normal((T, 4, 256)) * 3).astype(np.float16)
+        v = rng.standard_normal((T, 4, 256)).astype(np.float16)
+        wq = (rng.standard_normal(256) * 0.2).astype(np.float32)
+        wk = (rng.standard_normal(256) * 0.2).astype(np.float32)
+        qd, kd, vd = to_dev(qg, dev), to_dev(k, dev), to_dev(v, dev)
+        if kv8:
+            kc, vc = orc.kv8_buffer(cap), orc.kv8_buffer(cap)
+            q_o, k_o = orc.attn_prep_q8(qg, k, v, wq, wk, kc, vc, pos0=pos0, T=T, max_pos=cap)
+            kcd, vcd = fl.ops.kv8_cache(cap), fl.ops.kv8_cache(cap)
+            fl.ops.attn_prep_q8(qd, kd, vd, to_dev(wq, dev), to_dev(wk, dev), kcd, vcd,
+                                pos0=pos0, max_pos=cap)
+        else:
+            kc = np.zeros((cap, 4, 256), np.float16)
+            vc = np.zeros_like(kc)
+            q_o, k_o = orc.attn_prep(qg, k, v, wq, wk, kc, vc, pos0=pos0, T=T, max_pos=cap)
+            kcd = torch.zeros((cap, 4, 256), dtype=torch.float16, device=dev)
+            vcd = torch.zeros_like(kcd)
+            fl.ops.attn_prep(qd, kd, vd, to_dev(wq, dev), to_dev(wk, dev), kcd, vcd, pos0=pos0)
+        torch.cuda.synchronize()
+        assert _ulps(qd.cpu().numpy(), q_o) <= 1 and _ulps(kd.cpu().numpy(), k_o) <= 1, case
+        assert np.array_equal(kcd.cpu().numpy(), kc) and np.array_equal(vcd.cpu().numpy(), vc), \
+            f"seed {seed} case {case}: cache bytes"
+
+
+@pytest.mark.parametrize("seed", range(2))
+def test_random_conv(fl, dev, orc, seed):
+    """conv1d_causal over random channel counts (multiples of 8 and not),
+    widths 1..8, lengths and positions: y within 1 fp16 ulp of the oracle, the
+    new state bit for bit."""
+    rng = np.random.default_rng(8000 + seed)
+    for case in range(4):
+        dim = int(rng.choice([8, 64, 1000, 2048, 6144, 10240, 333]))
+        width = int(rng.integers(1, 9))
+        T = int(rng.integers(1, 70))
+        pos0 = int(rng.integers(0, 50))
+        stride = dim + int(rng.choice([0, 8, 16]))
+        print(f"seed {seed} case {case}: dim={dim} width={width} T={T} pos0={pos0}", flush=True)
+        x = rng.standard_normal((T, stride)).astype(np.float16)
+        w = (rng.standard_normal((dim, width)) * 0.5).astype(np.float16)
+        st = rng.standard_normal((dim, width - 1) if width > 1 else (8,)).astype(np.float16)
+        y = torch.zeros((T, stride), dtype=torch.float16, device=dev)
+        so = torch.empty(st.shape, dtype=torch.float16, device=dev)
+        fl.ops.conv1d_causal(to_dev(x, dev), to_dev(w, dev), to_dev(st, dev), y, so, dim=dim,
+                             T=T, pos0=pos0, row_stride=stride, width=width)
+        torch.cuda.synchronize()
+        y_r, so_r = orc.conv1d_causal(x, w, st, dim=dim, T=T, pos0=pos0, row_stride=stride,
+                                      width=width)
+        assert _ulps(y.cpu().numpy()[:, :dim], y_r[:, :dim]) <= 1, f"seed {seed} case {case}"
+        if width > 1:
+            assert np.array_equal(so.cpu().numpy(), so_r), f"seed {seed} case {case}: state"
