@@ -452,18 +452,22 @@ def test_chunked_degenerate_chunks_vs_recurrence(fl, dev, orc):
     assert ok, f"max|dy| {err}"
 
 
-@pytest.mark.parametrize("regime", ["strong", "none", "mixed"])
+@pytest.mark.parametrize("regime", ["strong", "zero", "none", "mixed"])
 def test_scans_extreme_decay_vs_recurrence(fl, dev, orc, regime):
     """Decay at its ends, for the recurrent and the chunked scan against the
     oracle's recurrence over 200 tokens: 'strong' ~e^-12 a token (the in-chunk
     ratios e^{g_i - g_j} underflow to 0 after a few tokens and the state is
-    all but erased every step), 'none' exactly 1, 'mixed' alternating heads of
-    the two with beta also at 0 and 1 for some tokens."""
+    all but erased every step), 'zero' exactly 0 for a third of the tokens
+    (the chunked form's log takes FLT_MIN there), 'none' exactly 1, 'mixed'
+    alternating heads of strong and none with beta also at 0 and 1 for some
+    tokens."""
     T = 200
-    rng = np.random.default_rng({"strong": 11, "none": 12, "mixed": 13}[regime])
+    rng = np.random.default_rng({"strong": 11, "zero": 14, "none": 12, "mixed": 13}[regime])
     ln, beta, decay, S0 = _scan_inputs(rng, T)
     if regime == "strong":
         decay[:] = np.exp(-rng.uniform(10, 14, decay.shape)).astype(np.float32)
+    elif regime == "zero":
+        decay[::3] = 0.0
     elif regime == "none":
         decay[:] = 1.0
     else:
