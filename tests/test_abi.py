@@ -202,3 +202,35 @@ def test_prefill_plan_falls_back_to_the_tile_grid(fl):
     assert lib.fl_attention_prefill_plan(8192, 0, 24, 3, 256, None, 0) == 0
     assert lib.fl_attention_prefill_plan(8192, 0, 24, 4, 250, None, 0) == 0
     assert lib.fl_attention_prefill_plan(8192, 0, 24, 4, 256, None, 0) == 64 + 1 + 192
+
+
+def test_integration_stub_matches_the_binding(fl):
+    """The ctypes stub INTEGRATION.md gives a maintainer for the reference
+    runtime declares the same argument lists as the package's own binding
+    (the one every test calls through), entry point by entry point."""
+    import ctypes
+    text = (REPO / "INTEGRATION.md").read_text()
+    block = text.split("```python", 1)[1].split("```", 1)[0]
+    sigs_src = block.split("_SIGS = ", 1)[1]
+    depth, end = 0, 0
+    for n, ch in enumerate(sigs_src):
+        depth += ch == "{"
+        depth -= ch == "}"
+        if depth == 0 and ch == "}":
+            end = n + 1
+            break
+    names = {"_P": ctypes.c_void_p, "_I": ctypes.c_int, "_F": ctypes.c_float,
+             "_LL": ctypes.c_longlong, "_SZ": ctypes.c_size_t,
+             "_PP": ctypes.POINTER(ctypes.c_void_p), "_IP": ctypes.POINTER(ctypes.c_int)}
+    stub = eval(sigs_src[:end], {"__builtins__": {}}, names)
+    table = fl._lib.SIGNATURES
+    assert len(stub) >= 25
+    for name, args in stub.items():
+        assert name in table, name
+        assert list(args) == list(table[name][1]), name
+    # the size queries the stub binds by hand
+    for name, n_args in (("fl_attn_decode_work_bytes", 5), ("fl_gdn_chunked_work_bytes", 5),
+                         ("fl_attention_prefill_work_bytes", 4),
+                         ("fl_attention_prefill_q8_stage_bytes", 5)):
+        assert name in block
+        assert table[name] == (ctypes.c_size_t, [ctypes.c_int] * n_args), name
