@@ -773,6 +773,88 @@ attn_merge_kernel(const float* __restrict__ pacc, const float* __restrict__ pm,
     }
 }
 
+// The same merge for fl_attention_merge's callers (the KV-split prefill: T up
+// to a chunk of 1024 tokens, so T x 24 (row, head) pairs of a few splits
+// each): one wavefront a pair, lane l holding dims 4 l .. 4 l + 3 (head_dim
+// <= 256), four pairs a workgroup, no LDS and no barrier. The splits are read
+// in batches of eight, every load issued before any is used, and weighed by
+// e^(m_s - M) against the running max M, rescaled when a batch raises it --
+// attn_merge_kernel's arithmetic with one running max instead of J (the J
+// group sums' order differs, so the two agree to rounding). A block a pair
+// spent most of its time on its barrier and LDS exchange: a 1024-token
+// chunk's 4 splits (101 MB of partials) took 39 us that way, 17 us this way.
+constexpr int MR_PAIRS = 4;   // (row, head) pairs a workgroup, one a wave
+__global__ void __launch_bounds__(64 * MR_PAIRS)
+attn_merge_rows_kernel(const float* __restrict__ pacc, const float* __restrict__ pm,
+                       const float* __restrict__ pd, f16* __restrict__ z,
+                       const f16* __restrict__ gate, int n_q_heads, int head_dim, int z_pitch,
+                       int g_pitch, int g_off, int split, long long n_pairs) {
+    const int lane = threadIdx.x & 63;
+    const long long rh = (long long)blockIdx.x * MR_PAIRS + (threadIdx.x >> 6);
+    if (rh >= n_pairs) return;                            // wave-uniform
+    const int C = head_dim >> 2;
+    const bool on = lane < C;
+    const int c = on ? lane : 0;                          // idle lanes read dims 0..3
+    const size_t p0 = (size_t)rh * split;
+    const float* pmr = pm + p0;
+    const float* pdr = pd + p0;
+    const f32x4* acc = (const f32x4*)(pacc + p0 * head_dim) + c;
+
+    float gv[4] = {0.f, 0.f, 0.f, 0.f};
+    if (gate != nullptr) {
+        const f16* gr = gate + (size_t)rh * g_pitch + g_off + 4 * c;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) gv[e] = (float)gr[e];
+    }
+    f32x4 num = (f32x4)(0.f);
+    float den = 0.f, M = -1e30f;
+    for (int s = 0; s < split; s += MG_BATCH) {
+        float mv[MG_BATCH], dv[MG_BATCH];
+        f32x4 av[MG_BATCH];
+#pragma unroll
+        for (int u = 0; u < MG_BATCH; ++u) {
+            const int si = min(s + u, split - 1);
+            mv[u] = pmr[si];
+            dv[u] = pdr[si];
+            av[u] = acc[(size_t)si * C];
+        }
+        float bm = M;
+#pragma unroll
+        for (int u = 0; u < MG_BATCH; ++u) {
+            const bool ok = s + u < split;
+            mv[u] = ok ? mv[u] : -1e30f;
+            dv[u] = ok ? dv[u] : 0.f;
+            av[u] = ok ? av[u] : (f32x4)(0.f);
+            bm = fmaxf(bm, mv[u]);
+        }
+        if (bm > M) {
+            const float corr = fast_exp2((M - bm) * FL_LOG2E);
+            num *= corr;
+            den *= corr;
+            M = bm;
+        }
+#pragma unroll
+        for (int u = 0; u < MG_BATCH; ++u) {
+            const float e = fast_exp2((mv[u] - M) * FL_LOG2E);
+            num[0] = fmaf(e, av[u][0], num[0]);
+            num[1] = fmaf(e, av[u][1], num[1]);
+            num[2] = fmaf(e, av[u][2], num[2]);
+            num[3] = fmaf(e, av[u][3], num[3]);
+            den = fmaf(e, dv[u], den);
+        }
+    }
+    if (!on) return;
+    const float inv = 1.f / den;
+    f16x4 out;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        f16 zv = f16_sat(num[e] * inv);
+        if (gate != nullptr) zv = f16_sat((float)zv * sigmoid_f(gv[e]));
+        out[e] = zv;
+    }
+    *(f16x4*)(z + (size_t)rh * z_pitch + 4 * c) = out;
+}
+
 // The output gate for layouts the 8-a-lane kernel below does not take (odd
 // head_dim, pitches or offsets, unaligned buffers): one wavefront a (token,
 // head) row, lane l taking elements l, l + 64, ... of it, with the same
@@ -1109,6 +1191,14 @@ int fl_attention_merge(const float* pacc, const float* pm, const float* pd, void
     FL_REQUIRE(T >= 1 && split >= 1 && n_q_heads >= 1, "T, split, n_q_heads >= 1");
     FL_REQUIRE(gate == nullptr || g_off + head_dim <= g_pitch, "g_off + head_dim <= g_pitch");
     FL_REQUIRE(aligned16(pacc), "16-byte aligned pacc");
+    if (head_dim <= 256 && z_pitch % 4 == 0 && ((uintptr_t)z & 7u) == 0) {
+        const long long pairs = (long long)T * n_q_heads;
+        hipLaunchKernelGGL(attn_merge_rows_kernel, dim3((unsigned)((pairs + MR_PAIRS - 1) / MR_PAIRS)),
+                           dim3(64 * MR_PAIRS), 0, (hipStream_t)stream, pacc, pm, pd, (f16*)z,
+                           (const f16*)gate, n_q_heads, head_dim, z_pitch, g_pitch, g_off, split,
+                           pairs);
+        return fl::check_launch("attn_merge_rows");
+    }
     hipLaunchKernelGGL(attn_merge_kernel<false>, dim3(n_q_heads, T), dim3(MG_THREADS), 0,
                        (hipStream_t)stream, pacc, pm, pd, (f16*)z, (const f16*)gate, n_q_heads,
                        head_dim, z_pitch, g_pitch, g_off, split, 0, 1);

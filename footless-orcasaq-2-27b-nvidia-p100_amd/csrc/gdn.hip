@@ -147,7 +147,7 @@ __device__ __forceinline__ void gather16(float (&dst)[16], const float* row, int
 // Causal conv over a run of tokens (a8) and a verify's rows (a9): one
 // "sliding window" kernel. A lane owns CPL adjacent channels -- 8 (one
 // 16-byte load of a token's row, one 16-byte store of y) when the layout
-// allows it, else 1 -- and a block of CONV_TB consecutive tokens. It requests
+// allows it, else 1 -- and a block of TB consecutive tokens. It requests
 // all of its block's rows first, then slides a register window of the W - 1
 // previous frames down them, so each x value is read from HBM once (a
 // block's W - 1 leading frames are the previous block's last rows, which L2
@@ -163,7 +163,19 @@ __device__ __forceinline__ void gather16(float (&dst)[16], const float* row, int
 // buffer, and a frame entering the window is rounded by f16_sat first, as the
 // reference's row form does (kernels.cu:1704-1711).
 // ---------------------------------------------------------------------------
-constexpr int CONV_TB = 16;       // tokens a lane
+// Tokens a lane: CONV_TB (the window's W - 1 history frames come from the
+// rows before the block, so at least W - 1: 8 for widths 6..8), halved to 2
+// for widths up to 3 while the grid has fewer than CONV_WAVES_PER_SIMD waves
+// a SIMD. A lane's work is its block's silu chain (~36 vector instructions a
+// token and channel), and a wave keeps its SIMD busy on its own, so a call
+// takes as long as the SIMD with the most waves, and a short block keeps the
+// grid even: at 10240 channels (W = 4) blocks of 16 / 8 / 4 tokens measured
+// 25 / 17 / 17 us at T = 1024 (16 tokens: 1280 waves for 1024 SIMDs, a
+// quarter of them running two in turn), 28.5 / 28.5 / 26.3 at 2048 and
+// 96 / 91 / 91 at 8192.
+constexpr int CONV_TB = 4;
+constexpr int CONV_TB_MIN = 2;
+constexpr int CONV_WAVES_PER_SIMD = 4;
 constexpr int CONV_WMAX = 8;      // widths 1 .. 8
 
 template <int CPL> struct ConvVec;
@@ -223,7 +235,7 @@ struct ConvStates {
     f16* st[3];   // the new state (st[0]), or a verify's one state a row
 };
 
-template <int W, int CPL, bool ROWS>
+template <int W, int CPL, bool ROWS, int TB>
 __global__ void __launch_bounds__(64)
 conv_window_kernel(const f16* __restrict__ x, const f16* __restrict__ w, const f16* st_in,
                    f16* __restrict__ y, ConvStates outs, int dim, int T, int pos0,
@@ -232,11 +244,11 @@ conv_window_kernel(const f16* __restrict__ x, const f16* __restrict__ w, const f
     constexpr bool VEC = CPL == 8;
     constexpr int H = W - 1;          // frames of history
     constexpr int HW = H > 0 ? H : 1;
-    static_assert(CONV_TB >= H, "a block's leading frames are the previous block's rows");
-    constexpr int NTOK = ROWS ? 3 : CONV_TB;   // a verify has at most 3 rows
+    static_assert(TB >= H, "a block's leading frames are the previous block's rows");
+    constexpr int NTOK = ROWS ? 3 : TB;   // a verify has at most 3 rows
     const int d = (blockIdx.x * 64 + threadIdx.x) * CPL;
     if (d >= dim) return;
-    const int t0 = blockIdx.y * CONV_TB;
+    const int t0 = blockIdx.y * TB;
     const int nt = min(NTOK, T - t0);
     // the block's rows, all requested before any arithmetic (a row past the
     // call re-reads the last one and is not used)
@@ -294,28 +306,56 @@ conv_window_kernel(const f16* __restrict__ x, const f16* __restrict__ w, const f
         if (t0 + nt == T) frames_out<H, CPL>(outs.st[0] + (size_t)d * H, win);
 }
 
-template <int W>
-void conv_launch(bool vec, bool rows, dim3 grid_tok, const f16* x, const f16* w,
-                 const f16* st_in, f16* y, ConvStates outs, int dim, int T, int pos0,
-                 int row_stride, hipStream_t stream) {
-    const int cpl = vec ? 8 : 1;
-    const dim3 grid((dim + 64 * cpl - 1) / (64 * cpl), grid_tok.y);
-    if (rows) {   // the verify form is width 4 only
-        if constexpr (W == 4) {
-            if (vec)
-                hipLaunchKernelGGL((conv_window_kernel<W, 8, true>), grid, dim3(64), 0, stream, x,
-                                   w, st_in, y, outs, dim, T, pos0, row_stride);
-            else
-                hipLaunchKernelGGL((conv_window_kernel<W, 1, true>), grid, dim3(64), 0, stream, x,
-                                   w, st_in, y, outs, dim, T, pos0, row_stride);
+// The block length for a call: CONV_TB, or the smallest power of two >= W - 1
+// where that is longer; then halved while the grid is short of
+// CONV_WAVES_PER_SIMD waves a SIMD and the block stays >= max(2, W - 1).
+int conv_tb(int W, int T, int channel_waves, int n_cu) {
+    const long long want = (long long)CONV_WAVES_PER_SIMD * 4 * n_cu;
+    int tb = CONV_TB;
+    while (tb < W - 1) tb *= 2;
+    while (tb / 2 >= CONV_TB_MIN && tb / 2 >= W - 1 &&
+           (long long)channel_waves * ((T + tb - 1) / tb) < want)
+        tb /= 2;
+    return tb;
+}
+
+template <int W, int CPL, int TB>
+void conv_launch_tb(bool rows, int tok_blocks, const f16* x, const f16* w, const f16* st_in,
+                    f16* y, ConvStates outs, int dim, int T, int pos0, int row_stride,
+                    hipStream_t stream) {
+    const dim3 grid((dim + 64 * CPL - 1) / (64 * CPL), tok_blocks);
+    if constexpr (TB >= W - 1) {
+        if (rows) {   // the verify form: width 4, one block of CONV_TB (T <= 3)
+            static_assert(CONV_TB >= 3, "a verify's rows are one block");
+            if constexpr (W == 4 && TB == CONV_TB)
+                hipLaunchKernelGGL((conv_window_kernel<W, CPL, true, TB>), grid, dim3(64), 0,
+                                   stream, x, w, st_in, y, outs, dim, T, pos0, row_stride);
+        } else {
+            hipLaunchKernelGGL((conv_window_kernel<W, CPL, false, TB>), grid, dim3(64), 0, stream,
+                               x, w, st_in, y, outs, dim, T, pos0, row_stride);
         }
-    } else if (vec) {
-        hipLaunchKernelGGL((conv_window_kernel<W, 8, false>), grid, dim3(64), 0, stream, x, w,
-                           st_in, y, outs, dim, T, pos0, row_stride);
-    } else {
-        hipLaunchKernelGGL((conv_window_kernel<W, 1, false>), grid, dim3(64), 0, stream, x, w,
-                           st_in, y, outs, dim, T, pos0, row_stride);
     }
+}
+
+template <int W>
+void conv_launch(bool vec, bool rows, int tb, const f16* x, const f16* w, const f16* st_in,
+                 f16* y, ConvStates outs, int dim, int T, int pos0, int row_stride,
+                 hipStream_t stream) {
+    const int blocks = (T + tb - 1) / tb;
+#define FL_CONV_TB(TBv)                                                                        \
+    case TBv:                                                                                  \
+        if (vec)                                                                               \
+            conv_launch_tb<W, 8, TBv>(rows, blocks, x, w, st_in, y, outs, dim, T, pos0,        \
+                                      row_stride, stream);                                     \
+        else                                                                                   \
+            conv_launch_tb<W, 1, TBv>(rows, blocks, x, w, st_in, y, outs, dim, T, pos0,        \
+                                      row_stride, stream);                                     \
+        break;
+    switch (tb) {
+        FL_CONV_TB(8) FL_CONV_TB(4) FL_CONV_TB(2)
+        default: break;
+    }
+#undef FL_CONV_TB
 }
 
 // ---------------------------------------------------------------------------
@@ -919,12 +959,15 @@ static int conv_dispatch(const void* x, const void* w, const void* st_in, void* 
                          int row_stride, int width, hipStream_t stream) {
     const f16* sts[3] = {outs.st[0], outs.st[1], outs.st[2]};
     const bool vec = conv_vec_ok(x, w, st_in, y, sts, n_st, dim, row_stride);
-    const dim3 tok(1, (T + CONV_TB - 1) / CONV_TB);
+    const int cpl = vec ? 8 : 1;
+    // a verify (T <= 3) is one block whatever its length
+    const int tb = rows ? CONV_TB : conv_tb(width, T, (dim + 64 * cpl - 1) / (64 * cpl),
+                                            gdn_cu_count());
     const f16 *xp = (const f16*)x, *wp = (const f16*)w, *sp = (const f16*)st_in;
     f16* yp = (f16*)y;
     switch (width) {
 #define FL_CONV_W(Wd) \
-    case Wd: conv_launch<Wd>(vec, rows, tok, xp, wp, sp, yp, outs, dim, T, pos0, row_stride, stream); break;
+    case Wd: conv_launch<Wd>(vec, rows, tb, xp, wp, sp, yp, outs, dim, T, pos0, row_stride, stream); break;
         FL_CONV_W(1) FL_CONV_W(2) FL_CONV_W(3) FL_CONV_W(4)
         FL_CONV_W(5) FL_CONV_W(6) FL_CONV_W(7) FL_CONV_W(8)
 #undef FL_CONV_W

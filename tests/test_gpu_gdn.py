@@ -56,11 +56,12 @@ def _conv_case(fl, dev, orc, rng, *, T, pos0, dim=ROW, stride=None, width=4):
     return y.cpu().numpy()[:, :dim], so, y_r[:, :dim], so_r
 
 
-# token counts around the 16-token block a lane walks: 1, 2 (shorter than the
-# 3 frames of history: the new state mixes old frames and new ones), a block
-# and one past it, many blocks with a ragged last one
+# token counts around the 4-token block a lane walks at width 4: 1, 2
+# (shorter than the 3 frames of history: the new state mixes old frames and
+# new ones), a block and one past it, many blocks with a ragged last one, and
+# long calls (1700, 4000: a thousand blocks down each lane's channels).
 @pytest.mark.parametrize("T,pos0", [(1, 0), (1, 9), (2, 5), (5, 0), (8, 3), (16, 1), (17, 2),
-                                    (64, 100), (333, 7)])
+                                    (64, 100), (333, 7), (1700, 4), (4000, 9)])
 def test_conv1d_vs_oracle(fl, dev, orc, rng, T, pos0):
     y, so, y_r, so_r = _conv_case(fl, dev, orc, rng, T=T, pos0=pos0)
     assert np.array_equal(so, so_r)
@@ -69,7 +70,7 @@ def test_conv1d_vs_oracle(fl, dev, orc, rng, T, pos0):
 
 # both lane layouts (8 channels a lane with 16-byte rows; a channel a lane for
 # an odd row stride / channel count) and every supported width
-@pytest.mark.parametrize("width", [1, 2, 3, 5, 8])
+@pytest.mark.parametrize("width", [1, 2, 3, 5, 6, 8])
 @pytest.mark.parametrize("layout", ["vec", "lane"])
 @pytest.mark.parametrize("T,pos0", [(2, 3), (21, 0)])
 def test_conv1d_widths_and_layouts(fl, dev, orc, rng, width, layout, T, pos0):
