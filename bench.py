@@ -611,6 +611,52 @@ def bench_prefill_flow(torch, fl, L, kv8=True, chunk=1024, reps=3):
     return out
 
 
+def bench_decode_flow(torch, fl, L, kv8=True, Bq=4):
+    """The serving loop's token step: one decode step of Bq sequences through
+    the model's 64 layers on HybridRuntime.forward_batch (the backend's
+    batched rows, runtime.py:3114-3146 and 2865-2878): per attention layer
+    each row's prep into its own cache and one batched decode attention
+    launch, per GDN layer one fused conv + delta-rule launch over the rows and
+    the gated output norm. The sequences hold L, L - 97, ... cached positions
+    (the caches' contents do not change the work). The step is captured in a
+    HIP graph and replayed -- each replay the same step, rewriting the same
+    cache rows and advancing the recurrences -- so the line is the GPU time of
+    a step without the host's launch cost, median over replays. Also timed:
+    the 16 attention layers alone and the 48 GDN layers alone."""
+    rtm = fl.runtime
+    dev = torch.device("cuda:0")
+    proj = _FlowProj(torch, Bq, dev, seed=6)
+    lens = [L - 97 * b for b in range(Bq)]
+    out = {"config": f"decode_flow_B{Bq}_L{L}" + ("_kv8" if kv8 else ""), "lens": lens}
+    scheds = {"all": rtm.LAYER_TYPES, "attn": ("full_attention",) * 16,
+              "gdn": ("linear_attention",) * 48}
+    row = 4 * 256 + 4 * 8 * 2 if kv8 else 4 * 256 * 2   # bytes of a position's K (or V)
+    attn_bytes = 2 * row * sum(lens)                          # K and V read a layer
+    gdn_bytes = gdn_decode_bytes(B=Bq) + 3 * Bq * 48 * 128 * 2   # + the output norm
+    for name, types in scheds.items():
+        rt = rtm.HybridRuntime(rtm.random_weights(types, seed=3, device=dev), layer_types=types,
+                               kv8=kv8, device=dev)
+        states = []
+        for n in lens:
+            st = rt.new_state()
+            rt.grow(st, n + 16)               # room for every step taken below
+            st.tokens = list(range(n))
+            st.fed = n
+            states.append(st)
+        g = graph_of(torch, lambda i: rt.forward_batch(states, proj, [1] * Bq), 1)
+        m = measure(torch, g, 1, DECODE_SAMPLES)
+        key = "" if name == "all" else name + "_"
+        nb = {"all": 16 * attn_bytes + 48 * gdn_bytes, "attn": 16 * attn_bytes,
+              "gdn": 48 * gdn_bytes}[name]
+        out[key + "us"] = round(m["us"], 1)
+        out[key + "hbm_frac"] = round(nb / (m["us"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 3)
+        if name == "all":
+            out["tok_s"] = round(Bq / (m["us"] * 1e-6))
+        del g, states, rt
+        torch.cuda.empty_cache()
+    return out
+
+
 # ---------------------------------------------------------------------------
 # CPU baseline: PyTorch fp32 on the host's cores
 # ---------------------------------------------------------------------------
@@ -839,6 +885,9 @@ EXTRA_CONFIGS = {
     "prefill_flow_L8192_kv8": (bench_prefill_flow, {"L": 8192}),
     "prefill_flow_L32768_kv8": (bench_prefill_flow, {"L": 32768, "reps": 1}),
     "prefill_flow_L8192": (bench_prefill_flow, {"L": 8192, "kv8": False}),
+    "decode_flow_B4_L8192": (bench_decode_flow, {"L": 8192, "kv8": False}),
+    "decode_flow_B4_L8192_kv8": (bench_decode_flow, {"L": 8192}),
+    "decode_flow_B4_L100000_kv8": (bench_decode_flow, {"L": 100000}),
 }
 
 

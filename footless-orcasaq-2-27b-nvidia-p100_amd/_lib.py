@@ -56,6 +56,8 @@ SIGNATURES = {
     "fl_kv_store_q8": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P]),
     "fl_attn_prep_q8": (_I, [_P, _I, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _F,
                              _F, _P]),
+    "fl_attn_prep_rows": (_I, [_P, _I, _P, _P, _P, _P, _PP, _PP, _IP, _IP, _I, _I, _I, _I, _I,
+                               _I, _F, _F, _P]),
     "fl_attention_split_gqa_q8": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _F,
                                        _I, _I, _I, _P]),
     "fl_attention_dec_q8": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _I, _I, _I, _P]),

@@ -50,22 +50,35 @@ struct RopeFreqs {
     double f[PR_MAXPAIRS];
 };
 
+// The rows of a batched decode step, each its own sequence's: row t goes to
+// cache kc[t] / vc[t] (capacity max_pos[t]) at position pos[t].
+struct PrepRows {
+    void* kc[FL_MAX_SEQS];
+    void* vc[FL_MAX_SEQS];
+    int pos[FL_MAX_SEQS];
+    int max_pos[FL_MAX_SEQS];
+};
+
 // flags: bit 0 norm, bit 1 rope, bit 2 KV store (k rows and their v rows),
 // bit 3 the store in the int8 format (caches of capacity max_pos); RPW rows a
-// wavefront
-template <int FLAGS, int RPW>
+// wavefront. ROWS: token t is row t of a batched decode step, its position,
+// cache and capacity from `rows` (pos0, kc, vc and max_pos unused).
+template <int FLAGS, int RPW, bool ROWS = false>
 __global__ void __launch_bounds__(64 * PR_WAVES)
 attn_prep_kernel(const f16* q, f16* qo, int q_pitch, f16* k, int k_pitch,
                  const f16* __restrict__ v, const float* __restrict__ wq,
-                 const float* __restrict__ wk, void* __restrict__ kc, void* __restrict__ vc,
-                 int n_q_heads, int n_kv_heads, int pos0, int max_pos, int rope_dim,
-                 const RopeFreqs freqs, float eps) {
+                 const float* __restrict__ wk, void* __restrict__ kc_, void* __restrict__ vc_,
+                 int n_q_heads, int n_kv_heads, int pos0, int max_pos_, int rope_dim,
+                 const RopeFreqs freqs, float eps, const PrepRows rows) {
     __shared__ float scs[PR_MAXPAIRS], ssn[PR_MAXPAIRS];
     __shared__ __attribute__((aligned(16))) f16 srow[PR_WAVES][PR_HD];
     constexpr bool NORM = FLAGS & 1, ROPE = FLAGS & 2, STORE = FLAGS & 4, Q8 = FLAGS & 8;
     const int t = blockIdx.x, hd0 = blockIdx.y * PR_WAVES * RPW;
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    const int pos = pos0 + t;
+    const int pos = ROWS ? rows.pos[t] : pos0 + t;
+    void* const kc = ROWS ? rows.kc[t] : kc_;
+    void* const vc = ROWS ? rows.vc[t] : vc_;
+    const int max_pos = ROWS ? rows.max_pos[t] : max_pos_;
     const int half_r = rope_dim >> 1;
     if (ROPE) {
         for (int j = threadIdx.x; j < half_r; j += 64 * PR_WAVES) {
@@ -194,13 +207,14 @@ int launch_prep(const f16* q, f16* qo, int q_pitch, f16* k, int k_pitch, const f
         hipLaunchKernelGGL((attn_prep_kernel<FLAGS, 1>),
                            dim3(T, (heads + PR_WAVES - 1) / PR_WAVES), dim3(64 * PR_WAVES), 0,
                            (hipStream_t)stream, q, qo, q_pitch, k, k_pitch, v, wq, wk, kc, vc,
-                           n_q_heads, n_kv_heads, pos0, max_pos, rope_dim, freqs, eps);
+                           n_q_heads, n_kv_heads, pos0, max_pos, rope_dim, freqs, eps,
+                           PrepRows{});
     } else {
         hipLaunchKernelGGL((attn_prep_kernel<FLAGS, 7>),
                            dim3(T, (heads + 7 * PR_WAVES - 1) / (7 * PR_WAVES)),
                            dim3(64 * PR_WAVES), 0, (hipStream_t)stream, q, qo, q_pitch, k,
                            k_pitch, v, wq, wk, kc, vc, n_q_heads, n_kv_heads, pos0, max_pos,
-                           rope_dim, freqs, eps);
+                           rope_dim, freqs, eps, PrepRows{});
     }
     return fl::check_launch("attn_prep");
 }
@@ -281,6 +295,41 @@ int fl_attn_prep_q8(void* qg, int q_pitch, void* k, const void* v, const float* 
     return launch_prep<15>((const f16*)qg, (f16*)qg, q_pitch, (f16*)k, head_dim, (const f16*)v, wq,
                            wk, kcache, vcache, n_q_heads, n_kv_heads, pos0, max_pos, T, rope_dim,
                            theta, eps, stream);
+}
+
+int fl_attn_prep_rows(void* qg, int q_pitch, void* k, const void* v, const float* wq,
+                      const float* wk, void* const* kcaches, void* const* vcaches,
+                      const int* pos, const int* max_pos, int B, int q8, int n_q_heads,
+                      int n_kv_heads, int head_dim, int rope_dim, float theta, float eps,
+                      fl_stream_t stream) {
+    FL_REQUIRE(kcaches && vcaches && pos && max_pos, "null pointer");
+    FL_REQUIRE(B >= 1 && B <= FL_MAX_SEQS, "1 <= B <= FL_MAX_SEQS");
+    PrepRows rows = {};
+    for (int b = 0; b < B; ++b) {
+        const int rc = check_prep(qg, k, v, wq, wk, kcaches[b], vcaches[b], q_pitch, n_q_heads,
+                                  n_kv_heads, head_dim, pos[b], max_pos[b], 1, rope_dim, eps);
+        if (rc) return rc;
+        FL_REQUIRE(q8 ? al(kcaches[b], 4) && al(vcaches[b], 4)
+                      : al(kcaches[b], 8) && al(vcaches[b], 8), "aligned caches");
+        rows.kc[b] = kcaches[b];
+        rows.vc[b] = vcaches[b];
+        rows.pos[b] = pos[b];
+        rows.max_pos[b] = max_pos[b];
+    }
+    RopeFreqs freqs = {};
+    rope_freqs(theta, rope_dim, freqs);
+    const dim3 grid(B, (n_q_heads + n_kv_heads + PR_WAVES - 1) / PR_WAVES);
+    if (q8)
+        hipLaunchKernelGGL((attn_prep_kernel<15, 1, true>), grid, dim3(64 * PR_WAVES), 0,
+                           (hipStream_t)stream, (const f16*)qg, (f16*)qg, q_pitch, (f16*)k,
+                           head_dim, (const f16*)v, wq, wk, nullptr, nullptr, n_q_heads,
+                           n_kv_heads, 0, 0, rope_dim, freqs, eps, rows);
+    else
+        hipLaunchKernelGGL((attn_prep_kernel<7, 1, true>), grid, dim3(64 * PR_WAVES), 0,
+                           (hipStream_t)stream, (const f16*)qg, (f16*)qg, q_pitch, (f16*)k,
+                           head_dim, (const f16*)v, wq, wk, nullptr, nullptr, n_q_heads,
+                           n_kv_heads, 0, 0, rope_dim, freqs, eps, rows);
+    return fl::check_launch("attn_prep_rows");
 }
 
 }  // extern "C"

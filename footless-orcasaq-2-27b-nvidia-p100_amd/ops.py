@@ -332,6 +332,35 @@ def attn_prep_q8(qg, k, v, wq, wk, kcache, vcache, *, pos0: int, max_pos: int,
               head_dim, pos0, max_pos, T, rope_dim, float(theta), float(eps), _stream())
 
 
+def attn_prep_rows(qg, k, v, wq, wk, kcaches, vcaches, pos, caps, *, kv8: bool,
+                   n_q_heads: int = N_HEADS, n_kv_heads: int = N_KV, head_dim: int = HEAD_DIM,
+                   q_pitch: int = Q_PITCH, rope_dim: int = ROPE_DIM, theta: float = ROPE_THETA,
+                   eps: float = NORM_EPS):
+    """The prep of a batched decode step's rows in one launch (the per-row
+    attn_prep / attn_prep_q8 calls of runtime.py:2873-2876): row b of qg [B,
+    n_q_heads, q_pitch], k / v [B, n_kv, head_dim] into kcaches[b] /
+    vcaches[b] (capacity caps[b]; fp16 [cap, n_kv, head_dim] or, kv8, the
+    int8 buffers) at position pos[b]."""
+    B = qg.shape[0]
+    row = n_kv_heads * head_dim
+    if not (len(kcaches) == len(vcaches) == len(pos) == len(caps) == B):
+        raise ValueError("one cache pair, position and capacity per row")
+    for b in range(B):
+        for name, c in (("kcache", kcaches[b]), ("vcache", vcaches[b])):
+            if kv8:
+                _kv8(c, name, caps[b], n_kv_heads, head_dim)
+            else:
+                _contig(c, name)
+                _ptr(c, F16, name, caps[b] * row)
+    _lib.call("fl_attn_prep_rows", _ptr(qg, F16, "qg", B * n_q_heads * q_pitch), q_pitch,
+              _ptr(k, F16, "k", B * row), _ptr(v, F16, "v", B * row),
+              _ptr(wq, F32, "wq", head_dim), _ptr(wk, F32, "wk", head_dim),
+              _lib.ptr_array([c.data_ptr() for c in kcaches]),
+              _lib.ptr_array([c.data_ptr() for c in vcaches]), _lib.int_array(pos),
+              _lib.int_array(caps), B, int(bool(kv8)), n_q_heads, n_kv_heads, head_dim, rope_dim,
+              float(theta), float(eps), _stream())
+
+
 def attention_split_gqa_q8(q, kcache, vcache, pacc, pm, pd, *, pos0: int, max_pos: int, T: int,
                            n_q_heads: int = N_HEADS, n_kv_heads: int = N_KV,
                            head_dim: int = HEAD_DIM, q_pitch: int = Q_PITCH,

@@ -439,10 +439,11 @@ class HybridRuntime:
     def forward_batch(self, states: Sequence[SeqState], proj: Projections,
                       tokens: Sequence[int]) -> None:
         """One decode step of several sequences (one token each), as
-        `_step_rows` runs it: per full-attention layer the prep of each row
-        into its own cache, then one attention launch over all rows; per GDN
-        layer one fused conv + delta-rule launch over all rows. `proj` hands
-        the B rows stacked ([B, ...] where forward takes [T, ...])."""
+        `_step_rows` runs it: per full-attention layer one launch of every
+        row's prep into its own cache, then one attention launch over all
+        rows; per GDN layer one fused conv + delta-rule launch over all rows.
+        `proj` hands the B rows stacked ([B, ...] where forward takes [T,
+        ...])."""
         B = len(states)
         if B != len(tokens) or B < 1:
             raise ValueError("one token a sequence")
@@ -458,14 +459,10 @@ class HybridRuntime:
                 qg, k, v = proj.full_attn_in(i, B)
                 kcs = [st.kk[li] for st in states]
                 vcs = [st.kv[li] for st in states]
-                for r, st in enumerate(states):
-                    if self.kv8:
-                        ops.attn_prep_q8(qg[r:r + 1], k[r:r + 1], v[r:r + 1], wt.q_norm,
-                                         wt.k_norm, kcs[r], vcs[r], pos0=pos0s[r],
-                                         max_pos=st.lcap[li], T=1)
-                    else:
-                        ops.attn_prep(qg[r:r + 1], k[r:r + 1], v[r:r + 1], wt.q_norm, wt.k_norm,
-                                      kcs[r], vcs[r], pos0=pos0s[r], T=1)
+                # every row's prep into its own cache, one launch (the same values
+                # as a prep a row)
+                ops.attn_prep_rows(qg, k, v, wt.q_norm, wt.k_norm, kcs, vcs, pos0s,
+                                   [st.lcap[li] for st in states], kv8=self.kv8)
                 if self.kv8:
                     z = ops.attn_decode_q8(qg[:, None], kcs, vcs, pos0s,
                                            [st.lcap[li] for st in states])

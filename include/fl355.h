@@ -191,6 +191,20 @@ int fl_attn_prep_q8(void* qg, int q_pitch, void* k, const void* v, const float* 
                     int n_kv_heads, int head_dim, int pos0, int max_pos, int T, int rope_dim,
                     float theta, float eps, fl_stream_t stream);
 
+/* The prep of a batched decode step's B rows (T = 1 each), every row into its
+ * own sequence's cache: row b of qg [B][n_q_heads][q_pitch], k / v
+ * [B][n_kv_heads][head_dim] goes to kcaches[b] / vcaches[b] (host arrays of
+ * device pointers; capacity max_pos[b]) at position pos[b], fp16 caches
+ * ([max_pos][n_kv_heads][head_dim], layer 0) or, with q8, the int8 format --
+ * the same values fl_attn_prep / fl_attn_prep_q8 give each row alone, in one
+ * launch. Replaces the per-row _attn_prep calls of _full_attn_rows
+ * (runtime.py:2873-2876). B <= FL_MAX_SEQS. */
+int fl_attn_prep_rows(void* qg, int q_pitch, void* k, const void* v, const float* wq,
+                      const float* wk, void* const* kcaches, void* const* vcaches,
+                      const int* pos, const int* max_pos, int B, int q8, int n_q_heads,
+                      int n_kv_heads, int head_dim, int rope_dim, float theta, float eps,
+                      fl_stream_t stream);
+
 /* attention_split_gqa_q8: fl_attention_split_gqa over an int8 cache (the same
  * split rule and partials). Replaces kernels.cu:910-1047, launched at
  * runtime.py:2832-2837 with KV8. */

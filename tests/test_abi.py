@@ -88,6 +88,16 @@ def test_argument_checks_refuse_before_launch(fl):
     # chunked scan with a chunk other than 64
     assert _call(fl, "fl_gdn_prefill_chunked", fake, fake, fake, fake, fake, fake, fake, 100, 16,
                  48, 128, 128, 10240, 10240, 6144, 0.1, 3, 32, fake, 1 << 30, None) == 1
+    # batched prep: no rows, more rows than FL_MAX_SEQS, a row past its capacity
+    arr = fl._lib.ptr_array([0x2000] * 17)
+    pos, caps = fl._lib.int_array([5] * 17), fl._lib.int_array([8] * 17)
+    for B in (0, 17):
+        assert _call(fl, "fl_attn_prep_rows", fake, 512, fake, fake, fake, fake, arr, arr, pos,
+                     caps, B, 0, 24, 4, 256, 64, 1e7, 1e-6, None) == 1
+    over = fl._lib.int_array([8] + [5] * 16)
+    assert _call(fl, "fl_attn_prep_rows", fake, 512, fake, fake, fake, fake, arr, arr, over, caps,
+                 2, 1, 24, 4, 256, 64, 1e7, 1e-6, None) == 1
+    assert b"max_pos" in lib.fl_last_error()
 
 
 def test_work_size_queries(fl):

@@ -108,3 +108,45 @@ def test_attn_prep_bad_geometry(fl, dev):
         fl.ops.attn_prep(q, k, k, w, w, kc, kc, pos0=3)
     with pytest.raises(ValueError):       # odd rotary width
         fl.ops.rope_partial(q, k, pos0=0, rope_dim=63)
+
+
+@pytest.mark.parametrize("kv8", [False, True])
+def test_attn_prep_rows_equals_a_prep_a_row(fl, dev, rng, kv8):
+    """fl_attn_prep_rows (a batched decode step's rows, one launch) against
+    one attn_prep (attn_prep_q8) call a row, bit for bit: q and k rewritten
+    in place and each row's K / V stored in its own cache at its own
+    position -- caches of different capacities, positions from 0 to deep in
+    a prompt, five rows -- and nothing else of the caches touched."""
+    caps = [64, 4096, 100000, 32, 2048]
+    pos = [0, 4095, 99999, 17, 1000]
+    B = len(caps)
+    qg = f16(rng.standard_normal((B, 24, 512)))
+    k = f16(rng.standard_normal((B, 4, 256)) * 2)
+    v = f16(rng.standard_normal((B, 4, 256)))
+    wq = to_dev((rng.standard_normal(256) * 0.2).astype(np.float32), dev)
+    wk = to_dev((rng.standard_normal(256) * 0.2).astype(np.float32), dev)
+
+    def caches():
+        if kv8:
+            return [fl.ops.kv8_cache(c) for c in caps], [fl.ops.kv8_cache(c) for c in caps]
+        return ([torch.full((c, 4, 256), 3.0, dtype=torch.float16, device=dev) for c in caps],
+                [torch.full((c, 4, 256), -2.0, dtype=torch.float16, device=dev) for c in caps])
+
+    kb, vb = caches()
+    qd, kd, vd = to_dev(qg, dev), to_dev(k, dev), to_dev(v, dev)
+    fl.ops.attn_prep_rows(qd, kd, vd, wq, wk, kb, vb, pos, caps, kv8=kv8)
+    ks, vs = caches()
+    q1, k1 = to_dev(qg, dev), to_dev(k, dev)
+    for b in range(B):
+        if kv8:
+            fl.ops.attn_prep_q8(q1[b:b + 1], k1[b:b + 1], vd[b:b + 1], wq, wk, ks[b], vs[b],
+                                pos0=pos[b], max_pos=caps[b], T=1)
+        else:
+            fl.ops.attn_prep(q1[b:b + 1], k1[b:b + 1], vd[b:b + 1], wq, wk, ks[b], vs[b],
+                             pos0=pos[b], T=1)
+    torch.cuda.synchronize()
+    assert torch.equal(qd, q1) and torch.equal(kd, k1)
+    for b in range(B):
+        assert torch.equal(kb[b], ks[b]) and torch.equal(vb[b], vs[b]), b
+    with pytest.raises(ValueError):                       # a position past its capacity
+        fl.ops.attn_prep_rows(qd, kd, vd, wq, wk, kb, vb, [0, 4096, 0, 0, 0], caps, kv8=kv8)
