@@ -284,16 +284,21 @@ chunk_prep_kernel(const f16* __restrict__ q, const f16* __restrict__ k,
         __syncthreads();   // the gates in; every K / Q read (or T / M o QK^T
                            // read of the previous head) done
 
-        // A = strictly lower beta_i e^{g_i - g_j} k_i.k_j and M o QK^T
+        // A = strictly lower beta_i e^{g_i - g_j} k_i.k_j and M o QK^T. The
+        // 32 x 32 block above the diagonal (wave 1) is left alone: nothing
+        // reads M there, and T's blocks below the diagonal are written there
+        // (transposed) before anything reads it
+        if (bi >= bj) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int i = 32 * bi + 8 * (r >> 2) + 4 * hh + (r & 3);
-            const int j = 32 * bj + ql;
-            // e^{g_i - g_j}, taken for every pair (above the diagonal it may be
-            // inf, and is not selected)
-            const float ratio = fast_exp2((sG[i] - sG[j]) * FL_LOG2E);
-            sA[i][j] = j < i ? sB[i] * ratio * kk[r] : 0.f;
-            sM[i][j] = j <= i ? ratio * qk[r] : 0.f;
+            for (int r = 0; r < 16; ++r) {
+                const int i = 32 * bi + 8 * (r >> 2) + 4 * hh + (r & 3);
+                const int j = 32 * bj + ql;
+                // e^{g_i - g_j}, taken for every pair (above the diagonal it may
+                // be inf, and is not selected)
+                const float ratio = fast_exp2((sG[i] - sG[j]) * FL_LOG2E);
+                sA[i][j] = j < i ? sB[i] * ratio * kk[r] : 0.f;
+                sM[i][j] = j <= i ? ratio * qk[r] : 0.f;
+            }
         }
         __syncthreads();
 
@@ -329,15 +334,19 @@ chunk_prep_kernel(const f16* __restrict__ q, const f16* __restrict__ k,
             __syncthreads();
         }
 
-        // the scales: block maxima of |T| and |M o QK^T|
+        // the scales: block maxima of |T| and |M o QK^T| over their lower
+        // triangles, a row of each a pass (the lanes along it: no bank
+        // conflicts). sA[r][c] holds T[c][r] where c >= r (A's values below)
         float mt = 0.f, mq = 0.f;
 #pragma unroll
         for (int m = 0; m < CK_C * CK_C / 256; ++m) {
-            const int idx = tid + 256 * m, i = idx >> 6, j = idx & 63;
-            float tv = sA[j][i];   // T[i][j], transposed: A's values where j > i
+            const int idx = tid + 256 * m, r = idx >> 6, c = idx & 63;
+            float tv = sA[r][c];
             keep(tv);
-            mt = fmaxf(mt, i >= j ? fabsf(tv) : 0.f);
-            mq = fmaxf(mq, fabsf(sM[i][j]));
+            mt = fmaxf(mt, c >= r ? fabsf(tv) : 0.f);
+            float qv = sM[r][c];
+            keep(qv);
+            mq = fmaxf(mq, c <= r ? fabsf(qv) : 0.f);
         }
         mt = wave_max(mt);
         mq = wave_max(mq);
@@ -355,23 +364,38 @@ chunk_prep_kernel(const f16* __restrict__ q, const f16* __restrict__ k,
         // the operands: slot (T or M o QK^T; block f, lane l = 16 g + i) holds
         // row 16 mb + i at columns 32 kq + kap(g, e), its hi and lo halves
         // 6 KiB apart
+        // (which matrix a pass takes is the same for a whole wave: 6 blocks x
+        // 64 lanes of T, then 6 of M o QK^T, over 3 passes of 256 threads)
 #pragma unroll
         for (int m = 0; m < 3; ++m) {
             const int s = tid + 256 * m;
             const bool isq = s >= CK_NF * 64;
             const int f = (s % (CK_NF * 64)) >> 6, l = s & 63;
             const int g = l >> 4, row = 16 * f_mb(f) + (l & 15), kq = f_kq(f);
+            float xs[8];
+            if (isq) {   // M o QK^T[row][32 kq + kap(g, e)]: two row segments of 4
+                const f32x4 a = *(const f32x4*)&sM[row][32 * kq + 4 * g];
+                const f32x4 b = *(const f32x4*)&sM[row][32 * kq + 16 + 4 * g];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    xs[e] = a[e] * q_sc;
+                    xs[4 + e] = b[e] * q_sc;
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const int col = 32 * kq + (e < 4 ? 4 * g + e : 12 + 4 * g + e);
+                    float ta = sA[col][row];   // T[row][col], transposed
+                    keep(ta);
+                    xs[e] = (row >= col ? ta : 0.f) * t_sc;
+                }
+            }
             f16x8 hi, lo;
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
-                const int col = 32 * kq + (e < 4 ? 4 * g + e : 12 + 4 * g + e);
-                float ta = sA[col][row];   // T[row][col], transposed
-                keep(ta);
-                const float mq_ = sM[row][col];
-                const float xs = isq ? mq_ * q_sc : (row >= col ? ta : 0.f) * t_sc;
-                const f16 h = (f16)xs;
+                const f16 h = (f16)xs[e];
                 hi[e] = h;
-                lo[e] = (f16)(xs - (float)h);
+                lo[e] = (f16)(xs[e] - (float)h);
             }
             char* dst = blk + (isq ? WS_Q_HI : WS_T_HI) + (f * 64 + l) * 16;
             *(f16x8*)dst = hi;
