@@ -495,3 +495,29 @@ def test_prefill_q8_kv_split_vs_oracle(fl, dev, orc, rng, T, pos0, split):
                                     T=T)
     err, ok = close_rel(z.cpu().numpy(), want, ATOL, RTOL)
     assert ok, f"T={T} pos0={pos0} split={split}: max|err| {err}"
+
+
+@pytest.mark.parametrize("head_dim,z_pitch,split,T", [(256, 256, 4, 300), (128, 128, 13, 7),
+                                                      (64, 72, 9, 5), (256, 258, 8, 3)])
+def test_merge_layouts_vs_oracle(fl, dev, orc, rng, head_dim, z_pitch, split, T):
+    """fl_attention_merge on random partials (empty ones among them) against
+    the oracle's merge: the wavefront-a-row kernel for head_dim <= 256 and a
+    pitch of 4 halves (head_dim 128 and 64 leave lanes without dims; 9 and 13
+    splits a partial batch of 8), the block-a-row kernel for an odd pitch
+    (258). Bar: the attention bar and 1e-2 max|want|."""
+    H = 24
+    pacc = rng.standard_normal((T, H, split, head_dim)).astype(np.float32)
+    pm = (rng.standard_normal((T, H, split)) * 3).astype(np.float32)
+    pd = rng.uniform(0.5, 4.0, (T, H, split)).astype(np.float32)
+    pm[:, :, 1::3] = -1e30                       # empty partials: m = -1e30, d = 0, acc = 0
+    pd[:, :, 1::3] = 0
+    pacc[:, :, 1::3] = 0
+    want = orc.attention_merge(pacc, pm, pd, H, head_dim, T, split, z_pitch=z_pitch)
+    z = torch.zeros((T, H, z_pitch), dtype=torch.float16, device=dev)
+    fl.ops.attention_merge(to_dev(pacc, dev), to_dev(pm, dev), to_dev(pd, dev), z,
+                           head_dim=head_dim, z_pitch=z_pitch, T=T, split=split)
+    torch.cuda.synchronize()
+    got = z.cpu().numpy()
+    err, ok = close_rel(got[..., :head_dim], want[..., :head_dim], ATOL, RTOL)
+    assert ok and err <= 1e-2 * float(np.abs(want[..., :head_dim].astype(np.float32)).max()), err
+    assert not got[..., head_dim:].any(), "wrote past head_dim"
