@@ -616,8 +616,8 @@ def bench_decode_flow(torch, fl, L, kv8=True, Bq=4):
     the model's 64 layers on HybridRuntime.forward_batch (the backend's
     batched rows, runtime.py:3114-3146 and 2865-2878): per attention layer
     each row's prep into its own cache and one batched decode attention
-    launch, per GDN layer one fused conv + delta-rule launch over the rows and
-    the gated output norm. The sequences hold L, L - 97, ... cached positions
+    launch, per GDN layer one launch over the rows of the conv, the delta rule
+    and the gated output norm. The sequences hold L, L - 97, ... cached positions
     (the caches' contents do not change the work). The step is captured in a
     HIP graph and replayed -- each replay the same step, rewriting the same
     cache rows and advancing the recurrences -- so the line is the GPU time of
@@ -632,7 +632,8 @@ def bench_decode_flow(torch, fl, L, kv8=True, Bq=4):
               "gdn": ("linear_attention",) * 48}
     row = 4 * 256 + 4 * 8 * 2 if kv8 else 4 * 256 * 2   # bytes of a position's K (or V)
     attn_bytes = 2 * row * sum(lens)                          # K and V read a layer
-    gdn_bytes = gdn_decode_bytes(B=Bq) + 3 * Bq * 48 * 128 * 2   # + the output norm
+    # the decode step's bytes (its output is the normed one) + the norm's gate z
+    gdn_bytes = gdn_decode_bytes(B=Bq) + Bq * 48 * 128 * 2
     for name, types in scheds.items():
         rt = rtm.HybridRuntime(rtm.random_weights(types, seed=3, device=dev), layer_types=types,
                                kv8=kv8, device=dev)

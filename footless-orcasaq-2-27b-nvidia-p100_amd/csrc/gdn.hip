@@ -772,19 +772,13 @@ gdn_decode_kernel(const f16* __restrict__ x, int x_stride, const f16* __restrict
 // and its __shfl_down tree over offsets 16, 8, 4, 2, 1 is lane exchanges at
 // distance 8, 4, 2, 1 then the in-lane pair; the 4 warp sums combine as
 // block_reduce_sum does, (r0 + r2) + (r1 + r3).
-__global__ void __launch_bounds__(GR_THREADS)
-rmsnorm_gated_kernel(const f16* __restrict__ o, const f16* __restrict__ z,
-                     const float* __restrict__ w, f16* __restrict__ y, int rows, int pitch,
-                     int n_rows, float eps) {
-    const int lane = threadIdx.x & 63;
-    const int rid = blockIdx.x * (GR_THREADS / 64) + (threadIdx.x >> 6);
-    if (rid >= n_rows) return;   // whole wavefronts; no workgroup barrier
-    const int t = rid / rows, r = rid - t * rows;
-    const size_t base = ((size_t)t * rows + r) * pitch + 2 * lane;
-    typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
-    const f16x2 ov = *(const f16x2*)(o + base);
-    const f16x2 zv = *(const f16x2*)(z + base);
-    const float x0 = (float)ov[0], x1 = (float)ov[1];
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+// One row's norm from a wave holding it two values a lane (x0 = o[2l], x1 =
+// o[2l + 1], z0 / z1 and w0 / w1 the gate and gamma there): the row's output
+// at the lane's two places.
+__device__ __forceinline__ f16x2 gated_rms_pair(float x0, float x1, float z0, float z1, float w0,
+                                                float w1, float eps) {
     float s0 = fmaf(x0, x0, 0.f), s1 = fmaf(x1, x1, 0.f);
 #pragma unroll
     for (int d = 8; d > 0; d >>= 1) {
@@ -797,9 +791,135 @@ rmsnorm_gated_kernel(const f16* __restrict__ o, const f16* __restrict__ z,
     };
     const float ss = (at(ws, 0) + at(ws, 32)) + (at(ws, 16) + at(ws, 48));
     const float inv = 1.f / sqrtf(ss / (float)GR_K + eps);
-    const f16x2 out = {f16_sat(x0 * inv * w[2 * lane] * silu_f((float)zv[0])),
-                       f16_sat(x1 * inv * w[2 * lane + 1] * silu_f((float)zv[1]))};
-    *(f16x2*)(y + base) = out;
+    return (f16x2){f16_sat(x0 * inv * w0 * silu_f(z0)), f16_sat(x1 * inv * w1 * silu_f(z1))};
+}
+
+__global__ void __launch_bounds__(GR_THREADS)
+rmsnorm_gated_kernel(const f16* __restrict__ o, const f16* __restrict__ z,
+                     const float* __restrict__ w, f16* __restrict__ y, int rows, int pitch,
+                     int n_rows, float eps) {
+    const int lane = threadIdx.x & 63;
+    const int rid = blockIdx.x * (GR_THREADS / 64) + (threadIdx.x >> 6);
+    if (rid >= n_rows) return;   // whole wavefronts; no workgroup barrier
+    const int t = rid / rows, r = rid - t * rows;
+    const size_t base = ((size_t)t * rows + r) * pitch + 2 * lane;
+    const f16x2 ov = *(const f16x2*)(o + base);
+    const f16x2 zv = *(const f16x2*)(z + base);
+    *(f16x2*)(y + base) = gated_rms_pair((float)ov[0], (float)ov[1], (float)zv[0], (float)zv[1],
+                                         w[2 * lane], w[2 * lane + 1], eps);
+}
+
+// A decode step (T = 1, the conv in the kernel) and the output norm after it
+// in one launch: a workgroup owns a whole v head (128 rows, 8 lanes a row, 16
+// waves), so the norm over the head's 128 outputs is a reduction inside the
+// workgroup instead of a second launch. Waves 0-1 convolve and sum the
+// squares of the k head's channels, waves 2-3 the q head's, waves 4-5 the
+// head's 128 v channels, wave 6 forms the gates -- barrier -- the k / q
+// channels are normalised into LDS -- barrier -- every wave runs the delta
+// rule on its 8 rows and stores them, the rows' outputs (rounded to fp16, the
+// value the unfused step writes) go to LDS -- barrier -- wave 0 runs the
+// norm on them (gated_rms_pair, the unfused norm's arithmetic) and writes the
+// head's 128 normed values. Every value equals the unfused pair's bit for
+// bit. One workgroup a head and sequence: 48 B workgroups, so below B = 5 a
+// CU holds at most one; the small inputs are issued ahead of the state as in
+// gdn_decode_kernel.
+constexpr int GN_ROWS = 128;                  // the v head's rows
+constexpr int GN_THREADS = 8 * GN_ROWS;       // 8 lanes a row
+
+__global__ void __launch_bounds__(GN_THREADS)
+gdn_decode_normed_kernel(const f16* __restrict__ x, int x_stride, const f16* __restrict__ conv_w,
+                         GdnSeqs seqs, const float* __restrict__ ga, const float* __restrict__ gb,
+                         int ab_stride, const float* __restrict__ A_log,
+                         const float* __restrict__ dt_bias, const f16* __restrict__ z,
+                         int z_pitch, const float* __restrict__ norm_w, f16* __restrict__ y,
+                         int y_pitch, int n_kheads, float out_scale, float l2eps, float norm_eps,
+                         int group) {
+    __shared__ __attribute__((aligned(16))) float ssq[8];   // k's, q's 32-channel sums of squares
+    __shared__ __attribute__((aligned(16))) float snorm[2 * GR_K];   // k | q, normalised
+    __shared__ float sv[GN_ROWS];                                    // the head's v values
+    __shared__ float sg[2];                                          // beta, decay
+    __shared__ __attribute__((aligned(16))) float so[GN_ROWS];       // the rows' fp16 outputs
+    const int hv = blockIdx.x, b = blockIdx.y;
+    float* const Sb = seqs.S[b];
+    const f16* const cst_in = seqs.cst_in[b];
+    f16* const cst_out = seqs.cst_out[b];
+    const int pos0 = seqs.pos0[b];
+    asm volatile("" ::"s"(Sb), "s"(cst_in), "s"(cst_out), "s"(pos0), "s"(x), "s"(conv_w), "s"(ga),
+                 "s"(gb), "s"(A_log), "s"(dt_bias), "s"(x_stride), "s"(ab_stride), "s"(z),
+                 "s"(z_pitch), "s"(norm_w), "s"(y), "s"(y_pitch), "s"(n_kheads), "s"(group),
+                 "s"(out_scale), "s"(l2eps), "s"(norm_eps));
+    __builtin_amdgcn_sched_barrier(0);
+    const int hk = hv / group;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int ri = tid >> 3, c0 = 4 * (tid & 7);
+    float* Srow = Sb + ((size_t)hv * GN_ROWS + ri) * GR_K + c0;
+    // waves 0-5: channel i of the k | q | v heads (uniform per wave)
+    const int role = w >> 1, i = tid & 127;
+    const int ch = role == 0   ? n_kheads * GR_K + hk * GR_K + i
+                   : role == 1 ? hk * GR_K + i
+                               : 2 * n_kheads * GR_K + hv * GN_ROWS + i;
+    const bool conv_wave = w < 6;
+    const f16* x0 = x + (size_t)b * x_stride;
+    ConvIn cc;
+    if (conv_wave) cc = conv1_load(x0, conv_w, cst_in, ch);
+    const int vz = opaque_zero();
+    const float dtb = dt_bias[hv + vz], A = A_log[hv + vz];
+    const size_t ab0 = (size_t)b * ab_stride + hv + vz;
+    const float ga0 = ga[ab0], gb0 = gb[ab0];
+    const size_t zo = (size_t)b * z_pitch + (size_t)hv * GN_ROWS + 2 * lane;
+    f16x2 zv = {};
+    float nw0 = 0.f, nw1 = 0.f;
+    if (w == 0) {
+        zv = *(const f16x2*)(z + zo);
+        nw0 = norm_w[2 * lane];
+        nw1 = norm_w[2 * lane + 1];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    float reg[16];
+    load_row16_nt(reg, Srow);
+    __builtin_amdgcn_sched_barrier(0);
+    float xv = 0.f;
+    if (conv_wave) {
+        xv = conv1_apply(cc, pos0 > 0);
+        if (role < 2) {
+            const float tr = warp32_tree_lane0(xv * xv);
+            if ((lane & 31) == 0) ssq[tid >> 5] = tr;
+        } else {
+            sv[i] = xv;
+        }
+    } else if (w == 6) {
+        const float bt_ = gdn_beta(gb0);
+        const float dt_ = gdn_decay(ga0 + dtb, A);
+        if (lane == 0) {
+            sg[0] = bt_;
+            sg[1] = dt_;
+        }
+    }
+    __syncthreads();
+    if (role < 2) {   // the reference's order (r0 + r2) + (r1 + r3)
+        const f32x4 r = *(const f32x4*)&ssq[4 * role];
+        const float den = sqrtf(((r[0] + r[2]) + (r[1] + r[3])) + l2eps);
+        snorm[tid] = (float)f16_sat(xv / den);
+    }
+    __syncthreads();
+    const float vt = sv[ri], bt = sg[0], dt = sg[1];
+    float kk[16], qq[16];
+    gather16(kk, snorm, c0);
+    gather16(qq, snorm + GR_K, c0);
+    __builtin_amdgcn_sched_barrier(0);
+    delta_update(reg, kk, vt, bt, dt);
+    store_row16_nt(Srow, reg);
+    const float o = delta_out(reg, qq);
+    if (c0 == 0) so[ri] = (float)f16_sat(o * out_scale);
+    __syncthreads();
+    if (w == 0) {
+        const float x0v = so[2 * lane], x1v = so[2 * lane + 1];
+        *(f16x2*)(y + (size_t)b * y_pitch + (size_t)hv * GN_ROWS + 2 * lane) =
+            gated_rms_pair(x0v, x1v, (float)zv[0], (float)zv[1], nw0, nw1, norm_eps);
+    }
+    if (conv_wave && (role == 2 || hv % group == 0))   // one v head a k head stores its ring
+        conv1_ring_store(cc, pos0 > 0, cst_out, ch);
 }
 
 // The same norm, 16-byte aligned rows: 16 lanes a row (lane j of the row holds
@@ -1120,6 +1240,46 @@ int fl_gdn_decode(const void* x, int x_stride, int conv_fused, const void* conv_
                            a, b, ab_stride, A_log, dt_bias, (f16*)y, y_stride, ck_step, T,
                            n_kheads, n_vheads, V, out_scale, l2eps, n_vheads / n_kheads, delay);
     return fl::check_launch("gdn_decode");
+}
+
+int fl_gdn_decode_normed(const void* x, int x_stride, const void* conv_w,
+                         const void* const* cst_in, void* const* cst_out, const int* pos0,
+                         const float* a, const float* b, int ab_stride, const float* A_log,
+                         const float* dt_bias, float* const* S, const void* z, int z_pitch,
+                         const float* norm_w, void* y, int y_pitch, int B, int n_kheads,
+                         int n_vheads, int K, int V, float out_scale, float l2eps, float norm_eps,
+                         fl_stream_t stream) {
+    FL_REQUIRE(x && conv_w && cst_in && cst_out && pos0 && a && b && A_log && dt_bias && S && z &&
+                   norm_w && y,
+               "null pointer");
+    FL_REQUIRE(B >= 1 && B <= FL_MAX_SEQS, "1 <= B <= FL_MAX_SEQS");
+    FL_REQUIRE(K == GR_K && V == GN_ROWS, "K and V must be 128");
+    FL_REQUIRE(n_kheads >= 1 && n_vheads >= 1 && n_vheads % n_kheads == 0,
+               "n_vheads % n_kheads == 0");
+    FL_REQUIRE(x_stride >= 2 * n_kheads * K + n_vheads * V, "x_stride covers q|k|v");
+    FL_REQUIRE(ab_stride >= n_vheads, "ab_stride >= n_vheads");
+    FL_REQUIRE(z_pitch >= n_vheads * V && y_pitch >= n_vheads * V && z_pitch % 2 == 0 &&
+                   y_pitch % 2 == 0,
+               "z_pitch, y_pitch >= n_vheads * V and even");
+    FL_REQUIRE(((uintptr_t)z & 3u) == 0 && ((uintptr_t)y & 3u) == 0 && ((uintptr_t)norm_w & 7u) == 0,
+               "aligned z, y, norm_w");
+    FL_REQUIRE(norm_eps >= 0.f, "norm_eps >= 0");
+    GdnSeqs seqs = {};
+    for (int i = 0; i < B; ++i) {
+        FL_REQUIRE(S[i] && aligned16(S[i]), "16-byte aligned S[b]");
+        FL_REQUIRE(pos0[i] >= 0, "pos0 >= 0");
+        FL_REQUIRE(cst_in[i] && cst_out[i] && cst_in[i] != cst_out[i],
+                   "cst_in[b], cst_out[b] distinct");
+        seqs.S[i] = S[i];
+        seqs.pos0[i] = pos0[i];
+        seqs.cst_in[i] = (const f16*)cst_in[i];
+        seqs.cst_out[i] = (f16*)cst_out[i];
+    }
+    hipLaunchKernelGGL(gdn_decode_normed_kernel, dim3(n_vheads, B), dim3(GN_THREADS), 0,
+                       (hipStream_t)stream, (const f16*)x, x_stride, (const f16*)conv_w, seqs, a, b,
+                       ab_stride, A_log, dt_bias, (const f16*)z, z_pitch, norm_w, (f16*)y, y_pitch,
+                       n_kheads, out_scale, l2eps, norm_eps, n_vheads / n_kheads);
+    return fl::check_launch("gdn_decode_normed");
 }
 
 

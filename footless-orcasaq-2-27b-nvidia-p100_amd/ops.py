@@ -600,6 +600,40 @@ def gdn_decode(x, S, a, b, A_log, dt_bias, y=None, *, T: int, pos0s, conv_fused:
     return y
 
 
+def gdn_decode_normed(x, S, a, b, A_log, dt_bias, z, norm_w, y=None, *, pos0s, conv_w, cst_in,
+                      cst_out, n_kheads: int = GDN_K_HEADS, n_vheads: int = GDN_V_HEADS,
+                      K: int = GDN_K, V: int = GDN_V, x_stride: int = QKV_ROWS,
+                      ab_stride: int = GDN_V_HEADS, out_scale: float = Q_SCALE,
+                      l2eps: float = L2_EPS, norm_eps: float = GDN_NORM_EPS):
+    """A plain decode step of B sequences and its output norm in one launch
+    (gdn_scan_rows_f with gdn_conv1, kernels.cu:2916-3070, then rmsnorm_gated,
+    kernels.cu:335-358, as runtime.py:3040-3053 and 3063-3065 run them): the
+    values gdn_decode(conv_fused=True) followed by rmsnorm_gated give. x [B,
+    x_stride] fp16 raw q|k|v rows; z [B, n_vheads * V] fp16 (rows at z's
+    stride); S, cst_in, cst_out: lists of B buffers; a, b [B, ab_stride] fp32.
+    Returns y [B, n_vheads * V] fp16 (new unless given)."""
+    B = len(S)
+    _contig(x, "x"), _contig(a, "a"), _contig(b, "b")
+    width = n_vheads * V
+    if y is None:
+        y = torch.empty((B, width), dtype=F16, device=x.device)
+    # one row a sequence, the heads contiguous inside it (view raises if not)
+    z_pitch, y_pitch = z.view(B, width).stride(0), y.view(B, width).stride(0)
+    state = n_vheads * V * K
+    ci = _lib.ptr_array([_ptr(c, F16, "cst_in[b]", x_stride * 3) for c in cst_in])
+    co = _lib.ptr_array([_ptr(c, F16, "cst_out[b]", x_stride * 3) for c in cst_out])
+    _lib.call("fl_gdn_decode_normed", _ptr(x, F16, "x", B * x_stride), x_stride,
+              _ptr(conv_w, F16, "conv_w", x_stride * 4), ci, co, _lib.int_array(pos0s),
+              _ptr(a, F32, "a", B * ab_stride), _ptr(b, F32, "b", B * ab_stride), ab_stride,
+              _ptr(A_log, F32, "A_log", n_vheads), _ptr(dt_bias, F32, "dt_bias", n_vheads),
+              _lib.ptr_array([_ptr(s, F32, "S[b]", state) for s in S]),
+              _ptr(z, F16, "z", (B - 1) * z_pitch + width), z_pitch,
+              _ptr(norm_w, F32, "norm_w", V), _ptr(y, F16, "y", (B - 1) * y_pitch + width),
+              y_pitch, B, n_kheads, n_vheads, K, V, float(out_scale), float(l2eps),
+              float(norm_eps), _stream())
+    return y
+
+
 def gdn_chunked_work_bytes(T: int, n_vheads: int = GDN_V_HEADS, K: int = GDN_K, V: int = GDN_V,
                            chunk: int = GDN_CHUNK) -> int:
     return int(_lib.lib().fl_gdn_chunked_work_bytes(T, n_vheads, K, V, chunk))

@@ -325,22 +325,23 @@ class HybridRuntime:
 
     def _gdn(self, st: SeqState, i: int, qkv, zg, a, b, T: int, pos0: int,
              verify: bool) -> torch.Tensor:
-        """runtime.py:2961-3112 for one sequence. Decode (T = 1): the conv runs
-        inside the fused step, conv[phase] -> conv[phase ^ 1]. Verify (T <=
-        1 + mtp_k): the conv rows leave row 0's state in place in conv[phase],
-        row 1's in conv[phase ^ 1], row 2's in the spare; the fused step keeps
-        the recurrent state after each row but the last as a checkpoint.
-        Prefill: conv over the chunk, the q / k L2 norm, the gates, and the
-        chunked WY scan. Then the gated output norm."""
+        """runtime.py:2961-3112 for one sequence. Decode (T = 1): one launch
+        runs the conv (conv[phase] -> conv[phase ^ 1]), the fused step and the
+        gated output norm. Verify (T <= 1 + mtp_k): the conv rows leave row
+        0's state in place in conv[phase], row 1's in conv[phase ^ 1], row 2's
+        in the spare; the fused step keeps the recurrent state after each row
+        but the last as a checkpoint. Prefill: conv over the chunk, the q / k
+        L2 norm, the gates, and the chunked WY scan. Verify and prefill end
+        with the gated output norm."""
         g = self.gdn_ord[i]
         wt = self.w[i]
         S = st.s[g]
         cin, cout = st.conv[st.phase, g], st.conv[st.phase ^ 1, g]
-        if T == 1 and not verify:
-            y = ops.gdn_decode(qkv[None], [S], a[None], b[None], wt.A_log, wt.dt_bias, T=1,
-                               pos0s=[pos0], conv_fused=True, conv_w=wt.conv_w,
-                               cst_in=[cin], cst_out=[cout])[0]
-        elif verify:
+        if T == 1 and not verify:   # the step and its output norm, one launch
+            return ops.gdn_decode_normed(qkv, [S], a, b, wt.A_log, wt.dt_bias, zg, wt.norm_w,
+                                         pos0s=[pos0], conv_w=wt.conv_w, cst_in=[cin],
+                                         cst_out=[cout]).view(1, GDN_V_HEADS, GDN_V)
+        if verify:
             c = torch.empty_like(qkv)
             ops.conv1d_causal_rows(qkv, wt.conv_w, cin, c, cin, cout, self.snap_c[g], T=T,
                                    pos0=pos0)
@@ -441,9 +442,9 @@ class HybridRuntime:
         """One decode step of several sequences (one token each), as
         `_step_rows` runs it: per full-attention layer one launch of every
         row's prep into its own cache, then one attention launch over all
-        rows; per GDN layer one fused conv + delta-rule launch over all rows.
-        `proj` hands the B rows stacked ([B, ...] where forward takes [T,
-        ...])."""
+        rows; per GDN layer one fused conv + delta-rule + output-norm launch
+        over all rows. `proj` hands the B rows stacked ([B, ...] where
+        forward takes [T, ...])."""
         B = len(states)
         if B != len(tokens) or B < 1:
             raise ValueError("one token a sequence")
@@ -472,13 +473,12 @@ class HybridRuntime:
             else:
                 g, wt = self.gdn_ord[i], self.w[i]
                 qkv, zg, a, b = proj.gdn_in(i, B)
-                y = ops.gdn_decode(qkv[:, None], [st.s[g] for st in states], a[:, None],
-                                   b[:, None], wt.A_log, wt.dt_bias, T=1, pos0s=pos0s,
-                                   conv_fused=True, conv_w=wt.conv_w,
-                                   cst_in=[st.conv[st.phase, g] for st in states],
-                                   cst_out=[st.conv[st.phase ^ 1, g] for st in states])
-                proj.layer_out(i, ops.rmsnorm_gated(y.view(B, GDN_V_HEADS, GDN_V), zg,
-                                                    wt.norm_w, T=B))
+                yn = ops.gdn_decode_normed(qkv, [st.s[g] for st in states], a, b, wt.A_log,
+                                           wt.dt_bias, zg, wt.norm_w, pos0s=pos0s,
+                                           conv_w=wt.conv_w,
+                                           cst_in=[st.conv[st.phase, g] for st in states],
+                                           cst_out=[st.conv[st.phase ^ 1, g] for st in states])
+                proj.layer_out(i, yn.view(B, GDN_V_HEADS, GDN_V))
         for st, t in zip(states, tokens):
             st.tokens.append(int(t))
             st.fed = len(st.tokens)

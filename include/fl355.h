@@ -396,6 +396,24 @@ int fl_gdn_decode(const void* x, int x_stride, int conv_fused, const void* conv_
 int fl_rmsnorm_gated(const void* o, const void* z, const float* w, void* y, int n, int rows,
                      int pitch, int T, float eps, fl_stream_t stream);
 
+/* ---- GDN decode step with its output norm -----------------------------------
+ * fl_gdn_decode with conv_fused = 1 and T = 1, followed by fl_rmsnorm_gated
+ * over its output, in one launch: y[b] = rmsnorm_gated(the step's output of
+ * sequence b, z[b], norm_w), bit for bit the pair's values. The step's own
+ * fp16 output is not written. z [B][z_pitch] f16 (the gate, head hv at
+ * hv*V), y [B][y_pitch] f16; the other arguments as fl_gdn_decode's.
+ * Replaces the pair kernels.cu:2954-3070 gdn_scan_rows_f (+ gdn_conv1
+ * 2916-2941) then kernels.cu:335-358 rmsnorm_gated as a decode step runs them
+ * (runtime.py:3040-3053, then 3063-3065). K == V == 128, B <= FL_MAX_SEQS;
+ * z and y 4-byte aligned, even pitches, norm_w 8-byte aligned. */
+int fl_gdn_decode_normed(const void* x, int x_stride, const void* conv_w,
+                         const void* const* cst_in, void* const* cst_out, const int* pos0,
+                         const float* a, const float* b, int ab_stride, const float* A_log,
+                         const float* dt_bias, float* const* S, const void* z, int z_pitch,
+                         const float* norm_w, void* y, int y_pitch, int B, int n_kheads,
+                         int n_vheads, int K, int V, float out_scale, float l2eps,
+                         float norm_eps, fl_stream_t stream);
+
 /* ---- GDN chunked prefill --------------------------------------------------
  * Chunked (WY / UT transform) GDN prefill: the same recurrence as
  * fl_gdn_scan over T tokens in chunks of `chunk` tokens, fp32 state carried

@@ -98,6 +98,20 @@ def test_argument_checks_refuse_before_launch(fl):
     assert _call(fl, "fl_attn_prep_rows", fake, 512, fake, fake, fake, fake, arr, arr, over, caps,
                  2, 1, 24, 4, 256, 64, 1e7, 1e-6, None) == 1
     assert b"max_pos" in lib.fl_last_error()
+    # decode + output norm: V other than 128, more rows than FL_MAX_SEQS, a
+    # sequence's two conv buffers aliased, an odd z pitch
+    pp = fl._lib.ptr_array([0x2000] * 17)
+    pq = fl._lib.ptr_array([0x3000] * 17)
+    p0 = fl._lib.int_array([5] * 17)
+
+    def normed(B, V, cin, z_pitch):
+        return _call(fl, "fl_gdn_decode_normed", fake, 10240, fake, cin, pq, p0, fake, fake, 48,
+                     fake, fake, pp, fake, z_pitch, fake, fake, 6144, B, 16, 48, 128, V, 0.088,
+                     1e-6, 1e-6, None)
+    assert normed(4, 64, pp, 6144) == 1
+    assert normed(17, 128, pp, 6144) == 1
+    assert normed(2, 128, pq, 6144) == 1 and b"distinct" in lib.fl_last_error()
+    assert normed(2, 128, pp, 6145) == 1 and b"pitch" in lib.fl_last_error()
 
 
 def test_work_size_queries(fl):

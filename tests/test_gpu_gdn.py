@@ -574,3 +574,62 @@ def test_rmsnorm_gated_vs_oracle(fl, dev, orc, rng, T):
     d = np.abs(got.view(np.int16).astype(np.int32) - want.view(np.int16).astype(np.int32))
     print(f"rmsnorm_gated T={T}: max {d.max()} ulp, {(d > 0).sum()} values differ")
     assert d.max() <= 1
+
+
+@pytest.mark.parametrize("B", [1, 4, 7])
+def test_decode_normed_equals_decode_then_norm(fl, dev, orc, rng, B):
+    """The one-launch decode step + output norm against the pair it replaces
+    (gdn_decode with the conv fused, then rmsnorm_gated) over three steps in
+    a row: the normed output, the state and both conv rings bit for bit.
+    Sequences start at pos0 0 (no history) and past it; with B = 7 the gate
+    and the output rows carry padding, which must stay untouched. Step 0 is
+    also checked against the oracle's pair."""
+    w, A_log, dt = _decode_weights(rng)
+    A_log = (rng.standard_normal(NV) * 0.3).astype(np.float32)
+    dt = (rng.standard_normal(NV) * 0.3).astype(np.float32)
+    nw = (1 + rng.standard_normal(128) * 0.2).astype(np.float32)
+    width = NV * 128
+    zp, yp = (width + 64, width + 32) if B == 7 else (width, width)
+    S0 = (rng.standard_normal((B, NV, 128, 128)) * 0.02).astype(np.float32)
+    ring0 = rng.standard_normal((B, ROW, 3)).astype(np.float16)
+    starts = [0 if b % 2 == 0 else 9 + b for b in range(B)]
+    wd, Ad, dtd, nwd = to_dev(w, dev), to_dev(A_log, dev), to_dev(dt, dev), to_dev(nw, dev)
+    Sf = [to_dev(S0[b], dev) for b in range(B)]
+    Su = [to_dev(S0[b], dev) for b in range(B)]
+    rf = [[to_dev(ring0[b], dev), torch.zeros((ROW, 3), dtype=torch.float16, device=dev)]
+          for b in range(B)]
+    ru = [[r[0].clone(), r[1].clone()] for r in rf]
+    for step in range(3):
+        x = rng.standard_normal((B, ROW)).astype(np.float16)
+        a = rng.standard_normal((B, NV)).astype(np.float32)
+        bb = rng.standard_normal((B, NV)).astype(np.float32)
+        z = np.zeros((B, zp), np.float16)
+        z[:, :width] = rng.standard_normal((B, width)) * 2
+        xd, ad, bd, zd = to_dev(x, dev), to_dev(a, dev), to_dev(bb, dev), to_dev(z, dev)
+        ph = step & 1
+        pos = [s + step for s in starts]
+        yf = torch.full((B, yp), 7.0, dtype=torch.float16, device=dev)
+        fl.ops.gdn_decode_normed(xd, Sf, ad, bd, Ad, dtd, zd[:, :width], nwd, yf[:, :width],
+                                 pos0s=pos, conv_w=wd, cst_in=[r[ph] for r in rf],
+                                 cst_out=[r[ph ^ 1] for r in rf])
+        yu = fl.ops.gdn_decode(xd[:, None], Su, ad[:, None], bd[:, None], Ad, dtd, T=1,
+                               pos0s=pos, conv_fused=True, conv_w=wd,
+                               cst_in=[r[ph] for r in ru], cst_out=[r[ph ^ 1] for r in ru])
+        zc = zd[:, :width].contiguous()
+        yn = fl.ops.rmsnorm_gated(yu.view(B, NV, 128), zc, nwd, T=B)
+        torch.cuda.synchronize()
+        yh = yf.cpu().numpy()
+        assert (yh[:, width:] == 7.0).all(), f"step {step}: wrote into the row padding"
+        assert torch.equal(yf[:, :width], yn.view(B, width)), f"step {step}: y differs"
+        for b in range(B):
+            assert torch.equal(Sf[b], Su[b]), f"step {step}, seq {b}: state differs"
+            assert torch.equal(rf[b][ph ^ 1], ru[b][ph ^ 1]), f"step {step}, seq {b}: ring"
+        if step == 0:
+            for b in range(B):
+                ring_r = [ring0[b].copy(), np.zeros((ROW, 3), np.float16)]
+                y_r = orc.gdn_decode(None, S0[b].copy(), a[b:b + 1], bb[b:b + 1], A_log, dt,
+                                     T=1, out_scale=QS, cx=x[b], cw=w, cst_in=ring_r[0],
+                                     cst_out=ring_r[1], pos0=pos[b])
+                want = orc.rmsnorm_gated(y_r.reshape(1, NV, 128), z[b:b + 1, :width], nw, T=1)
+                err, ok = close(yh[b, :width], want.reshape(-1), 2e-2, 2e-2)
+                assert ok, f"seq {b} against the oracle: max |dy| {err}"
