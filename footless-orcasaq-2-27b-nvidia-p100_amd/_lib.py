@@ -53,6 +53,8 @@ SIGNATURES = {
                                      _P, _I, _P, _SZ, _P]),
     "fl_attention_prefill_kv_q8": (_I, [_P, _I, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _I,
                                         _I, _P, _I, _P, _SZ, _P]),
+    "fl_attention_prefill_gated": (_I, [_P, _I, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _F,
+                                        _I, _I, _P, _I, _P, _SZ, _P]),
     "fl_kv_store_q8": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P]),
     "fl_attn_prep_q8": (_I, [_P, _I, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _F,
                              _F, _P]),

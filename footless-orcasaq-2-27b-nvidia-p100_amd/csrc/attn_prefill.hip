@@ -1145,12 +1145,21 @@ size_t split_work_bytes(int T, int n_q_heads, int head_dim, int split) {
     return (size_t)T * n_q_heads * split * ((size_t)head_dim * 4 + 8);
 }
 
+// gated: z *= sigmoid(gate) after the attention (attn_gate), the gate being
+// the second half of each head's q row (q | gate rows, q_pitch >= 2 head_dim):
+// applied by the merge when the KV is split, else by fl_attn_gate after it.
 template <bool Q8>
 int prefill(const void* q, int q_pitch, const void* k_new, const void* v_new, void* kcache,
             void* vcache, int layer, int n_q_heads, int n_kv_heads, int head_dim, int pos0,
             int max_pos, float scale, int T, void* z, int z_pitch, int split, void* work,
-            size_t work_bytes, fl_stream_t stream) {
+            size_t work_bytes, fl_stream_t stream, bool gated = false) {
     FL_REQUIRE(q && kcache && vcache && z, "null pointer");
+    FL_REQUIRE(!gated || q_pitch >= 2 * head_dim, "gated: q_pitch >= 2 head_dim (q | gate rows)");
+    const void* gate = gated ? q : nullptr;
+    auto gate_after = [&](int rc_) {
+        if (rc_ || !gated) return rc_;
+        return fl_attn_gate(z, q, n_q_heads, head_dim, z_pitch, q_pitch, head_dim, T, stream);
+    };
     FL_REQUIRE(head_dim == PF_HD, "head_dim must be 256");
     FL_REQUIRE(n_kv_heads > 0 && n_q_heads > 0 && n_q_heads % n_kv_heads == 0,
                "n_q_heads % n_kv_heads");
@@ -1225,7 +1234,7 @@ int prefill(const void* q, int q_pitch, const void* k_new, const void* v_new, vo
                            (const f16*)vc, (f16*)z, z_pitch, n_q_heads, n_kv_heads, pos0, T,
                            scale * FL_LOG2E, r64_tiles, bins, plan,
                            PfSplit{nullptr, nullptr, nullptr, 1});
-        return fl::check_launch("attn_prefill_r64");
+        return gate_after(fl::check_launch("attn_prefill_r64"));
     }
     if (!Q8 && split > 1 && use_r64_split(T, pos0, n_q_heads, n_kv_heads)) {
         const size_t parts = (size_t)T * n_q_heads * split;
@@ -1241,7 +1250,7 @@ int prefill(const void* q, int q_pitch, const void* k_new, const void* v_new, vo
         rc = fl::check_launch("attn_prefill_r64 (kv split)");
         if (rc) return rc;
         return fl_attention_merge(sp.pacc, sp.pm, sp.pd, z, n_q_heads, head_dim, z_pitch, T,
-                                  split, nullptr, 0, 0, stream);
+                                  split, gate, q_pitch, head_dim, stream);
     }
     const int n_row_tiles = (rows + PF_BQ - 1) / PF_BQ;
     if (split == 1) {
@@ -1249,7 +1258,7 @@ int prefill(const void* q, int q_pitch, const void* k_new, const void* v_new, vo
                            dim3(PF_THREADS), LDS_B, (hipStream_t)stream, (const f16*)q, q_pitch,
                            kc, vc, ksc, vsc, (f16*)z, z_pitch, n_q_heads, n_kv_heads, pos0, T,
                            scale * FL_LOG2E, n_row_tiles, PfSplit{nullptr, nullptr, nullptr, 1});
-        return fl::check_launch("attn_prefill");
+        return gate_after(fl::check_launch("attn_prefill"));
     }
     const size_t parts = (size_t)T * n_q_heads * split;
     PfSplit sp = {(float*)work, nullptr, nullptr, split};
@@ -1262,7 +1271,7 @@ int prefill(const void* q, int q_pitch, const void* k_new, const void* v_new, vo
     rc = fl::check_launch("attn_prefill (kv split)");
     if (rc) return rc;
     return fl_attention_merge(sp.pacc, sp.pm, sp.pd, z, n_q_heads, head_dim, z_pitch, T, split,
-                              nullptr, 0, 0, stream);
+                              gate, q_pitch, head_dim, stream);
 }
 
 }  // namespace
@@ -1327,6 +1336,22 @@ extern "C" int fl_attention_prefill_kv(const void* q, int q_pitch, const void* k
     return prefill<false>(q, q_pitch, k_new, v_new, kcache, vcache, layer, n_q_heads, n_kv_heads,
                           head_dim, pos0, max_pos, scale, T, z, z_pitch, split, work, work_bytes,
                           stream);
+}
+
+extern "C" int fl_attention_prefill_gated(const void* q, int q_pitch, const void* k_new,
+                                          const void* v_new, void* kcache, void* vcache,
+                                          int layer, int q8, int n_q_heads, int n_kv_heads,
+                                          int head_dim, int pos0, int max_pos, float scale, int T,
+                                          int split, void* z, int z_pitch, void* work,
+                                          size_t work_bytes, fl_stream_t stream) {
+    if (split == 0) split = split_policy(T, pos0, n_q_heads, n_kv_heads, q8 != 0);
+    if (q8)
+        return prefill<true>(q, q_pitch, k_new, v_new, kcache, vcache, layer, n_q_heads,
+                             n_kv_heads, head_dim, pos0, max_pos, scale, T, z, z_pitch, split, work,
+                             work_bytes, stream, true);
+    return prefill<false>(q, q_pitch, k_new, v_new, kcache, vcache, layer, n_q_heads, n_kv_heads,
+                          head_dim, pos0, max_pos, scale, T, z, z_pitch, split, work, work_bytes,
+                          stream, true);
 }
 
 extern "C" int fl_attention_prefill_kv_q8(const void* q, int q_pitch, const void* k_new,

@@ -229,14 +229,16 @@ def attention_prefill(q, kcache, vcache, *, pos0: int, T: int | None = None, z=N
                       k_new=None, v_new=None, layer: int = 0, n_q_heads: int = N_HEADS,
                       n_kv_heads: int = N_KV, q_pitch: int | None = None,
                       scale: float = ATTN_SCALE, max_pos: int | None = None,
-                      split: int | None = None, work=None):
+                      split: int | None = None, work=None, gated: bool = False):
     """attention_prefill_fh + attention_merge_fh (kernels.cu:2461-2807, host
     _attn_fh runtime.py:2943-2959), with kv_store (kernels.cu:465-484) of
     k_new / v_new [T, n_kv, head_dim] fused in front when given. q [T,
     n_q_heads, q_pitch] fp16 (q first in a head's row). split: the KV split
     (None: prefill_split_count's choice; a split > 1 leaves partials in `work`,
-    a uint8 tensor, allocated here unless given). Returns z [T, n_q_heads,
-    head_dim] fp16."""
+    a uint8 tensor, allocated here unless given). gated: attn_gate applied too
+    (kernels.cu:1585-1600, runtime.py:2860-2862), the gate the second half of
+    each head's q row -- in the merge when the KV is split. Returns z [T,
+    n_q_heads, head_dim] fp16."""
     T = q.shape[0] if T is None else T
     q_pitch = q.shape[-1] if q_pitch is None else q_pitch
     head_dim = kcache.shape[-1]
@@ -251,12 +253,22 @@ def attention_prefill(q, kcache, vcache, *, pos0: int, T: int | None = None, z=N
             _ptr(vcache, F16, "vcache", (layer + 1) * max_pos * row), layer, n_q_heads,
             n_kv_heads, head_dim, pos0, max_pos, float(scale), T)
     zargs = (_ptr(z, F16, "z", T * n_q_heads * z.shape[-1]), z.shape[-1])
-    if split == 1:
+    if gated:
+        _prefill_gated(args, 0, split, zargs, work)
+    elif split == 1:
         _lib.call("fl_attention_prefill", *args, *zargs, _stream())
     else:
         _lib.call("fl_attention_prefill_kv", *args, split, *zargs,
                   _ptr(work, torch.uint8, "work", work.numel()), work.numel(), _stream())
     return z
+
+
+def _prefill_gated(args, q8: int, split: int, zargs, work):
+    """fl_attention_prefill_gated over the (q .. T) arguments of the ungated
+    entry points (layer is args[6]; the cache flag goes after it)."""
+    wp = _ptr(work, torch.uint8, "work", work.numel()) if work is not None else None
+    _lib.call("fl_attention_prefill_gated", *args[:7], q8, *args[7:], split, *zargs, wp,
+              work.numel() if work is not None else 0, _stream())
 
 
 def prefill_split_count(T: int, pos0: int, n_q_heads: int = N_HEADS,
@@ -434,11 +446,13 @@ def attn_decode_q8(qg, kcaches, vcaches, pos0s, caps, *, z=None, gate: bool = Tr
 def attention_prefill_q8(q, kcache, vcache, *, pos0: int, max_pos: int, T: int | None = None,
                          z=None, k_new=None, v_new=None, n_q_heads: int = N_HEADS,
                          n_kv_heads: int = N_KV, q_pitch: int | None = None,
-                         scale: float = ATTN_SCALE, split: int | None = None, work=None):
+                         scale: float = ATTN_SCALE, split: int | None = None, work=None,
+                         gated: bool = False):
     """attention_prefill_fh_q8 (kernels.cu:2778-2786) over an int8 cache, with
     kv_store_q8 of k_new / v_new fused in front when given. Long prompts run
     the fp16 long-prompt kernel on an fp16 copy of the cache rows made first
-    (in `work`, allocated here when not given or too small)."""
+    (in `work`, allocated here when not given or too small). gated: as
+    attention_prefill's."""
     T = q.shape[0] if T is None else T
     q_pitch = q.shape[-1] if q_pitch is None else q_pitch
     row = n_kv_heads * HEAD_DIM
@@ -456,9 +470,11 @@ def attention_prefill_q8(q, kcache, vcache, *, pos0: int, max_pos: int, T: int |
     if split == 1:
         stage = int(_lib.lib().fl_attention_prefill_q8_stage_bytes(T, pos0, n_q_heads, n_kv_heads,
                                                                    HEAD_DIM))
-    if split == 1 and stage > 0:
-        if work is None or work.numel() < stage:
-            work = torch.empty(stage, dtype=torch.uint8, device=q.device)
+    if split == 1 and stage > 0 and (work is None or work.numel() < stage):
+        work = torch.empty(stage, dtype=torch.uint8, device=q.device)
+    if gated:
+        _prefill_gated(args, 1, split, zargs, work)
+    elif split == 1 and stage > 0:
         _lib.call("fl_attention_prefill_kv_q8", *args, 1, *zargs,
                   _ptr(work, torch.uint8, "work", stage), work.numel(), _stream())
     elif split == 1:

@@ -316,12 +316,11 @@ class HybridRuntime:
             if self.kv8:
                 return ops.attn_decode_q8(qg[None], [kc], [vc], [pos0], [lcap])[0]
             return ops.attn_decode(qg[None], [kc], [vc], [pos0])[0]
+        # gated by the gate half of each head's q | gate row (in the merge when
+        # the KV is split)
         if self.kv8:
-            z = ops.attention_prefill_q8(qg, kc, vc, pos0=pos0, max_pos=lcap)
-        else:
-            z = ops.attention_prefill(qg, kc, vc, pos0=pos0)
-        ops.attn_gate(z, qg, T=T)   # the gate half of each head's q | gate row
-        return z
+            return ops.attention_prefill_q8(qg, kc, vc, pos0=pos0, max_pos=lcap, gated=True)
+        return ops.attention_prefill(qg, kc, vc, pos0=pos0, gated=True)
 
     def _gdn(self, st: SeqState, i: int, qkv, zg, a, b, T: int, pos0: int,
              verify: bool) -> torch.Tensor:

@@ -297,6 +297,20 @@ int fl_attention_prefill_kv_q8(const void* q, int q_pitch, const void* k_new, co
                                int n_kv_heads, int head_dim, int pos0, int max_pos, float scale,
                                int T, int split, void* z, int z_pitch, void* work,
                                size_t work_bytes, fl_stream_t stream);
+/* A prefill chunk's attention output as the layer uses it: the prefill
+ * (fl_attention_prefill_kv, or fl_attention_prefill_kv_q8 when q8 != 0; split
+ * 0 takes that cache's split count) followed by attn_gate, z = f16_sat(z *
+ * sigmoid(gate)), the gate being the second half of each head's q row (q |
+ * gate rows of q_pitch >= 2*head_dim halves, the reference's qg buffer).
+ * When the KV is split the gate rides in the merge (one launch fewer); the
+ * values are the pair's bit for bit. Replaces the sequence _attn_fh then
+ * attn_gate, runtime.py:2943-2959 then 2860-2862 (kernels.cu:2461-2807,
+ * 1585-1600). */
+int fl_attention_prefill_gated(const void* q, int q_pitch, const void* k_new, const void* v_new,
+                               void* kcache, void* vcache, int layer, int q8, int n_q_heads,
+                               int n_kv_heads, int head_dim, int pos0, int max_pos, float scale,
+                               int T, int split, void* z, int z_pitch, void* work,
+                               size_t work_bytes, fl_stream_t stream);
 
 /* fl_attention_prefill over an int8 cache (k_new / v_new, when given, are
  * stored first with kv_store_q8). Replaces kernels.cu:2778-2786

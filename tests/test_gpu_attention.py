@@ -521,3 +521,44 @@ def test_merge_layouts_vs_oracle(fl, dev, orc, rng, head_dim, z_pitch, split, T)
     err, ok = close_rel(got[..., :head_dim], want[..., :head_dim], ATOL, RTOL)
     assert ok and err <= 1e-2 * float(np.abs(want[..., :head_dim].astype(np.float32)).max()), err
     assert not got[..., head_dim:].any(), "wrote past head_dim"
+
+
+# the KV-split prefills' merge carries the gate; the unsplit ones run the gate
+# after them: split 3 of the 128-row kernel, the 64-rows-a-wave kernel's own
+# split (683 tokens at 16000), the unsplit 128-row and long-prompt kernels,
+# and over an int8 cache its split, an unsplit call and a staged long prompt
+@pytest.mark.parametrize("kv8,T,pos0,split,splits", [
+    (False, 300, 500, 3, True), (False, 683, 16000, None, True), (False, 300, 500, 1, False),
+    (False, 4096, 0, None, False), (True, 300, 500, 3, True), (True, 1024, 8000, None, True),
+    (True, 300, 500, 1, False), (True, 4096, 512, None, False)])
+def test_prefill_gated_equals_prefill_then_gate(fl, dev, kv8, T, pos0, split, splits):
+    """fl_attention_prefill_gated (the layer's attention output: the gate half
+    of each head's q | gate row applied in the KV-split merge, or by
+    attn_gate after an unsplit prefill) against the prefill then attn_gate,
+    bit for bit."""
+    L = pos0 + T
+    if split is None:
+        count = (fl.ops.prefill_split_count_q8 if kv8 else fl.ops.prefill_split_count)(T, pos0)
+        assert (count > 1) == splits, count
+    g = torch.Generator(device=dev).manual_seed(T + pos0)
+    qg = torch.randn((T, 24, 512), generator=g, device=dev)
+    qg[..., :256] /= 16
+    qg = qg.half()
+    k = torch.randn((L, 4, 256), generator=g, device=dev).half()
+    v = torch.randn((L, 4, 256), generator=g, device=dev).half()
+    if kv8:
+        kd, vd = fl.ops.kv8_cache(L), fl.ops.kv8_cache(L)
+        fl.ops.kv_store_q8(k, v, kd, vd, pos0=0, max_pos=L)
+
+        def run(gated):
+            return fl.ops.attention_prefill_q8(qg, kd, vd, pos0=pos0, max_pos=L, split=split,
+                                               gated=gated)
+    else:
+        def run(gated):
+            return fl.ops.attention_prefill(qg, k, v, pos0=pos0, split=split, gated=gated)
+    zg = run(True)
+    z = run(False)
+    fl.ops.attn_gate(z, qg, T=T)
+    torch.cuda.synchronize()
+    assert torch.isfinite(zg.float()).all()
+    assert torch.equal(zg, z), f"kv8={kv8} T={T} pos0={pos0} split={split}"
