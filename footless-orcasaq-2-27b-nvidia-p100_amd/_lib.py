@@ -83,6 +83,8 @@ SIGNATURES = {
     "fl_gdn_chunked_work_bytes": (_SZ, [_I, _I, _I, _I, _I]),
     "fl_gdn_prefill_chunked": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I,
                                     _F, _I, _I, _P, _SZ, _P]),
+    "fl_gdn_prefill_chunked_logits": (_I, [_P, _P, _P, _P, _P, _I, _P, _P, _P, _P, _I, _I, _I,
+                                           _I, _I, _I, _I, _I, _F, _I, _I, _P, _SZ, _P]),
 }
 
 

@@ -61,6 +61,8 @@
 
 #pragma clang fp contract(off)
 
+#include "gdn_gates.hpp"
+
 namespace {
 
 constexpr int CK_C = 64;       // tokens a chunk
@@ -216,14 +218,26 @@ __device__ __forceinline__ float wave_prefix_sum(float v) {
     return v;
 }
 
+// The gates the prep reads: beta and decay [T][n_vheads] (gdn_scalars'
+// output), or, LOGITS, the logits a and b [T][ab_stride] with A_log and
+// dt_bias, from which a lane forms its token's beta and decay itself (the
+// gates kernel's functions: the same values).
+struct PrepGates {
+    const float* beta;     // or a
+    const float* decay;    // or b
+    const float* A_log;
+    const float* dt_bias;
+    int stride;            // n_vheads, or ab_stride
+};
+
 // One workgroup of 4 waves a (chunk, v head), a grid of chunks x v heads: it
 // loads its k head's K and Q rows of the chunk, forms K K^T and Q K^T (wave w
 // the 32 x 32 block (w / 2, w % 2)), then its v head's A, T and M o QK^T from
 // them with that head's gates, into the head's block of the workspace.
+template <bool LOGITS>
 __global__ void __launch_bounds__(256)
-chunk_prep_kernel(const f16* __restrict__ q, const f16* __restrict__ k,
-                  const float* __restrict__ beta, const float* __restrict__ decay, int T,
-                  int n_vheads, int qk_stride, int group, char* __restrict__ work) {
+chunk_prep_kernel(const f16* __restrict__ q, const f16* __restrict__ k, const PrepGates gates,
+                  int T, int n_vheads, int qk_stride, int group, char* __restrict__ work) {
     __shared__ __attribute__((aligned(16))) char smem[2 * CK_C * PK_P * 2];
     __shared__ float sG[CK_C], sB[CK_C], sRed[8];
     f16(*sK)[PK_P] = (f16(*)[PK_P])smem;
@@ -249,8 +263,17 @@ chunk_prep_kernel(const f16* __restrict__ q, const f16* __restrict__ k,
         kv8[m] = *(const f16x8*)(k + off);
         qv8[m] = *(const f16x8*)(q + off);
     }
-    const size_t gt = (size_t)(t0 + min(lane, n - 1)) * n_vheads;
-    float dec = decay[gt + hv0], bet = beta[gt + hv0];
+    const size_t gt = (size_t)(t0 + min(lane, n - 1)) * gates.stride + hv0;
+    float dec, bet;
+    if constexpr (LOGITS) {
+        const float av = gates.beta[gt], bv = gates.decay[gt];
+        const float dtb = gates.dt_bias[hv0], A = gates.A_log[hv0];
+        dec = gdn_decay(av + dtb, A);
+        bet = gdn_beta(bv);
+    } else {
+        dec = gates.decay[gt];
+        bet = gates.beta[gt];
+    }
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
         const int idx = tid + 256 * m, i = idx >> 4, c8 = (idx & 15) * 8;
@@ -941,12 +964,17 @@ size_t fl_gdn_chunked_work_bytes(int T, int n_vheads, int K, int V, int chunk) {
     return n_chunks * n_vheads * CK_BLK;
 }
 
-int fl_gdn_prefill_chunked(const void* q, const void* k, const void* v, const float* beta,
-                           const float* decay, float* S, void* y, int T, int n_kheads,
-                           int n_vheads, int K, int V, int qk_stride, int v_stride, int y_stride,
-                           float out_scale, int group, int chunk, void* work, size_t work_bytes,
-                           fl_stream_t stream) {
-    FL_REQUIRE(q && k && v && beta && decay && S && y && work, "null pointer");
+}  // extern "C"
+
+namespace {
+
+int prefill_chunked(const void* q, const void* k, const void* v, const PrepGates& gates,
+                    bool logits, float* S, void* y, int T, int n_kheads, int n_vheads, int K,
+                    int V, int qk_stride, int v_stride, int y_stride, float out_scale, int group,
+                    int chunk, void* work, size_t work_bytes, fl_stream_t stream) {
+    FL_REQUIRE(q && k && v && gates.beta && gates.decay && S && y && work, "null pointer");
+    FL_REQUIRE(!logits || (gates.A_log && gates.dt_bias && gates.stride >= n_vheads),
+               "A_log, dt_bias; ab_stride >= n_vheads");
     FL_REQUIRE(K == CK_K && V == CK_V, "K == V == 128");
     FL_REQUIRE(chunk == CK_C, "chunk == 64");
     FL_REQUIRE(T >= 1, "T >= 1");
@@ -963,9 +991,14 @@ int fl_gdn_prefill_chunked(const void* q, const void* k, const void* v, const fl
         return FL_ESCRATCH;
     }
     const int n_chunks = (T + CK_C - 1) / CK_C;
-    hipLaunchKernelGGL(chunk_prep_kernel, dim3(n_chunks, n_vheads), dim3(256), 0,
-                       (hipStream_t)stream, (const f16*)q, (const f16*)k, beta, decay, T, n_vheads,
-                       qk_stride, group, (char*)work);
+    if (logits)
+        hipLaunchKernelGGL(chunk_prep_kernel<true>, dim3(n_chunks, n_vheads), dim3(256), 0,
+                           (hipStream_t)stream, (const f16*)q, (const f16*)k, gates, T, n_vheads,
+                           qk_stride, group, (char*)work);
+    else
+        hipLaunchKernelGGL(chunk_prep_kernel<false>, dim3(n_chunks, n_vheads), dim3(256), 0,
+                           (hipStream_t)stream, (const f16*)q, (const f16*)k, gates, T, n_vheads,
+                           qk_stride, group, (char*)work);
     int rc = fl::check_launch("gdn_chunk_prep");
     if (rc) return rc;
     rc = raise_state_lds_limit();
@@ -975,6 +1008,31 @@ int fl_gdn_prefill_chunked(const void* q, const void* k, const void* v, const fl
                        (f16*)y, T, n_vheads, qk_stride, v_stride, y_stride, out_scale, group,
                        (const char*)work);
     return fl::check_launch("gdn_chunk_state");
+}
+
+}  // namespace
+
+extern "C" {
+
+int fl_gdn_prefill_chunked(const void* q, const void* k, const void* v, const float* beta,
+                           const float* decay, float* S, void* y, int T, int n_kheads,
+                           int n_vheads, int K, int V, int qk_stride, int v_stride, int y_stride,
+                           float out_scale, int group, int chunk, void* work, size_t work_bytes,
+                           fl_stream_t stream) {
+    return prefill_chunked(q, k, v, PrepGates{beta, decay, nullptr, nullptr, n_vheads}, false, S,
+                           y, T, n_kheads, n_vheads, K, V, qk_stride, v_stride, y_stride,
+                           out_scale, group, chunk, work, work_bytes, stream);
+}
+
+int fl_gdn_prefill_chunked_logits(const void* q, const void* k, const void* v, const float* a,
+                                  const float* b, int ab_stride, const float* A_log,
+                                  const float* dt_bias, float* S, void* y, int T, int n_kheads,
+                                  int n_vheads, int K, int V, int qk_stride, int v_stride,
+                                  int y_stride, float out_scale, int group, int chunk, void* work,
+                                  size_t work_bytes, fl_stream_t stream) {
+    return prefill_chunked(q, k, v, PrepGates{a, b, A_log, dt_bias, ab_stride}, true, S, y, T,
+                           n_kheads, n_vheads, K, V, qk_stride, v_stride, y_stride, out_scale,
+                           group, chunk, work, work_bytes, stream);
 }
 
 }  // extern "C"

@@ -678,3 +678,33 @@ def gdn_prefill_chunked(q, k, v, beta, decay, S, y=None, *, T: int, n_kheads: in
               V, qk_stride, v_stride, y.shape[-1], float(out_scale), group, chunk,
               _ptr(work, torch.uint8, "work", need), work.numel(), _stream())
     return y
+
+
+def gdn_prefill_chunked_logits(q, k, v, a, b, A_log, dt_bias, S, y=None, *, T: int,
+                               ab_stride: int = GDN_V_HEADS, n_kheads: int = GDN_K_HEADS,
+                               n_vheads: int = GDN_V_HEADS, K: int = GDN_K, V: int = GDN_V,
+                               qk_stride: int = QKV_ROWS, v_stride: int = QKV_ROWS,
+                               out_scale: float = Q_SCALE, group: int = GDN_GROUP,
+                               chunk: int = GDN_CHUNK, work=None):
+    """gdn_scalars then gdn_prefill_chunked in one call (runtime.py:3072-3076,
+    3094-3100): the scan forms beta and decay from the logits a, b [T,
+    ab_stride] fp32 itself, the values gdn_scalars writes. Returns y [T,
+    n_vheads * V] fp16."""
+    _contig(S, "S")
+    if y is None:
+        y = torch.empty((T, n_vheads * V), dtype=F16, device=q.device)
+    need = gdn_chunked_work_bytes(T, n_vheads, K, V, chunk)
+    if work is None:
+        work = torch.empty(need, dtype=torch.uint8, device=q.device)
+    _lib.call("fl_gdn_prefill_chunked_logits",
+              _ptr(q, F16, "q", (T - 1) * qk_stride + n_kheads * K),
+              _ptr(k, F16, "k", (T - 1) * qk_stride + n_kheads * K),
+              _ptr(v, F16, "v", (T - 1) * v_stride + n_vheads * V),
+              _ptr(a, F32, "a", (T - 1) * ab_stride + n_vheads),
+              _ptr(b, F32, "b", (T - 1) * ab_stride + n_vheads), ab_stride,
+              _ptr(A_log, F32, "A_log", n_vheads), _ptr(dt_bias, F32, "dt_bias", n_vheads),
+              _ptr(S, F32, "S", n_vheads * V * K),
+              _ptr(y, F16, "y", (T - 1) * y.shape[-1] + n_vheads * V), T, n_kheads, n_vheads, K,
+              V, qk_stride, v_stride, y.shape[-1], float(out_scale), group, chunk,
+              _ptr(work, torch.uint8, "work", need), work.numel(), _stream())
+    return y

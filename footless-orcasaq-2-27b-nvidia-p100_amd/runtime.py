@@ -355,11 +355,10 @@ class HybridRuntime:
             # and reads back only these 32: the same bits for them)
             ln = torch.empty_like(c)
             ops.l2norm_scaled_strided(c, ln, rows=2 * GDN_K_HEADS, token_stride=QKV_ROWS, T=T)
-            beta = torch.empty((T, GDN_V_HEADS), dtype=F32, device=qkv.device)
-            decay = torch.empty_like(beta)
-            ops.gdn_scalars(a, b, wt.A_log, wt.dt_bias, beta, decay, T=T)
+            # the gates formed from a, b inside the scan (gdn_scalars' values)
             qn, kn = GDN_K_HEADS * GDN_K, 2 * GDN_K_HEADS * GDN_K
-            y = ops.gdn_prefill_chunked(ln[:, :qn], ln[:, qn:kn], c[:, kn:], beta, decay, S, T=T)
+            y = ops.gdn_prefill_chunked_logits(ln[:, :qn], ln[:, qn:kn], c[:, kn:], a, b,
+                                               wt.A_log, wt.dt_bias, S, T=T)
         yn = ops.rmsnorm_gated(y.view(T, GDN_V_HEADS, GDN_V), zg, wt.norm_w, T=T)
         return yn
 

@@ -444,6 +444,18 @@ int fl_gdn_prefill_chunked(const void* q, const void* k, const void* v, const fl
                            int n_vheads, int K, int V, int qk_stride, int v_stride,
                            int y_stride, float out_scale, int group, int chunk, void* work,
                            size_t work_bytes, fl_stream_t stream);
+/* fl_gdn_prefill_chunked with the gates formed from their logits inside it:
+ * beta = sigmoid(b), decay = exp(-e^A_log softplus(a + dt_bias)), the values
+ * fl_gdn_scalars writes, so the pair gdn_scalars then the scan
+ * (runtime.py:3072-3076, 3094-3100) is one call and no beta / decay buffers:
+ * a, b [T][ab_stride] f32 (head hv at hv), A_log, dt_bias [n_vheads] f32;
+ * the rest as fl_gdn_prefill_chunked. The same values bit for bit. */
+int fl_gdn_prefill_chunked_logits(const void* q, const void* k, const void* v, const float* a,
+                                  const float* b, int ab_stride, const float* A_log,
+                                  const float* dt_bias, float* S, void* y, int T, int n_kheads,
+                                  int n_vheads, int K, int V, int qk_stride, int v_stride,
+                                  int y_stride, float out_scale, int group, int chunk, void* work,
+                                  size_t work_bytes, fl_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -88,6 +88,15 @@ def test_argument_checks_refuse_before_launch(fl):
     # chunked scan with a chunk other than 64
     assert _call(fl, "fl_gdn_prefill_chunked", fake, fake, fake, fake, fake, fake, fake, 100, 16,
                  48, 128, 128, 10240, 10240, 6144, 0.1, 3, 32, fake, 1 << 30, None) == 1
+    # the chunked scan from logits without A_log, or with a logit row shorter
+    # than the v heads
+    assert _call(fl, "fl_gdn_prefill_chunked_logits", fake, fake, fake, fake, fake, 48, None,
+                 fake, fake, fake, 100, 16, 48, 128, 128, 10240, 10240, 6144, 0.1, 3, 64, fake,
+                 1 << 30, None) == 1
+    assert _call(fl, "fl_gdn_prefill_chunked_logits", fake, fake, fake, fake, fake, 40, fake,
+                 fake, fake, fake, 100, 16, 48, 128, 128, 10240, 10240, 6144, 0.1, 3, 64, fake,
+                 1 << 30, None) == 1
+    assert b"ab_stride" in lib.fl_last_error()
     # the gated prefill needs q | gate rows (q_pitch >= 2 head_dim)
     assert _call(fl, "fl_attention_prefill_gated", fake, 256, None, None, fake, fake, 0, 0, 24, 4,
                  256, 0, 64, 1.0, 8, 1, fake, 256, None, 0, None) == 1

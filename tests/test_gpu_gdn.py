@@ -633,3 +633,32 @@ def test_decode_normed_equals_decode_then_norm(fl, dev, orc, rng, B):
                 want = orc.rmsnorm_gated(y_r.reshape(1, NV, 128), z[b:b + 1, :width], nw, T=1)
                 err, ok = close(yh[b, :width], want.reshape(-1), 2e-2, 2e-2)
                 assert ok, f"seq {b} against the oracle: max |dy| {err}"
+
+
+@pytest.mark.parametrize("T,ab_stride", [(1, 48), (100, 48), (1024, 56)])
+def test_chunked_logits_equals_gates_then_scan(fl, dev, rng, T, ab_stride):
+    """The chunked scan forming beta and decay from the logits itself against
+    gdn_scalars then the scan on its output: y and the state bit for bit
+    (strong and weak decays, logits past softplus's x = 20 switch, a padded
+    logit row)."""
+    ln = (rng.standard_normal((T, ROW)) * 0.5).astype(np.float16)
+    a = (rng.standard_normal((T, ab_stride)) * 4).astype(np.float32)
+    a[:, 0] = 25.0                                       # softplus(x) = x branch
+    bb = (rng.standard_normal((T, ab_stride)) * 3).astype(np.float32)
+    A_log = (rng.standard_normal(NV) * 0.5).astype(np.float32)
+    dt = (rng.standard_normal(NV) * 0.5).astype(np.float32)
+    S0 = (rng.standard_normal((NV, 128, 128)) * 0.05).astype(np.float32)
+    lnd, ad, bd = to_dev(ln, dev), to_dev(a, dev), to_dev(bb, dev)
+    Ad, dtd = to_dev(A_log, dev), to_dev(dt, dev)
+    S1, S2 = to_dev(S0, dev), to_dev(S0, dev)
+    y1 = fl.ops.gdn_prefill_chunked_logits(lnd[:, :2048], lnd[:, 2048:4096], lnd[:, 4096:], ad, bd,
+                                           Ad, dtd, S1, T=T, ab_stride=ab_stride)
+    beta = torch.empty((T, NV), dtype=torch.float32, device=dev)
+    decay = torch.empty_like(beta)
+    fl.ops.gdn_scalars(ad, bd, Ad, dtd, beta, decay, T=T, a_stride=ab_stride, b_stride=ab_stride)
+    y2 = fl.ops.gdn_prefill_chunked(lnd[:, :2048], lnd[:, 2048:4096], lnd[:, 4096:], beta, decay,
+                                    S2, T=T)
+    torch.cuda.synchronize()
+    assert torch.isfinite(y1.float()).all()
+    assert torch.equal(y1, y2), f"T={T}: y differs"
+    assert torch.equal(S1, S2), f"T={T}: state differs"
