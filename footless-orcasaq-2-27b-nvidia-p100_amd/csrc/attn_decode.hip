@@ -972,16 +972,54 @@ int check_decode_geometry(int T, int n_q_heads, int n_kv, int head_dim, int q_pi
     return FL_OK;
 }
 
+// The current device's compute-unit count, looked up once per device.
+int dec_cu_count() {
+    static int cached[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cached[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            n <= 0)
+            n = 256;
+        cached[dev] = n;
+    }
+    return cached[dev];
+}
+
+// split_rows 0, the grid rule: S = ceil(W / (B n_kv)) splits a token (at most
+// `split`), W one workgroup a CU over fp16 caches and two over int8 ones,
+// fewer where the token's length leaves under 64 rows a split. Swept at B =
+// 1..16 and ~8k..~100k (forced split counts, graph-timed): the fp16 kernel is
+// fastest at one workgroup a CU (B = 4 at ~32k: 16 splits 85.3 us, 32: 88.9,
+// 64: 91.4; B = 1 at ~8k: 64 splits 14.4 us, 32: 16.7), the int8 kernel, with
+// three waves a SIMD, at two (B = 4 at ~32k: 32 splits 67.8 us, 16: 73.4,
+// 64: 69.1). A token's split count then depends on B as well as its length,
+// so a batched call's values can differ in the last bits from single calls';
+// split_rows > 0 keeps the length-only rule.
+constexpr int DEC_GRID_RULE = 0;
+
+void grid_rule(bool q8, int B, int n_kv, int split, int& rows, int& smax, int& floor_splits) {
+    const int W = (q8 ? 2 : 1) * dec_cu_count();
+    const int S = (W + B * n_kv - 1) / (B * n_kv);
+    smax = S < 1 ? 1 : (S > split ? split : S);
+    rows = DEC_FINE_ROWS;
+    floor_splits = 0;
+}
+
 template <bool Q8>
 int attn_decode_batched(const void* qg, int q_pitch, const void* const* kcache,
                         const void* const* vcache, const int* pos0, const int* cap, int B, int T,
                         int n_q_heads, int n_kv_heads, int head_dim, float scale, int split_rows,
                         int split, const void* gate, int g_pitch, int g_off, void* z, int z_pitch,
                         void* work, size_t work_bytes, fl_stream_t stream) {
-    int rc = check_decode_geometry(T, n_q_heads, n_kv_heads, head_dim, q_pitch, split, split_rows);
+    int rc = check_decode_geometry(T, n_q_heads, n_kv_heads, head_dim, q_pitch, split,
+                                   split_rows == DEC_GRID_RULE ? DEC_TILE : split_rows);
     if (rc) return rc;
     FL_REQUIRE(B >= 1 && B <= FL_MAX_SEQS, "1 <= B <= FL_MAX_SEQS");
     FL_REQUIRE(qg && kcache && vcache && pos0 && cap && z && work, "null pointer");
+    int rows = split_rows, smax = split, floor_splits = DEC_SPLIT_FLOOR;
+    if (split_rows == DEC_GRID_RULE) grid_rule(Q8, B, n_kv_heads, split, rows, smax, floor_splits);
     FL_REQUIRE(z_pitch >= head_dim, "z_pitch >= head_dim");
     FL_REQUIRE(gate == nullptr || g_off + head_dim <= g_pitch, "g_off + head_dim <= g_pitch");
     FL_REQUIRE(aligned16(qg) && aligned16(work), "16-byte aligned qg / work");
@@ -1005,7 +1043,7 @@ int attn_decode_batched(const void* qg, int q_pitch, const void* const* kcache,
             seqs.v[b] = (const f16*)vcache[b];
             seqs.pos0[b] = pos0[b];
         }
-        const int st = split_count(pos0[b] + T, split_rows, split, DEC_SPLIT_FLOOR);
+        const int st = split_count(pos0[b] + T, rows, smax, floor_splits);
         grid_split = st > grid_split ? st : grid_split;
     }
     const size_t parts = (size_t)B * T * n_q_heads * grid_split;
@@ -1013,8 +1051,8 @@ int attn_decode_batched(const void* qg, int q_pitch, const void* const* kcache,
     float* pm = pacc + parts * head_dim;
     float* pd = pm + parts;
     rc = launch_split<Q8, false>((const f16*)qg, seqs, pacc, pm, pd, B, T, n_q_heads, n_kv_heads,
-                                 q_pitch, grid_split, grid_split, split_rows, scale * FL_LOG2E,
-                                 (hipStream_t)stream, DEC_SPLIT_FLOOR);
+                                 q_pitch, grid_split, grid_split, rows, scale * FL_LOG2E,
+                                 (hipStream_t)stream, floor_splits);
     if (rc) return rc;
     hipLaunchKernelGGL(attn_merge_kernel<false>, dim3(n_q_heads, B * T), dim3(MG_THREADS), 0,
                        (hipStream_t)stream, pacc, pm, pd, (f16*)z, (const f16*)gate, n_q_heads,

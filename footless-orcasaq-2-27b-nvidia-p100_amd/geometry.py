@@ -38,6 +38,15 @@ GDN_NORM_EPS = 1e-6     # GDN output RMSNormGated          runtime.py:113
 # faster as 32 splits of 128.
 SPLIT_ROWS = 256
 SPLIT_MAX = 64
+# The batched decode's default: split_rows 0 asks the library for its grid
+# rule instead -- ceil(W / (B n_kv)) splits a token (W one workgroup a CU over
+# fp16 caches, two over int8 ones; at most SPLIT_MAX, at least 64 rows a
+# split), which beat the length rule at every batch size and context measured
+# (B = 4, T = 3: ~8k 32.2 -> 29.5 us, ~32k 100.2 -> 87.7, ~100k 260.5 ->
+# 245.7; B = 1 at ~8k 16.7 -> 14.4). Its split count depends on B, so a
+# sequence's values in a batch can differ in the last bits from a
+# single-sequence call's; SPLIT_ROWS keeps the length-only rule.
+DEC_SPLIT_ROWS = 0
 # The largest T the decode attention takes (MTP verify rows; runtime.py:299).
 SPLIT_T_MAX = 4
 

@@ -21,10 +21,10 @@ import ctypes
 import torch
 
 from . import _lib
-from .geometry import (ATTN_SCALE, DEC_SMAX, DEC_TMIN, GATE_OFF, GDN_CHUNK, GDN_GROUP, GDN_K,
-                       GDN_K_HEADS, GDN_NORM_EPS, GDN_V, GDN_V_HEADS, HEAD_DIM, L2_EPS, LOG2E,
-                       N_HEADS, N_KV, NORM_EPS, Q_PITCH, Q_SCALE, QKV_ROWS, ROPE_DIM, ROPE_THETA,
-                       SPLIT_MAX, SPLIT_ROWS, kv8_nbytes)
+from .geometry import (ATTN_SCALE, DEC_SMAX, DEC_SPLIT_ROWS, DEC_TMIN, GATE_OFF, GDN_CHUNK,
+                       GDN_GROUP, GDN_K, GDN_K_HEADS, GDN_NORM_EPS, GDN_V, GDN_V_HEADS, HEAD_DIM,
+                       L2_EPS, LOG2E, N_HEADS, N_KV, NORM_EPS, Q_PITCH, Q_SCALE, QKV_ROWS, ROPE_DIM,
+                       ROPE_THETA, SPLIT_MAX, SPLIT_ROWS, kv8_nbytes)
 
 F16, F32, I8 = torch.float16, torch.float32, torch.int8
 
@@ -165,14 +165,15 @@ def attn_decode_work_bytes(B: int, T: int, n_q_heads: int = N_HEADS, head_dim: i
 
 
 def attn_decode(qg, kcaches, vcaches, pos0s, *, z=None, gate: bool = True,
-                n_kv_heads: int = N_KV, scale: float = ATTN_SCALE, split_rows: int = SPLIT_ROWS,
-                split: int = SPLIT_MAX, work=None):
+                n_kv_heads: int = N_KV, scale: float = ATTN_SCALE,
+                split_rows: int = DEC_SPLIT_ROWS, split: int = SPLIT_MAX, work=None):
     """The decode / MTP-verify attention block of B sequences (runtime.py:
     2828-2862 and the per-sequence loop of 2865-2878): split partials + merge
     + sigmoid gate. qg [B, T, n_q_heads, q_pitch] fp16 with q | gate per head;
     kcaches / vcaches: per-sequence layer caches [cap, n_kv, head_dim] fp16;
-    pos0s: each sequence's first query position. Returns z [B, T, n_q_heads,
-    head_dim] fp16."""
+    pos0s: each sequence's first query position. split_rows: 0 (default) the
+    library's grid-sized split, > 0 the length-only rule (geometry.py).
+    Returns z [B, T, n_q_heads, head_dim] fp16."""
     B, T, n_q_heads, q_pitch = qg.shape
     head_dim = kcaches[0].shape[-1]
     _contig(qg, "qg")
@@ -418,7 +419,7 @@ def attention_dec_merge(pacc, pm, pd, z, *, pos0: int, T: int, n_q_heads: int = 
 
 def attn_decode_q8(qg, kcaches, vcaches, pos0s, caps, *, z=None, gate: bool = True,
                    n_kv_heads: int = N_KV, scale: float = ATTN_SCALE,
-                   split_rows: int = SPLIT_ROWS, split: int = SPLIT_MAX, work=None):
+                   split_rows: int = DEC_SPLIT_ROWS, split: int = SPLIT_MAX, work=None):
     """attn_decode over int8 caches: kcaches / vcaches per-sequence int8 buffers
     of capacities caps. Returns z [B, T, n_q_heads, 256] fp16."""
     B, T, n_q_heads, q_pitch = qg.shape

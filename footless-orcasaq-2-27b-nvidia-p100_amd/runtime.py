@@ -39,8 +39,8 @@ from typing import Protocol, Sequence
 import torch
 
 from . import ops, state_blob
-from .geometry import (GDN_K, GDN_K_HEADS, GDN_V, GDN_V_HEADS, HEAD_DIM, N_KV,
-                       QKV_ROWS, SPLIT_T_MAX, kv8_nbytes)
+from .geometry import (DEC_SPLIT_ROWS, GDN_K, GDN_K_HEADS, GDN_V, GDN_V_HEADS, HEAD_DIM,
+                       N_KV, QKV_ROWS, SPLIT_T_MAX, kv8_nbytes)
 
 F16, F32 = torch.float16, torch.float32
 
@@ -121,11 +121,15 @@ class HybridRuntime:
 
     layer_types: the schedule (full attention or linear attention a layer);
     weights: per layer index, FullWeights or GdnWeights; kv8: the int8 KV
-    format (the reference's shipped default) instead of fp16."""
+    format (the reference's shipped default) instead of fp16; split_rows: the
+    decode attention's split rule (0: sized to the grid, so a sequence's
+    attention values in a batch may differ in the last bits from its own
+    single step's; > 0: the length-only rule, batched == single bit for bit)."""
 
     def __init__(self, weights: dict, *, layer_types: Sequence[str] = LAYER_TYPES,
                  kv8: bool = False, device="cuda", max_context: int = MAX_CONTEXT,
-                 mtp_k: int = MTP_K) -> None:
+                 mtp_k: int = MTP_K, split_rows: int = DEC_SPLIT_ROWS) -> None:
+        self.split_rows = split_rows
         self.layer_types = tuple(layer_types)
         self.full_ord = {i: k for k, i in enumerate(
             j for j, t in enumerate(self.layer_types) if t == "full_attention")}
@@ -314,8 +318,9 @@ class HybridRuntime:
             ops.attn_prep(qg, k, v, wt.q_norm, wt.k_norm, kc, vc, pos0=pos0, T=T)
         if T <= SPLIT_T_MAX:
             if self.kv8:
-                return ops.attn_decode_q8(qg[None], [kc], [vc], [pos0], [lcap])[0]
-            return ops.attn_decode(qg[None], [kc], [vc], [pos0])[0]
+                return ops.attn_decode_q8(qg[None], [kc], [vc], [pos0], [lcap],
+                                          split_rows=self.split_rows)[0]
+            return ops.attn_decode(qg[None], [kc], [vc], [pos0], split_rows=self.split_rows)[0]
         # gated by the gate half of each head's q | gate row (in the merge when
         # the KV is split)
         if self.kv8:
@@ -464,9 +469,10 @@ class HybridRuntime:
                                    [st.lcap[li] for st in states], kv8=self.kv8)
                 if self.kv8:
                     z = ops.attn_decode_q8(qg[:, None], kcs, vcs, pos0s,
-                                           [st.lcap[li] for st in states])
+                                           [st.lcap[li] for st in states],
+                                           split_rows=self.split_rows)
                 else:
-                    z = ops.attn_decode(qg[:, None], kcs, vcs, pos0s)
+                    z = ops.attn_decode(qg[:, None], kcs, vcs, pos0s, split_rows=self.split_rows)
                 proj.layer_out(i, z[:, 0])
             else:
                 g, wt = self.gdn_ord[i], self.w[i]

@@ -129,8 +129,14 @@ int fl_attn_gate(void* z, const void* g, int n_heads, int head_dim, int z_pitch,
  * A token of length len gets clamp(max(len / split_rows, min(len / 64, 32)),
  * 1, split) splits: the reference's rule (kernels.cu:535-544) with a floor of
  * 64-row splits for short contexts, up to 32 of them.
- * Each token's values equal a T = 1 call at its own position, bit for bit
- * (the split depends on the token's own length only; runtime.py:2062-2069).
+ * split_rows 0 sizes the split to the grid instead: S = ceil(W / (B *
+ * n_kv_heads)) splits a token, W the device's CU count (fp16 caches) or
+ * twice it (int8), at most `split`, and at most len / 64 (>= 1) for a token
+ * of length len -- faster for every batch size measured, at the price that a
+ * token's values then depend on B (in the last bits: the partials' number).
+ * Either way each token's values equal a T = 1 call at its own position with
+ * the same B, bit for bit (runtime.py:2062-2069); with split_rows > 0 they
+ * equal single-sequence calls too.
  * Replaces the per-sequence loop of runtime.py:2865-2878 / 2828-2862. */
 size_t fl_attn_decode_work_bytes(int B, int T, int n_q_heads, int head_dim, int split);
 int fl_attn_decode(const void* qg, int q_pitch, const void* const* kcache,

@@ -102,15 +102,27 @@ def test_verify_rows_equal_t1_calls_bit_exact(fl, dev, rng, L):
 
 
 def test_batched_equals_single_bit_exact(fl, dev, rng):
+    """The length-only split rule (split_rows > 0): a batched call gives every
+    sequence the bits of its own single call. The default grid rule sizes the
+    split to the batch, so there a sequence's values may differ in the last
+    bits from its single call's; both stay within the attention bar of the
+    oracle and of each other."""
     lens = [3000, 17, 9000, 1]
     caches = [rand_cache(rng, L) for L in lens]
     qg = np.stack([rand_qg(rng, 1) for _ in lens])
     ks = [to_dev(c[0], dev) for c in caches]
     vs = [to_dev(c[1], dev) for c in caches]
-    zb = fl.ops.attn_decode(to_dev(qg, dev), ks, vs, [L - 1 for L in lens])
+    sr = fl.geometry.SPLIT_ROWS
+    zb = fl.ops.attn_decode(to_dev(qg, dev), ks, vs, [L - 1 for L in lens], split_rows=sr)
+    zg = fl.ops.attn_decode(to_dev(qg, dev), ks, vs, [L - 1 for L in lens])
     for b, L in enumerate(lens):
-        z1 = fl.ops.attn_decode(to_dev(qg[b:b + 1], dev), [ks[b]], [vs[b]], [L - 1])
+        z1 = fl.ops.attn_decode(to_dev(qg[b:b + 1], dev), [ks[b]], [vs[b]], [L - 1], split_rows=sr)
         assert torch.equal(zb[b], z1[0]), b
+        g1 = fl.ops.attn_decode(to_dev(qg[b:b + 1], dev), [ks[b]], [vs[b]], [L - 1])
+        for got in (zg[b], g1[0]):
+            err, ok = close_rel(got.cpu().numpy(), z1[0].cpu().numpy().astype(np.float64), ATOL,
+                                RTOL)
+            assert ok, f"seq {b}: grid rule against the length rule {err}"
 
 
 def test_split_count_independence(fl, dev, orc, rng):

@@ -151,10 +151,12 @@ def test_decode_q8_batched_vs_single_and_oracle(fl, dev, orc, rng):
     ks = [to_dev(c[2], dev) for c in caches]
     vs = [to_dev(c[3], dev) for c in caches]
     pos0s = [L - 1 for L in lens]
-    zb = fl.ops.attn_decode_q8(to_dev(qg, dev), ks, vs, pos0s, caps)
+    sr = fl.geometry.SPLIT_ROWS   # the length-only rule: batched == single
+    zb = fl.ops.attn_decode_q8(to_dev(qg, dev), ks, vs, pos0s, caps, split_rows=sr)
     torch.cuda.synchronize()
     for b, L in enumerate(lens):
-        z1 = fl.ops.attn_decode_q8(to_dev(qg[b:b + 1], dev), [ks[b]], [vs[b]], [L - 1], [caps[b]])
+        z1 = fl.ops.attn_decode_q8(to_dev(qg[b:b + 1], dev), [ks[b]], [vs[b]], [L - 1], [caps[b]],
+                                   split_rows=sr)
         assert torch.equal(zb[b], z1[0]), b
         want = orc.attention_decode_q8(qg[b], caches[b][2], caches[b][3], L - 1, max_pos=caps[b],
                                        scale=SCALE)

@@ -251,12 +251,17 @@ def test_runtime_stack_continuation_prefill(fl, dev, orc, kv8):
     _check_state(rt, st, ref, "after decode")
 
 
+@pytest.mark.parametrize("rule", ["length", "grid"])
 @pytest.mark.parametrize("kv8", [False, True])
-def test_runtime_batched_decode_equals_single(fl, dev, kv8):
+def test_runtime_batched_decode_equals_single(fl, dev, kv8, rule):
     """forward_batch over two sequences at different positions gives each the
-    outputs and state its own single-sequence step gives, bit for bit."""
+    state its own single-sequence step gives, bit for bit, and the same
+    outputs: bit for bit under the length-only split rule; under the default
+    grid rule (the split sized to the batch) the attention layers' outputs
+    within the attention bar and every other output bit for bit."""
     rt_mod = fl.runtime
-    rt = rt_mod.HybridRuntime(rt_mod.random_weights(seed=6), device=dev, kv8=kv8)
+    sr = fl.geometry.SPLIT_ROWS if rule == "length" else fl.geometry.DEC_SPLIT_ROWS
+    rt = rt_mod.HybridRuntime(rt_mod.random_weights(seed=6), device=dev, kv8=kv8, split_rows=sr)
     types = rt.layer_types
     a, b = rt.new_state(), rt.new_state()
     rt.forward(a, GpuProj(Inputs(types, 20, seed=2), dev), list(range(20)))
@@ -273,8 +278,12 @@ def test_runtime_batched_decode_equals_single(fl, dev, kv8):
     rt.forward(b1, pb1, [8])
     torch.cuda.synchronize()
     for i in pb.out:
-        assert np.array_equal(pb.out[i][0:1].view(np.int16), pa.out[i].view(np.int16)), i
-        assert np.array_equal(pb.out[i][1:2].view(np.int16), pb1.out[i].view(np.int16)), i
+        for got, want in ((pb.out[i][0:1], pa.out[i]), (pb.out[i][1:2], pb1.out[i])):
+            if rule == "grid" and types[i] == "full_attention":
+                err, ok = close(got, want, ATOL, RTOL)
+                assert ok, (i, err)
+            else:
+                assert np.array_equal(got.view(np.int16), want.view(np.int16)), i
     for x, y in ((a, a1), (b, b1)):
         assert x.tokens == y.tokens and x.phase == y.phase
         assert torch.equal(x.s, y.s) and torch.equal(x.conv, y.conv)

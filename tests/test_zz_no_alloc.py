@@ -24,7 +24,7 @@ def _noalloc(fl, qg, ks, vs, pos0s, z):
     lib.call("fl_attn_decode_noalloc", qg.data_ptr(), qp,
              lib.ptr_array([k.data_ptr() for k in ks]), lib.ptr_array([v.data_ptr() for v in vs]),
              lib.int_array(pos0s), lib.int_array([k.shape[0] for k in ks]), B, T, H, 4, 256,
-             float(g.ATTN_SCALE), g.SPLIT_ROWS, g.SPLIT_MAX, qg.data_ptr(), qp, g.GATE_OFF,
+             float(g.ATTN_SCALE), g.DEC_SPLIT_ROWS, g.SPLIT_MAX, qg.data_ptr(), qp, g.GATE_OFF,
              z.data_ptr(), 256, torch.cuda.current_stream().cuda_stream)
 
 
