@@ -658,6 +658,48 @@ def bench_decode_flow(torch, fl, L, kv8=True, Bq=4):
     return out
 
 
+def bench_verify_flow(torch, fl, L, kv8=True, T=3):
+    """The single-sequence serving step with MTP drafts on (the reference's
+    MTP_K = 2 round, runtime.py:2142-2215: batched rows do not speculate,
+    runtime.py:1793-1838): ONE verify forward of T = 3 rows [p, d1, d2]
+    through the 64 layers (HybridRuntime.forward(verify=True)) -- per
+    attention layer the prep and the T = 3 decode attention, per GDN layer the
+    conv rows and one launch of the delta rule (a checkpoint after every row
+    but the last) with the gated output norm. One sequence holding L cached
+    positions, captured in a HIP graph and replayed like the decode flow (each
+    replay the same round). Its HBM fraction counts the K / V rows read and
+    the GDN state read, written and checkpointed. Also timed: the attention
+    layers alone and the GDN layers alone."""
+    rtm = fl.runtime
+    dev = torch.device("cuda:0")
+    proj = _FlowProj(torch, T, dev, seed=8)
+    out = {"config": f"verify_flow_T{T}_L{L}" + ("_kv8" if kv8 else ""), "len": L}
+    scheds = {"all": rtm.LAYER_TYPES, "attn": ("full_attention",) * 16,
+              "gdn": ("linear_attention",) * 48}
+    row = 4 * 256 + 4 * 8 * 2 if kv8 else 4 * 256 * 2
+    attn_bytes = 2 * row * (L + T)
+    gdn_bytes = (2 + (T - 1)) * 48 * 128 * 128 * 4
+    for name, types in scheds.items():
+        rt = rtm.HybridRuntime(rtm.random_weights(types, seed=4, device=dev), layer_types=types,
+                               kv8=kv8, device=dev)
+        st = rt.new_state()
+        rt.grow(st, L + 16)
+        st.tokens = list(range(L))
+        st.fed = L
+        g = graph_of(torch, lambda i: rt.forward(st, proj, [1, 2, 3][:T], verify=True), 1)
+        m = measure(torch, g, 1, DECODE_SAMPLES)
+        key = "" if name == "all" else name + "_"
+        nb = {"all": 16 * attn_bytes + 48 * gdn_bytes, "attn": 16 * attn_bytes,
+              "gdn": 48 * gdn_bytes}[name]
+        out[key + "us"] = round(m["us"], 1)
+        out[key + "hbm_frac"] = round(nb / (m["us"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 3)
+        if name == "all":
+            out["rounds_s"] = round(1 / (m["us"] * 1e-6))
+        del g, st, rt
+        torch.cuda.empty_cache()
+    return out
+
+
 # ---------------------------------------------------------------------------
 # CPU baseline: PyTorch fp32 on the host's cores
 # ---------------------------------------------------------------------------
@@ -889,6 +931,8 @@ EXTRA_CONFIGS = {
     "decode_flow_B4_L8192": (bench_decode_flow, {"L": 8192, "kv8": False}),
     "decode_flow_B4_L8192_kv8": (bench_decode_flow, {"L": 8192}),
     "decode_flow_B4_L100000_kv8": (bench_decode_flow, {"L": 100000}),
+    "verify_flow_T3_L8192_kv8": (bench_verify_flow, {"L": 8192}),
+    "verify_flow_T3_L100000_kv8": (bench_verify_flow, {"L": 100000}),
 }
 
 

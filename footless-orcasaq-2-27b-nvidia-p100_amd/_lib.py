@@ -78,8 +78,9 @@ SIGNATURES = {
                          _LL, _P]),
     "fl_gdn_decode": (_I, [_P, _I, _I, _P, _PP, _PP, _IP, _P, _P, _I, _P, _P, _PP, _P, _I, _PP,
                            _LL, _I, _I, _I, _I, _I, _I, _F, _F, _P]),
-    "fl_gdn_decode_normed": (_I, [_P, _I, _P, _PP, _PP, _IP, _P, _P, _I, _P, _P, _PP, _P, _I, _P,
-                                  _P, _I, _I, _I, _I, _I, _I, _F, _F, _F, _P]),
+    "fl_gdn_decode_normed": (_I, [_P, _I, _I, _P, _PP, _PP, _IP, _P, _P, _I, _P, _P, _PP, _PP,
+                                  _LL, _P, _I, _P, _P, _I, _I, _I, _I, _I, _I, _I, _F, _F, _F,
+                                  _P]),
     "fl_gdn_chunked_work_bytes": (_SZ, [_I, _I, _I, _I, _I]),
     "fl_gdn_prefill_chunked": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I,
                                     _F, _I, _I, _P, _SZ, _P]),

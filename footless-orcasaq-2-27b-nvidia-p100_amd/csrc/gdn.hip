@@ -783,31 +783,35 @@ rmsnorm_gated_kernel(const f16* __restrict__ o, const f16* __restrict__ z,
                                          w[2 * lane], w[2 * lane + 1], eps);
 }
 
-// A decode step (T = 1, the conv in the kernel) and the output norm after it
-// in one launch: a workgroup owns a whole v head (128 rows, 8 lanes a row, 16
-// waves), so the norm over the head's 128 outputs is a reduction inside the
-// workgroup instead of a second launch. Waves 0-1 convolve and sum the
-// squares of the k head's channels, waves 2-3 the q head's, waves 4-5 the
-// head's 128 v channels, wave 6 forms the gates -- barrier -- the k / q
-// channels are normalised into LDS -- barrier -- every wave runs the delta
-// rule on its 8 rows and stores them, the rows' outputs (rounded to fp16, the
-// value the unfused step writes) go to LDS -- barrier -- wave 0 runs the
-// norm on them (gated_rms_pair, the unfused norm's arithmetic) and writes the
-// head's 128 normed values. Every value equals the unfused pair's bit for
-// bit. One workgroup a head and sequence: 48 B workgroups, so below B = 5 a
-// CU holds at most one; the small inputs are issued ahead of the state as in
-// gdn_decode_kernel.
+// A decode step (T = 1, the conv in the kernel) or a verify's rows (T <= 3,
+// the conv rows done before it, a checkpoint of the state after every row but
+// the last) with the output norm after every row, in one launch: a workgroup
+// owns a whole v head (128 rows, 8 lanes a row, 16 waves), so the norm over
+// the head's 128 outputs is a reduction inside the workgroup instead of a
+// second launch. Per row: waves 0-1 convolve (or read) and sum the squares of
+// the k head's channels, waves 2-3 the q head's, waves 4-5 the head's 128 v
+// channels, wave 6 forms the gates -- barrier -- the k / q channels are
+// normalised into LDS -- barrier -- every wave runs the delta rule on its 8
+// rows and stores them (or their checkpoint), the rows' outputs (rounded to
+// fp16, the value the unfused step writes) go to LDS -- barrier -- wave 0 runs
+// the norm on them (gated_rms_pair, the unfused norm's arithmetic) and writes
+// the head's 128 normed values while the others start the next row (that
+// barrier also ends every read of the row's LDS values). Every value equals
+// the unfused pair's bit for bit. One workgroup a head and sequence: 48 B
+// workgroups, so below B = 5 a CU holds at most one; the small inputs are
+// issued ahead of the state as in gdn_decode_kernel.
 constexpr int GN_ROWS = 128;                  // the v head's rows
 constexpr int GN_THREADS = 8 * GN_ROWS;       // 8 lanes a row
 
+template <bool CONV>
 __global__ void __launch_bounds__(GN_THREADS)
 gdn_decode_normed_kernel(const f16* __restrict__ x, int x_stride, const f16* __restrict__ conv_w,
                          GdnSeqs seqs, const float* __restrict__ ga, const float* __restrict__ gb,
                          int ab_stride, const float* __restrict__ A_log,
                          const float* __restrict__ dt_bias, const f16* __restrict__ z,
                          int z_pitch, const float* __restrict__ norm_w, f16* __restrict__ y,
-                         int y_pitch, int n_kheads, float out_scale, float l2eps, float norm_eps,
-                         int group) {
+                         int y_pitch, long long ck_step, int T, int n_kheads, float out_scale,
+                         float l2eps, float norm_eps, int group) {
     __shared__ __attribute__((aligned(16))) float ssq[8];   // k's, q's 32-channel sums of squares
     __shared__ __attribute__((aligned(16))) float snorm[2 * GR_K];   // k | q, normalised
     __shared__ float sv[GN_ROWS];                                    // the head's v values
@@ -817,35 +821,40 @@ gdn_decode_normed_kernel(const f16* __restrict__ x, int x_stride, const f16* __r
     float* const Sb = seqs.S[b];
     const f16* const cst_in = seqs.cst_in[b];
     f16* const cst_out = seqs.cst_out[b];
+    float* const Ck = seqs.Ck[b];
     const int pos0 = seqs.pos0[b];
-    asm volatile("" ::"s"(Sb), "s"(cst_in), "s"(cst_out), "s"(pos0), "s"(x), "s"(conv_w), "s"(ga),
-                 "s"(gb), "s"(A_log), "s"(dt_bias), "s"(x_stride), "s"(ab_stride), "s"(z),
+    asm volatile("" ::"s"(Sb), "s"(cst_in), "s"(cst_out), "s"(Ck), "s"(pos0), "s"(x), "s"(conv_w),
+                 "s"(ga), "s"(gb), "s"(A_log), "s"(dt_bias), "s"(x_stride), "s"(ab_stride), "s"(z),
                  "s"(z_pitch), "s"(norm_w), "s"(y), "s"(y_pitch), "s"(n_kheads), "s"(group),
-                 "s"(out_scale), "s"(l2eps), "s"(norm_eps));
+                 "s"(out_scale), "s"(l2eps), "s"(norm_eps), "s"(ck_step), "s"(T));
     __builtin_amdgcn_sched_barrier(0);
     const int hk = hv / group;
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int ri = tid >> 3, c0 = 4 * (tid & 7);
-    float* Srow = Sb + ((size_t)hv * GN_ROWS + ri) * GR_K + c0;
+    const size_t srow = ((size_t)hv * GN_ROWS + ri) * GR_K + c0;
+    float* Srow = Sb + srow;
     // waves 0-5: channel i of the k | q | v heads (uniform per wave)
     const int role = w >> 1, i = tid & 127;
     const int ch = role == 0   ? n_kheads * GR_K + hk * GR_K + i
                    : role == 1 ? hk * GR_K + i
                                : 2 * n_kheads * GR_K + hv * GN_ROWS + i;
     const bool conv_wave = w < 6;
-    const f16* x0 = x + (size_t)b * x_stride;
+    const size_t bt0 = (size_t)b * T;   // the sequence's first row
+    const f16* x0 = x + bt0 * x_stride;
     ConvIn cc;
-    if (conv_wave) cc = conv1_load(x0, conv_w, cst_in, ch);
+    if (conv_wave) {
+        if constexpr (CONV) cc = conv1_load(x0, conv_w, cst_in, ch);
+        else cc.x = x0[ch];
+    }
     const int vz = opaque_zero();
     const float dtb = dt_bias[hv + vz], A = A_log[hv + vz];
-    const size_t ab0 = (size_t)b * ab_stride + hv + vz;
+    const size_t ab0 = bt0 * ab_stride + hv + vz;
     const float ga0 = ga[ab0], gb0 = gb[ab0];
-    const size_t zo = (size_t)b * z_pitch + (size_t)hv * GN_ROWS + 2 * lane;
     f16x2 zv = {};
     float nw0 = 0.f, nw1 = 0.f;
     if (w == 0) {
-        zv = *(const f16x2*)(z + zo);
+        zv = *(const f16x2*)(z + bt0 * z_pitch + (size_t)hv * GN_ROWS + 2 * lane);
         nw0 = norm_w[2 * lane];
         nw1 = norm_w[2 * lane + 1];
     }
@@ -853,47 +862,63 @@ gdn_decode_normed_kernel(const f16* __restrict__ x, int x_stride, const f16* __r
     float reg[16];
     load_row16_nt(reg, Srow);
     __builtin_amdgcn_sched_barrier(0);
-    float xv = 0.f;
-    if (conv_wave) {
-        xv = conv1_apply(cc, pos0 > 0);
-        if (role < 2) {
-            const float tr = warp32_tree_lane0(xv * xv);
-            if ((lane & 31) == 0) ssq[tid >> 5] = tr;
-        } else {
-            sv[i] = xv;
+    auto row = [&](int t, float a_t, float b_t) {
+        const size_t bt = bt0 + t;
+        float xv = 0.f;
+        if (conv_wave) {
+            if constexpr (CONV) xv = conv1_apply(cc, pos0 > 0);
+            else xv = (float)cc.x;
+            if (role < 2) {
+                const float tr = warp32_tree_lane0(xv * xv);
+                if ((lane & 31) == 0) ssq[tid >> 5] = tr;
+            } else {
+                sv[i] = xv;
+            }
+        } else if (w == 6) {
+            const float bt_ = gdn_beta(b_t);
+            const float dt_ = gdn_decay(a_t + dtb, A);
+            if (lane == 0) {
+                sg[0] = bt_;
+                sg[1] = dt_;
+            }
         }
-    } else if (w == 6) {
-        const float bt_ = gdn_beta(gb0);
-        const float dt_ = gdn_decay(ga0 + dtb, A);
-        if (lane == 0) {
-            sg[0] = bt_;
-            sg[1] = dt_;
+        __syncthreads();
+        if (role < 2) {   // the reference's order (r0 + r2) + (r1 + r3)
+            const f32x4 r = *(const f32x4*)&ssq[4 * role];
+            const float den = sqrtf(((r[0] + r[2]) + (r[1] + r[3])) + l2eps);
+            snorm[tid] = (float)f16_sat(xv / den);
         }
+        __syncthreads();
+        const float vt = sv[ri], bet = sg[0], dec = sg[1];
+        float kk[16], qq[16];
+        gather16(kk, snorm, c0);
+        gather16(qq, snorm + GR_K, c0);
+        __builtin_amdgcn_sched_barrier(0);
+        delta_update(reg, kk, vt, bet, dec);
+        if (t == T - 1)
+            store_row16_nt(Srow, reg);
+        else if (Ck != nullptr)
+            store_row16_nt(Ck + (size_t)t * ck_step + srow, reg);
+        const float o = delta_out(reg, qq);
+        if (c0 == 0) so[ri] = (float)f16_sat(o * out_scale);
+        __syncthreads();
+        if (w == 0) {
+            const float x0v = so[2 * lane], x1v = so[2 * lane + 1];
+            *(f16x2*)(y + bt * y_pitch + (size_t)hv * GN_ROWS + 2 * lane) =
+                gated_rms_pair(x0v, x1v, (float)zv[0], (float)zv[1], nw0, nw1, norm_eps);
+        }
+    };
+    row(0, ga0, gb0);
+    for (int t = 1; t < T; ++t) {   // verify rows (the conv in the kernel is T == 1 only)
+        const size_t bt = bt0 + t;
+        if (conv_wave) cc.x = x[bt * x_stride + ch];
+        if (w == 0) zv = *(const f16x2*)(z + bt * z_pitch + (size_t)hv * GN_ROWS + 2 * lane);
+        row(t, ga[bt * ab_stride + hv + vz], gb[bt * ab_stride + hv + vz]);
     }
-    __syncthreads();
-    if (role < 2) {   // the reference's order (r0 + r2) + (r1 + r3)
-        const f32x4 r = *(const f32x4*)&ssq[4 * role];
-        const float den = sqrtf(((r[0] + r[2]) + (r[1] + r[3])) + l2eps);
-        snorm[tid] = (float)f16_sat(xv / den);
+    if constexpr (CONV) {   // T == 1
+        if (conv_wave && (role == 2 || hv % group == 0))   // one v head a k head stores its ring
+            conv1_ring_store(cc, pos0 > 0, cst_out, ch);
     }
-    __syncthreads();
-    const float vt = sv[ri], bt = sg[0], dt = sg[1];
-    float kk[16], qq[16];
-    gather16(kk, snorm, c0);
-    gather16(qq, snorm + GR_K, c0);
-    __builtin_amdgcn_sched_barrier(0);
-    delta_update(reg, kk, vt, bt, dt);
-    store_row16_nt(Srow, reg);
-    const float o = delta_out(reg, qq);
-    if (c0 == 0) so[ri] = (float)f16_sat(o * out_scale);
-    __syncthreads();
-    if (w == 0) {
-        const float x0v = so[2 * lane], x1v = so[2 * lane + 1];
-        *(f16x2*)(y + (size_t)b * y_pitch + (size_t)hv * GN_ROWS + 2 * lane) =
-            gated_rms_pair(x0v, x1v, (float)zv[0], (float)zv[1], nw0, nw1, norm_eps);
-    }
-    if (conv_wave && (role == 2 || hv % group == 0))   // one v head a k head stores its ring
-        conv1_ring_store(cc, pos0 > 0, cst_out, ch);
 }
 
 // The same norm, 16-byte aligned rows: 16 lanes a row (lane j of the row holds
@@ -1216,17 +1241,17 @@ int fl_gdn_decode(const void* x, int x_stride, int conv_fused, const void* conv_
     return fl::check_launch("gdn_decode");
 }
 
-int fl_gdn_decode_normed(const void* x, int x_stride, const void* conv_w,
+int fl_gdn_decode_normed(const void* x, int x_stride, int conv_fused, const void* conv_w,
                          const void* const* cst_in, void* const* cst_out, const int* pos0,
                          const float* a, const float* b, int ab_stride, const float* A_log,
-                         const float* dt_bias, float* const* S, const void* z, int z_pitch,
-                         const float* norm_w, void* y, int y_pitch, int B, int n_kheads,
-                         int n_vheads, int K, int V, float out_scale, float l2eps, float norm_eps,
+                         const float* dt_bias, float* const* S, float* const* Ck,
+                         long long ck_step, const void* z, int z_pitch, const float* norm_w,
+                         void* y, int y_pitch, int B, int T, int n_kheads, int n_vheads, int K,
+                         int V, float out_scale, float l2eps, float norm_eps,
                          fl_stream_t stream) {
-    FL_REQUIRE(x && conv_w && cst_in && cst_out && pos0 && a && b && A_log && dt_bias && S && z &&
-                   norm_w && y,
-               "null pointer");
+    FL_REQUIRE(x && pos0 && a && b && A_log && dt_bias && S && z && norm_w && y, "null pointer");
     FL_REQUIRE(B >= 1 && B <= FL_MAX_SEQS, "1 <= B <= FL_MAX_SEQS");
+    FL_REQUIRE(T >= 1 && T <= 3, "1 <= T <= 3");
     FL_REQUIRE(K == GR_K && V == GN_ROWS, "K and V must be 128");
     FL_REQUIRE(n_kheads >= 1 && n_vheads >= 1 && n_vheads % n_kheads == 0,
                "n_vheads % n_kheads == 0");
@@ -1238,21 +1263,38 @@ int fl_gdn_decode_normed(const void* x, int x_stride, const void* conv_w,
     FL_REQUIRE(((uintptr_t)z & 3u) == 0 && ((uintptr_t)y & 3u) == 0 && ((uintptr_t)norm_w & 7u) == 0,
                "aligned z, y, norm_w");
     FL_REQUIRE(norm_eps >= 0.f, "norm_eps >= 0");
+    FL_REQUIRE(!conv_fused || (T == 1 && conv_w && cst_in && cst_out), "conv_fused: T == 1 and "
+               "conv_w, cst_in, cst_out");
     GdnSeqs seqs = {};
     for (int i = 0; i < B; ++i) {
         FL_REQUIRE(S[i] && aligned16(S[i]), "16-byte aligned S[b]");
         FL_REQUIRE(pos0[i] >= 0, "pos0 >= 0");
-        FL_REQUIRE(cst_in[i] && cst_out[i] && cst_in[i] != cst_out[i],
-                   "cst_in[b], cst_out[b] distinct");
         seqs.S[i] = S[i];
         seqs.pos0[i] = pos0[i];
-        seqs.cst_in[i] = (const f16*)cst_in[i];
-        seqs.cst_out[i] = (f16*)cst_out[i];
+        if (conv_fused) {
+            FL_REQUIRE(cst_in[i] && cst_out[i] && cst_in[i] != cst_out[i],
+                       "cst_in[b], cst_out[b] distinct");
+            seqs.cst_in[i] = (const f16*)cst_in[i];
+            seqs.cst_out[i] = (f16*)cst_out[i];
+        }
+        if (Ck != nullptr && Ck[i] != nullptr) {
+            FL_REQUIRE(aligned16(Ck[i]) && ck_step % 4 == 0, "16-byte aligned Ck");
+            seqs.Ck[i] = Ck[i];
+        }
     }
-    hipLaunchKernelGGL(gdn_decode_normed_kernel, dim3(n_vheads, B), dim3(GN_THREADS), 0,
-                       (hipStream_t)stream, (const f16*)x, x_stride, (const f16*)conv_w, seqs, a, b,
-                       ab_stride, A_log, dt_bias, (const f16*)z, z_pitch, norm_w, (f16*)y, y_pitch,
-                       n_kheads, out_scale, l2eps, norm_eps, n_vheads / n_kheads);
+    const int group = n_vheads / n_kheads;
+    if (conv_fused)
+        hipLaunchKernelGGL(gdn_decode_normed_kernel<true>, dim3(n_vheads, B), dim3(GN_THREADS), 0,
+                           (hipStream_t)stream, (const f16*)x, x_stride, (const f16*)conv_w, seqs,
+                           a, b, ab_stride, A_log, dt_bias, (const f16*)z, z_pitch, norm_w,
+                           (f16*)y, y_pitch, ck_step, T, n_kheads, out_scale, l2eps, norm_eps,
+                           group);
+    else
+        hipLaunchKernelGGL(gdn_decode_normed_kernel<false>, dim3(n_vheads, B), dim3(GN_THREADS), 0,
+                           (hipStream_t)stream, (const f16*)x, x_stride, (const f16*)conv_w, seqs,
+                           a, b, ab_stride, A_log, dt_bias, (const f16*)z, z_pitch, norm_w,
+                           (f16*)y, y_pitch, ck_step, T, n_kheads, out_scale, l2eps, norm_eps,
+                           group);
     return fl::check_launch("gdn_decode_normed");
 }
 

@@ -617,36 +617,51 @@ def gdn_decode(x, S, a, b, A_log, dt_bias, y=None, *, T: int, pos0s, conv_fused:
     return y
 
 
-def gdn_decode_normed(x, S, a, b, A_log, dt_bias, z, norm_w, y=None, *, pos0s, conv_w, cst_in,
-                      cst_out, n_kheads: int = GDN_K_HEADS, n_vheads: int = GDN_V_HEADS,
-                      K: int = GDN_K, V: int = GDN_V, x_stride: int = QKV_ROWS,
-                      ab_stride: int = GDN_V_HEADS, out_scale: float = Q_SCALE,
-                      l2eps: float = L2_EPS, norm_eps: float = GDN_NORM_EPS):
-    """A plain decode step of B sequences and its output norm in one launch
-    (gdn_scan_rows_f with gdn_conv1, kernels.cu:2916-3070, then rmsnorm_gated,
-    kernels.cu:335-358, as runtime.py:3040-3053 and 3063-3065 run them): the
-    values gdn_decode(conv_fused=True) followed by rmsnorm_gated give. x [B,
-    x_stride] fp16 raw q|k|v rows; z [B, n_vheads * V] fp16 (rows at z's
-    stride); S, cst_in, cst_out: lists of B buffers; a, b [B, ab_stride] fp32.
-    Returns y [B, n_vheads * V] fp16 (new unless given)."""
+def gdn_decode_normed(x, S, a, b, A_log, dt_bias, z, norm_w, y=None, *, pos0s, T: int = 1,
+                      conv_fused: bool = True, conv_w=None, cst_in=None, cst_out=None, ck=None,
+                      ck_step: int = 0, n_kheads: int = GDN_K_HEADS,
+                      n_vheads: int = GDN_V_HEADS, K: int = GDN_K, V: int = GDN_V,
+                      x_stride: int = QKV_ROWS, ab_stride: int = GDN_V_HEADS,
+                      out_scale: float = Q_SCALE, l2eps: float = L2_EPS,
+                      norm_eps: float = GDN_NORM_EPS):
+    """A decode step or a verify round of B sequences and its output norm in
+    one launch (gdn_scan_rows_f, kernels.cu:2916-3070, then rmsnorm_gated,
+    kernels.cu:335-358, as runtime.py:3040-3053 / 3131-3142 and 3063-3065
+    run them): the values gdn_decode followed by rmsnorm_gated give. x [B * T,
+    x_stride] fp16 -- the raw q|k|v rows when conv_fused (T == 1, the conv
+    from cst_in[b] into cst_out[b]), else the conv output; z [B * T, n_vheads
+    * V] fp16 (rows at z's stride); S: list of B states; a, b [B * T,
+    ab_stride] fp32; ck: optional list of B checkpoint buffers (a verify's
+    state after every row but the last, at ck + t * ck_step). Returns y [B *
+    T, n_vheads * V] fp16 (new unless given)."""
     B = len(S)
+    rows = B * T
     _contig(x, "x"), _contig(a, "a"), _contig(b, "b")
     width = n_vheads * V
     if y is None:
-        y = torch.empty((B, width), dtype=F16, device=x.device)
-    # one row a sequence, the heads contiguous inside it (view raises if not)
-    z_pitch, y_pitch = z.view(B, width).stride(0), y.view(B, width).stride(0)
+        y = torch.empty((rows, width), dtype=F16, device=x.device)
+    # one row a (sequence, token), the heads contiguous inside it (view raises if not)
+    z_pitch, y_pitch = z.view(rows, width).stride(0), y.view(rows, width).stride(0)
     state = n_vheads * V * K
-    ci = _lib.ptr_array([_ptr(c, F16, "cst_in[b]", x_stride * 3) for c in cst_in])
-    co = _lib.ptr_array([_ptr(c, F16, "cst_out[b]", x_stride * 3) for c in cst_out])
-    _lib.call("fl_gdn_decode_normed", _ptr(x, F16, "x", B * x_stride), x_stride,
-              _ptr(conv_w, F16, "conv_w", x_stride * 4), ci, co, _lib.int_array(pos0s),
-              _ptr(a, F32, "a", B * ab_stride), _ptr(b, F32, "b", B * ab_stride), ab_stride,
+    ci = co = None
+    if conv_fused:
+        if cst_in is None or cst_out is None or conv_w is None:
+            raise ValueError("conv_fused needs conv_w, cst_in and cst_out")
+        ci = _lib.ptr_array([_ptr(c, F16, "cst_in[b]", x_stride * 3) for c in cst_in])
+        co = _lib.ptr_array([_ptr(c, F16, "cst_out[b]", x_stride * 3) for c in cst_out])
+    ck_arr = None
+    if ck is not None:
+        ck_arr = _lib.ptr_array([_ptr(c, F32, "ck[b]", max(T - 2, 0) * ck_step + state)
+                                 if c is not None else None for c in ck])
+    _lib.call("fl_gdn_decode_normed", _ptr(x, F16, "x", rows * x_stride), x_stride,
+              1 if conv_fused else 0, _ptr(conv_w, F16, "conv_w", x_stride * 4), ci, co,
+              _lib.int_array(pos0s), _ptr(a, F32, "a", rows * ab_stride),
+              _ptr(b, F32, "b", rows * ab_stride), ab_stride,
               _ptr(A_log, F32, "A_log", n_vheads), _ptr(dt_bias, F32, "dt_bias", n_vheads),
-              _lib.ptr_array([_ptr(s, F32, "S[b]", state) for s in S]),
-              _ptr(z, F16, "z", (B - 1) * z_pitch + width), z_pitch,
-              _ptr(norm_w, F32, "norm_w", V), _ptr(y, F16, "y", (B - 1) * y_pitch + width),
-              y_pitch, B, n_kheads, n_vheads, K, V, float(out_scale), float(l2eps),
+              _lib.ptr_array([_ptr(s, F32, "S[b]", state) for s in S]), ck_arr, ck_step,
+              _ptr(z, F16, "z", (rows - 1) * z_pitch + width), z_pitch,
+              _ptr(norm_w, F32, "norm_w", V), _ptr(y, F16, "y", (rows - 1) * y_pitch + width),
+              y_pitch, B, T, n_kheads, n_vheads, K, V, float(out_scale), float(l2eps),
               float(norm_eps), _stream())
     return y
 

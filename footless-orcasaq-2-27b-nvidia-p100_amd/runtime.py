@@ -334,9 +334,9 @@ class HybridRuntime:
         gated output norm. Verify (T <= 1 + mtp_k): the conv rows leave row
         0's state in place in conv[phase], row 1's in conv[phase ^ 1], row 2's
         in the spare; the fused step keeps the recurrent state after each row
-        but the last as a checkpoint. Prefill: conv over the chunk, the q / k
-        L2 norm, the gates, and the chunked WY scan. Verify and prefill end
-        with the gated output norm."""
+        but the last as a checkpoint; then the gated output norm. Prefill:
+        conv over the chunk, the q / k L2 norm, the chunked WY scan with the
+        gates, then the gated output norm."""
         g = self.gdn_ord[i]
         wt = self.w[i]
         S = st.s[g]
@@ -345,27 +345,27 @@ class HybridRuntime:
             return ops.gdn_decode_normed(qkv, [S], a, b, wt.A_log, wt.dt_bias, zg, wt.norm_w,
                                          pos0s=[pos0], conv_w=wt.conv_w, cst_in=[cin],
                                          cst_out=[cout]).view(1, GDN_V_HEADS, GDN_V)
+        c = torch.empty_like(qkv)
         if verify:
-            c = torch.empty_like(qkv)
+            # the one-launch step + norm gives one sequence's rows 48 workgroups
+            # (a v head each): slower here than the 192 of the step alone
             ops.conv1d_causal_rows(qkv, wt.conv_w, cin, c, cin, cout, self.snap_c[g], T=T,
                                    pos0=pos0)
             y = ops.gdn_decode(c[None], [S], a[None], b[None], wt.A_log, wt.dt_bias, T=T,
                                pos0s=[pos0], ck=[self.snap_s[0, g]],
                                ck_step=self.n_gdn * self.layer_s_elems)[0]
-        else:
-            c = torch.empty_like(qkv)
-            ops.conv1d_causal(qkv, wt.conv_w, cin, c, cout, T=T, pos0=pos0)
-            # the L2 norm of the q and k head rows (the reference launches it
-            # over all 80 head-sized rows of the conv'd row, runtime.py:3070,
-            # and reads back only these 32: the same bits for them)
-            ln = torch.empty_like(c)
-            ops.l2norm_scaled_strided(c, ln, rows=2 * GDN_K_HEADS, token_stride=QKV_ROWS, T=T)
-            # the gates formed from a, b inside the scan (gdn_scalars' values)
-            qn, kn = GDN_K_HEADS * GDN_K, 2 * GDN_K_HEADS * GDN_K
-            y = ops.gdn_prefill_chunked_logits(ln[:, :qn], ln[:, qn:kn], c[:, kn:], a, b,
-                                               wt.A_log, wt.dt_bias, S, T=T)
-        yn = ops.rmsnorm_gated(y.view(T, GDN_V_HEADS, GDN_V), zg, wt.norm_w, T=T)
-        return yn
+            return ops.rmsnorm_gated(y.view(T, GDN_V_HEADS, GDN_V), zg, wt.norm_w, T=T)
+        ops.conv1d_causal(qkv, wt.conv_w, cin, c, cout, T=T, pos0=pos0)
+        # the L2 norm of the q and k head rows (the reference launches it over
+        # all 80 head-sized rows of the conv'd row, runtime.py:3070, and reads
+        # back only these 32: the same bits for them)
+        ln = torch.empty_like(c)
+        ops.l2norm_scaled_strided(c, ln, rows=2 * GDN_K_HEADS, token_stride=QKV_ROWS, T=T)
+        # the gates formed from a, b inside the scan (gdn_scalars' values)
+        qn, kn = GDN_K_HEADS * GDN_K, 2 * GDN_K_HEADS * GDN_K
+        y = ops.gdn_prefill_chunked_logits(ln[:, :qn], ln[:, qn:kn], c[:, kn:], a, b, wt.A_log,
+                                           wt.dt_bias, S, T=T)
+        return ops.rmsnorm_gated(y.view(T, GDN_V_HEADS, GDN_V), zg, wt.norm_w, T=T)
 
     def _ensure_verify_buffers(self) -> None:
         if self.snap_s is None:

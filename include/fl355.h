@@ -416,23 +416,31 @@ int fl_gdn_decode(const void* x, int x_stride, int conv_fused, const void* conv_
 int fl_rmsnorm_gated(const void* o, const void* z, const float* w, void* y, int n, int rows,
                      int pitch, int T, float eps, fl_stream_t stream);
 
-/* ---- GDN decode step with its output norm -----------------------------------
- * fl_gdn_decode with conv_fused = 1 and T = 1, followed by fl_rmsnorm_gated
- * over its output, in one launch: y[b] = rmsnorm_gated(the step's output of
- * sequence b, z[b], norm_w), bit for bit the pair's values. The step's own
- * fp16 output is not written. z [B][z_pitch] f16 (the gate, head hv at
- * hv*V), y [B][y_pitch] f16; the other arguments as fl_gdn_decode's.
+/* ---- GDN decode / verify step with its output norm --------------------------
+ * fl_gdn_decode (T <= 3 rows a sequence; conv_fused = 1 at T == 1, else x is
+ * the conv output and Ck receives the per-row checkpoints) followed by
+ * fl_rmsnorm_gated over every output row, in one launch: y[b][t] =
+ * rmsnorm_gated(the step's output row, z[b][t], norm_w), bit for bit the
+ * pair's values; the step's own fp16 output is not written. z [B][T][z_pitch]
+ * f16 (the gate, head hv at hv*V), y [B][T][y_pitch] f16; the other arguments
+ * as fl_gdn_decode's (cst_in / cst_out and conv_w only read when conv_fused).
  * Replaces the pair kernels.cu:2954-3070 gdn_scan_rows_f (+ gdn_conv1
- * 2916-2941) then kernels.cu:335-358 rmsnorm_gated as a decode step runs them
- * (runtime.py:3040-3053, then 3063-3065). K == V == 128, B <= FL_MAX_SEQS;
- * z and y 4-byte aligned, even pitches, norm_w 8-byte aligned. */
-int fl_gdn_decode_normed(const void* x, int x_stride, const void* conv_w,
+ * 2916-2941) then kernels.cu:335-358 rmsnorm_gated as a decode step or a
+ * verify round runs them (runtime.py:3040-3053 / 3131-3142, then 3063-3065 /
+ * 3143-3145). One workgroup a (sequence, v head): the pair is faster where B
+ * is small and T > 1 (one sequence's verify rows: 14.3 against 13.2 us a
+ * layer with the conv rows), the one launch where B * n_vheads workgroups
+ * fill the CUs or T == 1 (B = 1..8 decode steps: 5.0 against 6.0 .. 11.7
+ * against 13.3 us). K == V == 128, B <= FL_MAX_SEQS; z and y 4-byte aligned,
+ * even pitches, norm_w 8-byte aligned. */
+int fl_gdn_decode_normed(const void* x, int x_stride, int conv_fused, const void* conv_w,
                          const void* const* cst_in, void* const* cst_out, const int* pos0,
                          const float* a, const float* b, int ab_stride, const float* A_log,
-                         const float* dt_bias, float* const* S, const void* z, int z_pitch,
-                         const float* norm_w, void* y, int y_pitch, int B, int n_kheads,
-                         int n_vheads, int K, int V, float out_scale, float l2eps,
-                         float norm_eps, fl_stream_t stream);
+                         const float* dt_bias, float* const* S, float* const* Ck,
+                         long long ck_step, const void* z, int z_pitch, const float* norm_w,
+                         void* y, int y_pitch, int B, int T, int n_kheads, int n_vheads, int K,
+                         int V, float out_scale, float l2eps, float norm_eps,
+                         fl_stream_t stream);
 
 /* ---- GDN chunked prefill --------------------------------------------------
  * Chunked (WY / UT transform) GDN prefill: the same recurrence as

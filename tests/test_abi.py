@@ -117,14 +117,16 @@ def test_argument_checks_refuse_before_launch(fl):
     pq = fl._lib.ptr_array([0x3000] * 17)
     p0 = fl._lib.int_array([5] * 17)
 
-    def normed(B, V, cin, z_pitch):
-        return _call(fl, "fl_gdn_decode_normed", fake, 10240, fake, cin, pq, p0, fake, fake, 48,
-                     fake, fake, pp, fake, z_pitch, fake, fake, 6144, B, 16, 48, 128, V, 0.088,
-                     1e-6, 1e-6, None)
+    def normed(B, V, cin, z_pitch, T=1, conv=1):
+        return _call(fl, "fl_gdn_decode_normed", fake, 10240, conv, fake, cin, pq, p0, fake, fake,
+                     48, fake, fake, pp, None, 0, fake, z_pitch, fake, fake, 6144, B, T, 16, 48,
+                     128, V, 0.088, 1e-6, 1e-6, None)
     assert normed(4, 64, pp, 6144) == 1
     assert normed(17, 128, pp, 6144) == 1
     assert normed(2, 128, pq, 6144) == 1 and b"distinct" in lib.fl_last_error()
     assert normed(2, 128, pp, 6145) == 1 and b"pitch" in lib.fl_last_error()
+    assert normed(1, 128, pp, 6144, T=4, conv=0) == 1 and b"T <= 3" in lib.fl_last_error()
+    assert normed(1, 128, pp, 6144, T=3, conv=1) == 1 and b"conv_fused" in lib.fl_last_error()
 
 
 def test_work_size_queries(fl):

@@ -662,3 +662,37 @@ def test_chunked_logits_equals_gates_then_scan(fl, dev, rng, T, ab_stride):
     assert torch.isfinite(y1.float()).all()
     assert torch.equal(y1, y2), f"T={T}: y differs"
     assert torch.equal(S1, S2), f"T={T}: state differs"
+
+
+@pytest.mark.parametrize("B,T", [(1, 3), (1, 2), (3, 3)])
+def test_verify_normed_equals_verify_then_norm(fl, dev, rng, B, T):
+    """A verify round's rows through the one-launch step + output norm (the
+    conv rows done before it) against gdn_decode over the same rows with
+    checkpoints, then rmsnorm_gated: the normed rows, the final state and
+    every checkpoint bit for bit."""
+    A_log = (rng.standard_normal(NV) * 0.3).astype(np.float32)
+    dt = (rng.standard_normal(NV) * 0.3).astype(np.float32)
+    nw = (1 + rng.standard_normal(128) * 0.2).astype(np.float32)
+    width = NV * 128
+    c = (rng.standard_normal((B * T, ROW)) * 2).astype(np.float16)
+    a = rng.standard_normal((B * T, NV)).astype(np.float32)
+    bb = rng.standard_normal((B * T, NV)).astype(np.float32)
+    z = (rng.standard_normal((B * T, width)) * 2).astype(np.float16)
+    S0 = (rng.standard_normal((B, NV, 128, 128)) * 0.02).astype(np.float32)
+    cd, ad, bd, zd = to_dev(c, dev), to_dev(a, dev), to_dev(bb, dev), to_dev(z, dev)
+    Ad, dtd, nwd = to_dev(A_log, dev), to_dev(dt, dev), to_dev(nw, dev)
+    state = NV * 128 * 128
+    Sf = [to_dev(S0[i], dev) for i in range(B)]
+    Su = [to_dev(S0[i], dev) for i in range(B)]
+    ckf = [torch.full((max(T - 1, 1), NV, 128, 128), 9.0, device=dev) for _ in range(B)]
+    cku = [t.clone() for t in ckf]
+    yf = fl.ops.gdn_decode_normed(cd, Sf, ad, bd, Ad, dtd, zd, nwd, pos0s=[50] * B, T=T,
+                                  conv_fused=False, ck=ckf, ck_step=state)
+    yu = fl.ops.gdn_decode(cd.view(B, T, ROW), Su, ad.view(B, T, NV), bd.view(B, T, NV), Ad, dtd,
+                           T=T, pos0s=[50] * B, ck=cku, ck_step=state)
+    yn = fl.ops.rmsnorm_gated(yu.view(B * T, NV, 128), zd, nwd, T=B * T)
+    torch.cuda.synchronize()
+    assert torch.equal(yf, yn.view(B * T, width)), "normed rows differ"
+    for i in range(B):
+        assert torch.equal(Sf[i], Su[i]), f"seq {i}: state differs"
+        assert torch.equal(ckf[i], cku[i]), f"seq {i}: checkpoints differ"
