@@ -987,21 +987,24 @@ int dec_cu_count() {
     return cached[dev];
 }
 
-// split_rows 0, the grid rule: S = ceil(W / (B n_kv)) splits a token (at most
-// `split`), W one workgroup a CU over fp16 caches and two over int8 ones,
-// fewer where the token's length leaves under 64 rows a split. Swept at B =
-// 1..16 and ~8k..~100k (forced split counts, graph-timed): the fp16 kernel is
-// fastest at one workgroup a CU (B = 4 at ~32k: 16 splits 85.3 us, 32: 88.9,
-// 64: 91.4; B = 1 at ~8k: 64 splits 14.4 us, 32: 16.7), the int8 kernel, with
-// three waves a SIMD, at two (B = 4 at ~32k: 32 splits 67.8 us, 16: 73.4,
-// 64: 69.1). A token's split count then depends on B as well as its length,
-// so a batched call's values can differ in the last bits from single calls';
+// split_rows 0, the grid rule: S = floor(W / (B n_kv)) splits a token (at
+// least 1, at most `split`), W one workgroup a CU over fp16 caches and two
+// over int8 ones, fewer where the token's length leaves under 64 rows a
+// split. Swept at B = 1..16 and ~8k..~100k (forced split counts,
+// graph-timed): the fp16 kernel is fastest at one workgroup a CU (B = 4 at
+// ~32k: 16 splits 85.3 us, 32: 88.9, 64: 91.4; B = 1 at ~8k: 64 splits
+// 14.4 us, 32: 16.7), the int8 kernel, with three waves a SIMD, at two (B =
+// 4 at ~32k: 32 splits 67.8 us, 16: 73.4, 64: 69.1). The optimum is sharp and
+// a partial second round costs more than idle CUs (B = 4, T = 3 at ~8k / ~100k:
+// 14 splits 30.5 / 260.8 us, 16: 29.2 / 244.6, 18: 40.8 / 341.9), hence the
+// floor. A token's split count then depends on B as well as its length, so a
+// batched call's values can differ in the last bits from single calls';
 // split_rows > 0 keeps the length-only rule.
 constexpr int DEC_GRID_RULE = 0;
 
 void grid_rule(bool q8, int B, int n_kv, int split, int& rows, int& smax, int& floor_splits) {
     const int W = (q8 ? 2 : 1) * dec_cu_count();
-    const int S = (W + B * n_kv - 1) / (B * n_kv);
+    const int S = W / (B * n_kv);
     smax = S < 1 ? 1 : (S > split ? split : S);
     rows = DEC_FINE_ROWS;
     floor_splits = 0;

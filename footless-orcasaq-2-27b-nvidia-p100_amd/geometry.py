@@ -39,7 +39,7 @@ GDN_NORM_EPS = 1e-6     # GDN output RMSNormGated          runtime.py:113
 SPLIT_ROWS = 256
 SPLIT_MAX = 64
 # The batched decode's default: split_rows 0 asks the library for its grid
-# rule instead -- ceil(W / (B n_kv)) splits a token (W one workgroup a CU over
+# rule instead -- floor(W / (B n_kv)) splits a token (W one workgroup a CU over
 # fp16 caches, two over int8 ones; at most SPLIT_MAX, at least 64 rows a
 # split), which beat the length rule at every batch size and context measured
 # (B = 4, T = 3: ~8k 32.2 -> 29.5 us, ~32k 100.2 -> 87.7, ~100k 260.5 ->

@@ -129,8 +129,8 @@ int fl_attn_gate(void* z, const void* g, int n_heads, int head_dim, int z_pitch,
  * A token of length len gets clamp(max(len / split_rows, min(len / 64, 32)),
  * 1, split) splits: the reference's rule (kernels.cu:535-544) with a floor of
  * 64-row splits for short contexts, up to 32 of them.
- * split_rows 0 sizes the split to the grid instead: S = ceil(W / (B *
- * n_kv_heads)) splits a token, W the device's CU count (fp16 caches) or
+ * split_rows 0 sizes the split to the grid instead: S = floor(W / (B *
+ * n_kv_heads)) (>= 1) splits a token, W the device's CU count (fp16 caches) or
  * twice it (int8), at most `split`, and at most len / 64 (>= 1) for a token
  * of length len -- faster for every batch size measured, at the price that a
  * token's values then depend on B (in the last bits: the partials' number).
